@@ -1,0 +1,198 @@
+"""Benchmark: SeeML LoRA update steps on one MI355X through the gfx950 backend.
+
+A "step" is one TrainImpl iteration of the compiled plan (update_engine.cc:
+736-753): step scalars, device-resident batch staged into the plan's I/O
+slots, the train program replayed as one hipGraph, the loss read back and
+checked. Inputs are resident in HBM before timing starts.
+
+Default workload: BASELINE configs[1] (C2, the single large LoRA linear
+layer, 8192 x 4096 x 4096, r16). --config selects c1..c5.
+
+Emits ONE JSON line (rank 0) with, besides the driver's fields:
+  roofline      the dominant kernel (largest share of step time) measured
+                with HIP events on the engine stream: algorithmic FLOPs (or
+                bytes) of one launch / mean launch time, vs MI355X peak
+  cpu_baseline  the reference's own executor kernels (oracle/_ref, built
+                from the reference sources) timed on this host on a bounded
+                sample of the same workload
+  kernels       per-opcode time split, dense-GEMM MFMA utilisation and the
+                HBM throughput of the bandwidth-bound kernels
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "see-ml_amd"))
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, plan, cores, budget_s=20.0):
+    """The reference executor (oracle/_ref: runtime/executor/*.cc compiled
+    from the reference sources) running the same plan on host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle
+    from helpers import HostPlanRunner
+    from seeml_amd import configs
+
+    if oracle.ref_available():
+        lib, kind = oracle.ref(), "reference"
+        lib.set_threads(cores)
+    else:
+        lib, kind, cores = oracle.oracle(), "port", 1
+    r = HostPlanRunner(plan, lib)
+    x, y = configs.batch(w, 0)
+    t0 = time.perf_counter()
+    r.train_step(x, y)  # warm-up (page-in)
+    warm = time.perf_counter() - t0
+    n = max(1, min(5, int(budget_s / max(warm, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        r.train_step(x, y)
+    dt = time.perf_counter() - t0
+    tokens = w.cfg.batch * n
+    return dict(value=tokens / dt, unit="tokens/s", cores=cores, kind=kind,
+                sample=f"{n} full {w.name} train steps ({w.cfg.batch} tokens each) of the same "
+                       f"plan after 1 warm-up step; {dt / n * 1e3:.1f} ms/step on the host")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-autotune", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-reps", type=int, default=3)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not "
+              "supported (the multi-GPU design is described, not built)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from seeml_amd import DeviceUpdateEngine, PROGRAM_TRAIN, configs, planner, workmodel
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    w = configs.make(args.config)
+    t0 = time.perf_counter()
+    plan = planner.compile_update(w.model, w.cfg)
+    log(f"plan {w.name}: {len(plan.train)} train instrs, arena {plan.header['arena_size'] / 1e9:.2f} GB, "
+        f"rodata {plan.header['rodata_size'] / 1e9:.2f} GB ({time.perf_counter() - t0:.1f}s)")
+    e = DeviceUpdateEngine(plan.blob)
+    log("engine open")
+    if not args.no_autotune:
+        t0 = time.perf_counter()
+        e.autotune(16)
+        log(f"autotuned GEMM tiles ({time.perf_counter() - t0:.1f}s)")
+
+    dev = torch.device("cuda:0")
+    batches = []
+    for s in range(2):
+        x, y = configs.batch(w, s)
+        batches.append((torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev)))
+    torch.cuda.synchronize()
+
+    losses = []
+    for s in range(args.warmup):
+        xb, yb = batches[s % 2]
+        losses.append(e.train_step(xb, yb))
+    log(f"warmup done, loss {losses[-1] if losses else float('nan'):.6f}")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        xb, yb = batches[s % 2]
+        losses.append(e.train_step(xb, yb))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    tokens_per_s = w.cfg.batch * args.steps / dt
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.1f} tok/s")
+
+    # Per-instruction breakdown (eager replay with events; outside the timed region).
+    ms = e.profile(PROGRAM_TRAIN, reps=args.profile_reps)
+    summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS)
+    rows = summ["rows"]
+    dom = max(range(len(rows)), key=lambda i: rows[i]["ms"])
+    dom_row = rows[dom]
+    dom_ms = e.time_instruction(PROGRAM_TRAIN, dom, reps=10)
+    if dom_row["cls"] == "mfma" or (dom_row["cls"] == "attn" and dom_row["flops"]):
+        achieved = dom_row["flops"] / (dom_ms * 1e-3) / 1e12
+        roof = dict(bound="mfma", achieved=round(achieved, 3), peak=PEAK_FP32_MFMA_TFLOPS,
+                    unit="TFLOP/s", frac=round(achieved / PEAK_FP32_MFMA_TFLOPS, 4))
+    else:
+        achieved = dom_row["bytes"] / (dom_ms * 1e-3) / 1e9
+        roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBPS, unit="GB/s",
+                    frac=round(achieved / PEAK_HBM_GBPS, 4))
+    roof.update(kernel=f"{dom_row['op']} {'x'.join(map(str, dom_row['shape']))} "
+                       f"(instruction {dom}, {e.gemm_choice(PROGRAM_TRAIN, dom) if dom_row['op'] in workmodel.GEMMS else ''})".replace(", )", ")"),
+                launch_ms=round(dom_ms, 4), traffic=None,
+                algorithmic=(f"{dom_row['flops']} FLOP" if roof["bound"] == "mfma"
+                             else f"{dom_row['bytes']} B"))
+    by_op = {k: dict(count=v["count"], ms=round(v["ms"], 4),
+                     share=round(v["ms"] / summ["total_ms"], 4)) for k, v in
+             sorted(summ["by_op"].items(), key=lambda kv: -kv[1]["ms"])}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cores = min(16, os.cpu_count() or 1)
+        log(f"cpu baseline on {cores} cores ...")
+        try:
+            cpu = cpu_baseline(w, plan, cores)
+        except Exception as ex:  # reported, never fatal for the GPU figure
+            cpu = dict(value=None, unit="tokens/s", cores=cores, kind="reference",
+                       sample=f"unavailable: {ex}")
+    out = {
+        "metric": "train tokens/sec per update step on 1 MI355X; GEMM MFMA util %; HBM GB/s",
+        "value": round(tokens_per_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded; weights/inputs generated, no dataset)",
+        "config": {
+            "workload": f"{w.name}: {w.description}",
+            "global_batch": w.cfg.batch,
+            "seq_len": w.seq or None,
+            "parallelism": "none (1 GPU)",
+            "train_instructions": len(plan.train),
+            "autotuned": not args.no_autotune,
+        },
+        "gemm_dense_mfma_util": summ["gemm_dense_mfma_util"],
+        "gemm_all_mfma_util": summ["gemm_all_mfma_util"],
+        "hbm_kernels_gbps": summ["hbm_kernels_gbps"],
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": by_op,
+        "final_loss": losses[-1],
+    }
+    print(json.dumps(out), flush=True)
+    e.close()
+
+
+if __name__ == "__main__":
+    main()

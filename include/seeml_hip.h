@@ -1,0 +1,234 @@
+/*
+ * seeml_hip.h — C-ABI of the MI355X (gfx950) backend for SeeML's compiled
+ * LoRA update step.
+ *
+ * The backend is a drop-in for the reference's op-dispatch seam: it consumes
+ * the same .seeu plan bytes (same 64-byte instructions, opcodes, arena
+ * offsets decided by the compiler, same load-time validator checks) and
+ * executes the train / merge / eval programs on one GPU. All signatures are
+ * plain pointers and sizes; no C++ or framework types cross this boundary.
+ *
+ * Errors: functions return SEEML_HIP_OK (0) or SEEML_HIP_ERROR (1). The
+ * message reads "<unit>: <message>" with the reference's unit names
+ * ("UpdateEngine", "PlanValidator") — runtime/diagnostics/diagnostic.h:30-41.
+ * Engine errors are read with seeml_hip_last_error(); the standalone kernel
+ * entry points report through seeml_hip_kernel_error().
+ *
+ * Threading: one host thread per engine handle; every engine owns one HIP
+ * stream, on which all of its work is ordered.
+ */
+#ifndef SEEML_HIP_H_
+#define SEEML_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SEEML_HIP_OK 0
+#define SEEML_HIP_ERROR 1
+
+/* Program ids: the plan's three instruction streams (schema.h:83-158). */
+#define SEEML_HIP_PROGRAM_TRAIN 0
+#define SEEML_HIP_PROGRAM_MERGE 1
+#define SEEML_HIP_PROGRAM_EVAL 2
+
+typedef struct seeml_hip_engine seeml_hip_engine;
+
+/* ---- Plan integrity and validation (host only; no GPU touched) ----------- */
+
+/* Every load-time proof UpdateEngine::Initialize runs before it allocates
+ * (runtime/engine/update_engine.cc:80-225): magic, version window v4..v7,
+ * PlanSelfHash seal, VerifyPlanContract (contract.cc:35-100),
+ * VerifyExecutorContract incl. ValidateInstruction on every instruction of
+ * every program (contract.cc:102-168, plan_validator.cc:9-344), softmax-width
+ * and token-plan scans. */
+int seeml_hip_verify_plan(const uint8_t* plan, uint64_t plan_size, char* err,
+                          uint64_t err_cap);
+/* Replaces ValidateInstruction (runtime/validator/plan_validator.h:45-47) for
+ * one 64-byte instruction word. */
+int seeml_hip_validate_instruction(const void* instr64, uint64_t arena_size,
+                                   uint64_t rodata_size, uint32_t plan_version,
+                                   char* err, uint64_t err_cap);
+/* PlanSelfHash / ContentHash64 (source/identity/hash.h:103-161). */
+uint64_t seeml_hip_plan_self_hash(const uint8_t* plan, uint64_t size,
+                                  uint64_t hash_offset);
+uint64_t seeml_hip_content_hash64(const uint8_t* data, uint64_t size);
+/* UpdateEngine::EffectiveLr (update_engine.cc:515-534) for a 280-byte
+ * PlanHeader image at `header` and a 1-indexed step. */
+float seeml_hip_effective_lr(const uint8_t* header, uint64_t step);
+
+/* ---- Engine lifecycle (replaces UpdateEngine, update_engine.h:119-242) --- */
+
+/* LoadFromMemory + Initialize (update_engine.cc:57-65, 80-276): verifies the
+ * plan, then allocates ONE device arena of round64(arena_size) bytes (zeroed,
+ * persistent image uploaded) plus a device copy of rodata. The plan bytes
+ * are not retained. `device` is the HIP device ordinal. */
+int seeml_hip_open(const uint8_t* plan, uint64_t plan_size, int device,
+                   seeml_hip_engine** out, char* err, uint64_t err_cap);
+void seeml_hip_close(seeml_hip_engine* e);
+const char* seeml_hip_last_error(const seeml_hip_engine* e);
+
+/* Decodes a program into its plan-ordered launch list and captures it once
+ * as a hipGraph on the engine's stream (replayed by seeml_hip_run).
+ * use_graph = 0 selects eager dispatch of the same launch list instead. */
+int seeml_hip_build(seeml_hip_engine* e, int program);
+int seeml_hip_set_graph_mode(seeml_hip_engine* e, int use_graph);
+
+/* Batch staging into the plan's I/O slots (BatchPipeline::NextBatch,
+ * runtime/feeder/batch_pipeline.cc:61-79): input_bytes must equal
+ * input_floats*4 and label_bytes the plan's label_bytes. With on_device = 0
+ * the buffers are host memory and token ids / class labels are checked
+ * against the plan's vocab / class bounds before the copy (the feeder
+ * contract, contract.cc:170-235); with on_device = 1 they are device
+ * pointers and out-of-range ids poison the loss instead of reading out of
+ * bounds. */
+int seeml_hip_stage(seeml_hip_engine* e, const void* input, uint64_t input_bytes,
+                    const void* labels, uint64_t label_bytes, int on_device);
+
+/* The engine's 1-indexed step_ (AdamW bias correction, LR schedule). Setting
+ * it uploads this step's scalars (EffectiveLr, 1/(1-beta^step)). */
+int seeml_hip_set_step(seeml_hip_engine* e, uint64_t step);
+uint64_t seeml_hip_get_step(const seeml_hip_engine* e);
+
+/* Replays a program (Execute / ExecuteTrainProgram, update_engine.cc:278-304)
+ * asynchronously on the engine stream. */
+int seeml_hip_run(seeml_hip_engine* e, int program);
+int seeml_hip_sync(seeml_hip_engine* e);
+/* LossValue (update_engine.cc:511-513): synchronizes, then reads the f32 at
+ * the plan's loss_ref. */
+int seeml_hip_loss(seeml_hip_engine* e, float* loss);
+
+/* One iteration of TrainImpl's loop (update_engine.cc:736-753): step_ += 1,
+ * scalars, stage, train program, loss read, non-finite abort. */
+int seeml_hip_train_step(seeml_hip_engine* e, const void* input, uint64_t input_bytes,
+                         const void* labels, uint64_t label_bytes, int on_device,
+                         float* loss);
+
+/* RunMerge (update_engine.cc:789-811): the merge program, then a finiteness
+ * scan of every emit-table delta. */
+int seeml_hip_run_merge(seeml_hip_engine* e);
+
+/* Arena / rodata probes (test/support/probes.cc:25-60; checkpointing of the
+ * persistent prefix). `ref` is a plan tensor reference: bit 63 = rodata. */
+int seeml_hip_read(seeml_hip_engine* e, uint64_t ref, void* dst, uint64_t bytes);
+int seeml_hip_write(seeml_hip_engine* e, uint64_t ref, const void* src, uint64_t bytes);
+void* seeml_hip_arena_device_ptr(seeml_hip_engine* e);
+void* seeml_hip_stream(seeml_hip_engine* e);
+uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
+
+/* GEMM tile autotuning (compiler/backend/tuner/bandit.cc:14-53,
+ * autotuner.cc:21-80 retargeted to GPU tiles): for every distinct GEMM shape
+ * of the train program, a deterministic UCB1 bandit over tile/split-K arms,
+ * reward = measured GFLOP/s; picks are installed and graphs rebuilt.
+ * budget = launches per shape (>= number of arms). */
+int seeml_hip_autotune(seeml_hip_engine* e, int budget);
+/* Describe the GEMM plan chosen for instruction `index` of `program`:
+ * writes "cfg-name splits=S" into buf. */
+int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
+                          uint64_t cap);
+
+/* Profiling (outside any timed step): replays `program` eagerly `reps`
+ * times on the engine stream with a HIP event pair around every
+ * instruction, and writes each instruction's mean duration in ms to
+ * ms_out[count] (count = the program's instruction count). The program's
+ * side effects happen `reps` times (optimizer state moves). */
+int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,
+                              uint64_t count);
+/* Mean duration (ms) of one instruction's launch sequence, relaunched
+ * `reps` times between two events on the engine stream. */
+int seeml_hip_time_instruction(seeml_hip_engine* e, int program, uint64_t index, int reps,
+                               float* avg_ms);
+uint64_t seeml_hip_program_length(const seeml_hip_engine* e, int program);
+
+/* ---- Standalone kernels (update_kernels.h:27-162 on device pointers) ------
+ * Same argument meaning as the reference kernels; `stream` is a hipStream_t
+ * (NULL = default stream). Scratch comes from a library-owned per-device
+ * workspace; calls on one device must not overlap. */
+const char* seeml_hip_kernel_error(void);
+int seeml_hip_gemm_nn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, const float* bias, int act, void* stream);
+int seeml_hip_gemm_nt(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, void* stream);
+int seeml_hip_gemm_tn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, void* stream);
+int seeml_hip_gemm_acc_nn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                          uint64_t K, float alpha, void* stream);
+int seeml_hip_gemm_nn_q8(const float* A, const int8_t* B, float* C, uint64_t M, uint64_t N,
+                         uint64_t K, float scale, int act, void* stream);
+int seeml_hip_gemm_nt_q8(const float* A, const int8_t* B, float* C, uint64_t M, uint64_t N,
+                         uint64_t K, float scale, void* stream);
+/* GEMM with an explicit tile config / split count (autotuner arms, tests). */
+int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, uint64_t M,
+                          uint64_t N, uint64_t K, int cfg, int splits, void* stream);
+int seeml_hip_gemm_config_count(void);
+
+int seeml_hip_add_ew(const float* x, const float* y, float* out, uint64_t n, void* stream);
+int seeml_hip_mul_ew(const float* x, const float* y, float* out, uint64_t n, void* stream);
+int seeml_hip_add_bias(const float* x, const float* b, float* out, uint64_t rows, uint64_t cols,
+                       void* stream);
+int seeml_hip_scale(const float* x, float* out, float alpha, uint64_t n, void* stream);
+int seeml_hip_reduce_rows(const float* dy, float* db, uint64_t rows, uint64_t cols, void* stream);
+int seeml_hip_relu_fwd(const float* x, float* out, uint64_t n, void* stream);
+int seeml_hip_relu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream);
+int seeml_hip_gelu_fwd(const float* x, float* out, uint64_t n, void* stream);
+int seeml_hip_gelu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream);
+int seeml_hip_silu_fwd(const float* x, float* out, uint64_t n, void* stream);
+int seeml_hip_silu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream);
+int seeml_hip_embed_fwd(const int32_t* tokens, const float* table, float* out, uint64_t rows,
+                        uint64_t dim, uint64_t vocab, void* stream);
+int seeml_hip_fill(float* dst, float value, uint64_t n, void* stream);
+int seeml_hip_copy(const float* src, float* dst, uint64_t n, void* stream);
+int seeml_hip_layer_norm_fwd(const float* x, const float* gamma, const float* beta, float* y,
+                             float* mean, float* rstd, uint64_t rows, uint64_t cols, void* stream);
+int seeml_hip_layer_norm_bwd(const float* dy, const float* x, const float* gamma,
+                             const float* mean, const float* rstd, float* dx, uint64_t rows,
+                             uint64_t cols, void* stream);
+int seeml_hip_rms_norm_fwd(const float* x, const float* gamma, float* y, float* rstd,
+                           uint64_t rows, uint64_t cols, void* stream);
+int seeml_hip_rms_norm_bwd(const float* dy, const float* x, const float* gamma,
+                           const float* rstd, float* dx, uint64_t rows, uint64_t cols,
+                           void* stream);
+int seeml_hip_rope_fwd(const float* x, float* y, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                       float base, void* stream);
+int seeml_hip_rope_bwd(const float* dy, float* dx, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                       float base, void* stream);
+int seeml_hip_attn_fwd(const float* q, const float* k, const float* v, float* o, float* probs,
+                       uint64_t B, uint64_t S, uint64_t H, uint64_t d, void* stream);
+int seeml_hip_attn_dp(const float* dout, const float* v, float* dp, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream);
+int seeml_hip_attn_dv(const float* probs, const float* dout, float* dv, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream);
+int seeml_hip_softmax_rows_bwd(const float* probs, const float* dp, float* ds, uint64_t rows,
+                               uint64_t cols, void* stream);
+int seeml_hip_attn_dq(const float* ds, const float* k, float* dq, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream);
+int seeml_hip_attn_dk(const float* ds, const float* q, float* dk, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream);
+int seeml_hip_softmax_xent_fwd(const float* logits, const int32_t* labels, float* loss,
+                               float* probs, uint64_t N, uint64_t C, void* stream);
+int seeml_hip_softmax_xent_bwd(const float* probs, const int32_t* labels, const float* seed,
+                               float* dlogits, uint64_t N, uint64_t C, void* stream);
+int seeml_hip_mse_fwd(const float* pred, const float* target, float* loss, uint64_t n,
+                      void* stream);
+int seeml_hip_mse_bwd(const float* pred, const float* target, const float* seed, float* dpred,
+                      uint64_t n, void* stream);
+int seeml_hip_kl_distill_fwd(const float* s_logits, const float* t_logits, float* loss,
+                             float* p_s, float* p_t, uint64_t N, uint64_t C, float T,
+                             void* stream);
+int seeml_hip_kl_distill_bwd(const float* p_s, const float* p_t, const float* seed,
+                             float* dlogits, uint64_t N, uint64_t C, float T, void* stream);
+int seeml_hip_clip_norm(float* g, uint64_t n, float max_norm, void* stream);
+int seeml_hip_sgd_step(float* p, const float* g, uint64_t n, float lr, float weight_decay,
+                       void* stream);
+int seeml_hip_adamw_step(float* p, const float* g, float* m, float* v, uint64_t n, float lr,
+                         float beta1, float beta2, float eps, float weight_decay, uint64_t step,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEEML_HIP_H_ */

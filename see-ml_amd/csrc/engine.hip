@@ -1,0 +1,1067 @@
+// engine.hip — the device execution engine and the C-ABI (include/seeml_hip.h).
+//
+// Reference boundary: UpdateEngine (runtime/engine/update_engine.h:119-242)
+// loads a plan, proves it, allocates one arena and dispatches each program's
+// instructions into the executor kernels (ExecuteRange,
+// update_engine.cc:306-509). This engine keeps that contract on one MI355X:
+//
+//   open     every load-time proof (plan_checks.cc), then ONE hipMalloc'd
+//            arena of round64(arena_size) bytes (zeroed, persistent image
+//            uploaded) and a device copy of rodata — plan offsets are used
+//            unchanged: pointer = base + RefOffset(ref).
+//   build    decodes a program into its plan-ordered launch list (GEMM tile
+//            plans chosen per instruction, workspace sized to the largest
+//            need) and captures it once as a hipGraph on the engine stream.
+//   step     step_ += 1, per-step scalars (EffectiveLr, AdamW bias
+//            corrections) uploaded to a device block read by the optimizer
+//            kernels, batch staged into the I/O slots, graph replayed, the
+//            4-byte loss read back and checked for finiteness.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/seeml_hip.h"
+#include "kernels.h"
+#include "plan_checks.h"
+
+namespace seeml_hip {
+namespace {
+
+constexpr size_t kAlign = 64;
+size_t Round64(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+Status HipOk(hipError_t e, const char* what) {
+  if (e == hipSuccess) return Status::Ok();
+  return Status::Fail(kUnitEngine, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline uint64_t Hi(uint64_t w) { return w >> 32; }
+inline uint64_t Lo(uint64_t w) { return w & 0xFFFFFFFFu; }
+float Bits(uint64_t b) {
+  const uint32_t u = static_cast<uint32_t>(b);
+  float f;
+  std::memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+bool IsGemmOp(uint16_t op) {
+  return op == static_cast<uint16_t>(Op::kGemmNN) || op == static_cast<uint16_t>(Op::kGemmNT) ||
+         op == static_cast<uint16_t>(Op::kGemmTN) || op == static_cast<uint16_t>(Op::kGemmAccNN) ||
+         op == static_cast<uint16_t>(Op::kGemmNNQ8) || op == static_cast<uint16_t>(Op::kGemmNTQ8);
+}
+
+// ---- UCB1 bandit (compiler/backend/tuner/bandit.cc:14-53) -----------------
+// Deterministic: untried arms first in index order, score ties to the lowest
+// index, no RNG.
+class Ucb1 {
+ public:
+  explicit Ucb1(size_t arms, double c = 1.0) : pulls_(arms, 0), mean_(arms, 0.0), c_(c) {}
+  size_t Select() const {
+    for (size_t i = 0; i < pulls_.size(); ++i)
+      if (pulls_[i] == 0) return i;
+    size_t best = 0;
+    double best_score = -INFINITY;
+    const double log_total = std::log(static_cast<double>(total_));
+    for (size_t i = 0; i < pulls_.size(); ++i) {
+      const double score =
+          mean_[i] + c_ * std::sqrt(2.0 * log_total / static_cast<double>(pulls_[i]));
+      if (score > best_score) {
+        best_score = score;
+        best = i;
+      }
+    }
+    return best;
+  }
+  void Update(size_t arm, double reward) {
+    ++pulls_[arm];
+    ++total_;
+    mean_[arm] += (reward - mean_[arm]) / static_cast<double>(pulls_[arm]);
+  }
+  size_t Best() const {
+    size_t best = 0;
+    for (size_t i = 1; i < pulls_.size(); ++i)
+      if (pulls_[i] > 0 && (pulls_[best] == 0 || mean_[i] > mean_[best])) best = i;
+    return best;
+  }
+
+ private:
+  std::vector<uint64_t> pulls_;
+  std::vector<double> mean_;
+  uint64_t total_ = 0;
+  double c_;
+};
+
+}  // namespace
+
+class Engine {
+ public:
+  ~Engine() { Release(); }
+
+  Status Open(const uint8_t* plan, size_t plan_size, int device) {
+    if (Status s = DecodeAndVerifyPlan(plan, plan_size, &plan_); !s) return s;
+    device_ = device;
+    if (Status s = HipOk(hipSetDevice(device), "hipSetDevice"); !s) return s;
+    if (Status s = HipOk(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "stream"); !s)
+      return s;
+    const PlanHeader& h = plan_.header;
+    arena_bytes_ = Round64(h.arena_size);
+    if (arena_bytes_ == 0) arena_bytes_ = kAlign;
+    if (Status s = HipOk(hipMalloc(&arena_, arena_bytes_), "arena allocation failed"); !s)
+      return s;
+    if (Status s = HipOk(hipMemsetAsync(arena_, 0, arena_bytes_, stream_), "arena clear"); !s)
+      return s;
+    if (h.persist_init_size)
+      if (Status s = HipOk(hipMemcpyAsync(arena_, plan + h.persist_init_offset,
+                                          h.persist_init_size, hipMemcpyHostToDevice, stream_),
+                           "persistent image upload");
+          !s)
+        return s;
+    rodata_bytes_ = Round64(std::max<uint64_t>(h.rodata_size, 1));
+    if (Status s = HipOk(hipMalloc(&rodata_, rodata_bytes_), "rodata allocation failed"); !s)
+      return s;
+    if (h.rodata_size)
+      if (Status s = HipOk(hipMemcpyAsync(rodata_, plan + h.rodata_offset, h.rodata_size,
+                                          hipMemcpyHostToDevice, stream_),
+                           "rodata upload");
+          !s)
+        return s;
+    if (Status s = HipOk(hipMalloc(&d_scalars_, sizeof(StepScalars)), "scalars"); !s) return s;
+    if (Status s = HipOk(hipHostMalloc(&h_scalars_, sizeof(StepScalars)), "pinned scalars"); !s)
+      return s;
+    if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
+    for (int p = 0; p < 3; ++p) plans_[p].assign(plan_.program[p].size(), GemmPlan{});
+    for (int p = 0; p < 3; ++p)
+      for (size_t i = 0; i < plan_.program[p].size(); ++i)
+        if (IsGemmOp(plan_.program[p][i].opcode)) plans_[p][i] = PlanGemm(DescOf(plan_.program[p][i]));
+    if (Status s = SetStep(0); !s) return s;
+    return HipOk(hipStreamSynchronize(stream_), "open");
+  }
+
+  // ---- instruction decode ------------------------------------------------
+  const float* RP(uint64_t ref) const {
+    return reinterpret_cast<const float*>((IsRodataRef(ref) ? rodata_ : arena_) + RefOffset(ref));
+  }
+  float* WP(uint64_t ref) const { return reinterpret_cast<float*>(arena_ + RefOffset(ref)); }
+  const int32_t* IP(uint64_t ref) const { return reinterpret_cast<const int32_t*>(RP(ref)); }
+
+  // The GEMM family's operand layouts (gemm.cc:173-228, instruction.h:29-33).
+  GemmDesc DescOf(const UpdateInstruction& ins) const {
+    const auto op = static_cast<Op>(ins.opcode);
+    const int64_t M = ins.out[0], N = ins.out[1], K = ins.out[2];
+    const float* A = RP(ins.in[0]);
+    const void* B = RP(ins.in[1]);
+    float* C = WP(ins.in[2]);
+    GemmDesc d;
+    switch (op) {
+      case Op::kGemmNT: d = GemmNTDesc(A, static_cast<const float*>(B), C, M, N, K); break;
+      case Op::kGemmTN: d = GemmTNDesc(A, static_cast<const float*>(B), C, M, N, K); break;
+      case Op::kGemmNTQ8:
+        d = GemmNTDesc(A, nullptr, C, M, N, K);
+        d.B = B;
+        d.b_int8 = true;
+        d.alpha = Bits(ins.in[3]);
+        break;
+      default:
+        d = GemmNNDesc(A, nullptr, C, M, N, K);
+        d.B = B;
+        break;
+    }
+    if (op == Op::kGemmNN) {
+      if (ins.flags & kFlagEpilogueBias) d.bias = RP(ins.in[3]);
+      d.act = static_cast<int>(ActOf(ins.flags));
+    } else if (op == Op::kGemmAccNN) {
+      d.alpha = Bits(ins.in[3]);
+      d.accumulate = true;
+    } else if (op == Op::kGemmNNQ8) {
+      d.b_int8 = true;
+      d.alpha = Bits(ins.in[3]);
+      d.act = static_cast<int>(ActOf(ins.flags));
+    }
+    return d;
+  }
+
+  size_t WorkspaceFor(int program, size_t idx) const {
+    const UpdateInstruction& ins = plan_.program[program][idx];
+    const auto op = static_cast<Op>(ins.opcode);
+    if (IsGemmOp(ins.opcode)) return plans_[program][idx].ws_bytes;
+    switch (op) {
+      case Op::kMseFwd: return MseFwdWorkspace(ins.out[0]);
+      case Op::kClipNorm: return ClipNormWorkspace(ins.out[0]);
+      case Op::kSoftmaxXEntFwd: return SoftmaxXEntFwdWorkspace(ins.out[0]);
+      case Op::kKLDistillFwd: return KLDistillFwdWorkspace(Hi(ins.out[1]));
+      default: return 0;
+    }
+  }
+
+  // ExecuteRange's switch (update_engine.cc:309-508), one launch sequence per
+  // instruction.
+  Status Dispatch(int program, size_t idx, const Ctx& c) const {
+    const UpdateInstruction& ins = plan_.program[program][idx];
+    const uint64_t d0 = ins.out[0], d1 = ins.out[1], d2 = ins.out[2];
+    switch (static_cast<Op>(ins.opcode)) {
+      case Op::kNop: return Status::Ok();
+      case Op::kGemmNN: case Op::kGemmNT: case Op::kGemmTN: case Op::kGemmAccNN:
+      case Op::kGemmNNQ8: case Op::kGemmNTQ8:
+        return LaunchGemm(DescOf(ins), plans_[program][idx], c);
+      case Op::kAddEW: return AddEW(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kMulEW: return MulEW(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kAddBias: return AddBias(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, d1, c);
+      case Op::kReluFwd: return ReluFwd(RP(ins.in[0]), WP(ins.in[1]), d0, c);
+      case Op::kReluBwd: return ReluBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kGeluFwd: return GeluFwd(RP(ins.in[0]), WP(ins.in[1]), d0, c);
+      case Op::kGeluBwd: return GeluBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kSiluFwd: return SiluFwd(RP(ins.in[0]), WP(ins.in[1]), d0, c);
+      case Op::kSiluBwd: return SiluBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kScale: return Scale(RP(ins.in[0]), WP(ins.in[1]), Bits(ins.in[2]), d0, c);
+      case Op::kReduceRows: return ReduceRows(RP(ins.in[0]), WP(ins.in[1]), d0, d1, c);
+      case Op::kLayerNormFwd:
+        return LayerNormFwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]),
+                            WP(ins.out[1]), WP(ins.out[2]), Hi(d0), Lo(d0), c);
+      case Op::kLayerNormBwd:
+        return LayerNormBwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), RP(ins.out[0]),
+                            RP(ins.out[1]), WP(ins.in[3]), Hi(d2), Lo(d2), c);
+      case Op::kClipNorm: return ClipNorm(WP(ins.in[0]), d0, Bits(ins.in[1]), c);
+      case Op::kSoftmaxXEntFwd:
+        return SoftmaxXEntFwd(RP(ins.in[0]), IP(ins.in[1]), WP(ins.in[2]), WP(ins.in[3]), d0, d1,
+                              c);
+      case Op::kSoftmaxXEntBwd:
+        return SoftmaxXEntBwd(RP(ins.in[0]), IP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]), d0, d1,
+                              c);
+      case Op::kMseFwd: return MseFwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
+      case Op::kMseBwd:
+        return MseBwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]), d0, c);
+      case Op::kKLDistillFwd:
+        return KLDistillFwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), WP(ins.in[3]),
+                            WP(ins.out[0]), Hi(d1), Lo(d1), Bits(d2), c);
+      case Op::kKLDistillBwd:
+        return KLDistillBwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]), Hi(d0),
+                            Lo(d0), Bits(d1), c);
+      case Op::kSgdStep: return SgdStep(WP(ins.in[0]), RP(ins.in[1]), d0, c);
+      case Op::kAdamWStep:
+        return AdamWStep(WP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), WP(ins.in[3]), d0, c);
+      case Op::kFill: return Fill(WP(ins.in[0]), Bits(ins.in[1]), d0, c);
+      case Op::kCopy: return Copy(RP(ins.in[0]), WP(ins.in[1]), d0, c);
+      case Op::kRmsNormFwd:
+        return RmsNormFwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), WP(ins.in[3]), Hi(d0),
+                          Lo(d0), c);
+      case Op::kRmsNormBwd:
+        return RmsNormBwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), RP(ins.out[0]),
+                          WP(ins.in[3]), Hi(d1), Lo(d1), c);
+      case Op::kRopeFwd:
+        return RopeFwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), Bits(d2), c);
+      case Op::kRopeBwd:
+        return RopeBwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), Bits(d2), c);
+      case Op::kAttnFwd:
+        return AttnFwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]),
+                       WP(ins.out[0]), Hi(d1), Lo(d1), Hi(d2), Lo(d2), c);
+      case Op::kAttnDP:
+        return AttnDP(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
+      case Op::kAttnDV:
+        return AttnDV(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
+      case Op::kSoftmaxRowsBwd:
+        return SoftmaxRowsBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), c);
+      case Op::kAttnDQ:
+        return AttnDQ(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
+      case Op::kAttnDK:
+        return AttnDK(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
+      case Op::kEmbedFwd:
+        return EmbedFwd(IP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, Lo(d1), Hi(d1), c);
+    }
+    return Status::Fail(kUnitEngine, "unknown opcode " + std::to_string(ins.opcode));
+  }
+
+  Ctx MakeCtx() const {
+    Ctx c;
+    c.stream = stream_;
+    c.ws = ws_;
+    c.ws_bytes = ws_bytes_;
+    c.scalars = d_scalars_;
+    return c;
+  }
+
+  Status EnsureWorkspace(int program) {
+    size_t need = 0;
+    for (size_t i = 0; i < plan_.program[program].size(); ++i)
+      need = std::max(need, WorkspaceFor(program, i));
+    if (need <= ws_bytes_) return Status::Ok();
+    // Growing the workspace moves it: every captured graph holds the old
+    // address, so all of them are rebuilt on next use.
+    if (Status s = HipOk(hipStreamSynchronize(stream_), "workspace sync"); !s) return s;
+    if (ws_) (void)hipFree(ws_);
+    ws_ = nullptr;
+    ws_bytes_ = 0;
+    if (Status s = HipOk(hipMalloc(&ws_, Round64(need)), "workspace allocation"); !s) return s;
+    ws_bytes_ = Round64(need);
+    for (int p = 0; p < 3; ++p) DropGraph(p);
+    return Status::Ok();
+  }
+
+  void DropGraph(int p) {
+    if (exec_[p]) (void)hipGraphExecDestroy(exec_[p]);
+    if (graph_[p]) (void)hipGraphDestroy(graph_[p]);
+    exec_[p] = nullptr;
+    graph_[p] = nullptr;
+    built_[p] = false;
+  }
+
+  Status RunEager(int program) {
+    const Ctx c = MakeCtx();
+    for (size_t i = 0; i < plan_.program[program].size(); ++i)
+      if (Status s = Dispatch(program, i, c); !s) return s;
+    return Status::Ok();
+  }
+
+  Status Build(int program) {
+    if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    if (Status s = EnsureWorkspace(program); !s) return s;
+    DropGraph(program);
+    if (!use_graph_ || plan_.program[program].empty()) {
+      built_[program] = true;
+      return Status::Ok();
+    }
+    if (Status s = HipOk(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
+                         "graph capture begin");
+        !s)
+      return s;
+    Status launched = RunEager(program);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(stream_, &g);
+    if (!launched) {
+      if (g) (void)hipGraphDestroy(g);
+      return launched;
+    }
+    if (Status s = HipOk(end, "graph capture end"); !s) return s;
+    graph_[program] = g;
+    if (Status s = HipOk(hipGraphInstantiate(&exec_[program], g, nullptr, nullptr, 0),
+                         "graph instantiate");
+        !s)
+      return s;
+    built_[program] = true;
+    return Status::Ok();
+  }
+
+  Status Run(int program) {
+    if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    if (!built_[program])
+      if (Status s = Build(program); !s) return s;
+    if (plan_.program[program].empty()) return Status::Ok();
+    if (use_graph_) return HipOk(hipGraphLaunch(exec_[program], stream_), "graph launch");
+    return RunEager(program);
+  }
+
+  Status SetStep(uint64_t step) {
+    step_ = step;
+    *h_scalars_ = MakeStepScalars(plan_.header, step == 0 ? 1 : step);
+    return HipOk(hipMemcpyAsync(d_scalars_, h_scalars_, sizeof(StepScalars),
+                                hipMemcpyHostToDevice, stream_),
+                 "step scalars upload");
+  }
+
+  // The feeder contract's bounds (contract.cc:173-207) on host-staged ids.
+  Status CheckIds(const int32_t* ids, size_t n, uint64_t bound, const char* what) const {
+    for (size_t i = 0; i < n; ++i)
+      if (ids[i] < 0 || static_cast<uint64_t>(ids[i]) >= bound)
+        return Status::Fail(kUnitEngine, std::string(what) + " " + std::to_string(ids[i]) +
+                                             " at row " + std::to_string(i) +
+                                             " is outside [0, " + std::to_string(bound) + ")");
+    return Status::Ok();
+  }
+
+  Status Stage(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
+               bool on_device) {
+    const PlanHeader& h = plan_.header;
+    if (input_bytes != h.input_floats * 4)
+      return Status::Fail(kUnitEngine, "staged input size does not match the plan input slot");
+    if (h.label_kind != 0 && label_bytes != h.label_bytes)
+      return Status::Fail(kUnitEngine, "staged label size does not match the plan label slot");
+    if (!on_device) {
+      if (h.input_kind == 1) {
+        uint64_t bound = plan_.vocab_bound;
+        if (plan_.num_classes && plan_.num_classes < bound) bound = plan_.num_classes;
+        if (Status s = CheckIds(static_cast<const int32_t*>(input), h.input_floats, bound,
+                                "token id");
+            !s)
+          return s;
+      }
+      if (h.label_kind == 1 && labels)
+        if (Status s = CheckIds(static_cast<const int32_t*>(labels), label_bytes / 4,
+                                plan_.num_classes, "class label");
+            !s)
+          return s;
+    }
+    const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    if (input_bytes)
+      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.input_ref), input, input_bytes,
+                                          kind, stream_),
+                           "input staging");
+          !s)
+        return s;
+    if (h.label_kind != 0 && labels && label_bytes)
+      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.label_ref), labels, label_bytes,
+                                          kind, stream_),
+                           "label staging");
+          !s)
+        return s;
+    return Status::Ok();
+  }
+
+  Status Loss(float* out) {
+    if (Status s = HipOk(hipMemcpyAsync(h_loss_, arena_ + RefOffset(plan_.header.loss_ref),
+                                        sizeof(float), hipMemcpyDeviceToHost, stream_),
+                         "loss read");
+        !s)
+      return s;
+    if (Status s = HipOk(hipStreamSynchronize(stream_), "step"); !s) return s;
+    *out = *h_loss_;
+    return Status::Ok();
+  }
+
+  Status TrainStep(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
+                   bool on_device, float* loss) {
+    if (Status s = SetStep(step_ + 1); !s) return s;
+    if (Status s = Stage(input, input_bytes, labels, label_bytes, on_device); !s) return s;
+    if (Status s = Run(static_cast<int>(Program::kTrain)); !s) return s;
+    float l = 0.0f;
+    if (Status s = Loss(&l); !s) return s;
+    if (loss) *loss = l;
+    if (!std::isfinite(l))
+      return Status::Fail(kUnitEngine, "loss became non-finite at step " + std::to_string(step_) +
+                                           " — aborting the update");
+    return Status::Ok();
+  }
+
+  Status RunMerge() {
+    if (Status s = Run(static_cast<int>(Program::kMerge)); !s) return s;
+    if (Status s = HipOk(hipStreamSynchronize(stream_), "merge"); !s) return s;
+    std::vector<float> buf;
+    for (const EmitEntry& e : plan_.emit) {
+      buf.resize(e.byte_size / 4);
+      if (Status s = HipOk(hipMemcpy(buf.data(), arena_ + e.arena_offset, e.byte_size,
+                                     hipMemcpyDeviceToHost),
+                           "delta read");
+          !s)
+        return s;
+      for (float v : buf)
+        if (!std::isfinite(v))
+          return Status::Fail(kUnitEngine,
+                              "merged delta contains a non-finite value — the adapters are "
+                              "numerically poisoned; refusing to stage a commit");
+    }
+    return Status::Ok();
+  }
+
+  Status Access(uint64_t ref, void* host, size_t bytes, bool write) {
+    const bool ro = IsRodataRef(ref);
+    if (write && ro) return Status::Fail(kUnitEngine, "rodata is not writable");
+    const uint64_t off = RefOffset(ref);
+    const uint64_t space = ro ? plan_.header.rodata_size : plan_.header.arena_size;
+    if (!RangeOk(off, bytes, space)) return Status::Fail(kUnitEngine, "probe out of bounds");
+    uint8_t* dev = (ro ? rodata_ : arena_) + off;
+    if (Status s = HipOk(hipStreamSynchronize(stream_), "probe sync"); !s) return s;
+    return HipOk(write ? hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice)
+                       : hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost),
+                 "probe copy");
+  }
+
+  // ---- GEMM tile autotuning ------------------------------------------------
+  Status Autotune(int budget) {
+    const int program = static_cast<int>(Program::kTrain);
+    const auto& prog = plan_.program[program];
+    const uint64_t persist = plan_.header.persistent_size;
+    std::map<std::tuple<uint16_t, uint64_t, uint64_t, uint64_t>, std::vector<size_t>> groups;
+    for (size_t i = 0; i < prog.size(); ++i) {
+      const UpdateInstruction& ins = prog[i];
+      if (!IsGemmOp(ins.opcode) || ins.opcode == static_cast<uint16_t>(Op::kGemmAccNN)) continue;
+      // Tune only in scratch-safe places: the output must be a transient,
+      // never the persistent segment the optimizer state lives in.
+      if (RefOffset(ins.in[2]) < persist) continue;
+      groups[{ins.opcode, ins.out[0], ins.out[1], ins.out[2]}].push_back(i);
+    }
+    hipEvent_t t0, t1;
+    if (Status s = HipOk(hipEventCreate(&t0), "event"); !s) return s;
+    if (Status s = HipOk(hipEventCreate(&t1), "event"); !s) return s;
+    Status result = Status::Ok();
+    for (auto& [key, idxs] : groups) {
+      const size_t first = idxs.front();
+      const GemmDesc d = DescOf(prog[first]);
+      const GemmPlan hint = plans_[program][first];
+      // Arms: the heuristic hint and its neighbourhood — every other tile
+      // shape at the hint's split, and the hint's tile at half/double split.
+      std::vector<GemmPlan> arms{hint};
+      auto add = [&](int cfg, int splits) {
+        GemmPlan p = PlanGemmWith(d, cfg, splits);
+        for (const auto& a : arms)
+          if (a.cfg == p.cfg && a.splits == p.splits) return;
+        arms.push_back(p);
+      };
+      for (int cfg = 0; cfg < GemmConfigCount(); ++cfg) add(cfg, hint.splits);
+      if (hint.splits > 1) add(hint.cfg, std::max(1, hint.splits / 2));
+      add(hint.cfg, std::min(64, hint.splits * 2));
+      size_t need = 0;
+      for (const auto& a : arms) need = std::max(need, a.ws_bytes);
+      if (need > ws_bytes_) {
+        if (Status s = HipOk(hipStreamSynchronize(stream_), "tune sync"); !s) { result = s; break; }
+        if (ws_) (void)hipFree(ws_);
+        ws_ = nullptr;
+        ws_bytes_ = 0;
+        if (Status s = HipOk(hipMalloc(&ws_, Round64(need)), "workspace"); !s) { result = s; break; }
+        ws_bytes_ = Round64(need);
+        for (int p = 0; p < 3; ++p) DropGraph(p);
+      }
+      const Ctx c = MakeCtx();
+      const double flops = 2.0 * static_cast<double>(d.M) * d.N * d.K;
+      for (const auto& a : arms)  // one untimed warm-up launch per arm
+        if (Status s = LaunchGemm(d, a, c); !s) { result = s; break; }
+      if (!result) break;
+      Ucb1 bandit(arms.size());
+      const int trials = std::max<int>(budget, static_cast<int>(arms.size()));
+      for (int t = 0; t < trials; ++t) {
+        const size_t arm = bandit.Select();
+        (void)hipEventRecord(t0, stream_);
+        if (Status s = LaunchGemm(d, arms[arm], c); !s) { result = s; break; }
+        (void)hipEventRecord(t1, stream_);
+        (void)hipEventSynchronize(t1);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, t0, t1);
+        bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / 1e9 : 0.0);
+      }
+      if (!result) break;
+      const GemmPlan best = arms[bandit.Best()];
+      for (size_t i : idxs) plans_[program][i] = best;
+    }
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (!result) return result;
+    for (int p = 0; p < 3; ++p) DropGraph(p);
+    return HipOk(hipStreamSynchronize(stream_), "autotune");
+  }
+
+  Status Profile(int program, int reps, float* ms_out, size_t count) {
+    if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    const size_t n = plan_.program[program].size();
+    if (count < n) return Status::Fail(kUnitEngine, "profile output too small");
+    if (Status s = EnsureWorkspace(program); !s) return s;
+    std::vector<hipEvent_t> ev(n + 1);
+    for (auto& e : ev)
+      if (Status s = HipOk(hipEventCreate(&e), "event"); !s) return s;
+    std::vector<double> acc(n, 0.0);
+    const Ctx c = MakeCtx();
+    Status result = Status::Ok();
+    for (int r = 0; r < reps && result; ++r) {
+      (void)hipEventRecord(ev[0], stream_);
+      for (size_t i = 0; i < n; ++i) {
+        if (Status s = Dispatch(program, i, c); !s) { result = s; break; }
+        (void)hipEventRecord(ev[i + 1], stream_);
+      }
+      if (!result) break;
+      if (Status s = HipOk(hipEventSynchronize(ev[n]), "profile sync"); !s) { result = s; break; }
+      for (size_t i = 0; i < n; ++i) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+        acc[i] += ms;
+      }
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    if (!result) return result;
+    for (size_t i = 0; i < n; ++i) ms_out[i] = static_cast<float>(acc[i] / std::max(reps, 1));
+    return Status::Ok();
+  }
+
+  Status TimeInstruction(int program, size_t idx, int reps, float* avg_ms) {
+    if (program < 0 || program > 2 || idx >= plan_.program[program].size())
+      return Status::Fail(kUnitEngine, "instruction index out of range");
+    if (Status s = EnsureWorkspace(program); !s) return s;
+    const Ctx c = MakeCtx();
+    hipEvent_t t0, t1;
+    if (Status s = HipOk(hipEventCreate(&t0), "event"); !s) return s;
+    if (Status s = HipOk(hipEventCreate(&t1), "event"); !s) return s;
+    Status result = Dispatch(program, idx, c);  // warm-up
+    if (result) {
+      (void)hipEventRecord(t0, stream_);
+      for (int r = 0; r < reps && result; ++r) result = Dispatch(program, idx, c);
+      (void)hipEventRecord(t1, stream_);
+      if (result) result = HipOk(hipEventSynchronize(t1), "time sync");
+    }
+    float ms = 0.0f;
+    if (result) (void)hipEventElapsedTime(&ms, t0, t1);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (!result) return result;
+    *avg_ms = ms / static_cast<float>(std::max(reps, 1));
+    return Status::Ok();
+  }
+
+  std::string GemmChoice(int program, size_t idx) const {
+    const GemmPlan& p = plans_[program][idx];
+    return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits);
+  }
+
+  void Release() {
+    for (int p = 0; p < 3; ++p) DropGraph(p);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (arena_) (void)hipFree(arena_);
+    if (rodata_) (void)hipFree(rodata_);
+    if (ws_) (void)hipFree(ws_);
+    if (d_scalars_) (void)hipFree(d_scalars_);
+    if (h_scalars_) (void)hipHostFree(h_scalars_);
+    if (h_loss_) (void)hipHostFree(h_loss_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+    arena_ = rodata_ = nullptr;
+    ws_ = nullptr;
+    d_scalars_ = h_scalars_ = nullptr;
+    h_loss_ = nullptr;
+    stream_ = nullptr;
+  }
+
+  DecodedPlan plan_;
+  std::vector<GemmPlan> plans_[3];
+  int device_ = 0;
+  hipStream_t stream_ = nullptr;
+  uint8_t* arena_ = nullptr;
+  size_t arena_bytes_ = 0;
+  uint8_t* rodata_ = nullptr;
+  size_t rodata_bytes_ = 0;
+  void* ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+  StepScalars* d_scalars_ = nullptr;
+  StepScalars* h_scalars_ = nullptr;
+  float* h_loss_ = nullptr;
+  hipGraph_t graph_[3] = {nullptr, nullptr, nullptr};
+  hipGraphExec_t exec_[3] = {nullptr, nullptr, nullptr};
+  bool built_[3] = {false, false, false};
+  bool use_graph_ = true;
+  uint64_t step_ = 0;
+  std::string error_;
+};
+
+// ---- standalone kernel context (per device, library-owned scratch) --------
+namespace {
+
+struct Standalone {
+  std::mutex mu;
+  std::map<int, std::pair<void*, size_t>> ws;       // device -> workspace
+  std::map<int, StepScalars*> scalars;              // device -> scalar block
+};
+Standalone& Shared() {
+  static Standalone s;
+  return s;
+}
+thread_local std::string g_kernel_error;
+
+int Report(const Status& s) {
+  if (s.ok) return SEEML_HIP_OK;
+  g_kernel_error = s.error;
+  return SEEML_HIP_ERROR;
+}
+
+Status StandaloneCtx(void* stream, size_t ws_need, Ctx* out) {
+  int dev = 0;
+  if (Status s = HipOk(hipGetDevice(&dev), "hipGetDevice"); !s) return s;
+  Standalone& st = Shared();
+  std::lock_guard<std::mutex> lock(st.mu);
+  auto& w = st.ws[dev];
+  if (ws_need > w.second) {
+    if (w.first) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(w.first);
+    }
+    w = {nullptr, 0};
+    if (Status s = HipOk(hipMalloc(&w.first, Round64(ws_need)), "standalone workspace"); !s)
+      return s;
+    w.second = Round64(ws_need);
+  }
+  auto& sc = st.scalars[dev];
+  if (!sc)
+    if (Status s = HipOk(hipMalloc(&sc, sizeof(StepScalars)), "standalone scalars"); !s) return s;
+  out->stream = static_cast<hipStream_t>(stream);
+  out->ws = w.first;
+  out->ws_bytes = w.second;
+  out->scalars = sc;
+  return Status::Ok();
+}
+
+void CopyError(const std::string& msg, char* err, uint64_t cap) {
+  if (!err || cap == 0) return;
+  const size_t n = std::min<size_t>(msg.size(), cap - 1);
+  std::memcpy(err, msg.data(), n);
+  err[n] = '\0';
+}
+
+}  // namespace
+}  // namespace seeml_hip
+
+using seeml_hip::Ctx;
+using seeml_hip::Engine;
+using seeml_hip::Status;
+
+struct seeml_hip_engine {
+  Engine impl;
+};
+
+namespace {
+int Ret(seeml_hip_engine* e, const Status& s) {
+  if (s.ok) return SEEML_HIP_OK;
+  e->impl.error_ = s.error;
+  return SEEML_HIP_ERROR;
+}
+}  // namespace
+
+extern "C" {
+
+int seeml_hip_verify_plan(const uint8_t* plan, uint64_t plan_size, char* err, uint64_t err_cap) {
+  seeml_hip::DecodedPlan d;
+  const Status s = seeml_hip::DecodeAndVerifyPlan(plan, plan_size, &d);
+  if (!s) seeml_hip::CopyError(s.error, err, err_cap);
+  return s.ok ? SEEML_HIP_OK : SEEML_HIP_ERROR;
+}
+
+int seeml_hip_validate_instruction(const void* instr64, uint64_t arena_size, uint64_t rodata_size,
+                                   uint32_t plan_version, char* err, uint64_t err_cap) {
+  seeml_hip::UpdateInstruction ins;
+  std::memcpy(&ins, instr64, sizeof ins);
+  const Status s = seeml_hip::ValidateInstruction(ins, arena_size, rodata_size, plan_version);
+  if (!s) seeml_hip::CopyError(s.error, err, err_cap);
+  return s.ok ? SEEML_HIP_OK : SEEML_HIP_ERROR;
+}
+
+uint64_t seeml_hip_plan_self_hash(const uint8_t* plan, uint64_t size, uint64_t hash_offset) {
+  return seeml_hip::PlanSelfHash(plan, size, hash_offset);
+}
+
+uint64_t seeml_hip_content_hash64(const uint8_t* data, uint64_t size) {
+  return seeml_hip::ContentHash64(data, size);
+}
+
+float seeml_hip_effective_lr(const uint8_t* header, uint64_t step) {
+  seeml_hip::PlanHeader h;
+  std::memcpy(&h, header, sizeof h);
+  return seeml_hip::EffectiveLr(h, step);
+}
+
+int seeml_hip_open(const uint8_t* plan, uint64_t plan_size, int device, seeml_hip_engine** out,
+                   char* err, uint64_t err_cap) {
+  if (!out) return SEEML_HIP_ERROR;
+  *out = nullptr;
+  auto* e = new seeml_hip_engine();
+  const Status s = e->impl.Open(plan, plan_size, device);
+  if (!s) {
+    seeml_hip::CopyError(s.error, err, err_cap);
+    delete e;
+    return SEEML_HIP_ERROR;
+  }
+  *out = e;
+  return SEEML_HIP_OK;
+}
+
+void seeml_hip_close(seeml_hip_engine* e) { delete e; }
+
+const char* seeml_hip_last_error(const seeml_hip_engine* e) {
+  return e ? e->impl.error_.c_str() : "UpdateEngine: null engine";
+}
+
+int seeml_hip_build(seeml_hip_engine* e, int program) { return Ret(e, e->impl.Build(program)); }
+
+int seeml_hip_set_graph_mode(seeml_hip_engine* e, int use_graph) {
+  e->impl.use_graph_ = use_graph != 0;
+  for (int p = 0; p < 3; ++p) e->impl.DropGraph(p);
+  return SEEML_HIP_OK;
+}
+
+int seeml_hip_stage(seeml_hip_engine* e, const void* input, uint64_t input_bytes,
+                    const void* labels, uint64_t label_bytes, int on_device) {
+  return Ret(e, e->impl.Stage(input, input_bytes, labels, label_bytes, on_device != 0));
+}
+
+int seeml_hip_set_step(seeml_hip_engine* e, uint64_t step) { return Ret(e, e->impl.SetStep(step)); }
+uint64_t seeml_hip_get_step(const seeml_hip_engine* e) { return e->impl.step_; }
+
+int seeml_hip_run(seeml_hip_engine* e, int program) { return Ret(e, e->impl.Run(program)); }
+
+int seeml_hip_sync(seeml_hip_engine* e) {
+  return Ret(e, seeml_hip::HipOk(hipStreamSynchronize(e->impl.stream_), "sync"));
+}
+
+int seeml_hip_loss(seeml_hip_engine* e, float* loss) { return Ret(e, e->impl.Loss(loss)); }
+
+int seeml_hip_train_step(seeml_hip_engine* e, const void* input, uint64_t input_bytes,
+                         const void* labels, uint64_t label_bytes, int on_device, float* loss) {
+  return Ret(e, e->impl.TrainStep(input, input_bytes, labels, label_bytes, on_device != 0, loss));
+}
+
+int seeml_hip_run_merge(seeml_hip_engine* e) { return Ret(e, e->impl.RunMerge()); }
+
+int seeml_hip_read(seeml_hip_engine* e, uint64_t ref, void* dst, uint64_t bytes) {
+  return Ret(e, e->impl.Access(ref, dst, bytes, false));
+}
+
+int seeml_hip_write(seeml_hip_engine* e, uint64_t ref, const void* src, uint64_t bytes) {
+  return Ret(e, e->impl.Access(ref, const_cast<void*>(src), bytes, true));
+}
+
+void* seeml_hip_arena_device_ptr(seeml_hip_engine* e) { return e->impl.arena_; }
+void* seeml_hip_stream(seeml_hip_engine* e) { return e->impl.stream_; }
+uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e) { return e->impl.ws_bytes_; }
+
+int seeml_hip_autotune(seeml_hip_engine* e, int budget) { return Ret(e, e->impl.Autotune(budget)); }
+
+int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
+                          uint64_t cap) {
+  if (program < 0 || program > 2 || index >= e->impl.plans_[program].size())
+    return Ret(e, Status::Fail(seeml_hip::kUnitEngine, "instruction index out of range"));
+  seeml_hip::CopyError(e->impl.GemmChoice(program, index), buf, cap);
+  return SEEML_HIP_OK;
+}
+
+int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,
+                              uint64_t count) {
+  return Ret(e, e->impl.Profile(program, reps, ms_out, count));
+}
+
+int seeml_hip_time_instruction(seeml_hip_engine* e, int program, uint64_t index, int reps,
+                               float* avg_ms) {
+  return Ret(e, e->impl.TimeInstruction(program, index, reps, avg_ms));
+}
+
+uint64_t seeml_hip_program_length(const seeml_hip_engine* e, int program) {
+  return program < 0 || program > 2 ? 0 : e->impl.plan_.program[program].size();
+}
+
+// ---- standalone kernels ---------------------------------------------------
+
+const char* seeml_hip_kernel_error(void) { return seeml_hip::g_kernel_error.c_str(); }
+
+#define SEEML_CTX(ws_need)                                                     \
+  Ctx ctx;                                                                     \
+  if (Status s_ = seeml_hip::StandaloneCtx(stream, (ws_need), &ctx); !s_)      \
+    return seeml_hip::Report(s_);
+
+static int RunGemm(seeml_hip::GemmDesc d, void* stream, int cfg = -1, int splits = -1) {
+  const seeml_hip::GemmPlan plan = seeml_hip::PlanGemmWith(d, cfg, splits);
+  SEEML_CTX(plan.ws_bytes);
+  return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
+}
+
+int seeml_hip_gemm_nn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, const float* bias, int act, void* stream) {
+  seeml_hip::GemmDesc d = seeml_hip::GemmNNDesc(A, B, C, M, N, K);
+  d.bias = bias;
+  d.act = act;
+  return RunGemm(d, stream);
+}
+int seeml_hip_gemm_nt(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, void* stream) {
+  return RunGemm(seeml_hip::GemmNTDesc(A, B, C, M, N, K), stream);
+}
+int seeml_hip_gemm_tn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                      uint64_t K, void* stream) {
+  return RunGemm(seeml_hip::GemmTNDesc(A, B, C, M, N, K), stream);
+}
+int seeml_hip_gemm_acc_nn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                          uint64_t K, float alpha, void* stream) {
+  seeml_hip::GemmDesc d = seeml_hip::GemmNNDesc(A, B, C, M, N, K);
+  d.alpha = alpha;
+  d.accumulate = true;
+  return RunGemm(d, stream);
+}
+int seeml_hip_gemm_nn_q8(const float* A, const int8_t* B, float* C, uint64_t M, uint64_t N,
+                         uint64_t K, float scale, int act, void* stream) {
+  seeml_hip::GemmDesc d = seeml_hip::GemmNNDesc(A, nullptr, C, M, N, K);
+  d.B = B;
+  d.b_int8 = true;
+  d.alpha = scale;
+  d.act = act;
+  return RunGemm(d, stream);
+}
+int seeml_hip_gemm_nt_q8(const float* A, const int8_t* B, float* C, uint64_t M, uint64_t N,
+                         uint64_t K, float scale, void* stream) {
+  seeml_hip::GemmDesc d = seeml_hip::GemmNTDesc(A, nullptr, C, M, N, K);
+  d.B = B;
+  d.b_int8 = true;
+  d.alpha = scale;
+  return RunGemm(d, stream);
+}
+int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, uint64_t M,
+                          uint64_t N, uint64_t K, int cfg, int splits, void* stream) {
+  seeml_hip::GemmDesc d = layout == 1   ? seeml_hip::GemmNTDesc(A, B, C, M, N, K)
+                          : layout == 2 ? seeml_hip::GemmTNDesc(A, B, C, M, N, K)
+                                        : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
+  return RunGemm(d, stream, cfg, splits);
+}
+int seeml_hip_gemm_config_count(void) { return seeml_hip::GemmConfigCount(); }
+
+#define SEEML_SIMPLE(call) \
+  SEEML_CTX(0);            \
+  return seeml_hip::Report(call)
+
+int seeml_hip_add_ew(const float* x, const float* y, float* out, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AddEW(x, y, out, n, ctx));
+}
+int seeml_hip_mul_ew(const float* x, const float* y, float* out, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::MulEW(x, y, out, n, ctx));
+}
+int seeml_hip_add_bias(const float* x, const float* b, float* out, uint64_t rows, uint64_t cols,
+                       void* stream) {
+  SEEML_SIMPLE(seeml_hip::AddBias(x, b, out, rows, cols, ctx));
+}
+int seeml_hip_scale(const float* x, float* out, float alpha, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::Scale(x, out, alpha, n, ctx));
+}
+int seeml_hip_reduce_rows(const float* dy, float* db, uint64_t rows, uint64_t cols, void* stream) {
+  SEEML_SIMPLE(seeml_hip::ReduceRows(dy, db, rows, cols, ctx));
+}
+int seeml_hip_relu_fwd(const float* x, float* out, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::ReluFwd(x, out, n, ctx));
+}
+int seeml_hip_relu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::ReluBwd(dy, x, dx, n, ctx));
+}
+int seeml_hip_gelu_fwd(const float* x, float* out, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::GeluFwd(x, out, n, ctx));
+}
+int seeml_hip_gelu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::GeluBwd(dy, x, dx, n, ctx));
+}
+int seeml_hip_silu_fwd(const float* x, float* out, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::SiluFwd(x, out, n, ctx));
+}
+int seeml_hip_silu_bwd(const float* dy, const float* x, float* dx, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::SiluBwd(dy, x, dx, n, ctx));
+}
+int seeml_hip_embed_fwd(const int32_t* tokens, const float* table, float* out, uint64_t rows,
+                        uint64_t dim, uint64_t vocab, void* stream) {
+  SEEML_SIMPLE(seeml_hip::EmbedFwd(tokens, table, out, rows, dim, vocab, ctx));
+}
+int seeml_hip_fill(float* dst, float value, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::Fill(dst, value, n, ctx));
+}
+int seeml_hip_copy(const float* src, float* dst, uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::Copy(src, dst, n, ctx));
+}
+int seeml_hip_layer_norm_fwd(const float* x, const float* gamma, const float* beta, float* y,
+                             float* mean, float* rstd, uint64_t rows, uint64_t cols, void* stream) {
+  SEEML_SIMPLE(seeml_hip::LayerNormFwd(x, gamma, beta, y, mean, rstd, rows, cols, ctx));
+}
+int seeml_hip_layer_norm_bwd(const float* dy, const float* x, const float* gamma,
+                             const float* mean, const float* rstd, float* dx, uint64_t rows,
+                             uint64_t cols, void* stream) {
+  SEEML_SIMPLE(seeml_hip::LayerNormBwd(dy, x, gamma, mean, rstd, dx, rows, cols, ctx));
+}
+int seeml_hip_rms_norm_fwd(const float* x, const float* gamma, float* y, float* rstd,
+                           uint64_t rows, uint64_t cols, void* stream) {
+  SEEML_SIMPLE(seeml_hip::RmsNormFwd(x, gamma, y, rstd, rows, cols, ctx));
+}
+int seeml_hip_rms_norm_bwd(const float* dy, const float* x, const float* gamma,
+                           const float* rstd, float* dx, uint64_t rows, uint64_t cols,
+                           void* stream) {
+  SEEML_SIMPLE(seeml_hip::RmsNormBwd(dy, x, gamma, rstd, dx, rows, cols, ctx));
+}
+int seeml_hip_rope_fwd(const float* x, float* y, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                       float base, void* stream) {
+  SEEML_SIMPLE(seeml_hip::RopeFwd(x, y, B, S, H, d, base, ctx));
+}
+int seeml_hip_rope_bwd(const float* dy, float* dx, uint64_t B, uint64_t S, uint64_t H, uint64_t d,
+                       float base, void* stream) {
+  SEEML_SIMPLE(seeml_hip::RopeBwd(dy, dx, B, S, H, d, base, ctx));
+}
+int seeml_hip_attn_fwd(const float* q, const float* k, const float* v, float* o, float* probs,
+                       uint64_t B, uint64_t S, uint64_t H, uint64_t d, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AttnFwd(q, k, v, o, probs, B, S, H, d, ctx));
+}
+int seeml_hip_attn_dp(const float* dout, const float* v, float* dp, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AttnDP(dout, v, dp, B, S, H, d, ctx));
+}
+int seeml_hip_attn_dv(const float* probs, const float* dout, float* dv, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AttnDV(probs, dout, dv, B, S, H, d, ctx));
+}
+int seeml_hip_softmax_rows_bwd(const float* probs, const float* dp, float* ds, uint64_t rows,
+                               uint64_t cols, void* stream) {
+  SEEML_SIMPLE(seeml_hip::SoftmaxRowsBwd(probs, dp, ds, rows, cols, ctx));
+}
+int seeml_hip_attn_dq(const float* ds, const float* k, float* dq, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AttnDQ(ds, k, dq, B, S, H, d, ctx));
+}
+int seeml_hip_attn_dk(const float* ds, const float* q, float* dk, uint64_t B, uint64_t S,
+                      uint64_t H, uint64_t d, void* stream) {
+  SEEML_SIMPLE(seeml_hip::AttnDK(ds, q, dk, B, S, H, d, ctx));
+}
+int seeml_hip_softmax_xent_fwd(const float* logits, const int32_t* labels, float* loss,
+                               float* probs, uint64_t N, uint64_t C, void* stream) {
+  SEEML_CTX(seeml_hip::SoftmaxXEntFwdWorkspace(N));
+  return seeml_hip::Report(seeml_hip::SoftmaxXEntFwd(logits, labels, loss, probs, N, C, ctx));
+}
+int seeml_hip_softmax_xent_bwd(const float* probs, const int32_t* labels, const float* seed,
+                               float* dlogits, uint64_t N, uint64_t C, void* stream) {
+  SEEML_SIMPLE(seeml_hip::SoftmaxXEntBwd(probs, labels, seed, dlogits, N, C, ctx));
+}
+int seeml_hip_mse_fwd(const float* pred, const float* target, float* loss, uint64_t n,
+                      void* stream) {
+  SEEML_CTX(seeml_hip::MseFwdWorkspace(n));
+  return seeml_hip::Report(seeml_hip::MseFwd(pred, target, loss, n, ctx));
+}
+int seeml_hip_mse_bwd(const float* pred, const float* target, const float* seed, float* dpred,
+                      uint64_t n, void* stream) {
+  SEEML_SIMPLE(seeml_hip::MseBwd(pred, target, seed, dpred, n, ctx));
+}
+int seeml_hip_kl_distill_fwd(const float* s_logits, const float* t_logits, float* loss,
+                             float* p_s, float* p_t, uint64_t N, uint64_t C, float T,
+                             void* stream) {
+  SEEML_CTX(seeml_hip::KLDistillFwdWorkspace(N));
+  return seeml_hip::Report(seeml_hip::KLDistillFwd(s_logits, t_logits, loss, p_s, p_t, N, C, T, ctx));
+}
+int seeml_hip_kl_distill_bwd(const float* p_s, const float* p_t, const float* seed,
+                             float* dlogits, uint64_t N, uint64_t C, float T, void* stream) {
+  SEEML_SIMPLE(seeml_hip::KLDistillBwd(p_s, p_t, seed, dlogits, N, C, T, ctx));
+}
+int seeml_hip_clip_norm(float* g, uint64_t n, float max_norm, void* stream) {
+  SEEML_CTX(seeml_hip::ClipNormWorkspace(n));
+  return seeml_hip::Report(seeml_hip::ClipNorm(g, n, max_norm, ctx));
+}
+
+static int UploadScalars(const Ctx& ctx, const seeml_hip::StepScalars& s) {
+  const Status st = seeml_hip::HipOk(
+      hipMemcpyAsync(const_cast<seeml_hip::StepScalars*>(ctx.scalars), &s, sizeof s,
+                     hipMemcpyHostToDevice, ctx.stream),
+      "scalars upload");
+  if (!st) return seeml_hip::Report(st);
+  // `s` lives on this host stack frame: complete the copy before returning.
+  return seeml_hip::Report(seeml_hip::HipOk(hipStreamSynchronize(ctx.stream), "scalars sync"));
+}
+
+int seeml_hip_sgd_step(float* p, const float* g, uint64_t n, float lr, float weight_decay,
+                       void* stream) {
+  SEEML_CTX(0);
+  seeml_hip::StepScalars s{};
+  s.lr = lr;
+  s.weight_decay = weight_decay;
+  if (int r = UploadScalars(ctx, s); r != SEEML_HIP_OK) return r;
+  return seeml_hip::Report(seeml_hip::SgdStep(p, g, n, ctx));
+}
+
+int seeml_hip_adamw_step(float* p, const float* g, float* m, float* v, uint64_t n, float lr,
+                         float beta1, float beta2, float eps, float weight_decay, uint64_t step,
+                         void* stream) {
+  SEEML_CTX(0);
+  seeml_hip::PlanHeader h{};
+  h.lr = lr;
+  h.beta1 = beta1;
+  h.beta2 = beta2;
+  h.eps = eps;
+  h.weight_decay = weight_decay;
+  h.lr_schedule = 0;
+  const seeml_hip::StepScalars s = seeml_hip::MakeStepScalars(h, step);
+  if (int r = UploadScalars(ctx, s); r != SEEML_HIP_OK) return r;
+  return seeml_hip::Report(seeml_hip::AdamWStep(p, g, m, v, n, ctx));
+}
+
+}  // extern "C"

@@ -1,0 +1,477 @@
+// k_pointwise.hip — bandwidth-bound elementwise kernels for gfx950.
+//
+// Reference semantics: runtime/executor/elementwise.cc, activation.cc,
+// optimizer.cc:37-69, loss.cc:61-72,91-97,134-140, attention.cc:39-92.
+// Layout: flat f32 arrays in the device arena. Each kernel is a grid-stride
+// loop over float4 vectors (when every pointer is 16-byte aligned) plus a
+// scalar tail, so HBM traffic is fully coalesced 16-byte accesses; the grid
+// is capped so one launch keeps every CU busy without oversubscribing.
+//
+// Bits: with -ffp-contract=off the per-element expressions below round
+// exactly where the reference's do, so AddEW/MulEW/Scale/AddBias/ReLU/
+// AdamW/SGD/Fill/Copy/Embed/loss-backward results are bit-identical to the
+// CPU executor; GELU/SiLU/RoPE go through device expf/tanhf/sinf/cosf and
+// match to within a few ulp.
+#include "device_common.h"
+#include "kernels.h"
+
+#include <math.h>
+
+#include <cmath>
+
+namespace seeml_hip {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr size_t kGridCap = 8192;
+
+struct AddF { __device__ float operator()(float a, float b) const { return a + b; } };
+struct MulF { __device__ float operator()(float a, float b) const { return a * b; } };
+struct ScaleF {
+  float alpha;
+  __device__ float operator()(float x) const { return alpha * x; }
+};
+struct ReluF { __device__ float operator()(float x) const { return dev_relu(x); } };
+struct ReluBwdF { __device__ float operator()(float dy, float x) const { return x > 0.0f ? dy : 0.0f; } };
+struct GeluF { __device__ float operator()(float x) const { return dev_gelu(x); } };
+struct SiluF { __device__ float operator()(float x) const { return dev_silu(x); } };
+struct GeluBwdF {
+  __device__ float operator()(float dy, float v) const {
+    const float kC = 0.7978845608028654f, kA = 0.044715f;
+    const float u = kC * (v + kA * v * v * v);
+    const float t = tanhf(u);
+    const float one_minus_t2 = 1.0f - t * t;
+    // Saturated tanh: the sech^2 factor is an exact zero while u' may
+    // overflow; drop the dead term (activation.cc:47-56).
+    const float tail = one_minus_t2 == 0.0f
+                           ? 0.0f
+                           : 0.5f * v * one_minus_t2 * (kC * (1.0f + 3.0f * kA * v * v));
+    return dy * (0.5f * (1.0f + t) + tail);
+  }
+};
+struct SiluBwdF {
+  __device__ float operator()(float dy, float x) const {
+    const float s = dev_sigmoid(x);
+    return dy * (s * (1.0f + x * (1.0f - s)));
+  }
+};
+struct FillF {
+  float v;
+  __device__ float operator()(float) const { return v; }
+};
+struct CopyF { __device__ float operator()(float x) const { return x; } };
+
+template <class F>
+__global__ __launch_bounds__(kBlock) void ew_unary(const float* __restrict__ x,
+                                                   float* __restrict__ out, size_t n, size_t nv,
+                                                   F f) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* o4 = reinterpret_cast<float4*>(out);
+  for (size_t i = gid; i < nv; i += stride) {
+    const float4 a = x4[i];
+    o4[i] = make_float4(f(a.x), f(a.y), f(a.z), f(a.w));
+  }
+  for (size_t i = nv * 4 + gid; i < n; i += stride) out[i] = f(x[i]);
+}
+
+template <class F>
+__global__ __launch_bounds__(kBlock) void ew_binary(const float* __restrict__ x,
+                                                    const float* __restrict__ y,
+                                                    float* __restrict__ out, size_t n, size_t nv,
+                                                    F f) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const float4* y4 = reinterpret_cast<const float4*>(y);
+  float4* o4 = reinterpret_cast<float4*>(out);
+  for (size_t i = gid; i < nv; i += stride) {
+    const float4 a = x4[i], b = y4[i];
+    o4[i] = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+  }
+  for (size_t i = nv * 4 + gid; i < n; i += stride) out[i] = f(x[i], y[i]);
+}
+
+// Fill writes only: a separate kernel so no read of uninitialised memory.
+__global__ __launch_bounds__(kBlock) void fill_kernel(float* __restrict__ out, size_t n, size_t nv,
+                                                      float v) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  float4* o4 = reinterpret_cast<float4*>(out);
+  for (size_t i = gid; i < nv; i += stride) o4[i] = make_float4(v, v, v, v);
+  for (size_t i = nv * 4 + gid; i < n; i += stride) out[i] = v;
+}
+
+template <class F>
+Status Unary(const float* x, float* out, size_t n, F f, const Ctx& c, const char* what) {
+  if (n == 0) return Status::Ok();
+  const size_t nv = (aligned16(x) && aligned16(out)) ? n / 4 : 0;
+  const size_t work = nv ? nv : n;
+  hipLaunchKernelGGL(ew_unary<F>, dim3(grid_for(work, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, x, out, n, nv, f);
+  return LaunchStatus(what);
+}
+
+template <class F>
+Status Binary(const float* x, const float* y, float* out, size_t n, F f, const Ctx& c,
+              const char* what) {
+  if (n == 0) return Status::Ok();
+  const size_t nv = (aligned16(x) && aligned16(y) && aligned16(out)) ? n / 4 : 0;
+  const size_t work = nv ? nv : n;
+  hipLaunchKernelGGL(ew_binary<F>, dim3(grid_for(work, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, x, y, out, n, nv, f);
+  return LaunchStatus(what);
+}
+
+// out[r, c] = x[r, c] + b[c]  (elementwise.cc:28-36)
+__global__ __launch_bounds__(kBlock) void add_bias_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ b,
+                                                          float* __restrict__ out, size_t n,
+                                                          size_t cols, int vec) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (vec) {
+    const size_t nv = n / 4, cv = cols / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    float4* o4 = reinterpret_cast<float4*>(out);
+    for (size_t i = gid; i < nv; i += stride) {
+      const float4 a = x4[i], bb = b4[i % cv];
+      o4[i] = make_float4(a.x + bb.x, a.y + bb.y, a.z + bb.z, a.w + bb.w);
+    }
+  } else {
+    for (size_t i = gid; i < n; i += stride) out[i] = x[i] + b[i % cols];
+  }
+}
+
+// Row gather out[t, :] = table[tokens[t], :] (elementwise.cc:44-53). A token
+// outside [0, vocab) — which the feeder contract excludes — yields a NaN row
+// instead of an out-of-bounds read, so the step's finite-loss guard trips.
+__global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* __restrict__ tokens,
+                                                       const float* __restrict__ table,
+                                                       float* __restrict__ out, size_t rows,
+                                                       size_t dim, size_t vocab, int vec) {
+  const int lane = threadIdx.x % kWave;
+  const size_t row0 = (static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x) / kWave;
+  const size_t rstride = static_cast<size_t>(gridDim.x) * (kBlock / kWave);
+  for (size_t r = row0; r < rows; r += rstride) {
+    const int32_t t = tokens[r];
+    float* dst = out + r * dim;
+    if (t < 0 || static_cast<size_t>(t) >= vocab) {
+      for (size_t c = lane; c < dim; c += kWave) dst[c] = __builtin_nanf("");
+      continue;
+    }
+    const float* src = table + static_cast<size_t>(t) * dim;
+    if (vec) {
+      const float4* s4 = reinterpret_cast<const float4*>(src);
+      float4* d4 = reinterpret_cast<float4*>(dst);
+      for (size_t c = lane; c < dim / 4; c += kWave) d4[c] = s4[c];
+    } else {
+      for (size_t c = lane; c < dim; c += kWave) dst[c] = src[c];
+    }
+  }
+}
+
+// db[c] = sum_r dy[r, c], rows in order per column (elementwise.cc:55-67):
+// one thread owns a column, so the f32 sum order — and the bits — are the
+// reference's.
+__global__ __launch_bounds__(kBlock) void reduce_rows_kernel(const float* __restrict__ dy,
+                                                             float* __restrict__ db, size_t rows,
+                                                             size_t cols) {
+  const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.0f;
+  for (size_t r = 0; r < rows; ++r) acc += dy[r * cols + c];
+  db[c] = acc;
+}
+
+// dlogits = (seed/N) * probs, minus seed/N at the label (loss.cc:61-72).
+__global__ __launch_bounds__(kBlock) void xent_bwd_kernel(const float* __restrict__ probs,
+                                                          const int32_t* __restrict__ labels,
+                                                          const float* __restrict__ seed,
+                                                          float* __restrict__ dl, size_t N,
+                                                          size_t C) {
+  const float scale = *seed / static_cast<float>(N);
+  const size_t total = N * C;
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+    const size_t n = i / C, c = i - n * C;
+    float v = scale * probs[i];
+    const int32_t lab = labels[n];
+    if (lab >= 0 && static_cast<size_t>(lab) == c) v -= scale;
+    dl[i] = v;
+  }
+}
+
+// dpred = (2*seed/n) * (pred - target)  (loss.cc:91-97)
+__global__ __launch_bounds__(kBlock) void mse_bwd_kernel(const float* __restrict__ pred,
+                                                         const float* __restrict__ target,
+                                                         const float* __restrict__ seed,
+                                                         float* __restrict__ dp, size_t n,
+                                                         size_t nv) {
+  const float scale = 2.0f * *seed / static_cast<float>(n);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const float4* p4 = reinterpret_cast<const float4*>(pred);
+  const float4* t4 = reinterpret_cast<const float4*>(target);
+  float4* d4 = reinterpret_cast<float4*>(dp);
+  for (size_t i = gid; i < nv; i += stride) {
+    const float4 a = p4[i], b = t4[i];
+    d4[i] = make_float4(scale * (a.x - b.x), scale * (a.y - b.y), scale * (a.z - b.z),
+                        scale * (a.w - b.w));
+  }
+  for (size_t i = nv * 4 + gid; i < n; i += stride) dp[i] = scale * (pred[i] - target[i]);
+}
+
+// dlogits = seed/(N*T) * (p_s - p_t)  (loss.cc:134-140)
+__global__ __launch_bounds__(kBlock) void kl_bwd_kernel(const float* __restrict__ ps,
+                                                        const float* __restrict__ pt,
+                                                        const float* __restrict__ seed,
+                                                        float* __restrict__ dl, size_t total,
+                                                        size_t N, float T) {
+  const float scale = *seed / (static_cast<float>(N) * T);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride)
+    dl[i] = scale * (ps[i] - pt[i]);
+}
+
+// p -= lr * (g + wd * p)  (optimizer.cc:37-42), lr = this step's EffectiveLr.
+__global__ __launch_bounds__(kBlock) void sgd_kernel(float* __restrict__ p,
+                                                     const float* __restrict__ g, size_t n,
+                                                     const StepScalars* __restrict__ s) {
+  const float lr = s->lr, wd = s->weight_decay;
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    p[i] -= lr * (g[i] + wd * p[i]);
+}
+
+// AdamW with host-hoisted bias corrections (optimizer.cc:44-69).
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, float lr,
+                                           float b1, float b2, float omb1, float omb2,
+                                           float ibc1, float ibc2, float eps, float wd) {
+  const float mi = b1 * m + omb1 * g;
+  const float vi = b2 * v + omb2 * g * g;
+  m = mi;
+  v = vi;
+  const float m_hat = mi * ibc1;
+  const float v_hat = vi * ibc2;
+  p -= lr * (__fdiv_rn(m_hat, __fsqrt_rn(v_hat) + eps) + wd * p);
+}
+
+__global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ p,
+                                                       const float* __restrict__ g,
+                                                       float* __restrict__ m,
+                                                       float* __restrict__ v, size_t n, size_t nv,
+                                                       const StepScalars* __restrict__ s) {
+  const float lr = s->lr, b1 = s->beta1, b2 = s->beta2, omb1 = s->om_b1, omb2 = s->om_b2;
+  const float ibc1 = s->inv_bc1, ibc2 = s->inv_bc2, eps = s->eps, wd = s->weight_decay;
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  float4* p4 = reinterpret_cast<float4*>(p);
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  float4* m4 = reinterpret_cast<float4*>(m);
+  float4* v4 = reinterpret_cast<float4*>(v);
+  for (size_t i = gid; i < nv; i += stride) {
+    float4 pp = p4[i], mm = m4[i], vv = v4[i];
+    const float4 gg = g4[i];
+    adamw_elem(pp.x, gg.x, mm.x, vv.x, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+    adamw_elem(pp.y, gg.y, mm.y, vv.y, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+    adamw_elem(pp.z, gg.z, mm.z, vv.z, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+    adamw_elem(pp.w, gg.w, mm.w, vv.w, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+    p4[i] = pp;
+    m4[i] = mm;
+    v4[i] = vv;
+  }
+  for (size_t i = nv * 4 + gid; i < n; i += stride) {
+    float pp = p[i], mm = m[i], vv = v[i];
+    adamw_elem(pp, g[i], mm, vv, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+    p[i] = pp;
+    m[i] = mm;
+    v[i] = vv;
+  }
+}
+
+// RoPE on interleaved pairs (attention.cc:39-92). One thread per pair; the
+// pair's frequency step^c is the reference's sequential recurrence
+// (freq *= step, c times), so theta carries the CPU bits; only sinf/cosf
+// are the device's. `dir` = +1 forward rotation, -1 its transpose.
+__global__ __launch_bounds__(kBlock) void rope_kernel(const float* __restrict__ x,
+                                                      float* __restrict__ y, size_t pairs,
+                                                      size_t S, size_t H, size_t half_d,
+                                                      float step, int dir) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t p = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; p < pairs; p += stride) {
+    const size_t c2 = p % half_d;
+    const size_t u = p / half_d;  // (row, head) unit
+    const size_t s = (u / H) % S;
+    float freq = 1.0f;
+    for (size_t i = 0; i < c2; ++i) freq *= step;
+    const float theta = static_cast<float>(s) * freq;
+    const float cs = cosf(theta), sn = sinf(theta);
+    const float a = x[2 * p], b2 = x[2 * p + 1];
+    if (dir > 0) {
+      y[2 * p] = a * cs - b2 * sn;
+      y[2 * p + 1] = a * sn + b2 * cs;
+    } else {
+      y[2 * p] = a * cs + b2 * sn;
+      y[2 * p + 1] = -a * sn + b2 * cs;
+    }
+  }
+}
+
+Status Rope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,
+            int dir, const Ctx& c, const char* what) {
+  if (d % 2 != 0) return Status::Fail(kUnitEngine, std::string(what) + ": odd head width");
+  const size_t pairs = B * S * H * (d / 2);
+  if (pairs == 0) return Status::Ok();
+  // step = base^(-2/d) evaluated on the host with the reference's powf.
+  const float step = ::powf(base, -2.0f / static_cast<float>(d));
+  hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, x, y, pairs, S, H, d / 2, step, dir);
+  return LaunchStatus(what);
+}
+
+}  // namespace
+
+Status AddEW(const float* x, const float* y, float* out, size_t n, const Ctx& c) {
+  return Binary(x, y, out, n, AddF{}, c, "AddEW");
+}
+Status MulEW(const float* x, const float* y, float* out, size_t n, const Ctx& c) {
+  return Binary(x, y, out, n, MulF{}, c, "MulEW");
+}
+Status Scale(const float* x, float* out, float alpha, size_t n, const Ctx& c) {
+  return Unary(x, out, n, ScaleF{alpha}, c, "Scale");
+}
+Status ReluFwd(const float* x, float* out, size_t n, const Ctx& c) {
+  return Unary(x, out, n, ReluF{}, c, "ReluFwd");
+}
+Status ReluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c) {
+  return Binary(dy, x, dx, n, ReluBwdF{}, c, "ReluBwd");
+}
+Status GeluFwd(const float* x, float* out, size_t n, const Ctx& c) {
+  return Unary(x, out, n, GeluF{}, c, "GeluFwd");
+}
+Status GeluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c) {
+  return Binary(dy, x, dx, n, GeluBwdF{}, c, "GeluBwd");
+}
+Status SiluFwd(const float* x, float* out, size_t n, const Ctx& c) {
+  return Unary(x, out, n, SiluF{}, c, "SiluFwd");
+}
+Status SiluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c) {
+  return Binary(dy, x, dx, n, SiluBwdF{}, c, "SiluBwd");
+}
+Status Copy(const float* src, float* dst, size_t n, const Ctx& c) {
+  return Unary(src, dst, n, CopyF{}, c, "Copy");
+}
+
+Status Fill(float* dst, float value, size_t n, const Ctx& c) {
+  if (n == 0) return Status::Ok();
+  const size_t nv = aligned16(dst) ? n / 4 : 0;
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(nv ? nv : n, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, dst, n, nv, value);
+  return LaunchStatus("Fill");
+}
+
+Status AddBias(const float* x, const float* b, float* out, size_t rows, size_t cols,
+               const Ctx& c) {
+  const size_t n = rows * cols;
+  if (n == 0) return Status::Ok();
+  const int vec = (cols % 4 == 0 && aligned16(x) && aligned16(b) && aligned16(out)) ? 1 : 0;
+  hipLaunchKernelGGL(add_bias_kernel, dim3(grid_for(vec ? n / 4 : n, kBlock, kGridCap)),
+                     dim3(kBlock), 0, c.stream, x, b, out, n, cols, vec);
+  return LaunchStatus("AddBias");
+}
+
+Status EmbedFwd(const int32_t* tokens, const float* table, float* out, size_t rows, size_t dim,
+                size_t vocab, const Ctx& c) {
+  if (rows == 0 || dim == 0) return Status::Ok();
+  const int vec = (dim % 4 == 0 && aligned16(table) && aligned16(out)) ? 1 : 0;
+  const size_t waves = rows;
+  hipLaunchKernelGGL(embed_kernel, dim3(grid_for(waves * kWave, kBlock, kGridCap)), dim3(kBlock),
+                     0, c.stream, tokens, table, out, rows, dim, vocab, vec);
+  return LaunchStatus("EmbedFwd");
+}
+
+Status ReduceRows(const float* dy, float* db, size_t rows, size_t cols, const Ctx& c) {
+  if (cols == 0) return Status::Ok();
+  hipLaunchKernelGGL(reduce_rows_kernel, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                     c.stream, dy, db, rows, cols);
+  return LaunchStatus("ReduceRows");
+}
+
+Status SoftmaxXEntBwd(const float* probs, const int32_t* labels, const float* seed,
+                      float* dlogits, size_t N, size_t C, const Ctx& c) {
+  if (N * C == 0) return Status::Ok();
+  hipLaunchKernelGGL(xent_bwd_kernel, dim3(grid_for(N * C, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, probs, labels, seed, dlogits, N, C);
+  return LaunchStatus("SoftmaxXEntBwd");
+}
+
+Status MseBwd(const float* pred, const float* target, const float* seed, float* dpred, size_t n,
+              const Ctx& c) {
+  if (n == 0) return Status::Ok();
+  const size_t nv = (aligned16(pred) && aligned16(target) && aligned16(dpred)) ? n / 4 : 0;
+  hipLaunchKernelGGL(mse_bwd_kernel, dim3(grid_for(nv ? nv : n, kBlock, kGridCap)), dim3(kBlock),
+                     0, c.stream, pred, target, seed, dpred, n, nv);
+  return LaunchStatus("MseBwd");
+}
+
+Status KLDistillBwd(const float* p_s, const float* p_t, const float* seed, float* dlogits,
+                    size_t N, size_t C, float T, const Ctx& c) {
+  if (N * C == 0) return Status::Ok();
+  hipLaunchKernelGGL(kl_bwd_kernel, dim3(grid_for(N * C, kBlock, kGridCap)), dim3(kBlock), 0,
+                     c.stream, p_s, p_t, seed, dlogits, N * C, N, T);
+  return LaunchStatus("KLDistillBwd");
+}
+
+Status SgdStep(float* p, const float* g, size_t n, const Ctx& c) {
+  if (n == 0) return Status::Ok();
+  if (!c.scalars) return Status::Fail(kUnitEngine, "SgdStep: no step scalars bound");
+  hipLaunchKernelGGL(sgd_kernel, dim3(grid_for(n, kBlock, kGridCap)), dim3(kBlock), 0, c.stream,
+                     p, g, n, c.scalars);
+  return LaunchStatus("SgdStep");
+}
+
+Status AdamWStep(float* p, const float* g, float* m, float* v, size_t n, const Ctx& c) {
+  if (n == 0) return Status::Ok();
+  if (!c.scalars) return Status::Fail(kUnitEngine, "AdamWStep: no step scalars bound");
+  const size_t nv =
+      (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) ? n / 4 : 0;
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(nv ? nv : n, kBlock, kGridCap)), dim3(kBlock),
+                     0, c.stream, p, g, m, v, n, nv, c.scalars);
+  return LaunchStatus("AdamWStep");
+}
+
+Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,
+               const Ctx& c) {
+  return Rope(x, y, B, S, H, d, base, +1, c, "RopeFwd");
+}
+Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t d, float base,
+               const Ctx& c) {
+  return Rope(dy, dx, B, S, H, d, base, -1, c, "RopeBwd");
+}
+
+StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step) {
+  StepScalars s{};
+  s.lr = EffectiveLr(h, step);
+  // optimizer.cc:52-58: float pow, hoisted reciprocal bias corrections.
+  s.inv_bc1 = 1.0f / (1.0f - ::powf(h.beta1, static_cast<float>(step)));
+  s.inv_bc2 = 1.0f / (1.0f - ::powf(h.beta2, static_cast<float>(step)));
+  s.beta1 = h.beta1;
+  s.beta2 = h.beta2;
+  s.om_b1 = 1.0f - h.beta1;
+  s.om_b2 = 1.0f - h.beta2;
+  s.eps = h.eps;
+  s.weight_decay = h.weight_decay;
+  return s;
+}
+
+Status LaunchStatus(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return Status::Ok();
+  return Status::Fail(kUnitEngine, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace seeml_hip

@@ -1,0 +1,473 @@
+// k_rows.hip — row-reduction kernels for gfx950: norms, softmaxes, losses.
+//
+// Reference semantics: runtime/executor/normalization.cc, loss.cc:21-59,
+// 74-89, 99-132, optimizer.cc:17-35, attention.cc:94-136 (softmax part) and
+// :185-201. Accumulator types follow the reference: the norm statistics,
+// loss totals, clip norm, attention denominator and softmax-backward rowsum
+// accumulate in double; the loss-side softmax max/sum in f32.
+//
+// Layout & mapping: one row per TPR threads (TPR = 64, one wavefront, for
+// rows up to ~2K; TPR = 256, one workgroup, for wider rows), elements of a
+// row strided by TPR so every pass is a coalesced sweep. Reductions are the
+// fixed trees of device_common.h; cross-row totals (losses, norms) go
+// through a per-row (or per-block) double workspace summed by one
+// workgroup in index order — deterministic, no atomics.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace seeml_hip {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int TPR>
+__device__ __forceinline__ double row_sum_d(double v, double* scratch) {
+  if constexpr (TPR == kWave) return wave_sum(v);
+  else return block_sum<double, kBlock>(v, scratch);
+}
+template <int TPR>
+__device__ __forceinline__ float row_sum_f(float v, float* scratch) {
+  if constexpr (TPR == kWave) return wave_sum(v);
+  else return block_sum<float, kBlock>(v, scratch);
+}
+template <int TPR>
+__device__ __forceinline__ float row_max_f(float v, float* scratch) {
+  if constexpr (TPR == kWave) return wave_max(v);
+  else return block_max<kBlock>(v, scratch);
+}
+
+// Sum of n doubles in index-strided order, one workgroup; out = total/div.
+__global__ __launch_bounds__(kBlock) void finish_mean_kernel(const double* __restrict__ terms,
+                                                             size_t n, double div,
+                                                             float* __restrict__ out) {
+  __shared__ double scratch[kBlock / kWave];
+  double acc = 0.0;
+  for (size_t i = threadIdx.x; i < n; i += kBlock) acc += terms[i];
+  const double total = block_sum<double, kBlock>(acc, scratch);
+  if (threadIdx.x == 0) *out = static_cast<float>(total / div);
+}
+
+// ---- MSE / ClipNorm partials ------------------------------------------------
+
+size_t PartialBlocks(size_t n) {
+  size_t g = (n + 16383) / 16384;
+  if (g < 1) g = 1;
+  if (g > 2048) g = 2048;
+  return g;
+}
+
+// Block b owns the contiguous range [b*chunk, (b+1)*chunk): a shape-only
+// decomposition, like ParallelFor's.
+__global__ __launch_bounds__(kBlock) void sq_diff_partials(const float* __restrict__ a,
+                                                           const float* __restrict__ b,
+                                                           size_t n, size_t chunk,
+                                                           double* __restrict__ out) {
+  __shared__ double scratch[kBlock / kWave];
+  const size_t begin = static_cast<size_t>(blockIdx.x) * chunk;
+  const size_t end = begin + chunk < n ? begin + chunk : n;
+  double acc = 0.0;
+  for (size_t i = begin + threadIdx.x; i < end; i += kBlock) {
+    const double d = b ? static_cast<double>(a[i]) - static_cast<double>(b[i])
+                       : static_cast<double>(a[i]);
+    acc += d * d;
+  }
+  const double t = block_sum<double, kBlock>(acc, scratch);
+  if (threadIdx.x == 0) out[blockIdx.x] = t;
+}
+
+// ClipNorm decision + scale on device (optimizer.cc:28-34): sum the
+// partials, norm = sqrt(total) in double, scale only if norm > max_norm.
+__global__ __launch_bounds__(kBlock) void clip_apply_kernel(float* __restrict__ g, size_t n,
+                                                            const double* __restrict__ partials,
+                                                            size_t np, float max_norm) {
+  __shared__ double scratch[kBlock / kWave];
+  double acc = 0.0;
+  for (size_t i = threadIdx.x; i < np; i += kBlock) acc += partials[i];
+  const double sq = block_sum<double, kBlock>(acc, scratch);
+  const double norm = sqrt(sq);
+  if (norm <= static_cast<double>(max_norm) || norm == 0.0) return;
+  const float s = static_cast<float>(static_cast<double>(max_norm) / norm);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    g[i] *= s;
+}
+
+// ---- softmax cross-entropy forward -------------------------------------------
+
+// One row per TPR threads: f32 max, f32 exp-sum, probs = e * (1/sum); the
+// row's -log(max(p_label, 1e-12)) term in double goes to terms[row]. NaN in
+// the row propagates (fmax scrubs NaN from the max, but exp(NaN) does not).
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void xent_fwd_rows(const float* __restrict__ logits,
+                                                        const int32_t* __restrict__ labels,
+                                                        float* __restrict__ probs, size_t N,
+                                                        size_t C, double* __restrict__ terms) {
+  __shared__ float fscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t n = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (n >= N) return;  // block-uniform when TPR == kBlock
+  const float* x = logits + n * C;
+  float* p = probs + n * C;
+  float mx = x[0];
+  for (size_t c = t; c < C; c += TPR) mx = fmaxf(mx, x[c]);
+  mx = row_max_f<TPR>(mx, fscratch);
+  float s = 0.0f;
+  for (size_t c = t; c < C; c += TPR) {
+    const float e = expf(x[c] - mx);
+    p[c] = e;
+    s += e;
+  }
+  const float sum = row_sum_f<TPR>(s, fscratch);
+  const float inv = 1.0f / sum;
+  for (size_t c = t; c < C; c += TPR) p[c] = p[c] * inv;
+  if (t == 0) {
+    const int32_t lab = labels[n];
+    double term;
+    if (lab < 0 || static_cast<size_t>(lab) >= C) {
+      term = __builtin_nan("");  // outside the feeder contract: poison the loss
+    } else {
+      const float pl = expf(x[lab] - mx) * inv;  // same expression as p[lab]
+      const double safe = isnan(pl) ? static_cast<double>(pl)
+                                    : static_cast<double>(fmaxf(pl, 1e-12f));
+      term = -log(safe);
+    }
+    terms[n] = term;
+  }
+}
+
+// ---- KL distillation forward ----------------------------------------------------
+
+template <int TPR>
+__device__ void row_softmax_T(const float* __restrict__ x, float* __restrict__ p, size_t C,
+                              float inv_T, int t, float* scratch) {
+  float mx = x[0] * inv_T;
+  for (size_t c = t; c < C; c += TPR) mx = fmaxf(mx, x[c] * inv_T);
+  mx = row_max_f<TPR>(mx, scratch);
+  float s = 0.0f;
+  for (size_t c = t; c < C; c += TPR) {
+    const float e = expf(x[c] * inv_T - mx);
+    p[c] = e;
+    s += e;
+  }
+  const float inv = 1.0f / row_sum_f<TPR>(s, scratch);
+  for (size_t c = t; c < C; c += TPR) p[c] = p[c] * inv;
+}
+
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void kl_fwd_rows(const float* __restrict__ s_logits,
+                                                      const float* __restrict__ t_logits,
+                                                      float* __restrict__ ps,
+                                                      float* __restrict__ pt, size_t N, size_t C,
+                                                      float inv_T, double* __restrict__ terms) {
+  __shared__ float fscratch[kBlock / kWave];
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t n = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (n >= N) return;
+  float* prs = ps + n * C;
+  float* prt = pt + n * C;
+  row_softmax_T<TPR>(s_logits + n * C, prs, C, inv_T, t, fscratch);
+  row_softmax_T<TPR>(t_logits + n * C, prt, C, inv_T, t, fscratch);
+  double acc = 0.0;
+  for (size_t c = t; c < C; c += TPR) {
+    const float q = prt[c];
+    if (q <= 0.0f) continue;
+    const float raw = prs[c];
+    const double s = isnan(raw) ? static_cast<double>(raw) : static_cast<double>(fmaxf(raw, 1e-12f));
+    acc += static_cast<double>(q) * (log(static_cast<double>(q)) - log(s));
+  }
+  const double total = row_sum_d<TPR>(acc, dscratch);
+  if (t == 0) terms[n] = total;
+}
+
+// ---- norms ---------------------------------------------------------------------
+
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void layer_norm_fwd_rows(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, size_t rows,
+    size_t cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (r >= rows) return;
+  const float* xr = x + r * cols;
+  double s = 0.0;
+  for (size_t c = t; c < cols; c += TPR) s += static_cast<double>(xr[c]);
+  const double sum = row_sum_d<TPR>(s, dscratch);
+  const float mu = static_cast<float>(sum / static_cast<double>(cols));
+  double v = 0.0;
+  for (size_t c = t; c < cols; c += TPR) {
+    const double d = static_cast<double>(xr[c]) - static_cast<double>(mu);
+    v += d * d;
+  }
+  const double var = row_sum_d<TPR>(v, dscratch);
+  const float rs =
+      __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(var / static_cast<double>(cols)) + 1e-5f));
+  if (t == 0) {
+    mean[r] = mu;
+    rstd[r] = rs;
+  }
+  float* yr = y + r * cols;
+  for (size_t c = t; c < cols; c += TPR) yr[c] = (xr[c] - mu) * rs * gamma[c] + beta[c];
+}
+
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void layer_norm_bwd_rows(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, float* __restrict__ dx,
+    size_t rows, size_t cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (r >= rows) return;
+  const float inv_d = __fdiv_rn(1.0f, static_cast<float>(cols));
+  const float* dyr = dy + r * cols;
+  const float* xr = x + r * cols;
+  const float mu = mean[r], rs = rstd[r];
+  double sg = 0.0, sgx = 0.0;
+  for (size_t c = t; c < cols; c += TPR) {
+    const float xhat = (xr[c] - mu) * rs;
+    const float g = dyr[c] * gamma[c];
+    sg += static_cast<double>(g);
+    sgx += static_cast<double>(g) * static_cast<double>(xhat);
+  }
+  const double sum_g = row_sum_d<TPR>(sg, dscratch);
+  const double sum_gx = row_sum_d<TPR>(sgx, dscratch);
+  const float mg = static_cast<float>(sum_g) * inv_d;
+  const float mgx = static_cast<float>(sum_gx) * inv_d;
+  float* dxr = dx + r * cols;
+  for (size_t c = t; c < cols; c += TPR) {
+    const float xhat = (xr[c] - mu) * rs;
+    const float g = dyr[c] * gamma[c];
+    dxr[c] = rs * (g - mg - xhat * mgx);
+  }
+}
+
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void rms_norm_fwd_rows(const float* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ rstd, size_t rows,
+                                                            size_t cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (r >= rows) return;
+  const float* xr = x + r * cols;
+  double s = 0.0;
+  for (size_t c = t; c < cols; c += TPR) s += static_cast<double>(xr[c]) * static_cast<double>(xr[c]);
+  const double ss = row_sum_d<TPR>(s, dscratch);
+  const float rs =
+      __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f));
+  if (t == 0) rstd[r] = rs;
+  float* yr = y + r * cols;
+  for (size_t c = t; c < cols; c += TPR) yr[c] = xr[c] * rs * gamma[c];
+}
+
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_rows(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, size_t cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (r >= rows) return;
+  const float inv_d = __fdiv_rn(1.0f, static_cast<float>(cols));
+  const float* dyr = dy + r * cols;
+  const float* xr = x + r * cols;
+  const float rs = rstd[r];
+  double s = 0.0;
+  for (size_t c = t; c < cols; c += TPR)
+    s += static_cast<double>(dyr[c] * gamma[c]) * static_cast<double>(xr[c]);
+  const float mgx = static_cast<float>(row_sum_d<TPR>(s, dscratch)) * inv_d;
+  float* dxr = dx + r * cols;
+  for (size_t c = t; c < cols; c += TPR)
+    dxr[c] = rs * (dyr[c] * gamma[c] - xr[c] * rs * rs * mgx);
+}
+
+// dS = P * (dP - rowsum(dP * P)), rowsum in double (attention.cc:185-201).
+template <int TPR>
+__global__ __launch_bounds__(kBlock) void softmax_rows_bwd_kernel(
+    const float* __restrict__ p, const float* __restrict__ dp, float* __restrict__ ds,
+    size_t rows, size_t cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  constexpr int kRows = kBlock / TPR;
+  const int t = threadIdx.x % TPR;
+  const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
+  if (r >= rows) return;
+  const float* pr = p + r * cols;
+  const float* dpr = dp + r * cols;
+  double s = 0.0;
+  for (size_t c = t; c < cols; c += TPR)
+    s += static_cast<double>(dpr[c]) * static_cast<double>(pr[c]);
+  const float sum = static_cast<float>(row_sum_d<TPR>(s, dscratch));
+  float* dsr = ds + r * cols;
+  for (size_t c = t; c < cols; c += TPR) dsr[c] = pr[c] * (dpr[c] - sum);
+}
+
+// Causal row softmax in place (attention.cc:106-125): row u = (b, h, i) holds
+// raw scaled scores for j <= i and exact zeros beyond (written by the score
+// GEMM). f32 max over the prefix, e = exp(s - max), denominator in double,
+// p = e * (1/(float)denom); masked entries are left at exact 0.
+__global__ __launch_bounds__(kBlock) void attn_softmax_rows_kernel(float* __restrict__ p,
+                                                                   size_t rows, size_t S) {
+  const int t = threadIdx.x % kWave;
+  const size_t u = static_cast<size_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
+  if (u >= rows) return;
+  const size_t i = u % S;
+  float* pr = p + u * S;
+  float mx = -__builtin_inff();
+  for (size_t j = t; j <= i; j += kWave) {
+    const float s = pr[j];
+    if (s > mx) mx = s;
+  }
+  mx = wave_max(mx);
+  double den = 0.0;
+  for (size_t j = t; j <= i; j += kWave) {
+    const float e = expf(pr[j] - mx);
+    pr[j] = e;
+    den += static_cast<double>(e);
+  }
+  den = wave_sum(den);
+  const float inv = 1.0f / static_cast<float>(den);
+  for (size_t j = t; j <= i; j += kWave) pr[j] = pr[j] * inv;
+}
+
+inline unsigned RowsGrid(size_t rows, int tpr) {
+  const size_t per = kBlock / tpr;
+  return static_cast<unsigned>((rows + per - 1) / per);
+}
+
+}  // namespace
+
+size_t MseFwdWorkspace(size_t n) { return PartialBlocks(n) * sizeof(double); }
+
+Status MseFwd(const float* pred, const float* target, float* loss, size_t n, const Ctx& c) {
+  if (n == 0) return Status::Fail(kUnitEngine, "MseFwd: empty input");
+  const size_t g = PartialBlocks(n);
+  if (c.ws_bytes < g * sizeof(double)) return Status::Fail(kUnitEngine, "MseFwd: workspace too small");
+  const size_t chunk = (n + g - 1) / g;
+  double* partials = static_cast<double*>(c.ws);
+  hipLaunchKernelGGL(sq_diff_partials, dim3(static_cast<unsigned>(g)), dim3(kBlock), 0, c.stream,
+                     pred, target, n, chunk, partials);
+  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, partials, g,
+                     static_cast<double>(n), loss);
+  return LaunchStatus("MseFwd");
+}
+
+size_t ClipNormWorkspace(size_t n) { return PartialBlocks(n) * sizeof(double); }
+
+Status ClipNorm(float* g, size_t n, float max_norm, const Ctx& c) {
+  if (n == 0) return Status::Ok();
+  const size_t blocks = PartialBlocks(n);
+  if (c.ws_bytes < blocks * sizeof(double))
+    return Status::Fail(kUnitEngine, "ClipNorm: workspace too small");
+  const size_t chunk = (n + blocks - 1) / blocks;
+  double* partials = static_cast<double*>(c.ws);
+  hipLaunchKernelGGL(sq_diff_partials, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                     c.stream, g, nullptr, n, chunk, partials);
+  hipLaunchKernelGGL(clip_apply_kernel, dim3(grid_for(n, kBlock, 4096)), dim3(kBlock), 0,
+                     c.stream, g, n, partials, blocks, max_norm);
+  return LaunchStatus("ClipNorm");
+}
+
+size_t SoftmaxXEntFwdWorkspace(size_t N) { return N * sizeof(double); }
+
+Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                      size_t N, size_t C, const Ctx& c) {
+  if (N == 0 || C == 0) return Status::Fail(kUnitEngine, "SoftmaxXEntFwd: empty input");
+  if (c.ws_bytes < N * sizeof(double))
+    return Status::Fail(kUnitEngine, "SoftmaxXEntFwd: workspace too small");
+  double* terms = static_cast<double*>(c.ws);
+  if (C >= 2048)
+    hipLaunchKernelGGL(xent_fwd_rows<kBlock>, dim3(RowsGrid(N, kBlock)), dim3(kBlock), 0,
+                       c.stream, logits, labels, probs, N, C, terms);
+  else
+    hipLaunchKernelGGL(xent_fwd_rows<kWave>, dim3(RowsGrid(N, kWave)), dim3(kBlock), 0, c.stream,
+                       logits, labels, probs, N, C, terms);
+  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, terms, N,
+                     static_cast<double>(N), loss);
+  return LaunchStatus("SoftmaxXEntFwd");
+}
+
+size_t KLDistillFwdWorkspace(size_t N) { return N * sizeof(double); }
+
+Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, float* p_t, size_t N,
+                    size_t C, float T, const Ctx& c) {
+  if (N == 0 || C == 0) return Status::Fail(kUnitEngine, "KLDistillFwd: empty input");
+  if (c.ws_bytes < N * sizeof(double))
+    return Status::Fail(kUnitEngine, "KLDistillFwd: workspace too small");
+  double* terms = static_cast<double*>(c.ws);
+  const float inv_T = 1.0f / T;
+  if (C >= 2048)
+    hipLaunchKernelGGL(kl_fwd_rows<kBlock>, dim3(RowsGrid(N, kBlock)), dim3(kBlock), 0, c.stream,
+                       s, t, p_s, p_t, N, C, inv_T, terms);
+  else
+    hipLaunchKernelGGL(kl_fwd_rows<kWave>, dim3(RowsGrid(N, kWave)), dim3(kBlock), 0, c.stream, s,
+                       t, p_s, p_t, N, C, inv_T, terms);
+  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, terms, N,
+                     static_cast<double>(N), loss);
+  return LaunchStatus("KLDistillFwd");
+}
+
+#define ROWS_DISPATCH(kernel, rows, cols, ...)                                                 \
+  do {                                                                                         \
+    if ((cols) >= 1024)                                                                        \
+      hipLaunchKernelGGL(kernel<kBlock>, dim3(RowsGrid(rows, kBlock)), dim3(kBlock), 0,        \
+                         c.stream, __VA_ARGS__);                                               \
+    else                                                                                       \
+      hipLaunchKernelGGL(kernel<kWave>, dim3(RowsGrid(rows, kWave)), dim3(kBlock), 0,          \
+                         c.stream, __VA_ARGS__);                                               \
+  } while (0)
+
+Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
+                    float* rstd, size_t rows, size_t cols, const Ctx& c) {
+  if (rows == 0 || cols == 0) return Status::Ok();
+  ROWS_DISPATCH(layer_norm_fwd_rows, rows, cols, x, gamma, beta, y, mean, rstd, rows, cols);
+  return LaunchStatus("LayerNormFwd");
+}
+
+Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const float* mean,
+                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c) {
+  if (rows == 0 || cols == 0) return Status::Ok();
+  ROWS_DISPATCH(layer_norm_bwd_rows, rows, cols, dy, x, gamma, mean, rstd, dx, rows, cols);
+  return LaunchStatus("LayerNormBwd");
+}
+
+Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
+                  size_t cols, const Ctx& c) {
+  if (rows == 0 || cols == 0) return Status::Ok();
+  ROWS_DISPATCH(rms_norm_fwd_rows, rows, cols, x, gamma, y, rstd, rows, cols);
+  return LaunchStatus("RmsNormFwd");
+}
+
+Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
+                  float* dx, size_t rows, size_t cols, const Ctx& c) {
+  if (rows == 0 || cols == 0) return Status::Ok();
+  ROWS_DISPATCH(rms_norm_bwd_rows, rows, cols, dy, x, gamma, rstd, dx, rows, cols);
+  return LaunchStatus("RmsNormBwd");
+}
+
+Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
+                      const Ctx& c) {
+  if (rows == 0 || cols == 0) return Status::Ok();
+  ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
+  return LaunchStatus("SoftmaxRowsBwd");
+}
+
+Status AttnSoftmaxRows(float* p, size_t rows, size_t S, const Ctx& c) {
+  if (rows == 0 || S == 0) return Status::Ok();
+  hipLaunchKernelGGL(attn_softmax_rows_kernel, dim3(RowsGrid(rows, kWave)), dim3(kBlock), 0,
+                     c.stream, p, rows, S);
+  return LaunchStatus("AttnFwd(softmax)");
+}
+
+}  // namespace seeml_hip

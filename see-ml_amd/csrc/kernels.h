@@ -1,0 +1,157 @@
+// kernels.h — host-side launchers for the gfx950 kernel set.
+//
+// One launcher per executor kernel of the reference
+// (runtime/executor/update_kernels.h:27-162), taking device pointers, the
+// same dims, and a launch context (stream, workspace, per-step scalars).
+// Launchers validate the shapes they are handed against what their grids
+// assume before launching anything, and never allocate: scratch comes from
+// the context's workspace, sized by the matching *_workspace_bytes query.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "plan_checks.h"
+
+namespace seeml_hip {
+
+// Per-step optimizer scalars, uploaded once per step before the step's
+// graph replays (graph kernel arguments are frozen at capture). Computed on
+// the host with the reference's float expressions (optimizer.cc:52-58,
+// update_engine.cc:515-534) so AdamW/SGD reproduce the CPU bits.
+struct alignas(64) StepScalars {
+  float lr;
+  float inv_bc1;
+  float inv_bc2;
+  float beta1;
+  float beta2;
+  float om_b1;
+  float om_b2;
+  float eps;
+  float weight_decay;
+  float pad[7];
+};
+StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step);
+
+struct Ctx {
+  hipStream_t stream = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  const StepScalars* scalars = nullptr;
+};
+
+// ---- GEMM engine (k_gemm.hip) -------------------------------------------
+enum class Causal : int {
+  kNone = 0,
+  kLowerOut = 1,  // write C(m,n) for n <= m, exact 0 above the diagonal
+  kKLeM = 2,      // reduce only k <= m (rows of a causal P)
+  kKGeM = 3,      // reduce only k >= m (columns of a causal P)
+};
+
+struct GemmDesc {
+  const void* A = nullptr;
+  const void* B = nullptr;
+  float* C = nullptr;
+  int64_t M = 0, N = 0, K = 0;
+  int64_t lda = 0, ldb = 0, ldc = 0;
+  bool a_kc = true;   // A(m,k) at A[m*lda + k]   (else A[k*lda + m])
+  bool b_kc = false;  // B(k,n) at B[n*ldb + k]   (else B[k*ldb + n])
+  bool b_int8 = false;
+  int64_t batch = 1, heads = 1;  // z -> (z / heads, z % heads)
+  int64_t a_sb = 0, a_sh = 0, b_sb = 0, b_sh = 0, c_sb = 0, c_sh = 0;
+  float alpha = 1.0f;
+  bool accumulate = false;  // C = C + alpha*AB instead of C = alpha*AB
+  const float* bias = nullptr;
+  int act = 0;
+  Causal causal = Causal::kNone;
+};
+
+struct GemmPlan {
+  int cfg = 0;      // tile configuration index
+  int splits = 1;   // deterministic split-K slices
+  size_t ws_bytes = 0;
+};
+GemmPlan PlanGemm(const GemmDesc& d);
+// `forced_cfg`/`forced_splits` >= 0 override the heuristic (autotuner arms).
+GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits);
+int GemmConfigCount();
+const char* GemmConfigName(int cfg);
+Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);
+
+// Row-major convenience forms of the reference's GEMM family.
+GemmDesc GemmNNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
+GemmDesc GemmNTDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
+GemmDesc GemmTNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
+
+// ---- pointwise family (k_pointwise.hip) ---------------------------------
+Status AddEW(const float* x, const float* y, float* out, size_t n, const Ctx& c);
+Status MulEW(const float* x, const float* y, float* out, size_t n, const Ctx& c);
+Status AddBias(const float* x, const float* b, float* out, size_t rows, size_t cols, const Ctx& c);
+Status Scale(const float* x, float* out, float alpha, size_t n, const Ctx& c);
+Status ReluFwd(const float* x, float* out, size_t n, const Ctx& c);
+Status ReluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c);
+Status GeluFwd(const float* x, float* out, size_t n, const Ctx& c);
+Status GeluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c);
+Status SiluFwd(const float* x, float* out, size_t n, const Ctx& c);
+Status SiluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c);
+Status Fill(float* dst, float value, size_t n, const Ctx& c);
+Status Copy(const float* src, float* dst, size_t n, const Ctx& c);
+Status EmbedFwd(const int32_t* tokens, const float* table, float* out, size_t rows, size_t dim,
+                size_t vocab, const Ctx& c);
+Status ReduceRows(const float* dy, float* db, size_t rows, size_t cols, const Ctx& c);
+Status SoftmaxXEntBwd(const float* probs, const int32_t* labels, const float* seed, float* dlogits,
+                      size_t N, size_t C, const Ctx& c);
+Status MseBwd(const float* pred, const float* target, const float* seed, float* dpred, size_t n,
+              const Ctx& c);
+Status KLDistillBwd(const float* p_s, const float* p_t, const float* seed, float* dlogits,
+                    size_t N, size_t C, float T, const Ctx& c);
+Status SgdStep(float* p, const float* g, size_t n, const Ctx& c);
+Status AdamWStep(float* p, const float* g, float* m, float* v, size_t n, const Ctx& c);
+Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,
+               const Ctx& c);
+Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t d, float base,
+               const Ctx& c);
+
+// ---- row / reduction family (k_rows.hip) ----------------------------------
+size_t MseFwdWorkspace(size_t n);
+Status MseFwd(const float* pred, const float* target, float* loss, size_t n, const Ctx& c);
+size_t ClipNormWorkspace(size_t n);
+Status ClipNorm(float* g, size_t n, float max_norm, const Ctx& c);
+size_t SoftmaxXEntFwdWorkspace(size_t N);
+Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                      size_t N, size_t C, const Ctx& c);
+size_t KLDistillFwdWorkspace(size_t N);
+Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, float* p_t, size_t N,
+                    size_t C, float T, const Ctx& c);
+Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
+                    float* rstd, size_t rows, size_t cols, const Ctx& c);
+Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const float* mean,
+                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c);
+Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
+                  size_t cols, const Ctx& c);
+Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
+                  float* dx, size_t rows, size_t cols, const Ctx& c);
+Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
+                      const Ctx& c);
+// Causal row softmax in place over raw scores (attention forward, step 2).
+Status AttnSoftmaxRows(float* p, size_t rows, size_t S, const Ctx& c);
+
+// ---- attention family (k_attention.hip): GEMM-engine compositions -------
+size_t AttnWorkspace(size_t B, size_t S, size_t H, size_t d);
+Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* probs, size_t B,
+               size_t S, size_t H, size_t d, const Ctx& c);
+Status AttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S, size_t H,
+              size_t d, const Ctx& c);
+Status AttnDV(const float* probs, const float* dout, float* dv, size_t B, size_t S, size_t H,
+              size_t d, const Ctx& c);
+Status AttnDQ(const float* ds, const float* k, float* dq, size_t B, size_t S, size_t H, size_t d,
+              const Ctx& c);
+Status AttnDK(const float* ds, const float* q, float* dk, size_t B, size_t S, size_t H, size_t d,
+              const Ctx& c);
+
+// Checks the last launch; returns "UpdateEngine: <what>: <hip error>".
+Status LaunchStatus(const char* what);
+
+}  // namespace seeml_hip

@@ -1,0 +1,89 @@
+"""ctypes binding of the backend's C-ABI (include/seeml_hip.h).
+
+Signatures are read from the header itself, so the Python view can never
+drift from the declared boundary. Loading fails loudly when the built
+library is missing: there is no CPU fallback for the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+HEADER = os.path.join(REPO_ROOT, "include", "seeml_hip.h")
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libseeml_hip.so")
+
+_TYPES = {
+    "int": C.c_int,
+    "void": None,
+    "float": C.c_float,
+    "uint64_t": C.c_uint64,
+    "uint32_t": C.c_uint32,
+}
+
+
+def _ctype(t: str):
+    t = t.strip()
+    t = re.sub(r"\s+", " ", t)
+    if t == "const char*":
+        return C.c_char_p
+    if t.endswith("*"):
+        return C.c_void_p
+    t = t.replace("const ", "")
+    if t not in _TYPES:
+        raise TypeError(f"unmapped C type in seeml_hip.h: {t!r}")
+    return _TYPES[t]
+
+
+def parse_header(path: str = HEADER) -> dict:
+    """name -> (restype, [argtypes]) for every prototype in the header."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    protos = {}
+    for m in re.finditer(r"^\s*([\w\s\*]+?)\s*\b(seeml_hip_\w+)\s*\(([^;]*?)\)\s*;", text, re.M):
+        ret, name, args = m.group(1), m.group(2), m.group(3)
+        ret = ret.strip()
+        if ret.endswith("*"):
+            rtype = C.c_char_p if ret.replace(" ", "") == "constchar*" else C.c_void_p
+        else:
+            rtype = _ctype(ret)
+        argtypes = []
+        args = " ".join(args.split())
+        if args and args != "void":
+            for a in args.split(","):
+                a = a.strip()
+                mm = re.match(r"(.*?)(\w+)$", a)
+                argtypes.append(_ctype(mm.group(1)))
+        protos[name] = (rtype, argtypes)
+    return protos
+
+
+_lib = None
+
+
+def lib():
+    """The loaded backend library with every header prototype bound."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is not built — run __graft_entry__.build() "
+                "(hipcc for gfx950); the backend has no CPU fallback")
+        handle = C.CDLL(LIB_PATH)
+        for name, (rtype, argtypes) in parse_header().items():
+            fn = getattr(handle, name)
+            fn.restype = rtype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def kernel_error() -> str:
+    return lib().seeml_hip_kernel_error().decode()
+
+
+def check_kernel(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: {kernel_error()}")

@@ -1,0 +1,142 @@
+"""Algorithmic work per plan instruction: FLOPs and compulsory HBM bytes.
+
+Bytes count each operand the reference kernel must read or write once, at
+4 B per f32/i32 element (1 B per int8 weight) — the traffic floor, not what
+a kernel happens to move. FLOPs count 2 per multiply-add of the
+contractions (causal attention counts only the j <= i half the kernels
+compute). These are the numbers `roofline.achieved` and the MFMA-utilisation
+/ HBM-throughput figures divide by measured kernel time.
+
+Classes: "mfma" for GEMM-family contractions with min(M, N, K) >= 64 (dense,
+compute-bound on the matrix cores); "hbm" for skinny LoRA GEMMs (a dim = r)
+and every non-contraction kernel; "attn" for the attention contractions,
+judged by min(compute, bandwidth).
+"""
+from __future__ import annotations
+
+from .planner import OP_NAME
+
+GEMMS = {"GemmNN", "GemmNT", "GemmTN", "GemmAccNN", "GemmNNQ8", "GemmNTQ8"}
+ATTN = {"AttnFwd", "AttnDP", "AttnDV", "AttnDQ", "AttnDK"}
+
+
+def _hi(w):
+    return w >> 32
+
+
+def _lo(w):
+    return w & 0xFFFFFFFF
+
+
+def work(ins: dict) -> dict:
+    """{'op', 'flops', 'bytes', 'cls', 'shape'} for one decoded instruction."""
+    name = OP_NAME.get(ins["opcode"], str(ins["opcode"]))
+    o = ins["out"]
+    flops, nbytes, cls, shape = 0, 0, "hbm", ()
+    if name in GEMMS:
+        M, N, K = o
+        bw = 1 if name in ("GemmNNQ8", "GemmNTQ8") else 4
+        flops = 2 * M * N * K
+        nbytes = 4 * M * K + bw * K * N + 4 * M * N
+        if name == "GemmAccNN":
+            nbytes += 4 * M * N
+        if ins["flags"] & 1:
+            nbytes += 4 * N
+        cls = "mfma" if min(M, N, K) >= 64 else "hbm"
+        shape = (M, N, K)
+    elif name in ATTN or name in ("RopeFwd", "RopeBwd"):
+        bs, hd = (o[1], o[2]) if name == "AttnFwd" else (o[0], o[1])
+        B, S, H, d = _hi(bs), _lo(bs), _hi(hd), _lo(hd)
+        TD, P = B * S * H * d, B * H * S * S
+        half = B * H * d * S * (S + 1)  # 2 flops x S(S+1)/2 causal pairs x d
+        shape = (B, S, H, d)
+        if name in ("RopeFwd", "RopeBwd"):
+            nbytes = 8 * TD
+        elif name == "AttnFwd":
+            flops, nbytes, cls = 2 * half, 4 * (4 * TD + P), "attn"
+        elif name == "AttnDP":
+            flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
+        else:  # DV / DQ / DK: read P-shaped + one activation, write one
+            flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
+    elif name in ("AddEW", "MulEW", "ReluBwd", "GeluBwd", "SiluBwd"):
+        nbytes, shape = 12 * o[0], (o[0],)
+    elif name in ("Scale", "ReluFwd", "GeluFwd", "SiluFwd", "Copy"):
+        nbytes, shape = 8 * o[0], (o[0],)
+    elif name == "Fill":
+        nbytes, shape = 4 * o[0], (o[0],)
+    elif name == "AddBias":
+        nbytes, shape = 8 * o[0] * o[1] + 4 * o[1], (o[0], o[1])
+    elif name == "ReduceRows":
+        nbytes, shape = 4 * o[0] * o[1] + 4 * o[1], (o[0], o[1])
+    elif name == "RmsNormFwd":
+        r, c = _hi(o[0]), _lo(o[0])
+        nbytes, shape = 8 * r * c + 4 * c + 4 * r, (r, c)
+    elif name == "RmsNormBwd":
+        r, c = _hi(o[1]), _lo(o[1])
+        nbytes, shape = 12 * r * c + 4 * c + 4 * r, (r, c)
+    elif name == "LayerNormFwd":
+        r, c = _hi(o[0]), _lo(o[0])
+        nbytes, shape = 8 * r * c + 8 * c + 8 * r, (r, c)
+    elif name == "LayerNormBwd":
+        r, c = _hi(o[2]), _lo(o[2])
+        nbytes, shape = 12 * r * c + 4 * c + 8 * r, (r, c)
+    elif name == "SoftmaxRowsBwd":
+        r, c = _hi(o[0]), _lo(o[0])
+        nbytes, shape = 12 * r * c, (r, c)
+    elif name == "EmbedFwd":
+        T, D = o[0], _lo(o[1])
+        nbytes, shape = 4 * T + 8 * T * D, (T, D)
+    elif name in ("SoftmaxXEntFwd", "SoftmaxXEntBwd"):
+        N, C = o[0], o[1]
+        nbytes, shape = 8 * N * C + 4 * N + 4, (N, C)
+    elif name == "MseFwd":
+        nbytes, shape = 8 * o[0] + 4, (o[0],)
+    elif name == "MseBwd":
+        nbytes, shape = 12 * o[0] + 4, (o[0],)
+    elif name == "AdamWStep":
+        nbytes, shape = 28 * o[0], (o[0],)
+    elif name == "SgdStep":
+        nbytes, shape = 12 * o[0], (o[0],)
+    elif name == "ClipNorm":
+        nbytes, shape = 12 * o[0], (o[0],)
+    elif name in ("KLDistillFwd",):
+        N, C = _hi(o[1]), _lo(o[1])
+        nbytes, shape = 16 * N * C + 4, (N, C)
+    elif name in ("KLDistillBwd",):
+        N, C = _hi(o[0]), _lo(o[0])
+        nbytes, shape = 12 * N * C + 4, (N, C)
+    return dict(op=name, flops=flops, bytes=nbytes, cls=cls, shape=shape)
+
+
+def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: float = 8000.0):
+    """Aggregate per-instruction timings into the BASELINE metric's parts."""
+    rows = [dict(work(ins), ms=t) for ins, t in zip(program, ms)]
+    dense = [r for r in rows if r["cls"] == "mfma"]
+    gem_all = [r for r in rows if r["op"] in GEMMS]
+    hbm = [r for r in rows if r["cls"] == "hbm" and r["op"] not in GEMMS]
+
+    def util(rs):
+        t = sum(r["ms"] for r in rs) * 1e-3
+        f = sum(r["flops"] for r in rs)
+        return (f / t / 1e12 / peak_tflops) if t > 0 else None
+
+    def gbps(rs):
+        t = sum(r["ms"] for r in rs) * 1e-3
+        b = sum(r["bytes"] for r in rs)
+        return (b / t / 1e9) if t > 0 else None
+
+    by_op = {}
+    for r in rows:
+        k = r["op"]
+        a = by_op.setdefault(k, dict(count=0, ms=0.0, flops=0, bytes=0))
+        a["count"] += 1
+        a["ms"] += r["ms"]
+        a["flops"] += r["flops"]
+        a["bytes"] += r["bytes"]
+    total_ms = sum(r["ms"] for r in rows)
+    return dict(
+        rows=rows, by_op=by_op, total_ms=total_ms,
+        gemm_dense_mfma_util=util(dense), gemm_all_mfma_util=util(gem_all),
+        hbm_kernels_gbps=gbps(hbm),
+        hbm_kernels_frac=(gbps(hbm) / peak_gbps) if gbps(hbm) else None,
+    )
