@@ -190,7 +190,15 @@ def main():
         "kernels": by_op,
         "final_loss": losses[-1],
     }
-    print(json.dumps(out), flush=True)
+    def plain(v):
+        if isinstance(v, dict):
+            return {k: plain(x) for k, x in v.items()}
+        if isinstance(v, (list, tuple)):
+            return [plain(x) for x in v]
+        if hasattr(v, "item"):
+            return v.item()
+        return v
+    print(json.dumps(plain(out)), flush=True)
     e.close()
 
 

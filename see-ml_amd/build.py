@@ -7,6 +7,8 @@ include/seeml_hip.h. Flags:
                                for the pointwise/optimizer kernels)
   -packed-fp32-ops disabled    no v_pk_*_f32 generation (unreliable on the
                                target pool)
+  correctly-rounded / and sqrtf (explicit; clang's HIP default) so AdamW and
+                               the norm statistics reproduce the CPU's bits
 """
 from __future__ import annotations
 
@@ -29,6 +31,7 @@ COMMON = [
 ]
 DEVICE = [
     f"--offload-arch={ARCH}",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

@@ -257,7 +257,9 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
   v = vi;
   const float m_hat = mi * ibc1;
   const float v_hat = vi * ibc2;
-  p -= lr * (__fdiv_rn(m_hat, __fsqrt_rn(v_hat) + eps) + wd * p);
+  // HIP device '/' and sqrtf are IEEE correctly rounded (clang's default
+  // -fhip-fp32-correctly-rounded-divide-sqrt), matching the CPU's bits.
+  p -= lr * (m_hat / (sqrtf(v_hat) + eps) + wd * p);
 }
 
 __global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ p,

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_rows(
   }
   const double var = row_sum_d<TPR>(v, dscratch);
   const float rs =
-      __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(var / static_cast<double>(cols)) + 1e-5f));
+      1.0f / sqrtf(static_cast<float>(var / static_cast<double>(cols)) + 1e-5f);
   if (t == 0) {
     mean[r] = mu;
     rstd[r] = rs;
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_rows(
   const int t = threadIdx.x % TPR;
   const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
   if (r >= rows) return;
-  const float inv_d = __fdiv_rn(1.0f, static_cast<float>(cols));
+  const float inv_d = 1.0f / static_cast<float>(cols);
   const float* dyr = dy + r * cols;
   const float* xr = x + r * cols;
   const float mu = mean[r], rs = rstd[r];
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_rows(const float* __restr
   for (size_t c = t; c < cols; c += TPR) s += static_cast<double>(xr[c]) * static_cast<double>(xr[c]);
   const double ss = row_sum_d<TPR>(s, dscratch);
   const float rs =
-      __fdiv_rn(1.0f, __fsqrt_rn(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f));
+      1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f);
   if (t == 0) rstd[r] = rs;
   float* yr = y + r * cols;
   for (size_t c = t; c < cols; c += TPR) yr[c] = xr[c] * rs * gamma[c];
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_rows(
   const int t = threadIdx.x % TPR;
   const size_t r = static_cast<size_t>(blockIdx.x) * kRows + threadIdx.x / TPR;
   if (r >= rows) return;
-  const float inv_d = __fdiv_rn(1.0f, static_cast<float>(cols));
+  const float inv_d = 1.0f / static_cast<float>(cols);
   const float* dyr = dy + r * cols;
   const float* xr = x + r * cols;
   const float rs = rstd[r];
