@@ -34,12 +34,11 @@ def _buf(a):
 class DeviceUpdateEngine:
     def __init__(self, plan: bytes, device: int = 0, use_graph: bool = True):
         self._L = _lib.lib()
-        self._plan = plan
         err = C.create_string_buffer(1024)
         h = C.c_void_p()
-        buf = (C.c_uint8 * len(plan)).from_buffer_copy(plan)
-        rc = self._L.seeml_hip_open(buf, len(plan), device, C.byref(h), err, len(err))
-        del buf
+        view = np.frombuffer(plan, np.uint8)  # no copy; the library reads only
+        rc = self._L.seeml_hip_open(view.ctypes.data, len(plan), device, C.byref(h), err, len(err))
+        del view
         if rc != 0:
             raise RuntimeError(err.value.decode())
         self._h = h

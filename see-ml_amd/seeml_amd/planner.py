@@ -731,7 +731,7 @@ class UpdateConfig:
 
 @dataclass
 class CompiledPlan:
-    blob: bytes
+    blob: bytearray  # the .seeu bytes (mutable buffer, never resized)
     header: dict
     train: list
     merge: list
@@ -741,13 +741,30 @@ class CompiledPlan:
     adapters: list        # [(id_base, A_ref, B_ref, (K, M), scale)]
 
 
-def _weight_values(t: Tensor, rng: np.random.Generator) -> np.ndarray:
-    n = int(np.prod(t.dims))
+_WEIGHT_CHUNK = 1 << 24
+
+
+def _fill_weights(out: np.ndarray, t: Tensor, seed: int, index: int, pool) -> list:
+    """Writes tensor `t`'s synthetic values into `out` (f32 view). Chunk c of
+    tensor `index` draws from its own stream SeedSequence([seed, index, c]),
+    so the values depend only on (seed, tensor, position) — never on how
+    many threads fill them."""
     if t.init == "ones":
-        return np.ones(n, np.float32)
+        out[:] = 1.0
+        return []
     if t.init == "zeros":
-        return np.zeros(n, np.float32)
-    return (rng.standard_normal(n, dtype=np.float32) * np.float32(t.std))
+        out[:] = 0.0
+        return []
+    std = np.float32(t.std)
+
+    def fill(c):
+        sl = out[c * _WEIGHT_CHUNK:(c + 1) * _WEIGHT_CHUNK]
+        g = np.random.Generator(np.random.PCG64(np.random.SeedSequence([seed, index, c])))
+        g.standard_normal(out=sl, dtype=np.float32)
+        sl *= std
+
+    n_chunks = (out.size + _WEIGHT_CHUNK - 1) // _WEIGHT_CHUNK
+    return [pool.submit(fill, c) for c in range(n_chunks)]
 
 
 def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: bool = True) -> CompiledPlan:
@@ -833,16 +850,11 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
             persist[off // 4: off // 4 + v.volume] = (
                 counter_randn(attrs["seed"], v.volume) * np.float32(attrs["std"]))
 
-    # --- rodata
-    rng = np.random.default_rng(cfg.weight_seed)
-    rodata = np.zeros(align_up(rodata_size) // 4 if materialize else 0, np.float32)
+    # --- rodata layout (values are written straight into the blob below)
     smf_offsets, smf_cursor = {}, 0
     for name, (v, t) in weights.items():
         smf_offsets[name] = smf_cursor
         smf_cursor = align_up(smf_cursor + v.nbytes)
-        if materialize:
-            off = rodata_offsets[name] // 4
-            rodata[off:off + v.volume] = _weight_values(t, rng)
 
     # --- emit table: delta arena range -> (synthetic) source-file range
     emit = []
@@ -887,14 +899,30 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
         return CompiledPlan(b"", h, **plan_info)
 
     blob = bytearray(off)
-    blob[h["train_instr_offset"]:h["train_instr_offset"] + 64 * len(train_words)] = encode(train_words)
-    blob[h["merge_instr_offset"]:h["merge_instr_offset"] + 64 * len(merge_words)] = encode(merge_words)
-    blob[h["eval_instr_offset"]:h["eval_instr_offset"] + 64 * len(eval_words)] = encode(eval_words)
-    ro = rodata.view(np.uint8)[:rodata_size]
-    blob[h["rodata_offset"]:h["rodata_offset"] + rodata_size] = ro.tobytes()
-    blob[h["persist_init_offset"]:h["persist_init_offset"] + persistent_size] = persist.tobytes()
+    view = np.frombuffer(blob, np.uint8)
+    view[h["train_instr_offset"]:h["train_instr_offset"] + 64 * len(train_words)] = \
+        np.frombuffer(encode(train_words), np.uint8)
+    view[h["merge_instr_offset"]:h["merge_instr_offset"] + 64 * len(merge_words)] = \
+        np.frombuffer(encode(merge_words), np.uint8)
+    view[h["eval_instr_offset"]:h["eval_instr_offset"] + 64 * len(eval_words)] = \
+        np.frombuffer(encode(eval_words), np.uint8)
+    # Frozen weights, generated in place by seeded per-chunk streams (no
+    # separate multi-GB staging copy).
+    import concurrent.futures as cf
+    import os
+    with cf.ThreadPoolExecutor(max(1, min(16, os.cpu_count() or 1))) as pool:
+        futs = []
+        for index, (name, (v, t)) in enumerate(weights.items()):
+            off0 = h["rodata_offset"] + rodata_offsets[name]
+            futs += _fill_weights(view[off0:off0 + v.nbytes].view(np.float32), t,
+                                  cfg.weight_seed, index, pool)
+        for f in futs:
+            f.result()
+    p0 = h["persist_init_offset"]
+    view[p0:p0 + persistent_size] = persist.view(np.uint8)
     for i, (a, b, c) in enumerate(emit):
         struct.pack_into("<3Q", blob, h["emit_table_offset"] + 24 * i, a, b, c)
+    del view
     h["plan_hash"] = 0
     HEADER.pack_into(blob, 0, *[h[n] for n, _ in HEADER_FIELDS])
     if hash_fn is None:
@@ -906,4 +934,4 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     else:
         h["plan_hash"] = hash_fn(bytes(blob), PLAN_HASH_OFFSET)
     struct.pack_into("<Q", blob, PLAN_HASH_OFFSET, h["plan_hash"])
-    return CompiledPlan(bytes(blob), h, **plan_info)
+    return CompiledPlan(blob, h, **plan_info)
