@@ -1,0 +1,496 @@
+// k_gemm_kernel.h — the fp32 MFMA GEMM kernel template for gfx950 (device code
+// shared by the per-layout instantiation units k_gemm_{nn,nt,tn,q8}.hip; host
+// planning and launch live in k_gemm.hip).
+//
+// Serves the reference's whole GEMM family (runtime/executor/gemm.cc:173-228:
+// GemmNN + fused bias/act epilogue, GemmNT, GemmTN, GemmAccNN, the int8-B
+// GemmNNQ8/NTQ8) and the attention contractions (attention.cc: QK^T, PV,
+// dO V^T, P^T dO, dS K, dS^T Q), all as one kernel template:
+//
+//   C[z](m,n) = epilogue(alpha * sum_k A[z](m,k) B[z](k,n))
+//
+// with each operand either k-contiguous or row-contiguous in memory (so NT/TN
+// read their operands in place, no transposes), a (b, h) batch decomposition
+// with arbitrary element strides (attention heads live interleaved in
+// [B*S, H*d] rows), and causal modes that skip whole tiles the causal mask
+// zeroes.
+//
+// Mapping to CDNA4: a workgroup of 4 or 8 wavefronts (64 lanes) owns an
+// MT_M x MT_N output tile; each wavefront owns a WM x WN sub-tile accumulated
+// with v_mfma_f32_32x32x2_f32 (32x32 outputs, 16 accumulators per lane, two
+// k values per instruction, one per half-wavefront). Operand tiles
+// (KT = 32 or 64 per config) are staged through LDS, double-buffered:
+// the next stage's 16-byte global loads are in flight while the matrix cores
+// consume the current one. The k loop carries no per-element address math:
+// each lane's offsets from the stage origin are fixed at kernel entry (rows
+// past the operand's end are clamped onto its last row — their products
+// reach only outputs that are never stored), the origin advances by a
+// uniform step, and only a final partial stage masks k.
+//
+// k assignment: a fragment group covers 8 k. Half-wavefront h of MFMA j
+// (j = 0..3) supplies k = 8g + 4h + j, for A and B alike, so a k-contiguous
+// operand kept in LDS as [o][k] rows is read with ONE 16-byte ds_read per
+// lane per four MFMAs; an o-contiguous operand is kept as [k][o] rows and
+// read as four 4-byte reads (consecutive lanes, consecutive addresses).
+//
+// Workgroup order: the 8 XCDs (each with its own L2) receive workgroups
+// round-robin, so the linear workgroup id is remapped to give each XCD a
+// contiguous run of tiles, walked in groups of 8 tile-rows so the tiles
+// resident on one XCD share A row-panels and B column-panels in its L2.
+//
+// Determinism: each output is owned by one lane of one workgroup and its k
+// order is fixed by the tile loop; split-K writes per-slice partials that a
+// second kernel sums in slice order. No atomics.
+//
+// Numerics: fp32 products, fp32 accumulation in the matrix core (full
+// IEEE single precision, not a reduced-precision xf32 mode). The reference
+// accumulates in a different order (4-wide k groups / sequential), so GEMM
+// outputs agree to within fp32 reordering error, not bit-for-bit.
+#pragma once
+
+#include "device_common.h"
+#include "kernels.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace seeml_hip {
+namespace gemm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int KG = 8;           // k covered by one fragment group
+constexpr int kXcds = 8;
+constexpr int kGroupRows = 8;   // tile-rows walked together (L2 panel sharing)
+constexpr int kSplitAlign = 64; // split-K slice depth: a multiple of every KT
+
+// LDS row strides in floats. [o][k] rows of KT + 4: the 16-byte fragment
+// reads of 8 consecutive lanes (8 rows, same k) cover the 32 banks once.
+// [k][o] rows padded by 8: the half-wavefronts (k and k + 4) fall in
+// disjoint bank halves.
+constexpr int KcStride(int kt) { return kt + 4; }
+constexpr int RcStride(int mt) { return mt + 8; }
+template <int MT, int KT, bool KC>
+constexpr int TileFloats() { return KC ? MT * KcStride(KT) : KT * RcStride(MT); }
+
+struct GemmKArgs {
+  const void* A;
+  const void* B;
+  float* C;
+  float* ws;
+  int64_t M, N, K, lda, ldb, ldc;
+  int64_t heads, batch;
+  int64_t a_sb, a_sh, b_sb, b_sh, c_sb, c_sh;
+  float alpha;
+  int accumulate;
+  const float* bias;
+  int act;
+  int causal;
+  int splits;
+  int64_t k_per_split;
+  int tiles_m, tiles_n;
+};
+
+// Tile configurations (the autotuner's arms).
+struct CfgInfo {
+  int mt_m, mt_n, kt, threads;
+  const char* name;
+};
+inline constexpr CfgInfo kCfgs[] = {
+    {128, 128, 32, 256, "128x128x32/w2x2"}, {128, 128, 32, 512, "128x128x32/w4x2"},
+    {256, 128, 32, 512, "256x128x32/w4x2"}, {128, 256, 32, 512, "128x256x32/w2x4"},
+    {128, 64, 32, 256, "128x64x32/w2x2"},   {64, 64, 32, 256, "64x64x32/w2x2"},
+    {128, 32, 32, 256, "128x32x32/w4x1"},   {32, 128, 32, 256, "32x128x32/w1x4"},
+    {64, 128, 32, 256, "64x128x32/w2x2"},   {128, 64, 32, 256, "128x64x32/w4x1"},
+    {128, 128, 16, 256, "128x128x16/w2x2"}, {64, 128, 16, 256, "64x128x16/w2x2"},
+};
+inline constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+inline constexpr int kCfgDefault = 0, kCfgSmall = 5, kCfgSkinnyN = 6, kCfgSkinnyM = 7;
+
+// One operand's MT x KT stage (outer index o = m for A / n for B), held in
+// registers between its global loads and its LDS store. KC = k-contiguous.
+//
+// VEC (16-byte aligned rows, contiguous extent a multiple of 4): 16-byte
+// loads at per-lane offsets fixed for the whole k loop; the stage origin is
+// uniform. A final partial stage (k beyond the reduction's end) zeroes its
+// out-of-range vectors, reading the row start instead.
+// !VEC (int8 B, odd shapes): element loads with an in-range mask applied at
+// the LDS store. Both forms are branch-free per element, so a stage's loads
+// are all in flight together and the first wait is at the LDS store.
+template <int MT, int KT, bool KC, typename T, int NT, bool VEC>
+struct Stage {
+  static constexpr int kVecs = MT * KT / 4;
+  static constexpr int kPer = kVecs / NT;
+  static_assert(kVecs % NT == 0 && kPer * 4 <= 64, "stage shape");
+  float r[kPer][4];
+  uint32_t off[kPer];  // VEC: element offset of vector i from the stage origin
+  uint64_t ok;         // !VEC: bit 4i+e set when element e of vector i is in range
+
+  __device__ __forceinline__ static void coords(int v, int& o, int& k) {
+    if constexpr (KC) {
+      o = v / (KT / 4);
+      k = (v % (KT / 4)) * 4;
+    } else {
+      k = v / (MT / 4);
+      o = (v % (MT / 4)) * 4;
+    }
+  }
+
+  // o0: first row of the tile (a multiple of 4); oe: the operand's extent.
+  __device__ __forceinline__ void init(int64_t ld, int64_t o0, int64_t oe) {
+    if constexpr (VEC) {
+      const int64_t last = oe - o0 - (KC ? 1 : 4);  // >= 0: the tile starts in range
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        int o, k;
+        coords(static_cast<int>(threadIdx.x) + i * NT, o, k);
+        const int64_t oc = std::min<int64_t>(o, last);
+        off[i] = static_cast<uint32_t>(KC ? oc * ld + k : k * ld + oc);
+      }
+    }
+  }
+
+  // A whole stage in range (VEC): one 16-byte load per vector, no masks.
+  __device__ __forceinline__ void load_full(const T* __restrict__ org) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const float4 q = *reinterpret_cast<const float4*>(org + off[i]);
+      r[i][0] = q.x; r[i][1] = q.y; r[i][2] = q.z; r[i][3] = q.w;
+    }
+  }
+
+  // Any stage: k beyond ke (and, for !VEC, rows beyond oe) read as zero.
+  __device__ __forceinline__ void load(const T* __restrict__ X, int64_t ld, int64_t o0,
+                                       int64_t oe, int64_t k0, int64_t ke) {
+    if constexpr (VEC) {
+      const T* org = X + (KC ? o0 * ld + k0 : k0 * ld + o0);
+      const int64_t kvalid = ke - k0;
+      if (kvalid >= KT) {
+        load_full(org);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          int o, k;
+          coords(static_cast<int>(threadIdx.x) + i * NT, o, k);
+          const bool in = k < kvalid;  // a KC vector is wholly in or out (K % 4 == 0)
+          const int64_t back = KC ? k : static_cast<int64_t>(k) * ld;
+          const float4 q = *reinterpret_cast<const float4*>(org + (off[i] - (in ? 0 : back)));
+          r[i][0] = in ? q.x : 0.0f;
+          r[i][1] = in ? q.y : 0.0f;
+          r[i][2] = in ? q.z : 0.0f;
+          r[i][3] = in ? q.w : 0.0f;
+        }
+      }
+    } else {
+      ok = 0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        int o, k;
+        coords(static_cast<int>(threadIdx.x) + i * NT, o, k);
+        const int64_t go = o0 + o, gk = k0 + k;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t eo = KC ? go : go + e;
+          const int64_t ek = KC ? gk + e : gk;
+          const bool in = eo < oe && ek < ke;
+          r[i][e] = static_cast<float>(X[in ? (KC ? eo * ld + ek : ek * ld + eo) : 0]);
+          ok |= (in ? uint64_t{1} : uint64_t{0}) << (4 * i + e);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      int o, k;
+      coords(static_cast<int>(threadIdx.x) + i * NT, o, k);
+      float* dst = KC ? lds + o * KcStride(KT) + k : lds + k * RcStride(MT) + o;
+      float4 q;
+      if constexpr (VEC) {
+        q = make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
+      } else {
+        q.x = (ok >> (4 * i + 0)) & 1 ? r[i][0] : 0.0f;
+        q.y = (ok >> (4 * i + 1)) & 1 ? r[i][1] : 0.0f;
+        q.z = (ok >> (4 * i + 2)) & 1 ? r[i][2] : 0.0f;
+        q.w = (ok >> (4 * i + 3)) & 1 ? r[i][3] : 0.0f;
+      }
+      *reinterpret_cast<float4*>(dst) = q;
+    }
+  }
+};
+
+// The 4 k values (8g + 4h + j, j = 0..3) of NB 32-wide fragments at o = w0 + 32i + r.
+template <int MT, int KT, bool KC, int NB>
+__device__ __forceinline__ void ReadFrags(const float* __restrict__ lds, int w0, int g, int h,
+                                          int r, float (&f)[NB][4]) {
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int o = w0 + 32 * i + r;
+    if constexpr (KC) {
+      const float4 q = *reinterpret_cast<const float4*>(lds + o * KcStride(KT) + g * KG + 4 * h);
+      f[i][0] = q.x; f[i][1] = q.y; f[i][2] = q.z; f[i][3] = q.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[i][j] = lds[(g * KG + 4 * h + j) * RcStride(MT) + o];
+    }
+  }
+}
+
+// Linear workgroup id -> logical id such that XCD x (= lin % 8) holds the
+// contiguous logical range of its share. A bijection on [0, total).
+__device__ __forceinline__ int64_t XcdLogical(int64_t lin, int64_t total) {
+  const int64_t per = total / kXcds, rem = total % kXcds;
+  const int64_t x = lin % kXcds, idx = lin / kXcds;
+  return x < rem ? x * (per + 1) + idx : rem * (per + 1) + (x - rem) * per + idx;
+}
+
+template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
+          bool VEC, bool SCHED>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
+  using BT = typename std::conditional<B_I8, int8_t, float>::type;
+  constexpr int NT = 64 * WAVES_M * WAVES_N;
+  constexpr int WM = MT_M / WAVES_M, WN = MT_N / WAVES_N;
+  constexpr int BM = WM / 32, BN = WN / 32;
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && KT % KG == 0 && kSplitAlign % KT == 0,
+                "tile shape");
+  constexpr int TA = TileFloats<MT_M, KT, A_KC>(), TB = TileFloats<MT_N, KT, B_KC>();
+  __shared__ __align__(16) float smem[2 * (TA + TB)];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+
+  // Logical work item of this workgroup: (tile, split slice, batch z).
+  const int64_t tiles = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+  const int64_t lin = blockIdx.x + static_cast<int64_t>(gridDim.x) *
+                                       (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
+  int64_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
+  const int64_t t_id = L % tiles;
+  L /= tiles;
+  const int slice = static_cast<int>(L % gridDim.y);
+  const int64_t z = L / gridDim.y;
+  const int64_t grp = t_id / (kGroupRows * p.tiles_n);
+  const int64_t first = grp * kGroupRows;
+  const int64_t gm = std::min<int64_t>(kGroupRows, p.tiles_m - first);
+  const int64_t in_grp = t_id - grp * kGroupRows * p.tiles_n;
+  const int64_t tm = first + in_grp % gm, tn = in_grp / gm;
+  const int64_t m0 = tm * MT_M, n0 = tn * MT_N;
+  const int64_t zb = z / p.heads, zh = z % p.heads;
+
+  const float* A = static_cast<const float*>(p.A) + zb * p.a_sb + zh * p.a_sh;
+  const BT* B = static_cast<const BT*>(p.B) + zb * p.b_sb + zh * p.b_sh;
+  float* C = p.C + zb * p.c_sb + zh * p.c_sh;
+
+  // Causal lower-triangular output: a tile wholly above the diagonal is
+  // exact zeros, with no reduction at all.
+  if (p.causal == static_cast<int>(Causal::kLowerOut) && n0 > m0 + MT_M - 1) {
+    for (int idx = threadIdx.x; idx < MT_M * MT_N; idx += NT) {
+      const int64_t m = m0 + idx / MT_N, n = n0 + idx % MT_N;
+      if (m < p.M && n < p.N) C[m * p.ldc + n] = 0.0f;
+    }
+    return;
+  }
+
+  int64_t kb = 0, ke = p.K;
+  if (p.causal == static_cast<int>(Causal::kKLeM)) ke = std::min<int64_t>(p.K, m0 + MT_M);
+  if (p.causal == static_cast<int>(Causal::kKGeM)) kb = std::min<int64_t>(p.K, m0);
+  if (p.splits > 1) {
+    kb = static_cast<int64_t>(slice) * p.k_per_split;
+    ke = std::min<int64_t>(p.K, kb + p.k_per_split);
+  }
+
+  floatx16 acc[BM][BN];
+#pragma unroll
+  for (int i = 0; i < BM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  constexpr bool kVecB = VEC && !B_I8;
+  using StageA = Stage<MT_M, KT, A_KC, float, NT, VEC>;
+  using StageB = Stage<MT_N, KT, B_KC, BT, NT, kVecB>;
+  // Two register sets: stage s is loaded into set s % 2 two iterations
+  // before it is computed, stored to LDS buffer s % 2 one iteration before.
+  StageA sa0, sa1;
+  StageB sb0, sb1;
+
+  // One stage's contraction out of LDS: 4 MFMAs per fragment group per
+  // (i, jj) block, the next group's fragments read while the current
+  // group's MFMAs run.
+  auto compute = [&](const float* __restrict__ as, const float* __restrict__ bs) {
+    float fa[2][BM][4], fb[2][BN][4];
+    ReadFrags<MT_M, KT, A_KC, BM>(as, wm0, 0, h, r, fa[0]);
+    ReadFrags<MT_N, KT, B_KC, BN>(bs, wn0, 0, h, r, fb[0]);
+#pragma unroll
+    for (int g = 0; g < KT / KG; ++g) {
+      const int c = g & 1;
+      if (g + 1 < KT / KG) {
+        ReadFrags<MT_M, KT, A_KC, BM>(as, wm0, g + 1, h, r, fa[c ^ 1]);
+        ReadFrags<MT_N, KT, B_KC, BN>(bs, wn0, g + 1, h, r, fb[c ^ 1]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < BM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < BN; ++jj)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[c][i][j], fb[c][jj][j],
+                                                               acc[i][jj], 0, 0, 0);
+    }
+  };
+  auto a_buf = [&](int i) { return smem + i * TA; };
+  auto b_buf = [&](int i) { return smem + 2 * TA + i * TB; };
+
+  const int64_t span = ke > kb ? ke - kb : 0;
+  const int64_t nfull = span / KT;
+  const int64_t ntiles = (span + KT - 1) / KT;
+  const int64_t a_step = A_KC ? KT : KT * p.lda;
+  const int64_t b_step = B_KC ? KT : KT * p.ldb;
+  const float* a_org = A + (A_KC ? m0 * p.lda + kb : kb * p.lda + m0);
+  const BT* b_org = B + (B_KC ? n0 * p.ldb + kb : kb * p.ldb + n0);
+  // Loads stage s into a register set (any stage: k beyond ke reads zero).
+  auto load_any = [&](StageA& xa, StageB& xb, int64_t s) {
+    xa.load(A, p.lda, m0, p.M, kb + s * KT, ke);
+    xb.load(B, p.ldb, n0, p.N, kb + s * KT, ke);
+  };
+  // Loads stage s < nfull (wholly in range).
+  auto load_full = [&](StageA& xa, StageB& xb, int64_t s) {
+    if constexpr (VEC) xa.load_full(a_org + s * a_step);
+    else xa.load(A, p.lda, m0, p.M, kb + s * KT, ke);
+    if constexpr (kVecB) xb.load_full(b_org + s * b_step);
+    else xb.load(B, p.ldb, n0, p.N, kb + s * KT, ke);
+  };
+  // Steady-state iteration on stage t (t + 2 < nfull): load stage t + 2 into
+  // set `ld`, contract stage t, store stage t + 1 from set `st`. With VEC the
+  // body is one basic block, scheduled as one interleave.
+  auto steady = [&](StageA& lda_, StageB& ldb_, const StageA& sta, const StageB& stb,
+                    int64_t t, int cur) {
+    load_full(lda_, ldb_, t + 2);
+    compute(a_buf(cur), b_buf(cur));
+    sta.store(a_buf(cur ^ 1));
+    stb.store(b_buf(cur ^ 1));
+    if constexpr (SCHED) {
+      // Per MFMA: one LDS fragment read for a later group; global loads
+      // over the first half; the next stage's LDS writes over the second.
+      constexpr int kMfma = (KT / KG) * 4 * BM * BN;
+      constexpr int kVmem = StageA::kPer + StageB::kPer;
+      constexpr int kDsw = kVmem;
+      constexpr int kDsrGroup = (A_KC ? BM : 2 * BM) + (B_KC ? BN : 2 * BN);
+      __builtin_amdgcn_sched_group_barrier(0x100, kDsrGroup, 0);
+#pragma unroll
+      for (int i = 0; i < kMfma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (i % 2 == 0 && i / 2 < kVmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (i >= kMfma / 2 && (i - kMfma / 2) % 2 == 0 && (i - kMfma / 2) / 2 < kDsw)
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+    }
+    __syncthreads();
+  };
+
+  if (ntiles > 0) {
+    sa0.init(p.lda, m0, p.M);
+    sb0.init(p.ldb, n0, p.N);
+    sa1.init(p.lda, m0, p.M);
+    sb1.init(p.ldb, n0, p.N);
+    load_any(sa0, sb0, 0);
+    if (ntiles > 1) load_any(sa1, sb1, 1);
+    sa0.store(a_buf(0));
+    sb0.store(b_buf(0));
+    __syncthreads();
+
+    int64_t t = 0;
+    for (; t + 3 < nfull; t += 2) {
+      steady(sa0, sb0, sa1, sb1, t, 0);
+      steady(sa1, sb1, sa0, sb0, t + 1, 1);
+    }
+    // The remaining stages (fewer than four): masked loads where needed.
+    for (; t < ntiles; ++t) {
+      const int cur = static_cast<int>(t & 1);
+      if (t + 2 < ntiles) {
+        if (cur) load_any(sa1, sb1, t + 2);
+        else load_any(sa0, sb0, t + 2);
+      }
+      compute(a_buf(cur), b_buf(cur));
+      if (t + 1 < ntiles) {
+        if (cur) {
+          sa0.store(a_buf(0));
+          sb0.store(b_buf(0));
+        } else {
+          sa1.store(a_buf(1));
+          sb1.store(b_buf(1));
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // Write-back. Lane (h, r) of the 32x32 block holds rows 8*(v/4) + 4*h + v%4
+  // of column r in accumulator element v.
+#pragma unroll
+  for (int i = 0; i < BM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int64_t n = n0 + wn0 + 32 * j + r;
+        if (m >= p.M || n >= p.N) continue;
+        float val = acc[i][j][v];
+        if (p.splits > 1) {
+          p.ws[(static_cast<int64_t>(slice) * p.M + m) * p.N + n] = val;
+          continue;
+        }
+        val = p.alpha * val;
+        if (p.accumulate) val = C[m * p.ldc + n] + val;
+        if (p.bias) val = val + p.bias[n];
+        val = dev_act(p.act, val);
+        if (p.causal == static_cast<int>(Causal::kLowerOut) && n > m) val = 0.0f;
+        C[m * p.ldc + n] = val;
+      }
+}
+
+// Launches config `cfg` of one operand-layout variant. The element-load
+// form (!VEC) exists only for the small tile; the host plans it as such.
+template <bool A_KC, bool B_KC, bool B_I8, bool VEC, bool SCHED = false>
+void LaunchVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+  const dim3 block(kCfgs[cfg].threads);
+#define SEEML_GEMM_CASE(I, MM, NN, KK, WM_, WN_)                                                \
+  case I:                                                                                     \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, B_I8, VEC, SCHED>), grid, \
+                       block, 0, s, a);                                                       \
+    break;
+  if constexpr (!VEC) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<64, 64, 32, 2, 2, A_KC, B_KC, B_I8, false, false>), grid,
+                       dim3(kCfgs[kCfgSmall].threads), 0, s, a);
+  } else {
+    switch (cfg) {
+      SEEML_GEMM_CASE(0, 128, 128, 32, 2, 2)
+      SEEML_GEMM_CASE(1, 128, 128, 32, 4, 2)
+      SEEML_GEMM_CASE(2, 256, 128, 32, 4, 2)
+      SEEML_GEMM_CASE(3, 128, 256, 32, 2, 4)
+      SEEML_GEMM_CASE(4, 128, 64, 32, 2, 2)
+      SEEML_GEMM_CASE(5, 64, 64, 32, 2, 2)
+      SEEML_GEMM_CASE(6, 128, 32, 32, 4, 1)
+      SEEML_GEMM_CASE(7, 32, 128, 32, 1, 4)
+      SEEML_GEMM_CASE(8, 64, 128, 32, 2, 2)
+      SEEML_GEMM_CASE(9, 128, 64, 32, 4, 1)
+      SEEML_GEMM_CASE(10, 128, 128, 16, 2, 2)
+      default:
+      SEEML_GEMM_CASE(11, 64, 128, 16, 2, 2)
+    }
+  }
+#undef SEEML_GEMM_CASE
+}
+
+// Per-layout entry points, one instantiation unit each (built in parallel).
+void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
+void LaunchNT(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
+void LaunchTN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
+void LaunchQ8(int cfg, bool b_kc, dim3 grid, hipStream_t s, const GemmKArgs& a);
+
+}  // namespace gemm
+}  // namespace seeml_hip
