@@ -90,7 +90,7 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
   }
 }
 
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline unsigned grid_for(size_t work_items, int block, size_t cap = 65536) {
   size_t g = (work_items + block - 1) / block;

@@ -319,6 +319,99 @@ class Engine {
     return Status::Ok();
   }
 
+  // Runs of consecutive AdamWStep instructions whose operands are pairwise
+  // disjoint (one per LoRA tensor, optimizer.cc:15-20) launch as one
+  // multi-tensor kernel in the captured graph. Order-independent by
+  // disjointness, element expression unchanged: same bits as one launch per
+  // instruction.
+  struct FusedRun {
+    size_t first = 0, count = 0;
+    size_t seg_offset = 0;  // into fused_segs_[program]
+    uint64_t blocks = 0;
+  };
+
+  Status PlanFusion(int program) {
+    fused_runs_[program].clear();
+    if (fused_segs_[program]) {
+      // A replay of the previous graph may still read the old table.
+      if (Status s = HipOk(hipStreamSynchronize(stream_), "fusion table sync"); !s) return s;
+      (void)hipFree(fused_segs_[program]);
+    }
+    fused_segs_[program] = nullptr;
+    const auto& prog = plan_.program[program];
+    std::vector<AdamWSegment> segs;
+    size_t i = 0;
+    while (i < prog.size()) {
+      if (static_cast<Op>(prog[i].opcode) != Op::kAdamWStep) {
+        ++i;
+        continue;
+      }
+      size_t j = i;
+      // [begin, end) byte ranges of every operand in the run; writes are p, m, v.
+      std::vector<std::pair<uint64_t, uint64_t>> ranges;
+      while (j < prog.size() && static_cast<Op>(prog[j].opcode) == Op::kAdamWStep) {
+        const UpdateInstruction& a = prog[j];
+        const uint64_t bytes = a.out[0] * sizeof(float);
+        bool clash = false;
+        for (int k = 0; k < 4 && !clash; ++k) {
+          const uint64_t b = reinterpret_cast<uint64_t>(k == 1 ? static_cast<const void*>(RP(a.in[k]))
+                                                                : static_cast<const void*>(WP(a.in[k])));
+          for (const auto& r : ranges)
+            if (b < r.second && r.first < b + bytes) clash = true;
+        }
+        if (clash) break;
+        for (int k = 0; k < 4; ++k) {
+          const uint64_t b = reinterpret_cast<uint64_t>(k == 1 ? static_cast<const void*>(RP(a.in[k]))
+                                                                : static_cast<const void*>(WP(a.in[k])));
+          ranges.emplace_back(b, b + bytes);
+        }
+        ++j;
+      }
+      if (j - i >= 2) {
+        FusedRun run;
+        run.first = i;
+        run.count = j - i;
+        run.seg_offset = segs.size();
+        for (size_t k = i; k < j; ++k) {
+          const UpdateInstruction& a = prog[k];
+          segs.push_back(AdamWSegment{WP(a.in[0]), RP(a.in[1]), WP(a.in[2]), WP(a.in[3]), a.out[0], 0});
+        }
+        run.blocks = AdamWMultiPlan(segs.data() + run.seg_offset, run.count);
+        fused_runs_[program].push_back(run);
+        i = j;
+      } else {
+        i = std::max(j, i + 1);
+      }
+    }
+    if (segs.empty()) return Status::Ok();
+    const size_t bytes = segs.size() * sizeof(AdamWSegment);
+    if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
+    return HipOk(hipMemcpy(fused_segs_[program], segs.data(), bytes, hipMemcpyHostToDevice),
+                 "fused AdamW table upload");
+  }
+
+  // The captured launch sequence: instructions in plan order, fused AdamW
+  // runs as one launch each.
+  Status RunFused(int program) {
+    const Ctx c = MakeCtx();
+    size_t r = 0;
+    const auto& runs = fused_runs_[program];
+    for (size_t i = 0; i < plan_.program[program].size();) {
+      if (r < runs.size() && runs[r].first == i) {
+        if (Status s = AdamWMulti(fused_segs_[program] + runs[r].seg_offset, runs[r].count,
+                                  runs[r].blocks, c);
+            !s)
+          return s;
+        i += runs[r].count;
+        ++r;
+        continue;
+      }
+      if (Status s = Dispatch(program, i, c); !s) return s;
+      ++i;
+    }
+    return Status::Ok();
+  }
+
   Status Build(int program) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     if (Status s = EnsureWorkspace(program); !s) return s;
@@ -327,11 +420,12 @@ class Engine {
       built_[program] = true;
       return Status::Ok();
     }
+    if (Status s = PlanFusion(program); !s) return s;
     if (Status s = HipOk(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
                          "graph capture begin");
         !s)
       return s;
-    Status launched = RunEager(program);
+    Status launched = RunFused(program);
     hipGraph_t g = nullptr;
     const hipError_t end = hipStreamEndCapture(stream_, &g);
     if (!launched) {
@@ -611,6 +705,11 @@ class Engine {
     if (rodata_) (void)hipFree(rodata_);
     if (ws_) (void)hipFree(ws_);
     if (d_scalars_) (void)hipFree(d_scalars_);
+    for (int p = 0; p < 3; ++p) {
+      if (fused_segs_[p]) (void)hipFree(fused_segs_[p]);
+      fused_segs_[p] = nullptr;
+      fused_runs_[p].clear();
+    }
     if (h_scalars_) (void)hipHostFree(h_scalars_);
     if (h_loss_) (void)hipHostFree(h_loss_);
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -632,6 +731,8 @@ class Engine {
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;
   StepScalars* d_scalars_ = nullptr;
+  AdamWSegment* fused_segs_[3] = {nullptr, nullptr, nullptr};
+  std::vector<FusedRun> fused_runs_[3];
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;
   hipGraph_t graph_[3] = {nullptr, nullptr, nullptr};

@@ -17,6 +17,7 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <cmath>
 
 namespace seeml_hip {
@@ -295,10 +296,99 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ p,
   }
 }
 
-// RoPE on interleaved pairs (attention.cc:39-92). One thread per pair; the
-// pair's frequency step^c is the reference's sequential recurrence
-// (freq *= step, c times), so theta carries the CPU bits; only sinf/cosf
-// are the device's. `dir` = +1 forward rotation, -1 its transpose.
+// Multi-tensor AdamW: workgroup b owns elements [lb*kAdamWChunk,
+// (lb+1)*kAdamWChunk) of the segment whose first_block <= b (binary search),
+// lb = b - first_block.
+constexpr uint64_t kAdamWChunk = 4096;
+
+__global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const AdamWSegment* __restrict__ segs,
+                                                             uint32_t nseg,
+                                                             const StepScalars* __restrict__ s) {
+  uint32_t lo = 0, hi = nseg - 1;
+  const uint64_t b = blockIdx.x;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) / 2;
+    if (segs[mid].first_block <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  const AdamWSegment sg = segs[lo];
+  const uint64_t begin = (b - sg.first_block) * kAdamWChunk;
+  const uint64_t end = begin + kAdamWChunk < sg.n ? begin + kAdamWChunk : sg.n;
+  const float lr = s->lr, b1 = s->beta1, b2 = s->beta2, omb1 = s->om_b1, omb2 = s->om_b2;
+  const float ibc1 = s->inv_bc1, ibc2 = s->inv_bc2, eps = s->eps, wd = s->weight_decay;
+  uint64_t i = begin + threadIdx.x * 4;
+  const bool vec = aligned16(sg.p) && aligned16(sg.g) && aligned16(sg.m) && aligned16(sg.v);
+  if (vec) {
+    for (; i + 3 < end; i += kBlock * 4) {
+      float4 p = *reinterpret_cast<float4*>(sg.p + i);
+      const float4 g = *reinterpret_cast<const float4*>(sg.g + i);
+      float4 m = *reinterpret_cast<float4*>(sg.m + i);
+      float4 v = *reinterpret_cast<float4*>(sg.v + i);
+      adamw_elem(p.x, g.x, m.x, v.x, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+      adamw_elem(p.y, g.y, m.y, v.y, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+      adamw_elem(p.z, g.z, m.z, v.z, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+      adamw_elem(p.w, g.w, m.w, v.w, lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+      *reinterpret_cast<float4*>(sg.p + i) = p;
+      *reinterpret_cast<float4*>(sg.m + i) = m;
+      *reinterpret_cast<float4*>(sg.v + i) = v;
+    }
+  }
+  // Element form: the unaligned case, and a segment's last partial vector.
+  for (uint64_t e = vec ? i : begin + threadIdx.x * 4; e < end; e += kBlock * 4)
+    for (uint64_t k = e; k < e + 4 && k < end; ++k)
+      adamw_elem(sg.p[k], sg.g[k], sg.m[k], sg.v[k], lr, b1, b2, omb1, omb2, ibc1, ibc2, eps, wd);
+}
+
+// RoPE on interleaved pairs (attention.cc:39-92). theta = s * freq_c with
+// freq_c = step^c built by the reference's recurrence freq *= step (c
+// multiplications in float, so freq_c has the CPU's bits); cos/sin are the
+// device's accurate cosf/sinf. Rows are [B*S] x [H*d]; s = row % S.
+//
+// Fast form (d % 4 == 0, 16-byte aligned rows): each workgroup builds the
+// d/2 frequencies once in LDS and streams whole rows as float4 = 2 pairs.
+constexpr int kRopeMaxHalf = 1024;
+
+template <int DIR>
+__global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restrict__ x,
+                                                           float* __restrict__ y, uint32_t rows,
+                                                           uint32_t S, uint32_t width,
+                                                           uint32_t d, float step) {
+  __shared__ float freq[kRopeMaxHalf];
+  const uint32_t half_d = d / 2;
+  for (uint32_t c = threadIdx.x; c < half_d; c += kBlock) {
+    float f = 1.0f;
+    for (uint32_t i = 0; i < c; ++i) f *= step;
+    freq[c] = f;
+  }
+  __syncthreads();
+  const uint32_t nv = width / 4;
+  for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float fs = static_cast<float>(row % S);
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * width);
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * width);
+    for (uint32_t j = threadIdx.x; j < nv; j += kBlock) {
+      const uint32_t c2 = ((4 * j) % d) / 2;
+      const float4 v = xr[j];
+      const float t0 = fs * freq[c2], t1 = fs * freq[c2 + 1];
+      const float c0 = cosf(t0), s0 = sinf(t0), c1 = cosf(t1), s1 = sinf(t1);
+      float4 o;
+      if constexpr (DIR > 0) {
+        o.x = v.x * c0 - v.y * s0;
+        o.y = v.x * s0 + v.y * c0;
+        o.z = v.z * c1 - v.w * s1;
+        o.w = v.z * s1 + v.w * c1;
+      } else {
+        o.x = v.x * c0 + v.y * s0;
+        o.y = -v.x * s0 + v.y * c0;
+        o.z = v.z * c1 + v.w * s1;
+        o.w = -v.z * s1 + v.w * c1;
+      }
+      yr[j] = o;
+    }
+  }
+}
+
+// General form: one thread per pair.
 __global__ __launch_bounds__(kBlock) void rope_kernel(const float* __restrict__ x,
                                                       float* __restrict__ y, size_t pairs,
                                                       size_t S, size_t H, size_t half_d,
@@ -330,8 +420,23 @@ Status Rope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, fl
   if (pairs == 0) return Status::Ok();
   // step = base^(-2/d) evaluated on the host with the reference's powf.
   const float step = ::powf(base, -2.0f / static_cast<float>(d));
-  hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, kBlock, kGridCap)), dim3(kBlock), 0,
-                     c.stream, x, y, pairs, S, H, d / 2, step, dir);
+  const size_t rows = B * S, width = H * d;
+  const bool fast = d % 4 == 0 && d / 2 <= static_cast<size_t>(kRopeMaxHalf) && aligned16(x) &&
+                    aligned16(y) && rows <= 0xFFFFFFFFu && width <= 0xFFFFFFFFu && S > 0;
+  if (fast) {
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>(rows, 4096));
+    if (dir > 0)
+      hipLaunchKernelGGL(rope_rows_kernel<1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
+                         static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), step);
+    else
+      hipLaunchKernelGGL(rope_rows_kernel<-1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
+                         static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), step);
+  } else {
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, kBlock, kGridCap)), dim3(kBlock), 0,
+                       c.stream, x, y, pairs, S, H, d / 2, step, dir);
+  }
   return LaunchStatus(what);
 }
 
@@ -434,6 +539,25 @@ Status SgdStep(float* p, const float* g, size_t n, const Ctx& c) {
   hipLaunchKernelGGL(sgd_kernel, dim3(grid_for(n, kBlock, kGridCap)), dim3(kBlock), 0, c.stream,
                      p, g, n, c.scalars);
   return LaunchStatus("SgdStep");
+}
+
+uint64_t AdamWMultiPlan(AdamWSegment* segs, size_t nseg) {
+  uint64_t blocks = 0;
+  for (size_t i = 0; i < nseg; ++i) {
+    segs[i].first_block = blocks;
+    blocks += (segs[i].n + kAdamWChunk - 1) / kAdamWChunk;
+  }
+  return blocks;
+}
+
+Status AdamWMulti(const AdamWSegment* segs, size_t nseg, uint64_t blocks, const Ctx& c) {
+  if (nseg == 0 || blocks == 0) return Status::Ok();
+  if (!c.scalars) return Status::Fail(kUnitEngine, "AdamWStep: no step scalars bound");
+  if (blocks > 0x7FFFFFFFu || nseg > 0xFFFFFFFFu)
+    return Status::Fail(kUnitEngine, "AdamWStep: fused launch too large");
+  hipLaunchKernelGGL(adamw_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                     c.stream, segs, static_cast<uint32_t>(nseg), c.scalars);
+  return LaunchStatus("AdamWStep(fused)");
 }
 
 Status AdamWStep(float* p, const float* g, float* m, float* v, size_t n, const Ctx& c) {

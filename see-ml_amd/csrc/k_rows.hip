@@ -137,6 +137,73 @@ __global__ __launch_bounds__(kBlock) void xent_fwd_rows(const float* __restrict_
   }
 }
 
+// Register-resident form for 16-byte aligned rows with C % 4 == 0 and
+// C <= NT * 4 * kXentVec: one workgroup per row holds the row in registers
+// (thread t owns float4s t, t + NT, ...), so logits are read once and probs
+// written once. Same expressions as xent_fwd_rows: f32 max, f32 exp-sum
+// (per-thread partials in index order, then the fixed block tree), probs =
+// e * (1/sum), the label term from the same expression as p[label].
+constexpr int kXentVec = 8;
+
+template <int NT>
+__global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict__ logits,
+                                                        const int32_t* __restrict__ labels,
+                                                        float* __restrict__ probs, size_t N,
+                                                        size_t C, double* __restrict__ terms) {
+  __shared__ float fscratch[NT / kWave];
+  const size_t n = blockIdx.x;
+  const float4* x4 = reinterpret_cast<const float4*>(logits + n * C);
+  float4* p4 = reinterpret_cast<float4*>(probs + n * C);
+  const int nv = static_cast<int>(C / 4);
+  const int t = threadIdx.x;
+  float4 v[kXentVec];
+  float mx = logits[n * C];
+#pragma unroll
+  for (int i = 0; i < kXentVec; ++i) {
+    const int j = t + i * NT;
+    if (j < nv) {
+      v[i] = x4[j];
+      mx = fmaxf(fmaxf(fmaxf(fmaxf(mx, v[i].x), v[i].y), v[i].z), v[i].w);
+    }
+  }
+  mx = block_max<NT>(mx, fscratch);
+  float sacc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kXentVec; ++i) {
+    const int j = t + i * NT;
+    if (j < nv) {
+      v[i].x = expf(v[i].x - mx);
+      v[i].y = expf(v[i].y - mx);
+      v[i].z = expf(v[i].z - mx);
+      v[i].w = expf(v[i].w - mx);
+      sacc += v[i].x;
+      sacc += v[i].y;
+      sacc += v[i].z;
+      sacc += v[i].w;
+    }
+  }
+  const float sum = block_sum<float, NT>(sacc, fscratch);
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int i = 0; i < kXentVec; ++i) {
+    const int j = t + i * NT;
+    if (j < nv) p4[j] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+  }
+  if (t == 0) {
+    const int32_t lab = labels[n];
+    double term;
+    if (lab < 0 || static_cast<size_t>(lab) >= C) {
+      term = __builtin_nan("");  // outside the feeder contract: poison the loss
+    } else {
+      const float pl = expf(logits[n * C + lab] - mx) * inv;  // same expression as p[lab]
+      const double safe = isnan(pl) ? static_cast<double>(pl)
+                                    : static_cast<double>(fmaxf(pl, 1e-12f));
+      term = -log(safe);
+    }
+    terms[n] = term;
+  }
+}
+
 // ---- KL distillation forward ----------------------------------------------------
 
 template <int TPR>
@@ -387,7 +454,18 @@ Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, f
   if (c.ws_bytes < N * sizeof(double))
     return Status::Fail(kUnitEngine, "SoftmaxXEntFwd: workspace too small");
   double* terms = static_cast<double*>(c.ws);
-  if (C >= 2048)
+  const bool reg = C >= 2048 && C % 4 == 0 && aligned16(logits) && aligned16(probs) &&
+                   N <= 0x7FFFFFFF;
+  if (reg && C <= static_cast<size_t>(256 * 4 * kXentVec))
+    hipLaunchKernelGGL(xent_fwd_rows_reg<256>, dim3(static_cast<unsigned>(N)), dim3(256), 0,
+                       c.stream, logits, labels, probs, N, C, terms);
+  else if (reg && C <= static_cast<size_t>(512 * 4 * kXentVec))
+    hipLaunchKernelGGL(xent_fwd_rows_reg<512>, dim3(static_cast<unsigned>(N)), dim3(512), 0,
+                       c.stream, logits, labels, probs, N, C, terms);
+  else if (reg && C <= static_cast<size_t>(1024 * 4 * kXentVec))
+    hipLaunchKernelGGL(xent_fwd_rows_reg<1024>, dim3(static_cast<unsigned>(N)), dim3(1024), 0,
+                       c.stream, logits, labels, probs, N, C, terms);
+  else if (C >= 2048)
     hipLaunchKernelGGL(xent_fwd_rows<kBlock>, dim3(RowsGrid(N, kBlock)), dim3(kBlock), 0,
                        c.stream, logits, labels, probs, N, C, terms);
   else

@@ -109,6 +109,21 @@ Status KLDistillBwd(const float* p_s, const float* p_t, const float* seed, float
                     size_t N, size_t C, float T, const Ctx& c);
 Status SgdStep(float* p, const float* g, size_t n, const Ctx& c);
 Status AdamWStep(float* p, const float* g, float* m, float* v, size_t n, const Ctx& c);
+
+// Several AdamWStep instructions with pairwise-disjoint operands as one
+// launch (same per-element expression, so the same bits). `segs` is a device
+// array; AdamWMultiPlan fills first_block on the host copy and returns the
+// grid size.
+struct AdamWSegment {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  uint64_t n;
+  uint64_t first_block;
+};
+uint64_t AdamWMultiPlan(AdamWSegment* host_segs, size_t nseg);
+Status AdamWMulti(const AdamWSegment* segs, size_t nseg, uint64_t blocks, const Ctx& c);
 Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,
                const Ctx& c);
 Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t d, float base,

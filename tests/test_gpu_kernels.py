@@ -249,8 +249,10 @@ def test_norms(env, orc, rows, cols):
     assert rel_err(env.H(tdx), dx) <= 1e-5
 
 
-def test_rope(env, orc):
-    B, S, H, d = 2, 300, 3, 64
+# d % 4 == 0 and d/2 <= 1024: the row-streaming float4 form; otherwise the
+# per-pair form.
+@pytest.mark.parametrize("B,S,H,d", [(2, 300, 3, 64), (2, 17, 3, 6), (1, 3, 1, 2052)])
+def test_rope(env, orc, B, S, H, d):
     n = B * S * H * d
     x = rnd(n, 70)
     for name, base in (("rope_fwd", 10000.0), ("rope_bwd", 500.0)):
@@ -307,7 +309,10 @@ def test_attention_family(env, orc, B, S, H, d):
         assert np.all(hp == 1.0) and same_bits(env.H(to), v)
 
 
-@pytest.mark.parametrize("N,C", [(32, 256), (100, 8192), (17, 32000), (3, 1)])
+# C < 2048: a wave per row; C % 4 == 0 up to 32768: the register-resident row
+# (256/512/1024 threads); otherwise the three-pass block per row.
+@pytest.mark.parametrize("N,C", [(32, 256), (100, 8192), (17, 32000), (3, 1), (5, 12000),
+                                 (4, 2050), (3, 40000)])
 def test_softmax_xent(env, orc, N, C):
     logits = rnd(N * C, 90, 3)
     labels = np.random.default_rng(91).integers(0, C, N).astype(np.int32)
