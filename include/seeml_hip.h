@@ -130,6 +130,88 @@ int seeml_hip_autotune(seeml_hip_engine* e, int budget);
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap);
 
+/* ---- Feeder (replaces runtime/feeder/dataset.h:39-177) --------------------
+ * A host dataset of fixed-shape samples: feature rows (f32) with class (i32)
+ * or dense (f32) labels, or token records of seq+1 i32 ids whose inputs are
+ * tokens[0..S) and labels the shifted view tokens[1..S]. Served sequentially
+ * with wraparound, or through a seeded splitmix64 Fisher-Yates permutation
+ * re-drawn every epoch; the served bytes and order are the reference's.
+ * Errors read "Dataset: <message>" (runtime/diagnostics/feeding/error.h). */
+typedef struct seeml_hip_dataset seeml_hip_dataset;
+/* splitmix64 step (dataset.cc:344-352). */
+uint64_t seeml_hip_splitmix64(uint64_t* state);
+/* Dataset::FromTokens / FromMemory / LoadFromFile (dataset.cc:34-197). */
+int seeml_hip_dataset_from_tokens(const int32_t* tokens, uint64_t count, uint64_t num_records,
+                                  uint64_t seq, seeml_hip_dataset** out, char* err,
+                                  uint64_t err_cap);
+int seeml_hip_dataset_from_memory(const float* inputs, uint64_t input_count,
+                                  const uint8_t* labels, uint64_t label_bytes,
+                                  uint64_t num_samples, uint64_t input_dim, uint32_t label_kind,
+                                  uint64_t label_dim, seeml_hip_dataset** out, char* err,
+                                  uint64_t err_cap);
+int seeml_hip_dataset_load(const char* path, seeml_hip_dataset** out, char* err,
+                           uint64_t err_cap);
+/* Dataset::SaveToFile (dataset.cc:230-286), the .sds bytes. */
+int seeml_hip_dataset_save(seeml_hip_dataset* d, const char* path);
+void seeml_hip_dataset_free(seeml_hip_dataset* d);
+const char* seeml_hip_dataset_error(const seeml_hip_dataset* d);
+uint64_t seeml_hip_dataset_num_samples(const seeml_hip_dataset* d);
+uint64_t seeml_hip_dataset_input_dim(const seeml_hip_dataset* d);
+uint32_t seeml_hip_dataset_label_kind(const seeml_hip_dataset* d);
+uint32_t seeml_hip_dataset_input_kind(const seeml_hip_dataset* d);
+uint64_t seeml_hip_dataset_label_bytes_per_sample(const seeml_hip_dataset* d);
+/* Dataset::ValidateClassLabels (dataset.cc:199-228). */
+int seeml_hip_dataset_validate_class_labels(seeml_hip_dataset* d, uint64_t num_classes);
+/* Dataset::FillBatch (dataset.cc:288-342) into HOST slots: token corpora
+ * take `batch` token rows (a whole number of records). */
+void seeml_hip_dataset_fill_batch(seeml_hip_dataset* d, uint64_t batch, void* input_slot,
+                                  void* label_slot);
+/* Rewind / EnableShuffle / SaveServingPos / RestoreServingPos / SkipServed /
+ * SplitValidation (dataset.h:95-150, dataset.cc:356-462). */
+void seeml_hip_dataset_rewind(seeml_hip_dataset* d);
+void seeml_hip_dataset_enable_shuffle(seeml_hip_dataset* d, uint64_t seed);
+void seeml_hip_dataset_get_serving_pos(const seeml_hip_dataset* d, uint64_t* cursor,
+                                       uint64_t* epoch);
+void seeml_hip_dataset_restore_serving_pos(seeml_hip_dataset* d, uint64_t cursor,
+                                           uint64_t epoch);
+int seeml_hip_dataset_skip_served(seeml_hip_dataset* d, uint64_t rows);
+int seeml_hip_dataset_split_validation(seeml_hip_dataset* d, double fraction,
+                                       seeml_hip_dataset** val);
+
+/* ---- Train / evaluate loops (UpdateEngine::Train / EvaluateMetrics) -------
+ * The engine drives the feeder itself: a host thread fills the next batch
+ * into pinned memory while the current step runs, and each step's batch is
+ * one H2D copy per I/O slot on the engine stream (batch_pipeline.cc). */
+typedef struct seeml_hip_eval_metrics {
+  float loss;           /* mean of per-batch eval losses, in double */
+  int32_t has_accuracy; /* class-label plan whose eval softmax covers the batch */
+  float accuracy;       /* strict-'>' argmax hits / real (unwrapped) rows */
+} seeml_hip_eval_metrics;
+typedef struct seeml_hip_train_report { /* TrainReport, update_engine.h:91-117 */
+  uint64_t steps;
+  float initial_avg_loss;
+  float final_avg_loss;
+  int32_t has_validation;
+  float val_initial_loss;
+  float val_final_loss;
+  int32_t has_val_accuracy;
+  float val_initial_accuracy;
+  float val_final_accuracy;
+  int32_t improved; /* TrainReport::improved(): the regression gate */
+} seeml_hip_train_report;
+/* EvaluateMetrics (update_engine.cc:557-650): snapshot + rewind the set, the
+ * eval program per compiled batch (the last batch wraps), loss mean in
+ * double, accuracy on device over the real rows, serving position restored. */
+int seeml_hip_evaluate_metrics(seeml_hip_engine* e, seeml_hip_dataset* d,
+                               seeml_hip_eval_metrics* out);
+/* TrainImpl (update_engine.cc:664-787): validation before/after when given,
+ * `steps` (0 = the plan's default_steps) train steps from the engine's
+ * step_, non-finite loss aborts, first/last-window loss means; loss_curve
+ * (optional) receives up to curve_cap per-step losses. */
+int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
+                    seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
+                    seeml_hip_train_report* out);
+
 /* Profiling (outside any timed step): replays `program` eagerly `reps`
  * times on the engine stream with a HIP event pair around every
  * instruction, and writes each instruction's mean duration in ms to
@@ -211,6 +293,10 @@ int seeml_hip_softmax_xent_fwd(const float* logits, const int32_t* labels, float
                                float* probs, uint64_t N, uint64_t C, void* stream);
 int seeml_hip_softmax_xent_bwd(const float* probs, const int32_t* labels, const float* seed,
                                float* dlogits, uint64_t N, uint64_t C, void* stream);
+/* EvaluateMetrics' accuracy count (update_engine.cc:619-633) on device
+ * pointers: rows whose first strict-'>' argmax equals a non-negative label. */
+int seeml_hip_argmax_correct(const float* probs, const int32_t* labels, uint64_t rows,
+                             uint64_t cols, uint64_t* correct, void* stream);
 int seeml_hip_mse_fwd(const float* pred, const float* target, float* loss, uint64_t n,
                       void* stream);
 int seeml_hip_mse_bwd(const float* pred, const float* target, const float* seed, float* dpred,

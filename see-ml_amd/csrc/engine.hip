@@ -30,6 +30,7 @@
 
 #include "../../include/seeml_hip.h"
 #include "kernels.h"
+#include "stager.h"
 #include "plan_checks.h"
 
 namespace seeml_hip {
@@ -552,6 +553,177 @@ class Engine {
     return Status::Ok();
   }
 
+  // ---- EvaluateMetrics / TrainImpl (update_engine.cc:557-787) ------------
+  struct EvalOut {
+    float loss = 0.0f;
+    bool has_accuracy = false;
+    float accuracy = 0.0f;
+  };
+  struct ReportOut {
+    uint64_t steps = 0;
+    float initial_avg_loss = 0.0f, final_avg_loss = 0.0f;
+    bool has_validation = false;
+    float val_initial_loss = 0.0f, val_final_loss = 0.0f;
+    bool has_val_accuracy = false;
+    float val_initial_accuracy = 0.0f, val_final_accuracy = 0.0f;
+    bool improved() const {
+      return has_validation ? val_final_loss < val_initial_loss
+                            : final_avg_loss < initial_avg_loss;
+    }
+  };
+
+  uint8_t* SlotPtr(uint64_t ref) const { return ref == kNullRef ? nullptr : arena_ + RefOffset(ref); }
+
+  Status EnsureArgmaxBuffers(uint64_t rows) {
+    const size_t need = ArgmaxPartials(rows);
+    if (need <= argmax_cap_ && d_argmax_) return Status::Ok();
+    if (d_argmax_) (void)hipFree(d_argmax_);
+    d_argmax_ = nullptr;
+    argmax_cap_ = 0;
+    // [total u64][partials u32 ...]
+    if (Status s = HipOk(hipMalloc(&d_argmax_, 8 + 4 * std::max<size_t>(need, 1)), "argmax buffers");
+        !s)
+      return s;
+    argmax_cap_ = need;
+    if (!h_count_)
+      if (Status s = HipOk(hipHostMalloc(&h_count_, sizeof(uint64_t)), "pinned count"); !s) return s;
+    return Status::Ok();
+  }
+
+  Status EvaluateMetrics(Dataset& data, EvalOut* out) {
+    const PlanHeader& h = plan_.header;
+    const int kEval = static_cast<int>(Program::kEval);
+    if (plan_.program[kEval].empty())
+      return Status::Fail(kUnitEngine, "plan carries no eval program");
+    if (Status s = VerifyFeederContract(h, data, plan_.num_classes, plan_.vocab_bound); !s)
+      return s;
+    // Every pass over a set scores the same samples: snapshot, rewind, and
+    // restore afterwards (the restore replays the permutation epoch).
+    const Dataset::ServingPos entry = data.SaveServingPos();
+    data.Rewind();
+    const bool has_labels = h.label_kind != 0;
+    const bool track = h.label_kind == 1 && plan_.eval_probs_ref != kNullRef &&
+                       plan_.eval_softmax_cols > 0 && plan_.eval_softmax_rows >= h.batch;
+    const uint64_t rows_per_sample = h.input_kind == 1 ? h.seq_len : 1;
+    const uint64_t per_step = h.batch / rows_per_sample;
+    const uint64_t n = data.num_samples();
+    const uint64_t batches = std::max<uint64_t>(1, (n + per_step - 1) / per_step);
+    double total = 0.0;
+    uint64_t correct = 0, counted = 0;
+    Status st = track ? EnsureArgmaxBuffers(h.batch) : Status::Ok();
+    if (st) {
+      BatchStager feeder(data, h.batch, h.input_floats * 4, has_labels ? h.label_bytes : 0);
+      st = feeder.Start();
+      for (uint64_t b = 0; st && b < batches; ++b) {
+        st = feeder.Next(SlotPtr(h.input_ref), has_labels ? SlotPtr(h.label_ref) : nullptr, stream_);
+        if (st) st = Run(kEval);
+        // Rows of the final batch past the set's end are wrapped duplicates:
+        // the loss mean keeps them, accuracy judges each real row once.
+        const uint64_t served = b * per_step;
+        const uint64_t real = std::min<uint64_t>(per_step, n > served ? n - served : 0) * rows_per_sample;
+        if (st && track && real) {
+          Ctx c = MakeCtx();
+          uint64_t* d_total = reinterpret_cast<uint64_t*>(d_argmax_);
+          uint32_t* partials = reinterpret_cast<uint32_t*>(d_argmax_ + 8);
+          st = ArgmaxCorrect(RP(plan_.eval_probs_ref),
+                             reinterpret_cast<const int32_t*>(SlotPtr(h.label_ref)), real,
+                             plan_.eval_softmax_cols, partials, d_total, c);
+          if (st)
+            st = HipOk(hipMemcpyAsync(h_count_, d_total, sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                      stream_),
+                       "accuracy read");
+        }
+        float l = 0.0f;
+        if (st) st = Loss(&l);  // synchronizes the stream (the count read too)
+        if (!st) break;
+        total += l;
+        if (track && real) {
+          correct += *h_count_;
+          counted += real;
+        }
+      }
+    }  // the feeder joins here and returns a staged, unconsumed batch
+    data.RestoreServingPos(entry);
+    if (!st) return st;
+    out->loss = static_cast<float>(total / static_cast<double>(batches));
+    out->has_accuracy = track && counted > 0;
+    out->accuracy = out->has_accuracy ? static_cast<float>(static_cast<double>(correct) /
+                                                           static_cast<double>(counted))
+                                      : 0.0f;
+    return Status::Ok();
+  }
+
+  Status Train(Dataset& data, uint64_t steps, Dataset* validation, float* curve,
+               uint64_t curve_cap, ReportOut* rep) {
+    const PlanHeader& h = plan_.header;
+    if (steps == 0) steps = h.default_steps;
+    if (steps == 0)
+      return Status::Fail(kUnitEngine, "no steps requested and the plan has no default");
+    if (Status s = VerifyFeederContract(h, data, plan_.num_classes, plan_.vocab_bound); !s)
+      return s;
+    if (validation)
+      if (Status s = VerifyFeederContract(h, *validation, plan_.num_classes, plan_.vocab_bound); !s)
+        return s;
+    ReportOut report;
+    if (validation) {
+      EvalOut v;
+      if (Status s = EvaluateMetrics(*validation, &v); !s) return s;
+      report.has_validation = true;
+      report.val_initial_loss = v.loss;
+      report.has_val_accuracy = v.has_accuracy;
+      report.val_initial_accuracy = v.accuracy;
+    }
+    const bool has_labels = h.label_kind != 0;
+    const uint64_t window = std::max<uint64_t>(1, std::min<uint64_t>(20, steps / 5));
+    double first_sum = 0.0, last_sum = 0.0;
+    uint64_t first_n = 0, last_n = 0, executed = 0;
+    const uint64_t start = step_;
+    Status st;
+    {
+      // The feeder stages step s+1's batch while step s runs; the served
+      // sequence is exactly the serial one.
+      BatchStager feeder(data, h.batch, h.input_floats * 4, has_labels ? h.label_bytes : 0);
+      st = feeder.Start();
+      for (uint64_t s = start; st && s < start + steps; ++s) {
+        st = SetStep(s + 1);  // 1-indexed step for AdamW bias correction
+        if (st)
+          st = feeder.Next(SlotPtr(h.input_ref), has_labels ? SlotPtr(h.label_ref) : nullptr,
+                           stream_);
+        if (st) st = Run(static_cast<int>(Program::kTrain));
+        float loss = 0.0f;
+        if (st) st = Loss(&loss);
+        if (!st) break;
+        ++executed;
+        if (!std::isfinite(loss)) {
+          st = Status::Fail(kUnitEngine, "loss became non-finite at step " +
+                                             std::to_string(step_) + " — aborting the update");
+          break;
+        }
+        if (curve && s - start < curve_cap) curve[s - start] = loss;
+        if (s - start < window) {
+          first_sum += loss;
+          ++first_n;
+        }
+        if (s - start >= steps - window) {
+          last_sum += loss;
+          ++last_n;
+        }
+      }
+    }
+    if (!st) return st;
+    report.steps = executed;
+    report.initial_avg_loss = first_n ? static_cast<float>(first_sum / first_n) : 0.0f;
+    report.final_avg_loss = last_n ? static_cast<float>(last_sum / last_n) : report.initial_avg_loss;
+    if (validation) {
+      EvalOut v;
+      if (Status s = EvaluateMetrics(*validation, &v); !s) return s;
+      report.val_final_loss = v.loss;
+      report.val_final_accuracy = v.accuracy;
+    }
+    *rep = report;
+    return Status::Ok();
+  }
+
   Status Access(uint64_t ref, void* host, size_t bytes, bool write) {
     const bool ro = IsRodataRef(ref);
     if (write && ro) return Status::Fail(kUnitEngine, "rodata is not writable");
@@ -710,6 +882,11 @@ class Engine {
       fused_segs_[p] = nullptr;
       fused_runs_[p].clear();
     }
+    if (d_argmax_) (void)hipFree(d_argmax_);
+    d_argmax_ = nullptr;
+    argmax_cap_ = 0;
+    if (h_count_) (void)hipHostFree(h_count_);
+    h_count_ = nullptr;
     if (h_scalars_) (void)hipHostFree(h_scalars_);
     if (h_loss_) (void)hipHostFree(h_loss_);
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -732,6 +909,9 @@ class Engine {
   size_t ws_bytes_ = 0;
   StepScalars* d_scalars_ = nullptr;
   AdamWSegment* fused_segs_[3] = {nullptr, nullptr, nullptr};
+  uint8_t* d_argmax_ = nullptr;
+  size_t argmax_cap_ = 0;
+  uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;
@@ -921,6 +1101,37 @@ int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char
   return SEEML_HIP_OK;
 }
 
+int seeml_hip_evaluate_metrics(seeml_hip_engine* e, seeml_hip_dataset* d,
+                               seeml_hip_eval_metrics* out) {
+  Engine::EvalOut m;
+  if (const Status s = e->impl.EvaluateMetrics(d->impl, &m); !s) return Ret(e, s);
+  out->loss = m.loss;
+  out->has_accuracy = m.has_accuracy ? 1 : 0;
+  out->accuracy = m.accuracy;
+  return SEEML_HIP_OK;
+}
+
+int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
+                    seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
+                    seeml_hip_train_report* out) {
+  Engine::ReportOut r;
+  if (const Status s = e->impl.Train(d->impl, steps, validation ? &validation->impl : nullptr,
+                                     loss_curve, curve_cap, &r);
+      !s)
+    return Ret(e, s);
+  out->steps = r.steps;
+  out->initial_avg_loss = r.initial_avg_loss;
+  out->final_avg_loss = r.final_avg_loss;
+  out->has_validation = r.has_validation ? 1 : 0;
+  out->val_initial_loss = r.val_initial_loss;
+  out->val_final_loss = r.val_final_loss;
+  out->has_val_accuracy = r.has_val_accuracy ? 1 : 0;
+  out->val_initial_accuracy = r.val_initial_accuracy;
+  out->val_final_accuracy = r.val_final_accuracy;
+  out->improved = r.improved() ? 1 : 0;
+  return SEEML_HIP_OK;
+}
+
 int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,
                               uint64_t count) {
   return Ret(e, e->impl.Profile(program, reps, ms_out, count));
@@ -1105,6 +1316,21 @@ int seeml_hip_softmax_xent_bwd(const float* probs, const int32_t* labels, const 
                                float* dlogits, uint64_t N, uint64_t C, void* stream) {
   SEEML_SIMPLE(seeml_hip::SoftmaxXEntBwd(probs, labels, seed, dlogits, N, C, ctx));
 }
+int seeml_hip_argmax_correct(const float* probs, const int32_t* labels, uint64_t rows,
+                             uint64_t cols, uint64_t* correct, void* stream) {
+  SEEML_CTX(8 + 4 * seeml_hip::ArgmaxPartials(rows));
+  uint64_t* total = static_cast<uint64_t*>(ctx.ws);
+  uint32_t* partials = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ctx.ws) + 8);
+  if (const Status s = seeml_hip::ArgmaxCorrect(probs, labels, rows, cols, partials, total, ctx); !s)
+    return seeml_hip::Report(s);
+  uint64_t v = 0;
+  if (hipMemcpyAsync(&v, total, sizeof v, hipMemcpyDeviceToHost, ctx.stream) != hipSuccess ||
+      hipStreamSynchronize(ctx.stream) != hipSuccess)
+    return seeml_hip::Report(Status::Fail(seeml_hip::kUnitEngine, "argmax: count read failed"));
+  *correct = v;
+  return SEEML_HIP_OK;
+}
+
 int seeml_hip_mse_fwd(const float* pred, const float* target, float* loss, uint64_t n,
                       void* stream) {
   SEEML_CTX(seeml_hip::MseFwdWorkspace(n));

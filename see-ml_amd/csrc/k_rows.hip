@@ -408,6 +408,63 @@ __global__ __launch_bounds__(kBlock) void attn_softmax_rows_kernel(float* __rest
   for (size_t j = t; j <= i; j += kWave) pr[j] = pr[j] * inv;
 }
 
+// Argmax hit count: a wavefront per row. Each lane keeps the first index
+// of its strided maximum (NaN skipped, strict '>'); lanes merge by larger
+// value, then lower index, which equals the sequential strict-'>' scan
+// whenever column 0 is not NaN.
+constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
+
+__global__ __launch_bounds__(kBlock) void argmax_correct_kernel(const float* __restrict__ probs,
+                                                                const int32_t* __restrict__ labels,
+                                                                uint64_t rows, uint32_t cols,
+                                                                uint32_t* __restrict__ partials) {
+  __shared__ uint32_t hits[kBlock / kWave];
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  const uint64_t r = static_cast<uint64_t>(blockIdx.x) * (kBlock / kWave) + w;
+  uint32_t hit = 0;
+  if (r < rows) {
+    const float* row = probs + r * cols;
+    float best = 0.0f;
+    uint32_t bi = kNoIndex;
+    for (uint32_t c = lane; c < cols; c += kWave) {
+      const float v = row[c];
+      if (v == v && (bi == kNoIndex || v > best)) {
+        best = v;
+        bi = c;
+      }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const float ob = __shfl_xor(best, off, kWave);
+      const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), off, kWave));
+      if (oi != kNoIndex && (bi == kNoIndex || ob > best || (ob == best && oi < bi))) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    const float first = row[0];
+    const uint32_t arg = first != first ? 0u : bi;
+    const int32_t lab = labels[r];
+    hit = (lab >= 0 && static_cast<uint32_t>(lab) == arg) ? 1u : 0u;
+  }
+  if (lane == 0) hits[w] = hit;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t s = 0;
+    for (int i = 0; i < kBlock / kWave; ++i) s += hits[i];
+    partials[blockIdx.x] = s;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void sum_u32_kernel(const uint32_t* __restrict__ partials,
+                                                         uint64_t n, uint64_t* __restrict__ total) {
+  __shared__ uint64_t scratch[kBlock / kWave];
+  uint64_t acc = 0;
+  for (uint64_t i = threadIdx.x; i < n; i += kBlock) acc += partials[i];
+  const uint64_t t = block_sum<uint64_t, kBlock>(acc, scratch);
+  if (threadIdx.x == 0) *total = t;
+}
+
 inline unsigned RowsGrid(size_t rows, int tpr) {
   const size_t per = kBlock / tpr;
   return static_cast<unsigned>((rows + per - 1) / per);
@@ -546,6 +603,21 @@ Status AttnSoftmaxRows(float* p, size_t rows, size_t S, const Ctx& c) {
   hipLaunchKernelGGL(attn_softmax_rows_kernel, dim3(RowsGrid(rows, kWave)), dim3(kBlock), 0,
                      c.stream, p, rows, S);
   return LaunchStatus("AttnFwd(softmax)");
+}
+
+size_t ArgmaxPartials(uint64_t rows) { return (rows + kBlock / kWave - 1) / (kBlock / kWave); }
+
+Status ArgmaxCorrect(const float* probs, const int32_t* labels, uint64_t rows, uint64_t cols,
+                     uint32_t* partials, uint64_t* total, const Ctx& c) {
+  if (cols == 0 || cols >= kNoIndex) return Status::Fail(kUnitEngine, "argmax: bad class count");
+  const size_t blocks = ArgmaxPartials(rows);
+  if (blocks > 0x7FFFFFFF) return Status::Fail(kUnitEngine, "argmax: too many rows");
+  if (blocks)
+    hipLaunchKernelGGL(argmax_correct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                       c.stream, probs, labels, rows, static_cast<uint32_t>(cols), partials);
+  hipLaunchKernelGGL(sum_u32_kernel, dim3(1), dim3(kBlock), 0, c.stream, partials,
+                     static_cast<uint64_t>(blocks), total);
+  return LaunchStatus("argmax");
 }
 
 }  // namespace seeml_hip

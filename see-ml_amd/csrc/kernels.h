@@ -123,6 +123,15 @@ struct AdamWSegment {
   uint64_t first_block;
 };
 uint64_t AdamWMultiPlan(AdamWSegment* host_segs, size_t nseg);
+
+// EvaluateMetrics' accuracy count (update_engine.cc:619-633): per row the
+// first index of the largest value under strict '>' scanning from column 0
+// (NaN never wins; a NaN in column 0 keeps index 0), compared with the
+// row's label (negative labels never match). `partials` holds
+// ArgmaxPartials(rows) u32; the exact integer total lands in *total.
+size_t ArgmaxPartials(uint64_t rows);
+Status ArgmaxCorrect(const float* probs, const int32_t* labels, uint64_t rows, uint64_t cols,
+                     uint32_t* partials, uint64_t* total, const Ctx& c);
 Status AdamWMulti(const AdamWSegment* segs, size_t nseg, uint64_t blocks, const Ctx& c);
 Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,
                const Ctx& c);

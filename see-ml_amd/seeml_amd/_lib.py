@@ -21,6 +21,8 @@ _TYPES = {
     "float": C.c_float,
     "uint64_t": C.c_uint64,
     "uint32_t": C.c_uint32,
+    "int32_t": C.c_int32,
+    "double": C.c_double,
 }
 
 

@@ -5,6 +5,8 @@ UpdateEngine (runtime/engine/update_engine.h:119-242) -> DeviceUpdateEngine:
   ExecuteTrainOnce / Train  -> train_step / train                   (seeml_hip_train_step)
   LossValue                 -> loss()
   Evaluate                  -> evaluate(batches)  (eval program + double mean)
+  Train(Dataset&, ...)      -> train_dataset(dataset, steps, validation)
+  EvaluateMetrics(Dataset&) -> evaluate_metrics(dataset)  (loss + argmax accuracy)
   RunMerge                  -> run_merge()
   arena probes              -> read / write (test/support/probes.cc:25-60)
 Errors surface as RuntimeError carrying the "<unit>: <message>" text.
@@ -18,6 +20,18 @@ import numpy as np
 from . import _lib
 
 PROGRAM_TRAIN, PROGRAM_MERGE, PROGRAM_EVAL = 0, 1, 2
+
+
+class _EvalMetrics(C.Structure):
+    _fields_ = [("loss", C.c_float), ("has_accuracy", C.c_int32), ("accuracy", C.c_float)]
+
+
+class _TrainReport(C.Structure):
+    _fields_ = [("steps", C.c_uint64), ("initial_avg_loss", C.c_float),
+                ("final_avg_loss", C.c_float), ("has_validation", C.c_int32),
+                ("val_initial_loss", C.c_float), ("val_final_loss", C.c_float),
+                ("has_val_accuracy", C.c_int32), ("val_initial_accuracy", C.c_float),
+                ("val_final_accuracy", C.c_float), ("improved", C.c_int32)]
 
 
 def _buf(a):
@@ -108,6 +122,28 @@ class DeviceUpdateEngine:
             total += self.loss()
             n += 1
         return float(np.float32(total / max(n, 1)))
+
+    def evaluate_metrics(self, dataset) -> dict:
+        """EvaluateMetrics (update_engine.cc:557-650) over a feeder Dataset."""
+        m = _EvalMetrics()
+        self._check(self._L.seeml_hip_evaluate_metrics(self._h, dataset._h, C.byref(m)),
+                    "evaluate_metrics")
+        return dict(loss=m.loss, has_accuracy=bool(m.has_accuracy), accuracy=m.accuracy)
+
+    def train_dataset(self, dataset, steps: int = 0, validation=None) -> dict:
+        """TrainImpl (update_engine.cc:664-787) with the native feeder; the
+        report's loss_curve holds every step's loss."""
+        r = _TrainReport()
+        cap = steps if steps else 0
+        curve = np.zeros(max(cap, 1), np.float32)
+        self._check(self._L.seeml_hip_train(self._h, dataset._h, steps,
+                                            validation._h if validation is not None else None,
+                                            curve.ctypes.data, cap, C.byref(r)), "train")
+        out = {f: getattr(r, f) for f, _ in _TrainReport._fields_}
+        for k in ("has_validation", "has_val_accuracy", "improved"):
+            out[k] = bool(out[k])
+        out["loss_curve"] = curve[:min(cap, r.steps)]
+        return out
 
     def run_merge(self):
         self._check(self._L.seeml_hip_run_merge(self._h), "run_merge")
