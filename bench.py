@@ -5,13 +5,17 @@ A "step" is one TrainImpl iteration of the compiled plan (update_engine.cc:
 slots, the train program replayed as one hipGraph, the loss read back and
 checked. Inputs are resident in HBM before timing starts.
 
-Default workload: BASELINE configs[1] (C2, the single large LoRA linear
-layer, 8192 x 4096 x 4096, r16). --config selects c1..c5.
+Default workload: BASELINE configs[3] (C4, the d_model-2048 decoder the
+north-star target is stated on: V32000, 16 layers, 16x128 heads, seq 1024 x
+8, SwiGLU 5504, LoRA r16 on q/k/v/o). --config selects c1..c5.
 
 Emits ONE JSON line (rank 0) with, besides the driver's fields:
-  roofline      the dominant kernel (largest share of step time) measured
-                with HIP events on the engine stream: algorithmic FLOPs (or
-                bytes) of one launch / mean launch time, vs MI355X peak
+  roofline      the dominant kernel — the (opcode, shape, tile) group with
+                the largest share of step time — one launch timed with HIP
+                events on the engine stream: algorithmic FLOPs (or bytes) of
+                one launch / mean launch time, vs MI355X peak; `traffic` is
+                the HBM bytes per launch from the committed rocprofv3 PMC
+                summary for that kernel (profiles/), when one matches
   cpu_baseline  the reference's own executor kernels (oracle/_ref, built
                 from the reference sources) timed on this host on a bounded
                 sample of the same workload
@@ -89,12 +93,26 @@ def cpu_baseline(w, plan, cores, budget_s=20.0):
                        f"{dt / steps * 1e3:.1f} ms/step for {sample_w.cfg.batch} tokens")
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 PMC
+    summary (profiles/*.md carrying a line
+    `traffic: kernel="<kernel>" bytes_per_launch=<B>`), else (None, None)."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        for line in open(path):
+            m = re.search(r'traffic: kernel="([^"]+)" bytes_per_launch=(\d+)', line)
+            if m and m.group(1) == kernel:
+                return int(m.group(2)), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2")
+    ap.add_argument("--config", default="c4")
     ap.add_argument("--no-autotune", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
@@ -139,24 +157,41 @@ def main():
         losses.append(e.train_step(xb, yb))
     log(f"warmup done, loss {losses[-1] if losses else float('nan'):.6f}")
 
+    # Per-instruction breakdown (eager replay with events, before the timed
+    # region) picks the dominant kernel: the (opcode, shape, tile) group with
+    # the largest share of the step.
+    ms = e.profile(PROGRAM_TRAIN, reps=args.profile_reps)
+    summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS)
+    rows = summ["rows"]
+    groups = {}
+    for i, r in enumerate(rows):
+        tile = e.gemm_choice(PROGRAM_TRAIN, i) if r["op"] in workmodel.GEMMS else ""
+        g = groups.setdefault((r["op"], tuple(r["shape"]), tile), [0.0, []])
+        g[0] += r["ms"]
+        g[1].append(i)
+    (dom_op, dom_shape, dom_tile), (dom_total, dom_idx) = max(groups.items(), key=lambda kv: kv[1][0])
+    dom_row = rows[dom_idx[0]]
+    # Its launches get event-record nodes in the train graph, timed live in
+    # every timed step on the engine stream.
+    e.mark_timed(PROGRAM_TRAIN, dom_idx)
+    e.build(PROGRAM_TRAIN)
+    xb, yb = batches[0]
+    losses.append(e.train_step(xb, yb))  # first replay of the rebuilt graph, untimed
+
     torch.cuda.synchronize()
+    launch_ms = []
     t0 = time.perf_counter()
     for s in range(args.steps):
         xb, yb = batches[s % 2]
-        losses.append(e.train_step(xb, yb))
+        losses.append(e.train_step(xb, yb))  # returns after the step's loss read (synchronized)
+        launch_ms.append(e.marked_times(PROGRAM_TRAIN))
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms_per_step = dt / args.steps * 1e3
     tokens_per_s = w.cfg.batch * args.steps / dt
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.1f} tok/s")
 
-    # Per-instruction breakdown (eager replay with events; outside the timed region).
-    ms = e.profile(PROGRAM_TRAIN, reps=args.profile_reps)
-    summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS)
-    rows = summ["rows"]
-    dom = max(range(len(rows)), key=lambda i: rows[i]["ms"])
-    dom_row = rows[dom]
-    dom_ms = e.time_instruction(PROGRAM_TRAIN, dom, reps=10)
+    dom_ms = float(np.mean(np.concatenate(launch_ms)))
     if dom_row["cls"] == "mfma" or (dom_row["cls"] == "attn" and dom_row["flops"]):
         achieved = dom_row["flops"] / (dom_ms * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 3), peak=PEAK_FP32_MFMA_TFLOPS,
@@ -165,11 +200,17 @@ def main():
         achieved = dom_row["bytes"] / (dom_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBPS, unit="GB/s",
                     frac=round(achieved / PEAK_HBM_GBPS, 4))
-    roof.update(kernel=f"{dom_row['op']} {'x'.join(map(str, dom_row['shape']))} "
-                       f"(instruction {dom}, {e.gemm_choice(PROGRAM_TRAIN, dom) if dom_row['op'] in workmodel.GEMMS else ''})".replace(", )", ")"),
-                launch_ms=round(dom_ms, 4), traffic=None,
+    kernel = f"{dom_op} {'x'.join(map(str, dom_shape))}" + (f" {dom_tile}" if dom_tile else "")
+    traffic, traffic_src = measured_traffic(kernel)
+    roof.update(kernel=kernel, launches_per_step=len(dom_idx),
+                step_share=round(dom_total / summ["total_ms"], 4),
+                launch_ms=round(dom_ms, 4),
+                timing=f"HIP events around its {len(dom_idx)} launches per step inside the "
+                       f"train graph, over the {args.steps} timed steps",
+                traffic=traffic, traffic_source=traffic_src,
                 algorithmic=(f"{dom_row['flops']} FLOP" if roof["bound"] == "mfma"
-                             else f"{dom_row['bytes']} B"))
+                             else f"{dom_row['bytes']} B"),
+                algorithmic_bytes=dom_row["bytes"])
     by_op = {k: dict(count=v["count"], ms=round(v["ms"], 4),
                      share=round(v["ms"] / summ["total_ms"], 4)) for k, v in
              sorted(summ["by_op"].items(), key=lambda kv: -kv[1]["ms"])}

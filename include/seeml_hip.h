@@ -122,8 +122,9 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
 /* GEMM tile autotuning (compiler/backend/tuner/bandit.cc:14-53,
  * autotuner.cc:21-80 retargeted to GPU tiles): for every distinct GEMM shape
  * of the train program, a deterministic UCB1 bandit over tile/split-K arms,
- * reward = measured GFLOP/s; picks are installed and graphs rebuilt.
- * budget = launches per shape (>= number of arms). */
+ * reward = measured fraction of fp32 MFMA peak; the pick is the lowest arm
+ * within 3% of the best mean; picks are installed and graphs rebuilt.
+ * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
 /* Describe the GEMM plan chosen for instruction `index` of `program`:
  * writes "cfg-name splits=S" into buf. */
@@ -219,6 +220,15 @@ int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
  * side effects happen `reps` times (optimizer state moves). */
 int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,
                               uint64_t count);
+/* Timing inside ordinary replays: the program's graph is split at `indices`
+ * (rebuilt on next run); each marked launch runs between graph segments on
+ * the engine stream, bracketed by HIP events. seeml_hip_marked_times returns
+ * each marked launch's duration (ms) in the latest completed replay, in
+ * ascending index order. Marked AdamW steps are left out of multi-tensor
+ * fusion. count = 0 removes the marks. */
+int seeml_hip_mark_timed(seeml_hip_engine* e, int program, const uint64_t* indices,
+                         uint64_t count);
+int seeml_hip_marked_times(seeml_hip_engine* e, int program, float* ms_out, uint64_t count);
 /* Mean duration (ms) of one instruction's launch sequence, relaunched
  * `reps` times between two events on the engine stream. */
 int seeml_hip_time_instruction(seeml_hip_engine* e, int program, uint64_t index, int reps,
@@ -246,6 +256,8 @@ int seeml_hip_gemm_nt_q8(const float* A, const int8_t* B, float* C, uint64_t M, 
 int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, uint64_t M,
                           uint64_t N, uint64_t K, int cfg, int splits, void* stream);
 int seeml_hip_gemm_config_count(void);
+/* Name of tile config `cfg` ("MTMxMTNxKT/wWMxWN"), "?" when out of range. */
+const char* seeml_hip_gemm_config_name(int cfg);
 
 int seeml_hip_add_ew(const float* x, const float* y, float* out, uint64_t n, void* stream);
 int seeml_hip_mul_ew(const float* x, const float* y, float* out, uint64_t n, void* stream);

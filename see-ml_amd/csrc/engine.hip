@@ -62,6 +62,11 @@ bool IsGemmOp(uint16_t op) {
 // ---- UCB1 bandit (compiler/backend/tuner/bandit.cc:14-53) -----------------
 // Deterministic: untried arms first in index order, score ties to the lowest
 // index, no RNG.
+// Autotune picks resolve ties inside this relative band to the lowest arm
+// (the planner's hint first, then the fixed config order).
+constexpr double kAutotuneTolerance = 0.03;
+constexpr double kPeakFp32MfmaFlops = 157.3e12;  // MI355X dense fp32 matrix peak
+
 class Ucb1 {
  public:
   explicit Ucb1(size_t arms, double c = 1.0) : pulls_(arms, 0), mean_(arms, 0.0), c_(c) {}
@@ -86,10 +91,14 @@ class Ucb1 {
     ++total_;
     mean_[arm] += (reward - mean_[arm]) / static_cast<double>(pulls_[arm]);
   }
-  size_t Best() const {
+  // The lowest-index pulled arm whose mean is within `tol` (relative) of the
+  // best mean: arms closer than timing noise resolve the same way every run.
+  size_t Best(double tol = 0.0) const {
     size_t best = 0;
     for (size_t i = 1; i < pulls_.size(); ++i)
       if (pulls_[i] > 0 && (pulls_[best] == 0 || mean_[i] > mean_[best])) best = i;
+    for (size_t i = 0; i < best; ++i)
+      if (pulls_[i] > 0 && mean_[i] >= (1.0 - tol) * mean_[best]) return i;
     return best;
   }
 
@@ -306,17 +315,24 @@ class Engine {
   }
 
   void DropGraph(int p) {
-    if (exec_[p]) (void)hipGraphExecDestroy(exec_[p]);
-    if (graph_[p]) (void)hipGraphDestroy(graph_[p]);
-    exec_[p] = nullptr;
-    graph_[p] = nullptr;
+    for (Segment& g : segs_[p]) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    segs_[p].clear();
     built_[p] = false;
   }
 
   Status RunEager(int program) {
     const Ctx c = MakeCtx();
-    for (size_t i = 0; i < plan_.program[program].size(); ++i)
+    size_t k = 0;
+    const auto& marks = marked_[program];
+    for (size_t i = 0; i < plan_.program[program].size(); ++i) {
+      const bool timed = k < marks.size() && marks[k] == i;
+      if (timed) (void)hipEventRecord(mark_ev_[program][2 * k], stream_);
       if (Status s = Dispatch(program, i, c); !s) return s;
+      if (timed) (void)hipEventRecord(mark_ev_[program][2 * k++ + 1], stream_);
+    }
     return Status::Ok();
   }
 
@@ -350,7 +366,8 @@ class Engine {
       size_t j = i;
       // [begin, end) byte ranges of every operand in the run; writes are p, m, v.
       std::vector<std::pair<uint64_t, uint64_t>> ranges;
-      while (j < prog.size() && static_cast<Op>(prog[j].opcode) == Op::kAdamWStep) {
+      while (j < prog.size() && static_cast<Op>(prog[j].opcode) == Op::kAdamWStep &&
+             !std::binary_search(marked_[program].begin(), marked_[program].end(), j)) {
         const UpdateInstruction& a = prog[j];
         const uint64_t bytes = a.out[0] * sizeof(float);
         bool clash = false;
@@ -391,14 +408,15 @@ class Engine {
                  "fused AdamW table upload");
   }
 
-  // The captured launch sequence: instructions in plan order, fused AdamW
-  // runs as one launch each.
-  Status RunFused(int program) {
+  // The captured launch sequence of instructions [begin, end): plan order,
+  // fused AdamW runs (wholly inside the range) as one launch each.
+  Status RunFused(int program, size_t begin, size_t end) {
     const Ctx c = MakeCtx();
-    size_t r = 0;
     const auto& runs = fused_runs_[program];
-    for (size_t i = 0; i < plan_.program[program].size();) {
-      if (r < runs.size() && runs[r].first == i) {
+    size_t r = 0;
+    while (r < runs.size() && runs[r].first < begin) ++r;
+    for (size_t i = begin; i < end;) {
+      if (r < runs.size() && runs[r].first == i && i + runs[r].count <= end) {
         if (Status s = AdamWMulti(fused_segs_[program] + runs[r].seg_offset, runs[r].count,
                                   runs[r].blocks, c);
             !s)
@@ -413,6 +431,73 @@ class Engine {
     return Status::Ok();
   }
 
+  // Timing inside ordinary replays: the program's graph is split at the
+  // marked instructions; each marked launch runs between graph segments on
+  // the engine stream, bracketed by HIP events, so its duration is measured
+  // in the bench's timed steps rather than in a separate relaunch loop.
+  // Marked AdamW instructions are left out of multi-tensor fusion.
+  Status MarkTimed(int program, const uint64_t* idx, size_t n) {
+    if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    std::vector<size_t> v;
+    for (size_t j = 0; j < n; ++j) {
+      if (idx[j] >= plan_.program[program].size())
+        return Status::Fail(kUnitEngine, "timed instruction index out of range");
+      v.push_back(idx[j]);
+    }
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+    if (Status s = HipOk(hipStreamSynchronize(stream_), "mark sync"); !s) return s;
+    for (hipEvent_t e : mark_ev_[program]) (void)hipEventDestroy(e);
+    mark_ev_[program].clear();
+    marked_[program] = v;
+    for (size_t j = 0; j < 2 * v.size(); ++j) {
+      hipEvent_t e = nullptr;
+      if (Status s = HipOk(hipEventCreate(&e), "timing event"); !s) return s;
+      mark_ev_[program].push_back(e);
+    }
+    DropGraph(program);  // rebuilt with the event nodes on next use
+    return Status::Ok();
+  }
+
+  // Durations (ms) of the marked launches in the most recent completed replay.
+  Status MarkedTimes(int program, float* ms, size_t n) {
+    if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    if (n < marked_[program].size()) return Status::Fail(kUnitEngine, "timing output too small");
+    for (size_t k = 0; k < marked_[program].size(); ++k) {
+      float t = 0.0f;
+      if (Status s = HipOk(hipEventElapsedTime(&t, mark_ev_[program][2 * k],
+                                               mark_ev_[program][2 * k + 1]),
+                           "timing read");
+          !s)
+        return s;
+      ms[k] = t;
+    }
+    return Status::Ok();
+  }
+
+  // Captures instructions [begin, end) as one graph segment.
+  Status Capture(int program, size_t begin, size_t end) {
+    if (Status s = HipOk(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
+                         "graph capture begin");
+        !s)
+      return s;
+    Status launched = RunFused(program, begin, end);
+    hipGraph_t g = nullptr;
+    const hipError_t stop = hipStreamEndCapture(stream_, &g);
+    if (!launched) {
+      if (g) (void)hipGraphDestroy(g);
+      return launched;
+    }
+    if (Status s = HipOk(stop, "graph capture end"); !s) return s;
+    Segment seg;
+    seg.graph = g;
+    seg.first = begin;
+    seg.count = end - begin;
+    segs_[program].push_back(seg);
+    return HipOk(hipGraphInstantiate(&segs_[program].back().exec, g, nullptr, nullptr, 0),
+                 "graph instantiate");
+  }
+
   Status Build(int program) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     if (Status s = EnsureWorkspace(program); !s) return s;
@@ -422,23 +507,23 @@ class Engine {
       return Status::Ok();
     }
     if (Status s = PlanFusion(program); !s) return s;
-    if (Status s = HipOk(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
-                         "graph capture begin");
-        !s)
-      return s;
-    Status launched = RunFused(program);
-    hipGraph_t g = nullptr;
-    const hipError_t end = hipStreamEndCapture(stream_, &g);
-    if (!launched) {
-      if (g) (void)hipGraphDestroy(g);
-      return launched;
+    // One graph for the whole program; with marked instructions, one graph
+    // per unmarked stretch and each marked launch between them.
+    const size_t n = plan_.program[program].size();
+    size_t begin = 0;
+    for (size_t k = 0; k <= marked_[program].size(); ++k) {
+      const size_t end = k < marked_[program].size() ? marked_[program][k] : n;
+      if (end > begin)
+        if (Status s = Capture(program, begin, end); !s) return s;
+      if (k < marked_[program].size()) {
+        Segment seg;
+        seg.first = end;
+        seg.count = 1;
+        seg.mark = static_cast<long>(k);
+        segs_[program].push_back(seg);
+        begin = end + 1;
+      }
     }
-    if (Status s = HipOk(end, "graph capture end"); !s) return s;
-    graph_[program] = g;
-    if (Status s = HipOk(hipGraphInstantiate(&exec_[program], g, nullptr, nullptr, 0),
-                         "graph instantiate");
-        !s)
-      return s;
     built_[program] = true;
     return Status::Ok();
   }
@@ -448,8 +533,18 @@ class Engine {
     if (!built_[program])
       if (Status s = Build(program); !s) return s;
     if (plan_.program[program].empty()) return Status::Ok();
-    if (use_graph_) return HipOk(hipGraphLaunch(exec_[program], stream_), "graph launch");
-    return RunEager(program);
+    if (!use_graph_) return RunEager(program);
+    const Ctx c = MakeCtx();
+    for (const Segment& g : segs_[program]) {
+      if (g.mark < 0) {
+        if (Status s = HipOk(hipGraphLaunch(g.exec, stream_), "graph launch"); !s) return s;
+        continue;
+      }
+      (void)hipEventRecord(mark_ev_[program][2 * g.mark], stream_);
+      if (Status s = Dispatch(program, g.first, c); !s) return s;
+      (void)hipEventRecord(mark_ev_[program][2 * g.mark + 1], stream_);
+    }
+    return Status::Ok();
   }
 
   Status SetStep(uint64_t step) {
@@ -577,6 +672,11 @@ class Engine {
   Status EnsureArgmaxBuffers(uint64_t rows) {
     const size_t need = ArgmaxPartials(rows);
     if (need <= argmax_cap_ && d_argmax_) return Status::Ok();
+    for (int p = 0; p < 3; ++p) {
+      for (hipEvent_t ev : mark_ev_[p]) (void)hipEventDestroy(ev);
+      mark_ev_[p].clear();
+      marked_[p].clear();
+    }
     if (d_argmax_) (void)hipFree(d_argmax_);
     d_argmax_ = nullptr;
     argmax_cap_ = 0;
@@ -787,8 +887,10 @@ class Engine {
       for (const auto& a : arms)  // one untimed warm-up launch per arm
         if (Status s = LaunchGemm(d, a, c); !s) { result = s; break; }
       if (!result) break;
+      // Rewards are the fraction of fp32 MFMA peak (UCB1's [0, 1] scale);
+      // every arm is pulled at least twice.
       Ucb1 bandit(arms.size());
-      const int trials = std::max<int>(budget, static_cast<int>(arms.size()));
+      const int trials = std::max<int>(budget, 2 * static_cast<int>(arms.size()));
       for (int t = 0; t < trials; ++t) {
         const size_t arm = bandit.Select();
         (void)hipEventRecord(t0, stream_);
@@ -797,10 +899,10 @@ class Engine {
         (void)hipEventSynchronize(t1);
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, t0, t1);
-        bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / 1e9 : 0.0);
+        bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
       }
       if (!result) break;
-      const GemmPlan best = arms[bandit.Best()];
+      const GemmPlan best = arms[bandit.Best(kAutotuneTolerance)];
       for (size_t i : idxs) plans_[program][i] = best;
     }
     (void)hipEventDestroy(t0);
@@ -909,14 +1011,21 @@ class Engine {
   size_t ws_bytes_ = 0;
   StepScalars* d_scalars_ = nullptr;
   AdamWSegment* fused_segs_[3] = {nullptr, nullptr, nullptr};
+  std::vector<size_t> marked_[3];
+  std::vector<hipEvent_t> mark_ev_[3];
   uint8_t* d_argmax_ = nullptr;
   size_t argmax_cap_ = 0;
   uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;
-  hipGraph_t graph_[3] = {nullptr, nullptr, nullptr};
-  hipGraphExec_t exec_[3] = {nullptr, nullptr, nullptr};
+  struct Segment {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    size_t first = 0, count = 0;
+    long mark = -1;  // >= 0: a marked launch, run eagerly between segments
+  };
+  std::vector<Segment> segs_[3];
   bool built_[3] = {false, false, false};
   bool use_graph_ = true;
   uint64_t step_ = 0;
@@ -1137,6 +1246,15 @@ int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float*
   return Ret(e, e->impl.Profile(program, reps, ms_out, count));
 }
 
+int seeml_hip_mark_timed(seeml_hip_engine* e, int program, const uint64_t* indices,
+                         uint64_t count) {
+  return Ret(e, e->impl.MarkTimed(program, indices, count));
+}
+
+int seeml_hip_marked_times(seeml_hip_engine* e, int program, float* ms_out, uint64_t count) {
+  return Ret(e, e->impl.MarkedTimes(program, ms_out, count));
+}
+
 int seeml_hip_time_instruction(seeml_hip_engine* e, int program, uint64_t index, int reps,
                                float* avg_ms) {
   return Ret(e, e->impl.TimeInstruction(program, index, reps, avg_ms));
@@ -1208,6 +1326,7 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
   return RunGemm(d, stream, cfg, splits);
 }
 int seeml_hip_gemm_config_count(void) { return seeml_hip::GemmConfigCount(); }
+const char* seeml_hip_gemm_config_name(int cfg) { return seeml_hip::GemmConfigName(cfg); }
 
 #define SEEML_SIMPLE(call) \
   SEEML_CTX(0);            \

@@ -168,6 +168,21 @@ class DeviceUpdateEngine:
                     "profile")
         return out[:n]
 
+    def mark_timed(self, program: int, indices) -> None:
+        """Event-record nodes around these instructions in the program's
+        graph: ordinary replays then time them (marked_times)."""
+        idx = np.ascontiguousarray(sorted(set(int(i) for i in indices)), np.uint64)
+        self._check(self._L.seeml_hip_mark_timed(self._h, program, idx.ctypes.data, idx.size),
+                    "mark_timed")
+        self._marked = idx.size
+
+    def marked_times(self, program: int = PROGRAM_TRAIN) -> np.ndarray:
+        """ms of each marked launch in the latest completed replay."""
+        out = np.zeros(max(getattr(self, "_marked", 0), 1), np.float32)
+        self._check(self._L.seeml_hip_marked_times(self._h, program, out.ctypes.data, out.size),
+                    "marked_times")
+        return out[:getattr(self, "_marked", 0)]
+
     def time_instruction(self, program: int, index: int, reps: int = 10) -> float:
         out = C.c_float()
         self._check(self._L.seeml_hip_time_instruction(self._h, program, index, reps, C.byref(out)),

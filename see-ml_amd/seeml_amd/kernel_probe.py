@@ -1,0 +1,67 @@
+"""Launches one backend GEMM (a bench workload's dominant kernel) and a
+plain copy of known size, for hardware-counter runs under rocprofv3:
+
+  python3 -m seeml_amd.kernel_probe --layout NN --m 8192 --n 5504 --k 2048 \\
+      --cfg 128x64x32/w4x1 --reps 3 --copy-mib 1024
+
+Each dispatch's FETCH_SIZE / WRITE_SIZE (KiB) is read from the profiler's
+counter file; the copy's counters against its known 2 x copy-mib MiB of
+traffic calibrate the GEMM's. Inputs are seeded normals in device memory.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import sys
+
+LAYOUTS = {"NN": 0, "NT": 1, "TN": 2}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--layout", default="NN", choices=sorted(LAYOUTS))
+    ap.add_argument("--m", type=int, required=True)
+    ap.add_argument("--n", type=int, required=True)
+    ap.add_argument("--k", type=int, required=True)
+    ap.add_argument("--cfg", required=True, help="tile config name, e.g. 128x64x32/w4x1")
+    ap.add_argument("--splits", type=int, default=1)
+    ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=1024)
+    a = ap.parse_args(argv)
+
+    import torch
+    from . import _lib
+
+    L = _lib.lib()
+    names = {}
+    for i in range(L.seeml_hip_gemm_config_count()):
+        names[L.seeml_hip_gemm_config_name(i).decode()] = i
+    if a.cfg not in names:
+        sys.exit(f"kernel_probe: unknown tile config {a.cfg!r}; have {sorted(names)}")
+    cfg = names[a.cfg]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    M, N, K = a.m, a.n, a.k
+    A = torch.randn(M * K, device=dev, generator=g)
+    B = torch.randn(K * N, device=dev, generator=g)
+    Cm = torch.empty(M * N, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(a.reps):
+        rc = L.seeml_hip_gemm_forced(LAYOUTS[a.layout], A.data_ptr(), B.data_ptr(), Cm.data_ptr(),
+                                     M, N, K, cfg, a.splits, s)
+        if rc != 0:
+            sys.exit(f"kernel_probe: {_lib.kernel_error()}")
+    n = a.copy_mib * (1 << 20) // 4
+    x = torch.randn(n, device=dev, generator=g)
+    y = torch.empty(n, device=dev)
+    for _ in range(a.reps):
+        rc = L.seeml_hip_copy(x.data_ptr(), y.data_ptr(), n, s)
+        if rc != 0:
+            sys.exit(f"kernel_probe: {_lib.kernel_error()}")
+    torch.cuda.synchronize()
+    print(f"kernel_probe: {a.layout} {M}x{N}x{K} {a.cfg} x{a.reps}, copy {a.copy_mib} MiB x{a.reps}",
+          flush=True)
+
+
+if __name__ == "__main__":
+    main()

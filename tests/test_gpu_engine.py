@@ -102,6 +102,32 @@ def test_bitwise_determinism_and_graph_equals_eager(torch_gpu, name):
         assert np.array_equal(st.view(np.uint32), runs[0][1].view(np.uint32))
 
 
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_in_graph_timing_is_transparent(torch_gpu, use_graph):
+    # Event nodes around marked launches (the bench's live roofline timing)
+    # change no result bit and time every marked launch, fused AdamW included.
+    w, p = compile_workload("c3s")
+    ops = [i["opcode"] for i in p.train]
+    from seeml_amd.planner import OP
+    marks = [i for i, o in enumerate(ops) if o in (OP["GemmNN"], OP["AdamWStep"])]
+    runs = []
+    for mark in (False, True):
+        e = engine(p, use_graph=use_graph)
+        if mark:
+            e.mark_timed(0, marks)
+        losses = []
+        for s in range(3):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+            if mark:
+                t = e.marked_times(0)
+                assert t.shape == (len(marks),) and np.all(t > 0)
+        runs.append((np.array(losses, np.float32), persistent(e, p)))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+
+
 def test_non_finite_loss_aborts_the_update(torch_gpu):
     """A NaN poked into a LoRA A (the reference probes the arena the same
     way, update_engine_test.cc:788-809) reaches the loss through RMSNorm /
