@@ -912,29 +912,62 @@ class Engine {
     return HipOk(hipStreamSynchronize(stream_), "autotune");
   }
 
+  // Per-instruction durations (ms, mean over reps) from an eager pass with a
+  // HIP event after every launch. A fused AdamW run is timed as the one
+  // launch the graph makes, its time split over the run's instructions by
+  // element count.
   Status Profile(int program, int reps, float* ms_out, size_t count) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     const size_t n = plan_.program[program].size();
     if (count < n) return Status::Fail(kUnitEngine, "profile output too small");
     if (Status s = EnsureWorkspace(program); !s) return s;
+    if (use_graph_ && !built_[program])
+      if (Status s = Build(program); !s) return s;
+    const auto& prog = plan_.program[program];
     std::vector<hipEvent_t> ev(n + 1);
     for (auto& e : ev)
       if (Status s = HipOk(hipEventCreate(&e), "event"); !s) return s;
     std::vector<double> acc(n, 0.0);
     const Ctx c = MakeCtx();
+    const auto& runs = use_graph_ ? fused_runs_[program] : std::vector<FusedRun>{};
     Status result = Status::Ok();
     for (int r = 0; r < reps && result; ++r) {
       (void)hipEventRecord(ev[0], stream_);
-      for (size_t i = 0; i < n; ++i) {
+      size_t fr = 0;
+      for (size_t i = 0; i < n;) {
+        if (fr < runs.size() && runs[fr].first == i) {
+          if (Status s = AdamWMulti(fused_segs_[program] + runs[fr].seg_offset, runs[fr].count,
+                                    runs[fr].blocks, c);
+              !s) {
+            result = s;
+            break;
+          }
+          i += runs[fr++].count;
+          (void)hipEventRecord(ev[i], stream_);
+          continue;
+        }
         if (Status s = Dispatch(program, i, c); !s) { result = s; break; }
-        (void)hipEventRecord(ev[i + 1], stream_);
+        (void)hipEventRecord(ev[++i], stream_);
       }
       if (!result) break;
       if (Status s = HipOk(hipEventSynchronize(ev[n]), "profile sync"); !s) { result = s; break; }
-      for (size_t i = 0; i < n; ++i) {
+      fr = 0;
+      for (size_t i = 0; i < n;) {
+        if (fr < runs.size() && runs[fr].first == i) {
+          const FusedRun& run = runs[fr++];
+          float ms = 0.0f;
+          (void)hipEventElapsedTime(&ms, ev[i], ev[i + run.count]);
+          double elems = 0.0;
+          for (size_t k = i; k < i + run.count; ++k) elems += static_cast<double>(prog[k].out[0]);
+          for (size_t k = i; k < i + run.count; ++k)
+            acc[k] += elems > 0.0 ? ms * static_cast<double>(prog[k].out[0]) / elems : 0.0;
+          i += run.count;
+          continue;
+        }
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
         acc[i] += ms;
+        ++i;
       }
     }
     for (auto& e : ev) (void)hipEventDestroy(e);

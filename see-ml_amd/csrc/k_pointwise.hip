@@ -189,20 +189,42 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(const float* __rest
 }
 
 // dlogits = (seed/N) * probs, minus seed/N at the label (loss.cc:61-72).
+// Row-structured: blockIdx.y strides over rows, so no per-element index
+// division; 16-byte rows (C % 4 == 0, aligned) stream as float4.
 __global__ __launch_bounds__(kBlock) void xent_bwd_kernel(const float* __restrict__ probs,
                                                           const int32_t* __restrict__ labels,
                                                           const float* __restrict__ seed,
                                                           float* __restrict__ dl, size_t N,
-                                                          size_t C) {
+                                                          size_t C, int vec) {
   const float scale = *seed / static_cast<float>(N);
-  const size_t total = N * C;
-  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
-    const size_t n = i / C, c = i - n * C;
-    float v = scale * probs[i];
+  const size_t cstride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t c0 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  for (size_t n = blockIdx.y; n < N; n += gridDim.y) {
     const int32_t lab = labels[n];
-    if (lab >= 0 && static_cast<size_t>(lab) == c) v -= scale;
-    dl[i] = v;
+    const size_t lc = lab >= 0 ? static_cast<size_t>(lab) : ~size_t{0};
+    if (vec) {
+      const float4* p4 = reinterpret_cast<const float4*>(probs + n * C);
+      float4* d4 = reinterpret_cast<float4*>(dl + n * C);
+      for (size_t j = c0; j < C / 4; j += cstride) {
+        const float4 p = p4[j];
+        float4 o = make_float4(scale * p.x, scale * p.y, scale * p.z, scale * p.w);
+        if (lc / 4 == j) {
+          if (lc % 4 == 0) o.x -= scale;
+          else if (lc % 4 == 1) o.y -= scale;
+          else if (lc % 4 == 2) o.z -= scale;
+          else o.w -= scale;
+        }
+        d4[j] = o;
+      }
+    } else {
+      const float* pr = probs + n * C;
+      float* dr = dl + n * C;
+      for (size_t cc = c0; cc < C; cc += cstride) {
+        float v = scale * pr[cc];
+        if (lc == cc) v -= scale;
+        dr[cc] = v;
+      }
+    }
   }
 }
 
@@ -344,33 +366,40 @@ __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const AdamWSegment*
 // multiplications in float, so freq_c has the CPU's bits); cos/sin are the
 // device's accurate cosf/sinf. Rows are [B*S] x [H*d]; s = row % S.
 //
-// Fast form (d % 4 == 0, 16-byte aligned rows): each workgroup builds the
-// d/2 frequencies once in LDS and streams whole rows as float4 = 2 pairs.
-constexpr int kRopeMaxHalf = 1024;
+// Fast form (d % 4 == 0, d/2 <= kRopeTable, 16-byte aligned rows): the
+// angle depends on (position, pair) only, not on the head, so a workgroup
+// owning R consecutive rows first evaluates cos/sin of their R * d/2 angles
+// once into LDS (the same float expressions, so the same bits), then
+// streams the rows' H heads as float4 = 2 pairs.
+constexpr int kRopeTable = 256;
 
 template <int DIR>
 __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restrict__ x,
                                                            float* __restrict__ y, uint32_t rows,
                                                            uint32_t S, uint32_t width,
-                                                           uint32_t d, float step) {
-  __shared__ float freq[kRopeMaxHalf];
+                                                           uint32_t d, uint32_t rpb, float step) {
+  __shared__ float2 cs[kRopeTable];
   const uint32_t half_d = d / 2;
-  for (uint32_t c = threadIdx.x; c < half_d; c += kBlock) {
+  const uint32_t row0 = blockIdx.x * rpb;
+  const uint32_t nrow = rows - row0 < rpb ? rows - row0 : rpb;
+  for (uint32_t e = threadIdx.x; e < nrow * half_d; e += kBlock) {
+    const uint32_t c = e % half_d, r = e / half_d;
     float f = 1.0f;
     for (uint32_t i = 0; i < c; ++i) f *= step;
-    freq[c] = f;
+    const float theta = static_cast<float>((row0 + r) % S) * f;
+    cs[e] = make_float2(cosf(theta), sinf(theta));
   }
   __syncthreads();
   const uint32_t nv = width / 4;
-  for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const float fs = static_cast<float>(row % S);
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * width);
-    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * width);
+  for (uint32_t r = 0; r < nrow; ++r) {
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row0 + r) * width);
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row0 + r) * width);
+    const float2* tr = cs + r * half_d;
     for (uint32_t j = threadIdx.x; j < nv; j += kBlock) {
       const uint32_t c2 = ((4 * j) % d) / 2;
       const float4 v = xr[j];
-      const float t0 = fs * freq[c2], t1 = fs * freq[c2 + 1];
-      const float c0 = cosf(t0), s0 = sinf(t0), c1 = cosf(t1), s1 = sinf(t1);
+      const float2 a = tr[c2], b = tr[c2 + 1];
+      const float c0 = a.x, s0 = a.y, c1 = b.x, s1 = b.y;
       float4 o;
       if constexpr (DIR > 0) {
         o.x = v.x * c0 - v.y * s0;
@@ -421,18 +450,19 @@ Status Rope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, fl
   // step = base^(-2/d) evaluated on the host with the reference's powf.
   const float step = ::powf(base, -2.0f / static_cast<float>(d));
   const size_t rows = B * S, width = H * d;
-  const bool fast = d % 4 == 0 && d / 2 <= static_cast<size_t>(kRopeMaxHalf) && aligned16(x) &&
+  const bool fast = d % 4 == 0 && d / 2 <= static_cast<size_t>(kRopeTable) && aligned16(x) &&
                     aligned16(y) && rows <= 0xFFFFFFFFu && width <= 0xFFFFFFFFu && S > 0;
   if (fast) {
-    const unsigned grid = static_cast<unsigned>(std::min<size_t>(rows, 4096));
+    const uint32_t rpb = static_cast<uint32_t>(kRopeTable / (d / 2));
+    const unsigned grid = static_cast<unsigned>((rows + rpb - 1) / rpb);
     if (dir > 0)
       hipLaunchKernelGGL(rope_rows_kernel<1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
                          static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
-                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), step);
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step);
     else
       hipLaunchKernelGGL(rope_rows_kernel<-1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
                          static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
-                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), step);
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step);
   } else {
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, kBlock, kGridCap)), dim3(kBlock), 0,
                        c.stream, x, y, pairs, S, H, d / 2, step, dir);
@@ -510,9 +540,15 @@ Status ReduceRows(const float* dy, float* db, size_t rows, size_t cols, const Ct
 
 Status SoftmaxXEntBwd(const float* probs, const int32_t* labels, const float* seed,
                       float* dlogits, size_t N, size_t C, const Ctx& c) {
-  if (N * C == 0) return Status::Ok();
-  hipLaunchKernelGGL(xent_bwd_kernel, dim3(grid_for(N * C, kBlock, kGridCap)), dim3(kBlock), 0,
-                     c.stream, probs, labels, seed, dlogits, N, C);
+  if (N == 0 || C == 0) return Status::Ok();
+  const bool vec = C % 4 == 0 && aligned16(probs) && aligned16(dlogits);
+  const size_t per_row = vec ? C / 4 : C;
+  // Columns: enough blocks to cover a row in ~4 passes; rows: up to 65535
+  // per grid row, striding beyond.
+  const unsigned gx = std::max(1u, grid_for((per_row + 3) / 4, kBlock, 64));
+  const unsigned gy = static_cast<unsigned>(std::min<size_t>(N, 65535));
+  hipLaunchKernelGGL(xent_bwd_kernel, dim3(gx, gy), dim3(kBlock), 0, c.stream, probs, labels,
+                     seed, dlogits, N, C, vec ? 1 : 0);
   return LaunchStatus("SoftmaxXEntBwd");
 }
 

@@ -15,6 +15,8 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <initializer_list>
+
 namespace seeml_hip {
 
 namespace {
@@ -380,6 +382,254 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_kernel(
   for (size_t c = t; c < cols; c += TPR) dsr[c] = pr[c] * (dpr[c] - sum);
 }
 
+// ---- register-resident rows -------------------------------------------------
+//
+// For 16-byte aligned rows with cols % 4 == 0 and cols <= TPR * 4 * V: TPR
+// threads own one row, thread t holding float4s t, t + TPR, ... (V of them,
+// zero past the row's end), so each input row is read from HBM once and each
+// output row written once, all as 16-byte accesses. A row reduction's
+// per-thread partial runs over the thread's own elements in ascending order
+// (zero padding adds exact zeros), then the fixed wave/block tree: the same
+// bits on every run. Expressions per element are the strided kernels' above.
+
+template <int TPR, int V>
+__device__ __forceinline__ void load_row(const float* __restrict__ row, int nv, int t,
+                                         float4 (&v)[V]) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    v[i] = j < nv ? r4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
+template <int TPR, int V>
+__device__ __forceinline__ void store_row(float* __restrict__ row, int nv, int t,
+                                          const float4 (&v)[V]) {
+  float4* r4 = reinterpret_cast<float4*>(row);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    if (j < nv) r4[j] = v[i];
+  }
+}
+
+// Row index and lane of this thread; false past the last row (uniform per
+// row group, and per block when TPR == kBlock).
+template <int TPR>
+__device__ __forceinline__ bool row_of(size_t rows, size_t* r, int* t) {
+  *t = static_cast<int>(threadIdx.x % TPR);
+  *r = static_cast<size_t>(blockIdx.x) * (kBlock / TPR) + threadIdx.x / TPR;
+  return *r < rows;
+}
+
+__device__ __forceinline__ double sq4(float4 a) {
+  double s = static_cast<double>(a.x) * static_cast<double>(a.x);
+  s += static_cast<double>(a.y) * static_cast<double>(a.y);
+  s += static_cast<double>(a.z) * static_cast<double>(a.z);
+  s += static_cast<double>(a.w) * static_cast<double>(a.w);
+  return s;
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restrict__ x,
+                                                           const float* __restrict__ gamma,
+                                                           float* __restrict__ y,
+                                                           float* __restrict__ rstd, size_t rows,
+                                                           int cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 xv[V];
+  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) s += sq4(xv[i]);
+  const double ss = row_sum_d<TPR>(s, dscratch);
+  const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f);
+  if (t == 0) rstd[r] = rs;
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    if (j < nv) {
+      const float4 g = g4[j];
+      xv[i] = make_float4(xv[i].x * rs * g.x, xv[i].y * rs * g.y, xv[i].z * rs * g.z,
+                          xv[i].w * rs * g.w);
+    }
+  }
+  store_row<TPR, V>(y + r * cols, nv, t, xv);
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, int cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  float4 gv[V], xv[V];
+  load_row<TPR, V>(dy + r * cols, nv, t, gv);
+  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    const float4 g = j < nv ? g4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    gv[i] = make_float4(gv[i].x * g.x, gv[i].y * g.y, gv[i].z * g.z, gv[i].w * g.w);
+    s += static_cast<double>(gv[i].x) * static_cast<double>(xv[i].x);
+    s += static_cast<double>(gv[i].y) * static_cast<double>(xv[i].y);
+    s += static_cast<double>(gv[i].z) * static_cast<double>(xv[i].z);
+    s += static_cast<double>(gv[i].w) * static_cast<double>(xv[i].w);
+  }
+  const float mgx = static_cast<float>(row_sum_d<TPR>(s, dscratch)) * inv_d;
+  const float rs = rstd[r];
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    gv[i] = make_float4(rs * (gv[i].x - xv[i].x * rs * rs * mgx),
+                        rs * (gv[i].y - xv[i].y * rs * rs * mgx),
+                        rs * (gv[i].z - xv[i].z * rs * rs * mgx),
+                        rs * (gv[i].w - xv[i].w * rs * rs * mgx));
+  store_row<TPR, V>(dx + r * cols, nv, t, gv);
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, size_t rows,
+    int cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 xv[V];
+  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    s += static_cast<double>(xv[i].x);
+    s += static_cast<double>(xv[i].y);
+    s += static_cast<double>(xv[i].z);
+    s += static_cast<double>(xv[i].w);
+  }
+  const double sum = row_sum_d<TPR>(s, dscratch);
+  const float mu = static_cast<float>(sum / static_cast<double>(cols));
+  const double dmu = static_cast<double>(mu);
+  double v = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (t + i * TPR < nv) {
+      const double d0 = static_cast<double>(xv[i].x) - dmu, d1 = static_cast<double>(xv[i].y) - dmu;
+      const double d2 = static_cast<double>(xv[i].z) - dmu, d3 = static_cast<double>(xv[i].w) - dmu;
+      v += d0 * d0;
+      v += d1 * d1;
+      v += d2 * d2;
+      v += d3 * d3;
+    }
+  }
+  const double var = row_sum_d<TPR>(v, dscratch);
+  const float rs = 1.0f / sqrtf(static_cast<float>(var / static_cast<double>(cols)) + 1e-5f);
+  if (t == 0) {
+    mean[r] = mu;
+    rstd[r] = rs;
+  }
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    if (j < nv) {
+      const float4 g = g4[j], b = b4[j];
+      xv[i] = make_float4((xv[i].x - mu) * rs * g.x + b.x, (xv[i].y - mu) * rs * g.y + b.y,
+                          (xv[i].z - mu) * rs * g.z + b.z, (xv[i].w - mu) * rs * g.w + b.w);
+    }
+  }
+  store_row<TPR, V>(y + r * cols, nv, t, xv);
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, float* __restrict__ dx,
+    size_t rows, int cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float inv_d = 1.0f / static_cast<float>(cols);
+  const float mu = mean[r], rs = rstd[r];
+  float4 gv[V], xv[V];
+  load_row<TPR, V>(dy + r * cols, nv, t, gv);
+  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  double sg = 0.0, sgx = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    if (j < nv) {
+      const float4 g = g4[j];
+      // xv becomes x-hat, gv becomes g = dy * gamma.
+      xv[i] = make_float4((xv[i].x - mu) * rs, (xv[i].y - mu) * rs, (xv[i].z - mu) * rs,
+                          (xv[i].w - mu) * rs);
+      gv[i] = make_float4(gv[i].x * g.x, gv[i].y * g.y, gv[i].z * g.z, gv[i].w * g.w);
+      sg += static_cast<double>(gv[i].x);
+      sgx += static_cast<double>(gv[i].x) * static_cast<double>(xv[i].x);
+      sg += static_cast<double>(gv[i].y);
+      sgx += static_cast<double>(gv[i].y) * static_cast<double>(xv[i].y);
+      sg += static_cast<double>(gv[i].z);
+      sgx += static_cast<double>(gv[i].z) * static_cast<double>(xv[i].z);
+      sg += static_cast<double>(gv[i].w);
+      sgx += static_cast<double>(gv[i].w) * static_cast<double>(xv[i].w);
+    }
+  }
+  const double sum_g = row_sum_d<TPR>(sg, dscratch);
+  const double sum_gx = row_sum_d<TPR>(sgx, dscratch);
+  const float mg = static_cast<float>(sum_g) * inv_d;
+  const float mgx = static_cast<float>(sum_gx) * inv_d;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    gv[i] = make_float4(rs * (gv[i].x - mg - xv[i].x * mgx), rs * (gv[i].y - mg - xv[i].y * mgx),
+                        rs * (gv[i].z - mg - xv[i].z * mgx), rs * (gv[i].w - mg - xv[i].w * mgx));
+  store_row<TPR, V>(dx + r * cols, nv, t, gv);
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __restrict__ p,
+                                                               const float* __restrict__ dp,
+                                                               float* __restrict__ ds,
+                                                               size_t rows, int cols) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 pv[V], dv[V];
+  load_row<TPR, V>(p + r * cols, nv, t, pv);
+  load_row<TPR, V>(dp + r * cols, nv, t, dv);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    s += static_cast<double>(dv[i].x) * static_cast<double>(pv[i].x);
+    s += static_cast<double>(dv[i].y) * static_cast<double>(pv[i].y);
+    s += static_cast<double>(dv[i].z) * static_cast<double>(pv[i].z);
+    s += static_cast<double>(dv[i].w) * static_cast<double>(pv[i].w);
+  }
+  const float sum = static_cast<float>(row_sum_d<TPR>(s, dscratch));
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    dv[i] = make_float4(pv[i].x * (dv[i].x - sum), pv[i].y * (dv[i].y - sum),
+                        pv[i].z * (dv[i].z - sum), pv[i].w * (dv[i].w - sum));
+  store_row<TPR, V>(ds + r * cols, nv, t, dv);
+}
+
 // Causal row softmax in place (attention.cc:106-125): row u = (b, h, i) holds
 // raw scaled scores for j <= i and exact zeros beyond (written by the score
 // GEMM). f32 max over the prefix, e = exp(s - max), denominator in double,
@@ -563,38 +813,96 @@ Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, flo
                          c.stream, __VA_ARGS__);                                               \
   } while (0)
 
+// Register-resident shape for rows of `cols` floats: case 0..3 = (64, 4),
+// (64, 8), (256, 4), (256, 8) threads per row x float4s per thread; -1 when
+// the row is too wide, not a whole number of float4s, or not 16-byte aligned.
+static int RegCase(size_t cols, std::initializer_list<const void*> rows_base) {
+  if (cols == 0 || cols % 4 != 0 || cols > 8192) return -1;
+  for (const void* p : rows_base)
+    if (p && !aligned16(p)) return -1;
+  if (cols <= 1024) return 0;
+  if (cols <= 2048) return 1;
+  if (cols <= 4096) return 2;
+  return 3;
+}
+
+#define REG_DISPATCH(kernel, rcase, rows, ...)                                                  \
+  do {                                                                                         \
+    switch (rcase) {                                                                           \
+      case 0:                                                                                  \
+        hipLaunchKernelGGL((kernel<kWave, 4>), dim3(RowsGrid(rows, kWave)), dim3(kBlock), 0,   \
+                           c.stream, __VA_ARGS__);                                             \
+        break;                                                                                 \
+      case 1:                                                                                  \
+        hipLaunchKernelGGL((kernel<kWave, 8>), dim3(RowsGrid(rows, kWave)), dim3(kBlock), 0,   \
+                           c.stream, __VA_ARGS__);                                             \
+        break;                                                                                 \
+      case 2:                                                                                  \
+        hipLaunchKernelGGL((kernel<kBlock, 4>), dim3(RowsGrid(rows, kBlock)), dim3(kBlock), 0, \
+                           c.stream, __VA_ARGS__);                                             \
+        break;                                                                                 \
+      default:                                                                                 \
+        hipLaunchKernelGGL((kernel<kBlock, 8>), dim3(RowsGrid(rows, kBlock)), dim3(kBlock), 0, \
+                           c.stream, __VA_ARGS__);                                             \
+        break;                                                                                 \
+    }                                                                                          \
+  } while (0)
+
 Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
                     float* rstd, size_t rows, size_t cols, const Ctx& c) {
   if (rows == 0 || cols == 0) return Status::Ok();
-  ROWS_DISPATCH(layer_norm_fwd_rows, rows, cols, x, gamma, beta, y, mean, rstd, rows, cols);
+  const int rc = RegCase(cols, {x, gamma, beta, y});
+  if (rc >= 0)
+    REG_DISPATCH(layer_norm_fwd_reg, rc, rows, x, gamma, beta, y, mean, rstd, rows,
+                 static_cast<int>(cols));
+  else
+    ROWS_DISPATCH(layer_norm_fwd_rows, rows, cols, x, gamma, beta, y, mean, rstd, rows, cols);
   return LaunchStatus("LayerNormFwd");
 }
 
 Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const float* mean,
                     const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c) {
   if (rows == 0 || cols == 0) return Status::Ok();
-  ROWS_DISPATCH(layer_norm_bwd_rows, rows, cols, dy, x, gamma, mean, rstd, dx, rows, cols);
+  const int rc = RegCase(cols, {dy, x, gamma, dx});
+  if (rc >= 0)
+    REG_DISPATCH(layer_norm_bwd_reg, rc, rows, dy, x, gamma, mean, rstd, dx, rows,
+                 static_cast<int>(cols));
+  else
+    ROWS_DISPATCH(layer_norm_bwd_rows, rows, cols, dy, x, gamma, mean, rstd, dx, rows, cols);
   return LaunchStatus("LayerNormBwd");
 }
 
 Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
                   size_t cols, const Ctx& c) {
   if (rows == 0 || cols == 0) return Status::Ok();
-  ROWS_DISPATCH(rms_norm_fwd_rows, rows, cols, x, gamma, y, rstd, rows, cols);
+  const int rc = RegCase(cols, {x, gamma, y});
+  if (rc >= 0)
+    REG_DISPATCH(rms_norm_fwd_reg, rc, rows, x, gamma, y, rstd, rows, static_cast<int>(cols));
+  else
+    ROWS_DISPATCH(rms_norm_fwd_rows, rows, cols, x, gamma, y, rstd, rows, cols);
   return LaunchStatus("RmsNormFwd");
 }
 
 Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
                   float* dx, size_t rows, size_t cols, const Ctx& c) {
   if (rows == 0 || cols == 0) return Status::Ok();
-  ROWS_DISPATCH(rms_norm_bwd_rows, rows, cols, dy, x, gamma, rstd, dx, rows, cols);
+  const int rc = RegCase(cols, {dy, x, gamma, dx});
+  if (rc >= 0)
+    REG_DISPATCH(rms_norm_bwd_reg, rc, rows, dy, x, gamma, rstd, dx, rows,
+                 static_cast<int>(cols));
+  else
+    ROWS_DISPATCH(rms_norm_bwd_rows, rows, cols, dy, x, gamma, rstd, dx, rows, cols);
   return LaunchStatus("RmsNormBwd");
 }
 
 Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
                       const Ctx& c) {
   if (rows == 0 || cols == 0) return Status::Ok();
-  ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
+  const int rc = RegCase(cols, {probs, dp, ds});
+  if (rc >= 0)
+    REG_DISPATCH(softmax_rows_bwd_reg, rc, rows, probs, dp, ds, rows, static_cast<int>(cols));
+  else
+    ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
   return LaunchStatus("SoftmaxRowsBwd");
 }
 

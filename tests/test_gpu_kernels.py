@@ -221,7 +221,11 @@ def test_embed_gather(env, orc):
     assert np.all(np.isnan(h[3])) and same_bits(h[4:], want.reshape(T, D)[4:])
 
 
-@pytest.mark.parametrize("rows,cols", [(257, 300), (64, 2048), (3, 5000)])
+# cols % 4 == 0 up to 8192 (16-byte rows): the register-resident row forms
+# (64 threads x 4 or 8 float4s, 256 threads x 4 or 8); otherwise the strided
+# two-pass rows.
+@pytest.mark.parametrize("rows,cols", [(257, 300), (64, 2048), (3, 5000), (33, 1024), (7, 4096),
+                                       (9, 8192), (5, 8196), (6, 1030)])
 def test_norms(env, orc, rows, cols):
     n = rows * cols
     x, dy, g, b = rnd(n, 60, 2), rnd(n, 61), rnd(cols, 62), rnd(cols, 63)
@@ -249,9 +253,11 @@ def test_norms(env, orc, rows, cols):
     assert rel_err(env.H(tdx), dx) <= 1e-5
 
 
-# d % 4 == 0 and d/2 <= 1024: the row-streaming float4 form; otherwise the
-# per-pair form.
-@pytest.mark.parametrize("B,S,H,d", [(2, 300, 3, 64), (2, 17, 3, 6), (1, 3, 1, 2052)])
+# d % 4 == 0 and d/2 <= 256: the row-streaming float4 form with a per-row
+# angle table (256/(d/2) rows per workgroup); otherwise the per-pair form.
+@pytest.mark.parametrize("B,S,H,d", [(2, 300, 3, 64), (2, 17, 3, 6), (1, 3, 1, 2052),
+                                     (2, 65, 4, 128), (1, 5, 2, 512), (1, 7, 2, 1024),
+                                     (3, 11, 1, 4)])
 def test_rope(env, orc, B, S, H, d):
     n = B * S * H * d
     x = rnd(n, 70)
@@ -307,6 +313,24 @@ def test_attention_family(env, orc, B, S, H, d):
     assert rel_err(env.H(tdk), dk) <= TOL_STEP
     if S == 1:  # S = 1: P is exactly 1 and O copies V (kernels_test.cc:795-805)
         assert np.all(hp == 1.0) and same_bits(env.H(to), v)
+
+
+def test_softmax_rows_bwd_widths(env, orc):
+    """Register-resident rows (cols % 4 == 0 up to 8192) and the strided
+    fallback, against the oracle, with masked-causal-like zero tails."""
+    rng = np.random.default_rng(95)
+    for rows, cols in ((37, 256), (65, 1024), (9, 2048), (5, 4096), (3, 8192), (4, 8200),
+                       (6, 1030)):
+        p = rng.random(rows * cols).astype(f32)
+        p.reshape(rows, cols)[:, cols // 2:] = 0.0
+        dp = rnd(rows * cols, 96)
+        want = np.zeros(rows * cols, f32)
+        orc.softmax_rows_bwd(p, dp, want, rows, cols)
+        out = env.T(np.full(rows * cols, np.nan, f32))
+        env.call("seeml_hip_softmax_rows_bwd", env.T(p), env.T(dp), out, rows, cols)
+        got = env.H(out)
+        assert rel_err(got, want) <= 1e-6, (rows, cols)
+        assert np.all(got.reshape(rows, cols)[:, cols // 2:] == 0.0)
 
 
 # C < 2048: a wave per row; C % 4 == 0 up to 32768: the register-resident row
