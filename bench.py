@@ -170,6 +170,12 @@ def main():
         g[0] += r["ms"]
         g[1].append(i)
     (dom_op, dom_shape, dom_tile), (dom_total, dom_idx) = max(groups.items(), key=lambda kv: kv[1][0])
+    log("top (op, shape, tile) groups by step share:")
+    for (op, shape, tile), (tot, idx) in sorted(groups.items(), key=lambda kv: -kv[1][0])[:20]:
+        r0 = rows[idx[0]]
+        rate = (f"{r0['flops'] * len(idx) / (tot * 1e-3) / 1e12:7.1f} TFLOP/s" if r0["flops"]
+                else f"{r0['bytes'] * len(idx) / (tot * 1e-3) / 1e9:7.0f} GB/s")
+        log(f"  {tot:8.3f} ms  x{len(idx):<4d} {op:15s} {'x'.join(map(str, shape)):22s} {tile:28s} {rate}")
     dom_row = rows[dom_idx[0]]
     # Its launches get event-record nodes in the train graph, timed live in
     # every timed step on the engine stream.

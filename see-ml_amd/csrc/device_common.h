@@ -90,6 +90,33 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
   }
 }
 
+// Streaming 16-byte accesses: non-temporal loads and stores (vector memory
+// instructions with the streaming cache policy). On streams larger than the
+// 256 MiB memory-side cache they give ~20% more HBM throughput than
+// default-policy float4; below that size the default policy wins overall,
+// because it leaves a freshly written tensor in the cache for its consumer
+// (the next GEMM reads it back from there). kStreamBytes is the switch.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream(const float* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream(float* p, float4 v) {
+  const f32x4 t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p));
+}
+
+__device__ __forceinline__ float4 ld4(const float* p, bool nt) {
+  return nt ? ld_stream(p) : *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ void st4(float* p, float4 v, bool nt) {
+  if (nt) st_stream(p, v);
+  else *reinterpret_cast<float4*>(p) = v;
+}
+inline constexpr size_t kStreamBytes = size_t{256} << 20;
+// Streaming policy for a kernel moving `traffic` bytes in total.
+inline bool StreamPolicy(size_t traffic) { return traffic > kStreamBytes; }
+
 __host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline unsigned grid_for(size_t work_items, int block, size_t cap = 65536) {

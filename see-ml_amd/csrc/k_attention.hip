@@ -57,10 +57,256 @@ float InvSqrtD(int64_t d) { return 1.0f / ::sqrtf(static_cast<float>(d)); }
 
 }  // namespace
 
+namespace {
+
+// ---- fused causal forward (d = 64 or 128) -----------------------------------
+//
+// One workgroup = 4 wavefronts = 128 queries of one (b, h); wavefront w owns
+// queries q0 + 32w .. + 31, one per lane column. Scores are computed
+// transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: the lane's Q row is
+// the B operand held in registers for the whole kernel, K tiles of 32 keys
+// are staged through LDS (double-buffered, shared by the 4 wavefronts).
+// Accumulator element v of lane (h, r) is key 8*(v/4) + 4h + v%4 of the tile
+// for query r, so each query's softmax statistics live in one lane pair
+// (r, r + 32) and each lane stores its probabilities as four float4 runs of
+// its query's P row.
+//
+// Pass 1 walks the causal key tiles for the row maximum m and the exp-sum l
+// (online: l = l * exp(m_old - m_new) + sum exp(s - m_new)). Pass 2 recomputes
+// the scores, forms p = exp(s - m) * (1/l) (exact 0 for j > i), writes P
+// once and accumulates O^T = V^T P^T with the probabilities straight from
+// the score registers as the B operand (MFMA t's k index is the lane's own
+// accumulator element t). The row tail beyond the diagonal tile is written
+// as exact zeros. QK^T is computed twice; P is written once and never read
+// back, against the three P-sized passes of scores -> softmax -> PV.
+//
+// Heavy (late) query blocks are scheduled first, for causal load balance.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kAttnQ = 128;  // queries per workgroup
+constexpr int kAttnK = 32;   // keys per tile
+constexpr int kAttnThreads = 256;
+
+template <int D>
+struct KvTile {
+  static constexpr int kStride = D + 4;  // floats per LDS row
+  static constexpr int kPer = kAttnK * D / 4 / kAttnThreads;
+  float4 r[kPer];
+  // Rows j0.. of a [S, ld] head view; rows past S are clamped onto row S-1
+  // (their keys are masked for every valid query).
+  __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int j0, int S) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int vi = static_cast<int>(threadIdx.x) + i * kAttnThreads;
+      const int row = vi / (D / 4), c4 = vi % (D / 4);
+      const int j = min(j0 + row, S - 1);
+      r[i] = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(j) * ld + 4 * c4);
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int vi = static_cast<int>(threadIdx.x) + i * kAttnThreads;
+      const int row = vi / (D / 4), c4 = vi % (D / 4);
+      *reinterpret_cast<float4*>(lds + row * kStride + 4 * c4) = r[i];
+    }
+  }
+};
+
+// S^T tile (32 keys x 32 queries) from the LDS K tile and the lane's Q
+// fragments: MFMA (g, jj) takes feature 8g + 4h + jj on both operands. Two
+// accumulators (even/odd g) keep consecutive MFMAs independent.
+template <int D>
+__device__ __forceinline__ floatx16 ScoreTile(const float* __restrict__ kt,
+                                              const float4 (&qf)[D / 8], int h, int r) {
+  floatx16 a0, a1;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    a0[e] = 0.0f;
+    a1[e] = 0.0f;
+  }
+  const float* row = kt + r * KvTile<D>::kStride + 4 * h;
+#pragma unroll
+  for (int g = 0; g < D / 8; ++g) {
+    const float4 kf = *reinterpret_cast<const float4*>(row + 8 * g);
+    floatx16& acc = (g & 1) ? a1 : a0;
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[g].x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[g].y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[g].z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[g].w, acc, 0, 0, 0);
+  }
+  return a0 + a1;
+}
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d) {
+  constexpr int TS = KvTile<D>::kStride;
+  constexpr int NB = D / 32;
+  __shared__ __align__(16) float kt[2][kAttnK * TS];
+  __shared__ __align__(16) float vt[2][kAttnK * TS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int BH = B * H;
+  const int nqb = (S + kAttnQ - 1) / kAttnQ;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / BH;
+  const int bh = static_cast<int>(blockIdx.x) % BH;
+  const int b = bh / H, hh = bh % H;
+  const int64_t ld = static_cast<int64_t>(H) * D;
+  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
+  const float* qh = q + head;
+  const float* kh = k + head;
+  const float* vh = v + head;
+  float* oh = o + head;
+  float* ph = probs + static_cast<int64_t>(bh) * S * S;
+
+  const int q0 = qb * kAttnQ;
+  const int qw = q0 + 32 * w;  // first query of this wavefront
+  const int i = qw + r;        // this lane's query
+  const int ic = min(i, S - 1);
+  const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
+  const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
+
+  float4 qf[D / 8];
+#pragma unroll
+  for (int g = 0; g < D / 8; ++g)
+    qf[g] = *reinterpret_cast<const float4*>(qh + static_cast<int64_t>(ic) * ld + 8 * g + 4 * h);
+
+  // ---- pass 1: row maximum and exp-sum ----
+  float m = -__builtin_inff(), l = 0.0f;
+  KvTile<D> ks, vs;
+  ks.load(kh, ld, 0, S);
+  ks.store(kt[0]);
+  __syncthreads();
+  for (int t = 0; t < tiles_wg; ++t) {
+    if (t + 1 < tiles_wg) ks.load(kh, ld, (t + 1) * kAttnK, S);
+    if (t < tiles_w) {
+      floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+        const float sv = j > i ? -__builtin_inff() : sc[e] * inv_sqrt_d;
+        sc[e] = sv;
+        tmax = fmaxf(tmax, sv);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mn = fmaxf(m, tmax);
+      const float alpha = m == -__builtin_inff() ? 0.0f : expf(m - mn);
+      float ssum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ssum += expf(sc[e] - mn);
+      ssum += __shfl_xor(ssum, 32, 64);
+      l = l * alpha + ssum;
+      m = mn;
+    }
+    if (t + 1 < tiles_wg) ks.store(kt[(t + 1) & 1]);
+    __syncthreads();
+  }
+
+  // ---- pass 2: probabilities, P, O ----
+  const float inv_l = 1.0f / l;
+  floatx16 oacc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[nb][e] = 0.0f;
+  ks.load(kh, ld, 0, S);
+  vs.load(vh, ld, 0, S);
+  ks.store(kt[0]);
+  vs.store(vt[0]);
+  __syncthreads();
+  const bool row_ok = i < S;
+  float* prow = ph + static_cast<int64_t>(ic) * S;
+  for (int t = 0; t < tiles_wg; ++t) {
+    if (t + 1 < tiles_wg) {
+      ks.load(kh, ld, (t + 1) * kAttnK, S);
+      vs.load(vh, ld, (t + 1) * kAttnK, S);
+    }
+    if (t < tiles_w) {
+      floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+        sc[e] = j > i ? 0.0f : expf(sc[e] * inv_sqrt_d - m) * inv_l;
+      }
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int j = t * kAttnK + 8 * q4 + 4 * h;
+        if (row_ok && j < S)
+          *reinterpret_cast<float4*>(prow + j) =
+              make_float4(sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]);
+      }
+      const float* vtile = vt[t & 1];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float* vrow = vtile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          oacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * nb], sc[e], oacc[nb], 0, 0, 0);
+      }
+    }
+    if (t + 1 < tiles_wg) {
+      ks.store(kt[(t + 1) & 1]);
+      vs.store(vt[(t + 1) & 1]);
+    }
+    __syncthreads();
+  }
+
+  if (row_ok) {
+    // O^T element e of block nb: feature 32*nb + 8*(e/4) + 4h + e%4 of query i.
+    float* orow = oh + static_cast<int64_t>(i) * ld;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
+            make_float4(oacc[nb][4 * q4], oacc[nb][4 * q4 + 1], oacc[nb][4 * q4 + 2],
+                        oacc[nb][4 * q4 + 3]);
+  }
+  // Causal tail: columns past this wavefront's diagonal tile are exact 0.
+  const int zc = tiles_w * kAttnK;
+  for (int rr = 0; rr < 32; ++rr) {
+    const int row = qw + rr;
+    if (row >= S) break;
+    float* pz = ph + static_cast<int64_t>(row) * S;
+    for (int c4 = zc / 4 + lane; c4 < S / 4; c4 += 64)
+      *reinterpret_cast<float4*>(pz + 4 * c4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
+bool FusedFwdEligible(const float* q, const float* k, const float* v, const float* o,
+                      const float* probs, size_t B, size_t S, size_t H, size_t d) {
+  if (d != 64 && d != 128) return false;
+  if (S == 0 || S % 4 != 0) return false;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(probs))
+    return false;
+  const size_t blocks = B * H * ((S + kAttnQ - 1) / kAttnQ);
+  return B * H <= 0x7FFFFFFFu && S <= 0x7FFFFFFFu && blocks <= 0x7FFFFFFFu &&
+         B * S * H * d < (size_t{1} << 62);
+}
+
+}  // namespace
+
 size_t AttnWorkspace(size_t, size_t, size_t, size_t) { return 0; }
 
 Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* probs, size_t B,
                size_t S, size_t H, size_t d, const Ctx& c) {
+  if (B * S * H * d == 0) return Status::Ok();
+  if (FusedFwdEligible(q, k, v, o, probs, B, S, H, d)) {
+    const unsigned blocks = static_cast<unsigned>(B * H * ((S + kAttnQ - 1) / kAttnQ));
+    const float inv = InvSqrtD(static_cast<int64_t>(d));
+    if (d == 128)
+      hipLaunchKernelGGL(attn_fwd_fused<128>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
+                         v, o, probs, static_cast<int>(B), static_cast<int>(S),
+                         static_cast<int>(H), inv);
+    else
+      hipLaunchKernelGGL(attn_fwd_fused<64>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
+                         v, o, probs, static_cast<int>(B), static_cast<int>(S),
+                         static_cast<int>(H), inv);
+    return LaunchStatus("AttnFwd");
+  }
   const Geo g = MakeGeo(B, S, H, d);
   // 1) raw scores s_ij = (q_i . k_j) * (1/sqrt(d)) for j <= i, exact 0 above.
   GemmDesc sc;

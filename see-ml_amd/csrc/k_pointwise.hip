@@ -63,36 +63,69 @@ struct FillF {
 };
 struct CopyF { __device__ float operator()(float x) const { return x; } };
 
-template <class F>
+// Each thread handles Unroll(NT) float4s per iteration, all loads issued
+// before any store. NT (streams larger than the memory-side cache) selects
+// the streaming cache policy and a 4-deep unroll; cache-resident streams run
+// one float4 per iteration with the default policy, which measured faster.
+constexpr int Unroll(bool nt) { return nt ? 4 : 1; }
+constexpr size_t kStreamGridCap = 16384;
+
+template <class F, bool NT>
 __global__ __launch_bounds__(kBlock) void ew_unary(const float* __restrict__ x,
                                                    float* __restrict__ out, size_t n, size_t nv,
                                                    F f) {
-  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  float4* o4 = reinterpret_cast<float4*>(out);
-  for (size_t i = gid; i < nv; i += stride) {
-    const float4 a = x4[i];
-    o4[i] = make_float4(f(a.x), f(a.y), f(a.z), f(a.w));
+  constexpr int kUnroll = Unroll(NT);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock * kUnroll;
+  for (size_t base = static_cast<size_t>(blockIdx.x) * kBlock * kUnroll + threadIdx.x; base < nv;
+       base += stride) {
+    float4 a[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+      if (i < nv) a[u] = ld4(x + 4 * i, NT);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+      if (i < nv) st4(out + 4 * i, make_float4(f(a[u].x), f(a[u].y), f(a[u].z), f(a[u].w)), NT);
+    }
   }
-  for (size_t i = nv * 4 + gid; i < n; i += stride) out[i] = f(x[i]);
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const size_t tstride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = nv * 4 + gid; i < n; i += tstride) out[i] = f(x[i]);
 }
 
-template <class F>
+template <class F, bool NT>
 __global__ __launch_bounds__(kBlock) void ew_binary(const float* __restrict__ x,
                                                     const float* __restrict__ y,
                                                     float* __restrict__ out, size_t n, size_t nv,
                                                     F f) {
-  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  const float4* y4 = reinterpret_cast<const float4*>(y);
-  float4* o4 = reinterpret_cast<float4*>(out);
-  for (size_t i = gid; i < nv; i += stride) {
-    const float4 a = x4[i], b = y4[i];
-    o4[i] = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+  constexpr int kUnroll = Unroll(NT);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock * kUnroll;
+  for (size_t base = static_cast<size_t>(blockIdx.x) * kBlock * kUnroll + threadIdx.x; base < nv;
+       base += stride) {
+    float4 a[kUnroll], b[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+      if (i < nv) {
+        a[u] = ld4(x + 4 * i, NT);
+        b[u] = ld4(y + 4 * i, NT);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+      if (i < nv)
+        st4(out + 4 * i,
+            make_float4(f(a[u].x, b[u].x), f(a[u].y, b[u].y), f(a[u].z, b[u].z),
+                        f(a[u].w, b[u].w)),
+            NT);
+    }
   }
-  for (size_t i = nv * 4 + gid; i < n; i += stride) out[i] = f(x[i], y[i]);
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const size_t tstride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = nv * 4 + gid; i < n; i += tstride) out[i] = f(x[i], y[i]);
 }
 
 // Fill writes only: a separate kernel so no read of uninitialised memory.
@@ -109,9 +142,13 @@ template <class F>
 Status Unary(const float* x, float* out, size_t n, F f, const Ctx& c, const char* what) {
   if (n == 0) return Status::Ok();
   const size_t nv = (aligned16(x) && aligned16(out)) ? n / 4 : 0;
-  const size_t work = nv ? nv : n;
-  hipLaunchKernelGGL(ew_unary<F>, dim3(grid_for(work, kBlock, kGridCap)), dim3(kBlock), 0,
-                     c.stream, x, out, n, nv, f);
+  const bool nt = StreamPolicy(8 * n);
+  const size_t work = nv ? (nv + Unroll(nt) - 1) / Unroll(nt) : n;
+  const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
+  if (nt)
+    hipLaunchKernelGGL((ew_unary<F, true>), grid, dim3(kBlock), 0, c.stream, x, out, n, nv, f);
+  else
+    hipLaunchKernelGGL((ew_unary<F, false>), grid, dim3(kBlock), 0, c.stream, x, out, n, nv, f);
   return LaunchStatus(what);
 }
 
@@ -120,9 +157,14 @@ Status Binary(const float* x, const float* y, float* out, size_t n, F f, const C
               const char* what) {
   if (n == 0) return Status::Ok();
   const size_t nv = (aligned16(x) && aligned16(y) && aligned16(out)) ? n / 4 : 0;
-  const size_t work = nv ? nv : n;
-  hipLaunchKernelGGL(ew_binary<F>, dim3(grid_for(work, kBlock, kGridCap)), dim3(kBlock), 0,
-                     c.stream, x, y, out, n, nv, f);
+  const bool nt = StreamPolicy(12 * n);
+  const size_t work = nv ? (nv + Unroll(nt) - 1) / Unroll(nt) : n;
+  const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
+  if (nt)
+    hipLaunchKernelGGL((ew_binary<F, true>), grid, dim3(kBlock), 0, c.stream, x, y, out, n, nv, f);
+  else
+    hipLaunchKernelGGL((ew_binary<F, false>), grid, dim3(kBlock), 0, c.stream, x, y, out, n, nv,
+                       f);
   return LaunchStatus(what);
 }
 
@@ -195,7 +237,7 @@ __global__ __launch_bounds__(kBlock) void xent_bwd_kernel(const float* __restric
                                                           const int32_t* __restrict__ labels,
                                                           const float* __restrict__ seed,
                                                           float* __restrict__ dl, size_t N,
-                                                          size_t C, int vec) {
+                                                          size_t C, int vec, int nt) {
   const float scale = *seed / static_cast<float>(N);
   const size_t cstride = static_cast<size_t>(gridDim.x) * kBlock;
   const size_t c0 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -203,10 +245,8 @@ __global__ __launch_bounds__(kBlock) void xent_bwd_kernel(const float* __restric
     const int32_t lab = labels[n];
     const size_t lc = lab >= 0 ? static_cast<size_t>(lab) : ~size_t{0};
     if (vec) {
-      const float4* p4 = reinterpret_cast<const float4*>(probs + n * C);
-      float4* d4 = reinterpret_cast<float4*>(dl + n * C);
       for (size_t j = c0; j < C / 4; j += cstride) {
-        const float4 p = p4[j];
+        const float4 p = ld4(probs + n * C + 4 * j, nt);
         float4 o = make_float4(scale * p.x, scale * p.y, scale * p.z, scale * p.w);
         if (lc / 4 == j) {
           if (lc % 4 == 0) o.x -= scale;
@@ -214,7 +254,7 @@ __global__ __launch_bounds__(kBlock) void xent_bwd_kernel(const float* __restric
           else if (lc % 4 == 2) o.z -= scale;
           else o.w -= scale;
         }
-        d4[j] = o;
+        st4(dl + n * C + 4 * j, o, nt);
       }
     } else {
       const float* pr = probs + n * C;
@@ -377,7 +417,8 @@ template <int DIR>
 __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restrict__ x,
                                                            float* __restrict__ y, uint32_t rows,
                                                            uint32_t S, uint32_t width,
-                                                           uint32_t d, uint32_t rpb, float step) {
+                                                           uint32_t d, uint32_t rpb, float step,
+                                                           int nt) {
   __shared__ float2 cs[kRopeTable];
   const uint32_t half_d = d / 2;
   const uint32_t row0 = blockIdx.x * rpb;
@@ -397,7 +438,7 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restri
     const float2* tr = cs + r * half_d;
     for (uint32_t j = threadIdx.x; j < nv; j += kBlock) {
       const uint32_t c2 = ((4 * j) % d) / 2;
-      const float4 v = xr[j];
+      const float4 v = ld4(reinterpret_cast<const float*>(xr + j), nt);
       const float2 a = tr[c2], b = tr[c2 + 1];
       const float c0 = a.x, s0 = a.y, c1 = b.x, s1 = b.y;
       float4 o;
@@ -412,7 +453,7 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restri
         o.z = v.z * c1 + v.w * s1;
         o.w = -v.z * s1 + v.w * c1;
       }
-      yr[j] = o;
+      st4(reinterpret_cast<float*>(yr + j), o, nt);
     }
   }
 }
@@ -454,15 +495,16 @@ Status Rope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, fl
                     aligned16(y) && rows <= 0xFFFFFFFFu && width <= 0xFFFFFFFFu && S > 0;
   if (fast) {
     const uint32_t rpb = static_cast<uint32_t>(kRopeTable / (d / 2));
+    const int nt = StreamPolicy(8 * rows * width) ? 1 : 0;
     const unsigned grid = static_cast<unsigned>((rows + rpb - 1) / rpb);
     if (dir > 0)
       hipLaunchKernelGGL(rope_rows_kernel<1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
                          static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
-                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step);
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step, nt);
     else
       hipLaunchKernelGGL(rope_rows_kernel<-1>, dim3(grid), dim3(kBlock), 0, c.stream, x, y,
                          static_cast<uint32_t>(rows), static_cast<uint32_t>(S),
-                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step);
+                         static_cast<uint32_t>(width), static_cast<uint32_t>(d), rpb, step, nt);
   } else {
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, kBlock, kGridCap)), dim3(kBlock), 0,
                        c.stream, x, y, pairs, S, H, d / 2, step, dir);
@@ -548,7 +590,7 @@ Status SoftmaxXEntBwd(const float* probs, const int32_t* labels, const float* se
   const unsigned gx = std::max(1u, grid_for((per_row + 3) / 4, kBlock, 64));
   const unsigned gy = static_cast<unsigned>(std::min<size_t>(N, 65535));
   hipLaunchKernelGGL(xent_bwd_kernel, dim3(gx, gy), dim3(kBlock), 0, c.stream, probs, labels,
-                     seed, dlogits, N, C, vec ? 1 : 0);
+                     seed, dlogits, N, C, vec ? 1 : 0, StreamPolicy(8 * N * C) ? 1 : 0);
   return LaunchStatus("SoftmaxXEntBwd");
 }
 

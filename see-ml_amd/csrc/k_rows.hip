@@ -151,11 +151,10 @@ template <int NT>
 __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict__ logits,
                                                         const int32_t* __restrict__ labels,
                                                         float* __restrict__ probs, size_t N,
-                                                        size_t C, double* __restrict__ terms) {
+                                                        size_t C, double* __restrict__ terms,
+                                                        int nt) {
   __shared__ float fscratch[NT / kWave];
   const size_t n = blockIdx.x;
-  const float4* x4 = reinterpret_cast<const float4*>(logits + n * C);
-  float4* p4 = reinterpret_cast<float4*>(probs + n * C);
   const int nv = static_cast<int>(C / 4);
   const int t = threadIdx.x;
   float4 v[kXentVec];
@@ -164,7 +163,7 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
   for (int i = 0; i < kXentVec; ++i) {
     const int j = t + i * NT;
     if (j < nv) {
-      v[i] = x4[j];
+      v[i] = ld4(logits + n * C + 4 * static_cast<size_t>(j), nt);
       mx = fmaxf(fmaxf(fmaxf(fmaxf(mx, v[i].x), v[i].y), v[i].z), v[i].w);
     }
   }
@@ -189,7 +188,9 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
 #pragma unroll
   for (int i = 0; i < kXentVec; ++i) {
     const int j = t + i * NT;
-    if (j < nv) p4[j] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+    if (j < nv)
+      st4(probs + n * C + 4 * static_cast<size_t>(j),
+          make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), nt);
   }
   if (t == 0) {
     const int32_t lab = labels[n];
@@ -394,23 +395,21 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_kernel(
 
 template <int TPR, int V>
 __device__ __forceinline__ void load_row(const float* __restrict__ row, int nv, int t,
-                                         float4 (&v)[V]) {
-  const float4* r4 = reinterpret_cast<const float4*>(row);
+                                         float4 (&v)[V], bool nt) {
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
-    v[i] = j < nv ? r4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    v[i] = j < nv ? ld4(row + 4 * j, nt) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
 }
 
 template <int TPR, int V>
 __device__ __forceinline__ void store_row(float* __restrict__ row, int nv, int t,
-                                          const float4 (&v)[V]) {
-  float4* r4 = reinterpret_cast<float4*>(row);
+                                          const float4 (&v)[V], bool nt) {
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
-    if (j < nv) r4[j] = v[i];
+    if (j < nv) st4(row + 4 * j, v[i], nt);
   }
 }
 
@@ -436,14 +435,14 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
                                                            const float* __restrict__ gamma,
                                                            float* __restrict__ y,
                                                            float* __restrict__ rstd, size_t rows,
-                                                           int cols) {
+                                                           int cols, int nt) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
   float4 xv[V];
-  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) s += sq4(xv[i]);
@@ -460,13 +459,13 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
                           xv[i].w * rs * g.w);
     }
   }
-  store_row<TPR, V>(y + r * cols, nv, t, xv);
+  store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
 
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, int cols) {
+    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, int cols, int nt) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
@@ -474,8 +473,8 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
   const int nv = cols / 4;
   const float inv_d = 1.0f / static_cast<float>(cols);
   float4 gv[V], xv[V];
-  load_row<TPR, V>(dy + r * cols, nv, t, gv);
-  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   const float4* g4 = reinterpret_cast<const float4*>(gamma);
   double s = 0.0;
 #pragma unroll
@@ -496,21 +495,21 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
                         rs * (gv[i].y - xv[i].y * rs * rs * mgx),
                         rs * (gv[i].z - xv[i].z * rs * rs * mgx),
                         rs * (gv[i].w - xv[i].w * rs * rs * mgx));
-  store_row<TPR, V>(dx + r * cols, nv, t, gv);
+  store_row<TPR, V>(dx + r * cols, nv, t, gv, nt);
 }
 
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
     float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, size_t rows,
-    int cols) {
+    int cols, int nt) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
   float4 xv[V];
-  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -551,14 +550,14 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
                           (xv[i].z - mu) * rs * g.z + b.z, (xv[i].w - mu) * rs * g.w + b.w);
     }
   }
-  store_row<TPR, V>(y + r * cols, nv, t, xv);
+  store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
 
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, float* __restrict__ dx,
-    size_t rows, int cols) {
+    size_t rows, int cols, int nt) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
@@ -567,8 +566,8 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mu = mean[r], rs = rstd[r];
   float4 gv[V], xv[V];
-  load_row<TPR, V>(dy + r * cols, nv, t, gv);
-  load_row<TPR, V>(x + r * cols, nv, t, xv);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   const float4* g4 = reinterpret_cast<const float4*>(gamma);
   double sg = 0.0, sgx = 0.0;
 #pragma unroll
@@ -598,22 +597,22 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
   for (int i = 0; i < V; ++i)
     gv[i] = make_float4(rs * (gv[i].x - mg - xv[i].x * mgx), rs * (gv[i].y - mg - xv[i].y * mgx),
                         rs * (gv[i].z - mg - xv[i].z * mgx), rs * (gv[i].w - mg - xv[i].w * mgx));
-  store_row<TPR, V>(dx + r * cols, nv, t, gv);
+  store_row<TPR, V>(dx + r * cols, nv, t, gv, nt);
 }
 
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __restrict__ p,
                                                                const float* __restrict__ dp,
                                                                float* __restrict__ ds,
-                                                               size_t rows, int cols) {
+                                                               size_t rows, int cols, int nt) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
   float4 pv[V], dv[V];
-  load_row<TPR, V>(p + r * cols, nv, t, pv);
-  load_row<TPR, V>(dp + r * cols, nv, t, dv);
+  load_row<TPR, V>(p + r * cols, nv, t, pv, nt);
+  load_row<TPR, V>(dp + r * cols, nv, t, dv, nt);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -627,7 +626,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __re
   for (int i = 0; i < V; ++i)
     dv[i] = make_float4(pv[i].x * (dv[i].x - sum), pv[i].y * (dv[i].y - sum),
                         pv[i].z * (dv[i].z - sum), pv[i].w * (dv[i].w - sum));
-  store_row<TPR, V>(ds + r * cols, nv, t, dv);
+  store_row<TPR, V>(ds + r * cols, nv, t, dv, nt);
 }
 
 // Causal row softmax in place (attention.cc:106-125): row u = (b, h, i) holds
@@ -763,15 +762,16 @@ Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, f
   double* terms = static_cast<double*>(c.ws);
   const bool reg = C >= 2048 && C % 4 == 0 && aligned16(logits) && aligned16(probs) &&
                    N <= 0x7FFFFFFF;
+  const int nt = StreamPolicy(8 * N * C) ? 1 : 0;
   if (reg && C <= static_cast<size_t>(256 * 4 * kXentVec))
     hipLaunchKernelGGL(xent_fwd_rows_reg<256>, dim3(static_cast<unsigned>(N)), dim3(256), 0,
-                       c.stream, logits, labels, probs, N, C, terms);
+                       c.stream, logits, labels, probs, N, C, terms, nt);
   else if (reg && C <= static_cast<size_t>(512 * 4 * kXentVec))
     hipLaunchKernelGGL(xent_fwd_rows_reg<512>, dim3(static_cast<unsigned>(N)), dim3(512), 0,
-                       c.stream, logits, labels, probs, N, C, terms);
+                       c.stream, logits, labels, probs, N, C, terms, nt);
   else if (reg && C <= static_cast<size_t>(1024 * 4 * kXentVec))
     hipLaunchKernelGGL(xent_fwd_rows_reg<1024>, dim3(static_cast<unsigned>(N)), dim3(1024), 0,
-                       c.stream, logits, labels, probs, N, C, terms);
+                       c.stream, logits, labels, probs, N, C, terms, nt);
   else if (C >= 2048)
     hipLaunchKernelGGL(xent_fwd_rows<kBlock>, dim3(RowsGrid(N, kBlock)), dim3(kBlock), 0,
                        c.stream, logits, labels, probs, N, C, terms);
@@ -854,7 +854,7 @@ Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float
   const int rc = RegCase(cols, {x, gamma, beta, y});
   if (rc >= 0)
     REG_DISPATCH(layer_norm_fwd_reg, rc, rows, x, gamma, beta, y, mean, rstd, rows,
-                 static_cast<int>(cols));
+                 static_cast<int>(cols), StreamPolicy(8 * rows * cols) ? 1 : 0);
   else
     ROWS_DISPATCH(layer_norm_fwd_rows, rows, cols, x, gamma, beta, y, mean, rstd, rows, cols);
   return LaunchStatus("LayerNormFwd");
@@ -866,7 +866,7 @@ Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const f
   const int rc = RegCase(cols, {dy, x, gamma, dx});
   if (rc >= 0)
     REG_DISPATCH(layer_norm_bwd_reg, rc, rows, dy, x, gamma, mean, rstd, dx, rows,
-                 static_cast<int>(cols));
+                 static_cast<int>(cols), StreamPolicy(12 * rows * cols) ? 1 : 0);
   else
     ROWS_DISPATCH(layer_norm_bwd_rows, rows, cols, dy, x, gamma, mean, rstd, dx, rows, cols);
   return LaunchStatus("LayerNormBwd");
@@ -877,7 +877,8 @@ Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, siz
   if (rows == 0 || cols == 0) return Status::Ok();
   const int rc = RegCase(cols, {x, gamma, y});
   if (rc >= 0)
-    REG_DISPATCH(rms_norm_fwd_reg, rc, rows, x, gamma, y, rstd, rows, static_cast<int>(cols));
+    REG_DISPATCH(rms_norm_fwd_reg, rc, rows, x, gamma, y, rstd, rows, static_cast<int>(cols),
+                 StreamPolicy(8 * rows * cols) ? 1 : 0);
   else
     ROWS_DISPATCH(rms_norm_fwd_rows, rows, cols, x, gamma, y, rstd, rows, cols);
   return LaunchStatus("RmsNormFwd");
@@ -889,7 +890,7 @@ Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const flo
   const int rc = RegCase(cols, {dy, x, gamma, dx});
   if (rc >= 0)
     REG_DISPATCH(rms_norm_bwd_reg, rc, rows, dy, x, gamma, rstd, dx, rows,
-                 static_cast<int>(cols));
+                 static_cast<int>(cols), StreamPolicy(12 * rows * cols) ? 1 : 0);
   else
     ROWS_DISPATCH(rms_norm_bwd_rows, rows, cols, dy, x, gamma, rstd, dx, rows, cols);
   return LaunchStatus("RmsNormBwd");
@@ -900,7 +901,8 @@ Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t row
   if (rows == 0 || cols == 0) return Status::Ok();
   const int rc = RegCase(cols, {probs, dp, ds});
   if (rc >= 0)
-    REG_DISPATCH(softmax_rows_bwd_reg, rc, rows, probs, dp, ds, rows, static_cast<int>(cols));
+    REG_DISPATCH(softmax_rows_bwd_reg, rc, rows, probs, dp, ds, rows, static_cast<int>(cols),
+                 StreamPolicy(12 * rows * cols) ? 1 : 0);
   else
     ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
   return LaunchStatus("SoftmaxRowsBwd");

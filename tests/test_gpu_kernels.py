@@ -272,7 +272,12 @@ def test_rope(env, orc, B, S, H, d):
         assert same_bits(h[:, 0], x.reshape(B, S, H * d)[:, 0])
 
 
-@pytest.mark.parametrize("B,S,H,d", [(2, 33, 3, 8), (1, 130, 2, 64), (2, 256, 2, 128), (1, 1, 2, 3)])
+# AttnFwd with d in {64, 128} and S % 4 == 0 runs the fused two-pass kernel
+# (partial query blocks and key tiles included); other shapes run scores ->
+# row softmax -> PV on the GEMM engine.
+@pytest.mark.parametrize("B,S,H,d", [(2, 33, 3, 8), (1, 130, 2, 64), (2, 256, 2, 128), (1, 1, 2, 3),
+                                     (1, 300, 2, 64), (2, 4, 1, 128), (1, 1024, 2, 128),
+                                     (3, 160, 2, 64), (1, 132, 1, 128)])
 def test_attention_family(env, orc, B, S, H, d):
     n, pn = B * S * H * d, B * H * S * S
     q, k, v, w = rnd(n, 80), rnd(n, 81), rnd(n, 82), rnd(n, 83)
