@@ -22,6 +22,8 @@
 
 #include <math.h>
 
+#include <initializer_list>
+
 namespace seeml_hip {
 
 namespace {
@@ -276,15 +278,279 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   }
 }
 
-bool FusedFwdEligible(const float* q, const float* k, const float* v, const float* o,
-                      const float* probs, size_t B, size_t S, size_t H, size_t d) {
+// ---- fused causal backward primitives (d = 64 or 128) ----------------------
+//
+// Same workgroup shape and MFMA layout as the forward.
+//
+// attn_dp_fused: dP = dO V^T for j <= i, exact 0 above (attention.cc:138-163).
+//   The score pass of the forward with dO as the register operand and V
+//   tiles in LDS, storing the raw dots.
+// attn_dq_fused: dQ(i) = sum_{j <= i} (dS(i, j) / sqrt(d)) K(j)
+//   (attention.cc:203-222). Per wavefront 32 queries; dQ^T = K^T dS^T with K
+//   tiles in LDS as the A operand and the lane's own dS row as the B
+//   operand (element t of the lane's 16 is key 8*(t/4) + 4h + t%4, read as
+//   four float4s), prefetched one tile ahead.
+// attn_dkv_fused: dK(j) = sum_{i >= j} (dS(i, j) / sqrt(d)) Q(i) and
+//   dV(j) = sum_{i >= j} P(i, j) dO(i) (attention.cc:165-183, 224-242). Per
+//   wavefront 32 keys, one per lane column; the workgroup walks the query
+//   tiles at and below its keys' diagonal, X (= Q or dO) tiles in LDS as the
+//   A operand, the (i, j) column entries of dS / P as the B operand (for
+//   each MFMA the 32 lanes of a half read 32 consecutive keys of one query
+//   row). Early key blocks (the longest walks) are scheduled first.
+// Entries outside the causal half are masked to exact zeros before use, as
+// the reference's loops never visit them.
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_dp_fused(
+    const float* __restrict__ dout, const float* __restrict__ v, float* __restrict__ dp, int B,
+    int S, int H) {
+  __shared__ __align__(16) float vt[2][kAttnK * KvTile<D>::kStride];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int BH = B * H;
+  const int nqb = (S + kAttnQ - 1) / kAttnQ;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / BH;
+  const int bh = static_cast<int>(blockIdx.x) % BH;
+  const int b = bh / H, hh = bh % H;
+  const int64_t ld = static_cast<int64_t>(H) * D;
+  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
+  const float* dh = dout + head;
+  const float* vh = v + head;
+  float* ph = dp + static_cast<int64_t>(bh) * S * S;
+  const int q0 = qb * kAttnQ;
+  const int qw = q0 + 32 * w;
+  const int i = qw + r;
+  const int ic = min(i, S - 1);
+  const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
+  const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
+  float4 qf[D / 8];
+#pragma unroll
+  for (int g = 0; g < D / 8; ++g)
+    qf[g] = *reinterpret_cast<const float4*>(dh + static_cast<int64_t>(ic) * ld + 8 * g + 4 * h);
+  const bool row_ok = i < S;
+  float* prow = ph + static_cast<int64_t>(ic) * S;
+  KvTile<D> vs;
+  vs.load(vh, ld, 0, S);
+  vs.store(vt[0]);
+  __syncthreads();
+  for (int t = 0; t < tiles_wg; ++t) {
+    if (t + 1 < tiles_wg) vs.load(vh, ld, (t + 1) * kAttnK, S);
+    if (t < tiles_w) {
+      floatx16 sc = ScoreTile<D>(vt[t & 1], qf, h, r);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int j = t * kAttnK + 8 * q4 + 4 * h;
+        if (row_ok && j < S)
+          *reinterpret_cast<float4*>(prow + j) =
+              make_float4(j + 0 > i ? 0.0f : sc[4 * q4], j + 1 > i ? 0.0f : sc[4 * q4 + 1],
+                          j + 2 > i ? 0.0f : sc[4 * q4 + 2], j + 3 > i ? 0.0f : sc[4 * q4 + 3]);
+      }
+    }
+    if (t + 1 < tiles_wg) vs.store(vt[(t + 1) & 1]);
+    __syncthreads();
+  }
+  const int zc = tiles_w * kAttnK;
+  for (int rr = 0; rr < 32; ++rr) {
+    const int row = qw + rr;
+    if (row >= S) break;
+    float* pz = ph + static_cast<int64_t>(row) * S;
+    for (int c4 = zc / 4 + lane; c4 < S / 4; c4 += 64)
+      *reinterpret_cast<float4*>(pz + 4 * c4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
+// The lane's 16 dS entries of key tile t for query i (masked j > i), scaled.
+__device__ __forceinline__ void LoadRowTile(const float* __restrict__ row, int t, int i, int h,
+                                            bool row_ok, float4 (&x)[4]) {
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const int j = t * kAttnK + 8 * q4 + 4 * h;
+    x[q4] = (row_ok && j <= i) ? *reinterpret_cast<const float4*>(row + j)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
+    const float* __restrict__ ds, const float* __restrict__ k, float* __restrict__ dq, int B,
+    int S, int H, float inv_sqrt_d) {
+  constexpr int TS = KvTile<D>::kStride;
+  constexpr int NB = D / 32;
+  __shared__ __align__(16) float kt[2][kAttnK * TS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int BH = B * H;
+  const int nqb = (S + kAttnQ - 1) / kAttnQ;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / BH;
+  const int bh = static_cast<int>(blockIdx.x) % BH;
+  const int b = bh / H, hh = bh % H;
+  const int64_t ld = static_cast<int64_t>(H) * D;
+  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
+  const float* kh = k + head;
+  float* oh = dq + head;
+  const int q0 = qb * kAttnQ;
+  const int qw = q0 + 32 * w;
+  const int i = qw + r;
+  const int ic = min(i, S - 1);
+  const bool row_ok = i < S;
+  const float* dsrow = ds + static_cast<int64_t>(bh) * S * S + static_cast<int64_t>(ic) * S;
+  const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
+  const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
+  floatx16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
+  KvTile<D> ks;
+  float4 x[4], xn[4];
+  ks.load(kh, ld, 0, S);
+  LoadRowTile(dsrow, 0, i, h, row_ok && 0 < tiles_w, x);
+  ks.store(kt[0]);
+  __syncthreads();
+  for (int t = 0; t < tiles_wg; ++t) {
+    if (t + 1 < tiles_wg) {
+      ks.load(kh, ld, (t + 1) * kAttnK, S);
+      LoadRowTile(dsrow, t + 1, i, h, row_ok && t + 1 < tiles_w, xn);
+    }
+    if (t < tiles_w) {
+      float g[16];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        g[4 * q4 + 0] = x[q4].x * inv_sqrt_d;
+        g[4 * q4 + 1] = x[q4].y * inv_sqrt_d;
+        g[4 * q4 + 2] = x[q4].z * inv_sqrt_d;
+        g[4 * q4 + 3] = x[q4].w * inv_sqrt_d;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (j > i) g[e] = 0.0f;
+      }
+      const float* ktile = kt[t & 1];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float* krow = ktile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[32 * nb], g[e], acc[nb], 0, 0, 0);
+      }
+    }
+    if (t + 1 < tiles_wg) {
+      ks.store(kt[(t + 1) & 1]);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) x[q4] = xn[q4];
+    }
+    __syncthreads();
+  }
+  if (row_ok) {
+    float* orow = oh + static_cast<int64_t>(i) * ld;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
+            make_float4(acc[nb][4 * q4], acc[nb][4 * q4 + 1], acc[nb][4 * q4 + 2],
+                        acc[nb][4 * q4 + 3]);
+  }
+}
+
+template <int D, bool SCALED>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_dkv_fused(
+    const float* __restrict__ pm, const float* __restrict__ x, float* __restrict__ out, int B,
+    int S, int H, float scale) {
+  constexpr int TS = KvTile<D>::kStride;
+  constexpr int NB = D / 32;
+  __shared__ __align__(16) float xt[2][kAttnK * TS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int BH = B * H;
+  const int kb = static_cast<int>(blockIdx.x) / BH;  // early key blocks first
+  const int bh = static_cast<int>(blockIdx.x) % BH;
+  const int b = bh / H, hh = bh % H;
+  const int64_t ld = static_cast<int64_t>(H) * D;
+  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
+  const float* xh = x + head;
+  float* oh = out + head;
+  const float* ph = pm + static_cast<int64_t>(bh) * S * S;
+  const int k0 = kb * kAttnQ;
+  const int kw = k0 + 32 * w;  // first key of this wavefront
+  const int j = kw + r;        // this lane's key
+  const bool col_ok = j < S;
+  const int ntiles = (S + kAttnK - 1) / kAttnK;
+  const int t0 = k0 / kAttnK;       // the workgroup's first query tile
+  const int tw = kw / kAttnK;       // this wavefront's first query tile
+  floatx16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
+  // Column entries (i = 32t + 8*(e/4) + 4h + e%4, j) of query tile t.
+  auto load_col = [&](int t, float (&g)[16]) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int ii = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+      g[e] = (col_ok && t >= tw && ii < S && ii >= j) ? ph[static_cast<int64_t>(ii) * S + j] : 0.0f;
+    }
+  };
+  KvTile<D> xs;
+  float g[16], gn[16];
+  xs.load(xh, ld, t0 * kAttnK, S);
+  load_col(t0, g);
+  xs.store(xt[0]);
+  __syncthreads();
+  for (int t = t0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) {
+      xs.load(xh, ld, (t + 1) * kAttnK, S);
+      load_col(t + 1, gn);
+    }
+    if (t >= tw && kw < S) {
+      if constexpr (SCALED) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) g[e] = g[e] * scale;
+      }
+      const float* xtile = xt[(t - t0) & 1];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float* xrow = xtile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xrow[32 * nb], g[e], acc[nb], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) {
+      xs.store(xt[(t + 1 - t0) & 1]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) g[e] = gn[e];
+    }
+    __syncthreads();
+  }
+  if (col_ok) {
+    float* orow = oh + static_cast<int64_t>(j) * ld;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
+            make_float4(acc[nb][4 * q4], acc[nb][4 * q4 + 1], acc[nb][4 * q4 + 2],
+                        acc[nb][4 * q4 + 3]);
+  }
+}
+
+// The fused kernels' shape gate: d in {64, 128}, S % 4 == 0 (16-byte P
+// rows), 16-byte aligned operands, 32-bit grid indices.
+bool FusedEligible(std::initializer_list<const float*> ptrs, size_t B, size_t S, size_t H,
+                   size_t d) {
   if (d != 64 && d != 128) return false;
   if (S == 0 || S % 4 != 0) return false;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(probs))
-    return false;
+  for (const float* p : ptrs)
+    if (!aligned16(p)) return false;
   const size_t blocks = B * H * ((S + kAttnQ - 1) / kAttnQ);
   return B * H <= 0x7FFFFFFFu && S <= 0x7FFFFFFFu && blocks <= 0x7FFFFFFFu &&
          B * S * H * d < (size_t{1} << 62);
+}
+
+unsigned FusedBlocks(size_t B, size_t S, size_t H) {
+  return static_cast<unsigned>(B * H * ((S + kAttnQ - 1) / kAttnQ));
 }
 
 }  // namespace
@@ -294,8 +560,8 @@ size_t AttnWorkspace(size_t, size_t, size_t, size_t) { return 0; }
 Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* probs, size_t B,
                size_t S, size_t H, size_t d, const Ctx& c) {
   if (B * S * H * d == 0) return Status::Ok();
-  if (FusedFwdEligible(q, k, v, o, probs, B, S, H, d)) {
-    const unsigned blocks = static_cast<unsigned>(B * H * ((S + kAttnQ - 1) / kAttnQ));
+  if (FusedEligible({q, k, v, o, probs}, B, S, H, d)) {
+    const unsigned blocks = FusedBlocks(B, S, H);
     const float inv = InvSqrtD(static_cast<int64_t>(d));
     if (d == 128)
       hipLaunchKernelGGL(attn_fwd_fused<128>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
@@ -337,6 +603,17 @@ Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* 
 
 Status AttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S, size_t H,
               size_t d, const Ctx& c) {
+  if (B * S * H * d == 0) return Status::Ok();
+  if (FusedEligible({dout, v, dp}, B, S, H, d)) {
+    const int iB = static_cast<int>(B), iS = static_cast<int>(S), iH = static_cast<int>(H);
+    if (d == 128)
+      hipLaunchKernelGGL(attn_dp_fused<128>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
+                         c.stream, dout, v, dp, iB, iS, iH);
+    else
+      hipLaunchKernelGGL(attn_dp_fused<64>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
+                         c.stream, dout, v, dp, iB, iS, iH);
+    return LaunchStatus("AttnDP");
+  }
   const Geo g = MakeGeo(B, S, H, d);
   GemmDesc x;
   x.A = dout; x.B = v; x.C = dp;
@@ -352,6 +629,17 @@ Status AttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S, 
 
 Status AttnDV(const float* probs, const float* dout, float* dv, size_t B, size_t S, size_t H,
               size_t d, const Ctx& c) {
+  if (B * S * H * d == 0) return Status::Ok();
+  if (FusedEligible({probs, dout, dv}, B, S, H, d)) {
+    const int iB = static_cast<int>(B), iS = static_cast<int>(S), iH = static_cast<int>(H);
+    if (d == 128)
+      hipLaunchKernelGGL((attn_dkv_fused<128, false>), dim3(FusedBlocks(B, S, H)),
+                         dim3(kAttnThreads), 0, c.stream, probs, dout, dv, iB, iS, iH, 1.0f);
+    else
+      hipLaunchKernelGGL((attn_dkv_fused<64, false>), dim3(FusedBlocks(B, S, H)),
+                         dim3(kAttnThreads), 0, c.stream, probs, dout, dv, iB, iS, iH, 1.0f);
+    return LaunchStatus("AttnDV");
+  }
   const Geo g = MakeGeo(B, S, H, d);
   GemmDesc x;  // dV(j, c) = sum_{i >= j} P(i, j) dO(i, c): A(m=j, k=i) = P[i][j]
   x.A = probs; x.B = dout; x.C = dv;
@@ -367,6 +655,18 @@ Status AttnDV(const float* probs, const float* dout, float* dv, size_t B, size_t
 
 Status AttnDQ(const float* ds, const float* k, float* dq, size_t B, size_t S, size_t H, size_t d,
               const Ctx& c) {
+  if (B * S * H * d == 0) return Status::Ok();
+  if (FusedEligible({ds, k, dq}, B, S, H, d)) {
+    const int iB = static_cast<int>(B), iS = static_cast<int>(S), iH = static_cast<int>(H);
+    const float inv = InvSqrtD(static_cast<int64_t>(d));
+    if (d == 128)
+      hipLaunchKernelGGL(attn_dq_fused<128>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
+                         c.stream, ds, k, dq, iB, iS, iH, inv);
+    else
+      hipLaunchKernelGGL(attn_dq_fused<64>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
+                         c.stream, ds, k, dq, iB, iS, iH, inv);
+    return LaunchStatus("AttnDQ");
+  }
   const Geo g = MakeGeo(B, S, H, d);
   GemmDesc x;  // dQ(i, c) = sum_{j <= i} dS(i, j) K(j, c) / sqrt(d)
   x.A = ds; x.B = k; x.C = dq;
@@ -383,6 +683,18 @@ Status AttnDQ(const float* ds, const float* k, float* dq, size_t B, size_t S, si
 
 Status AttnDK(const float* ds, const float* q, float* dk, size_t B, size_t S, size_t H, size_t d,
               const Ctx& c) {
+  if (B * S * H * d == 0) return Status::Ok();
+  if (FusedEligible({ds, q, dk}, B, S, H, d)) {
+    const int iB = static_cast<int>(B), iS = static_cast<int>(S), iH = static_cast<int>(H);
+    const float inv = InvSqrtD(static_cast<int64_t>(d));
+    if (d == 128)
+      hipLaunchKernelGGL((attn_dkv_fused<128, true>), dim3(FusedBlocks(B, S, H)),
+                         dim3(kAttnThreads), 0, c.stream, ds, q, dk, iB, iS, iH, inv);
+    else
+      hipLaunchKernelGGL((attn_dkv_fused<64, true>), dim3(FusedBlocks(B, S, H)),
+                         dim3(kAttnThreads), 0, c.stream, ds, q, dk, iB, iS, iH, inv);
+    return LaunchStatus("AttnDK");
+  }
   const Geo g = MakeGeo(B, S, H, d);
   GemmDesc x;  // dK(j, c) = sum_{i >= j} dS(i, j) Q(i, c) / sqrt(d)
   x.A = ds; x.B = q; x.C = dk;
