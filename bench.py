@@ -171,7 +171,7 @@ def main():
         g[1].append(i)
     (dom_op, dom_shape, dom_tile), (dom_total, dom_idx) = max(groups.items(), key=lambda kv: kv[1][0])
     log("top (op, shape, tile) groups by step share:")
-    for (op, shape, tile), (tot, idx) in sorted(groups.items(), key=lambda kv: -kv[1][0])[:20]:
+    for (op, shape, tile), (tot, idx) in sorted(groups.items(), key=lambda kv: -kv[1][0])[:40]:
         r0 = rows[idx[0]]
         rate = (f"{r0['flops'] * len(idx) / (tot * 1e-3) / 1e12:7.1f} TFLOP/s" if r0["flops"]
                 else f"{r0['bytes'] * len(idx) / (tot * 1e-3) / 1e9:7.0f} GB/s")

@@ -1002,6 +1002,8 @@ class Engine {
 
   std::string GemmChoice(int program, size_t idx) const {
     const GemmPlan& p = plans_[program][idx];
+    if (p.cfg == GemmSkinnyConfig())
+      return SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])));
     return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits);
   }
 

@@ -74,8 +74,9 @@ namespace {
 // its query's P row.
 //
 // Pass 1 walks the causal key tiles for the row maximum m and the exp-sum l
-// (online: l = l * exp(m_old - m_new) + sum exp(s - m_new)). Pass 2 recomputes
-// the scores, forms p = exp(s - m) * (1/l) (exact 0 for j > i), writes P
+// (online: l = l * exp(m_old - m_new) + sum exp(s - m_new)), in the base-2
+// domain on the hardware exp2. Pass 2 recomputes the scores, forms
+// p = exp(s - m) * (1/l) (exact 0 for j > i), writes P
 // once and accumulates O^T = V^T P^T with the probabilities straight from
 // the score registers as the B operand (MFMA t's k index is the lane's own
 // accumulator element t). The row tail beyond the diagonal tile is written
@@ -114,6 +115,17 @@ struct KvTile {
     }
   }
 };
+
+// On a wavefront's diagonal key tile t, sets the entries of keys j > i (the
+// lane's query) to `fill`; every earlier tile is wholly inside the causal
+// half (and a key >= S can only fall in the diagonal tile of a valid query).
+__device__ __forceinline__ void MaskDiagonal(floatx16& sc, int t, int i, int h, float fill) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+    if (j > i) sc[e] = fill;
+  }
+}
 
 // S^T tile (32 keys x 32 queries) from the LDS K tile and the lane's Q
 // fragments: MFMA (g, jj) takes feature 8g + 4h + jj on both operands. Two
@@ -169,6 +181,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   const int ic = min(i, S - 1);
   const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
   const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
+  // Scores are kept in the base-2 domain: s2 = dot * (1/sqrt(d)) * log2(e),
+  // so exp(s - max) is the hardware exp2 of s2 - max2.
+  const float c2 = inv_sqrt_d * 1.44269504088896340736f;
 
   float4 qf[D / 8];
 #pragma unroll
@@ -185,20 +200,18 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     if (t + 1 < tiles_wg) ks.load(kh, ld, (t + 1) * kAttnK, S);
     if (t < tiles_w) {
       floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = sc[e] * c2;
+      if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, -__builtin_inff());
       float tmax = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
-        const float sv = j > i ? -__builtin_inff() : sc[e] * inv_sqrt_d;
-        sc[e] = sv;
-        tmax = fmaxf(tmax, sv);
-      }
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float mn = fmaxf(m, tmax);
-      const float alpha = m == -__builtin_inff() ? 0.0f : expf(m - mn);
+      const float alpha = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
       float ssum = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) ssum += expf(sc[e] - mn);
+      for (int e = 0; e < 16; ++e) ssum += __builtin_amdgcn_exp2f(sc[e] - mn);
       ssum += __shfl_xor(ssum, 32, 64);
       l = l * alpha + ssum;
       m = mn;
@@ -229,10 +242,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     if (t < tiles_w) {
       floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
-        sc[e] = j > i ? 0.0f : expf(sc[e] * inv_sqrt_d - m) * inv_l;
-      }
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(sc[e] * c2 - m) * inv_l;
+      if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, 0.0f);
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int j = t * kAttnK + 8 * q4 + 4 * h;
@@ -337,13 +348,13 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dp_fused(
     if (t + 1 < tiles_wg) vs.load(vh, ld, (t + 1) * kAttnK, S);
     if (t < tiles_w) {
       floatx16 sc = ScoreTile<D>(vt[t & 1], qf, h, r);
+      if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, 0.0f);
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int j = t * kAttnK + 8 * q4 + 4 * h;
         if (row_ok && j < S)
           *reinterpret_cast<float4*>(prow + j) =
-              make_float4(j + 0 > i ? 0.0f : sc[4 * q4], j + 1 > i ? 0.0f : sc[4 * q4 + 1],
-                          j + 2 > i ? 0.0f : sc[4 * q4 + 2], j + 3 > i ? 0.0f : sc[4 * q4 + 3]);
+              make_float4(sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]);
       }
     }
     if (t + 1 < tiles_wg) vs.store(vt[(t + 1) & 1]);
@@ -421,10 +432,12 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
         g[4 * q4 + 2] = x[q4].z * inv_sqrt_d;
         g[4 * q4 + 3] = x[q4].w * inv_sqrt_d;
       }
+      if (t == tiles_w - 1) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (j > i) g[e] = 0.0f;
+        for (int e = 0; e < 16; ++e) {
+          const int j = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (j > i) g[e] = 0.0f;
+        }
       }
       const float* ktile = kt[t & 1];
 #pragma unroll

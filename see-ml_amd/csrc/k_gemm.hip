@@ -44,11 +44,24 @@ bool VecOk(const void* base, int64_t ld, int64_t sb, int64_t sh, int64_t contigu
 
 }  // namespace
 
-int GemmConfigCount() { return kNumCfgs; }
-const char* GemmConfigName(int cfg) { return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?"; }
+// Plan indices 0..kNumCfgs-1 are the MFMA tile configs; kNumCfgs selects the
+// skinny (LoRA-shaped) kernels where the shape admits them.
+int GemmSkinnyConfig() { return kNumCfgs; }
+int GemmConfigCount() { return kNumCfgs + 1; }
+const char* GemmConfigName(int cfg) {
+  if (cfg == kNumCfgs) return "skinny";
+  return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?";
+}
 
 GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
   GemmPlan plan;
+  const bool skinny = SkinnyKindOf(d) != SkinnyKind::kNone;
+  if (skinny && (forced_cfg == kNumCfgs || forced_cfg < 0)) {
+    plan.cfg = kNumCfgs;
+    plan.splits = 1;
+    plan.ws_bytes = SkinnyWorkspace(d);
+    return plan;
+  }
   if (forced_cfg >= 0 && forced_cfg < kNumCfgs) {
     plan.cfg = forced_cfg;
   } else if (d.N <= 32 && d.M > 32) {
@@ -83,6 +96,11 @@ GemmPlan PlanGemm(const GemmDesc& d) { return PlanGemmWith(d, -1, -1); }
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
+  if (plan.cfg == kNumCfgs) {
+    if (ctx.ws_bytes < SkinnyWorkspace(d))
+      return Status::Fail(kUnitEngine, "Gemm: workspace too small for the skinny kernel");
+    return LaunchSkinny(d, ctx);
+  }
   if (plan.cfg < 0 || plan.cfg >= kNumCfgs) return Status::Fail(kUnitEngine, "Gemm: bad tile config");
   if (plan.splits > 1 && (d.batch != 1 || d.causal != Causal::kNone))
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");

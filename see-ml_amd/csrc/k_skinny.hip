@@ -1,0 +1,509 @@
+// k_skinny.hip — the LoRA-shaped GEMMs: one dimension is the adapter rank r
+// (8..64), the others are a token count and a model width. They are bound
+// by streaming the one large operand (reads) or the large output (writes)
+// through HBM, not by the matrix cores, so each has its own kernel shaped
+// for full-width 16-byte traffic. Serves GemmNN / GemmNT / GemmTN of
+// runtime/executor/gemm.cc:173-200 at these shapes (the LoRA graft's
+// t = x A, u = t B and their VJPs, compiler/.../lora_grafter.cc:130-159).
+//
+//   outer   K <= 64 (u = t B, dx = dt A^T): C[M,N] written once. Computed
+//           transposed, C^T = B^T A^T, with v_mfma_f32_16x16x4_f32, so the
+//           four lanes of a row hold 16 consecutive outputs and C is stored
+//           as 64-byte row runs.
+//   rowdot  N <= 64, A k-contiguous (t = x A, dt = du B^T): the [M, K]
+//           operand is read once. 16 rows per workgroup with
+//           v_mfma_f32_16x16x4_f32 (lane quarter q supplies k = 16g + 4q + j,
+//           one float4 per group); the eight wavefronts take consecutive
+//           slices of K, prefetching one batch ahead, and their partial tiles
+//           are summed in wavefront order through LDS.
+//   colsum  TN with min(M, N) <= 64 (dA = x^T dt, dB = t^T du): the large
+//           [K, W] operand is read once, row by row, as float4 runs (MFMA c4
+//           of v_mfma_f32_16x16x4_f32 takes component c4 of the lane's four
+//           columns). A workgroup owns 64 columns and a k-group; its four
+//           wavefronts are summed in order through LDS into one partial per
+//           k-group, and a second kernel sums the k-group partials in group
+//           order and applies the epilogue.
+//
+// Every reduction has a fixed order: results are bit-identical run to run.
+#include "device_common.h"
+#include "kernels.h"
+
+#include <algorithm>
+
+namespace seeml_hip {
+
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+
+struct SkArgs {
+  const float* A;
+  const float* B;
+  float* C;
+  float* ws;
+  int64_t M, N, K, lda, ldb, ldc;
+  float alpha;
+  int accumulate;
+  const float* bias;
+  int act;
+  int b_kc;
+  // colsum
+  int64_t W, R;        // large and small output extents
+  int big_is_m;        // the large operand is A (W = M) or B (W = N)
+  int groups;          // k-groups (partials)
+  int64_t k_per_group;
+};
+
+__device__ __forceinline__ float Epilogue(const SkArgs& p, int64_t m, int64_t n, float acc) {
+  float val = p.alpha * acc;
+  if (p.accumulate) val = p.C[m * p.ldc + n] + val;
+  if (p.bias) val = val + p.bias[n];
+  return dev_act(p.act, val);
+}
+
+// ---- outer (small K) ----------------------------------------------------------
+//
+// C^T blocks of 16 n x 16 m with v_mfma_f32_16x16x4_f32: lane (q, c) supplies
+// A[m + c][16g + 4q + j] (one float4 per k group) and B(16g + 4q + j, n + c)
+// for MFMA j, and holds C[m + c][n + 4q .. 4q + 3] — the four lanes of a row
+// cover 64 contiguous bytes, so every store instruction writes 16 rows x 64 B
+// (32-byte runs measured ~30% slower on this write-bound shape). A wavefront
+// owns kOuterRB row blocks of 16 (their A fragments stay in registers) and
+// walks 16-column steps, each B fragment serving all its row blocks; the next
+// step's B fragment is loaded while the current one computes. A workgroup is
+// 4 wavefronts side by side in n: 16 * kOuterRB rows x 4 * kOuterWN columns.
+
+constexpr int kOuterRB = 4;     // row blocks of 16 per wavefront
+constexpr int kOuterWN = 128;   // columns per wavefront
+constexpr int kOuterRows = 16 * kOuterRB;
+constexpr int kOuterN = 4 * kOuterWN;
+
+template <int KG>  // k groups of 16: ceil(K / 16)
+__device__ __forceinline__ void OuterLoadB(const SkArgs& p, int64_t n, int q, float4 (&bf)[KG]) {
+#pragma unroll
+  for (int g = 0; g < KG; ++g) {
+    const int64_t k0 = 16 * g + 4 * q;
+    if (p.b_kc) {
+      bf[g] = k0 < p.K ? *reinterpret_cast<const float4*>(p.B + n * p.ldb + k0)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+      bf[g].x = k0 + 0 < p.K ? p.B[(k0 + 0) * p.ldb + n] : 0.0f;
+      bf[g].y = k0 + 1 < p.K ? p.B[(k0 + 1) * p.ldb + n] : 0.0f;
+      bf[g].z = k0 + 2 < p.K ? p.B[(k0 + 2) * p.ldb + n] : 0.0f;
+      bf[g].w = k0 + 3 < p.K ? p.B[(k0 + 3) * p.ldb + n] : 0.0f;
+    }
+  }
+}
+
+template <int KG>
+__global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kOuterRows;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kOuterN + w * kOuterWN;
+  if (n0 >= p.N) return;
+  float4 af[kOuterRB][KG];
+#pragma unroll
+  for (int rb = 0; rb < kOuterRB; ++rb) {
+    const int64_t m = std::min<int64_t>(m0 + 16 * rb + c, p.M - 1);
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      const int64_t k0 = 16 * g + 4 * q;
+      af[rb][g] = k0 < p.K ? *reinterpret_cast<const float4*>(p.A + m * p.lda + k0)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+  const int64_t nend = std::min<int64_t>(p.N, n0 + kOuterWN);
+  float4 bf[KG], bn[KG];
+  OuterLoadB<KG>(p, std::min<int64_t>(n0 + c, p.N - 1), q, bf);
+  for (int64_t nb = n0; nb < nend; nb += 16) {
+    if (nb + 16 < nend) OuterLoadB<KG>(p, std::min<int64_t>(nb + 16 + c, p.N - 1), q, bn);
+    floatx4 acc[kOuterRB];
+#pragma unroll
+    for (int rb = 0; rb < kOuterRB; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < KG; ++g)
+#pragma unroll
+      for (int rb = 0; rb < kOuterRB; ++rb) {
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].x, af[rb][g].x, acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].y, af[rb][g].y, acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].z, af[rb][g].z, acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].w, af[rb][g].w, acc[rb], 0, 0, 0);
+      }
+    const int64_t n = nb + 4 * q;
+    if (n < p.N) {
+#pragma unroll
+      for (int rb = 0; rb < kOuterRB; ++rb) {
+        const int64_t mo = m0 + 16 * rb + c;
+        if (mo < p.M)
+          *reinterpret_cast<float4*>(p.C + mo * p.ldc + n) =
+              make_float4(Epilogue(p, mo, n + 0, acc[rb][0]), Epilogue(p, mo, n + 1, acc[rb][1]),
+                          Epilogue(p, mo, n + 2, acc[rb][2]), Epilogue(p, mo, n + 3, acc[rb][3]));
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < KG; ++g) bf[g] = bn[g];
+  }
+}
+
+// ---- rowdot (small N, A k-contiguous) -----------------------------------------
+
+constexpr int kRowdotM = 16;
+constexpr int kRowdotWaves = 8;   // wavefronts per workgroup, each a slice of K
+// k groups per batch (the next batch is in flight), fewer for wider N to stay
+// within the register file.
+constexpr int RowdotUnroll(int nb) { return nb == 1 ? 4 : (nb == 2 ? 2 : 1); }
+
+template <int NB>  // ceil(N / 16)
+__global__ __launch_bounds__(64 * kRowdotWaves) void skinny_rowdot(SkArgs p) {
+  constexpr int kRowdotUnroll = RowdotUnroll(NB);
+  __shared__ floatx4 red[kRowdotWaves][NB][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kRowdotM;
+  const int64_t m = std::min<int64_t>(m0 + c, p.M - 1);
+  const int64_t ngroups = (p.K + 15) / 16;
+  const int64_t per = (ngroups + kRowdotWaves - 1) / kRowdotWaves;
+  const int64_t gb = w * per, ge = std::min<int64_t>(gb + per, ngroups);
+  const float* arow = p.A + m * p.lda;
+  int64_t ncol[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) ncol[nb] = std::min<int64_t>(16 * nb + c, p.N - 1);
+  floatx4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto load = [&](int64_t g, float4& a, float4 (&b)[NB]) {
+    const int64_t k0 = 16 * g + 4 * q;
+    const bool in = g < ge && k0 < p.K;  // K % 4 == 0: a float4 is wholly in or out
+    a = in ? *reinterpret_cast<const float4*>(arow + k0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (p.b_kc) {
+        b[nb] = in ? *reinterpret_cast<const float4*>(p.B + ncol[nb] * p.ldb + k0)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      } else {
+        b[nb].x = in ? p.B[(k0 + 0) * p.ldb + ncol[nb]] : 0.0f;
+        b[nb].y = in ? p.B[(k0 + 1) * p.ldb + ncol[nb]] : 0.0f;
+        b[nb].z = in ? p.B[(k0 + 2) * p.ldb + ncol[nb]] : 0.0f;
+        b[nb].w = in ? p.B[(k0 + 3) * p.ldb + ncol[nb]] : 0.0f;
+      }
+    }
+  };
+  float4 a[kRowdotUnroll], b[kRowdotUnroll][NB];
+  float4 an[kRowdotUnroll], bn[kRowdotUnroll][NB];
+#pragma unroll
+  for (int u = 0; u < kRowdotUnroll; ++u) load(gb + u, a[u], b[u]);
+  for (int64_t g = gb; g < ge; g += kRowdotUnroll) {
+    if (g + kRowdotUnroll < ge)
+#pragma unroll
+      for (int u = 0; u < kRowdotUnroll; ++u) load(g + kRowdotUnroll + u, an[u], bn[u]);
+#pragma unroll
+    for (int u = 0; u < kRowdotUnroll; ++u)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u][nb].x, acc[nb], 0, 0, 0);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u][nb].y, acc[nb], 0, 0, 0);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u][nb].z, acc[nb], 0, 0, 0);
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u][nb].w, acc[nb], 0, 0, 0);
+      }
+#pragma unroll
+    for (int u = 0; u < kRowdotUnroll; ++u) {
+      a[u] = an[u];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) b[u][nb] = bn[u][nb];
+    }
+  }
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) red[w][nb][lane] = acc[nb];
+  __syncthreads();
+  if (w != 0) return;
+  // Lane (q, c) element i: C[m0 + 4q + i][16 nb + c]; wavefront partials in order.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    floatx4 s = red[0][nb][lane];
+#pragma unroll
+    for (int ww = 1; ww < kRowdotWaves; ++ww) s += red[ww][nb][lane];
+    const int64_t n = 16 * nb + c;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t mo = m0 + 4 * q + i;
+      if (mo < p.M) p.C[mo * p.ldc + n] = Epilogue(p, mo, n, s[i]);
+    }
+  }
+}
+
+// ---- colsum (TN, small M or N) --------------------------------------------------
+//
+// P[w][n'] = sum_k X[k][w] Y[k][n'] with v_mfma_f32_16x16x4_f32: lane (q, c)
+// loads the float4 X[k0 + q][w0 + 4c .. 4c + 3] (4 rows x 256 contiguous
+// bytes per instruction) and Y[k0 + q][16 nb + c]; MFMA c4 takes component c4,
+// so its row i is column w0 + 4i + c4. A wavefront owns 64 columns and a run
+// of k quads (the next batch in flight); the workgroup's four wavefronts are
+// summed in order through LDS into one partial per k-group.
+
+constexpr int kColW = 64;  // columns w per workgroup
+
+template <int NBN>  // ceil(R / 16)
+__global__ __launch_bounds__(kThreads) void skinny_colsum(SkArgs p) {
+  __shared__ floatx4 red[4][NBN][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kColW;
+  const int g = static_cast<int>(blockIdx.y);
+  const float* X = p.big_is_m ? p.A : p.B;  // X[k][w]
+  const float* Y = p.big_is_m ? p.B : p.A;  // Y[k][n']
+  const int64_t ldx = p.big_is_m ? p.lda : p.ldb;
+  const int64_t ldy = p.big_is_m ? p.ldb : p.lda;
+  const int64_t kb0 = static_cast<int64_t>(g) * p.k_per_group;
+  const int64_t ke0 = std::min<int64_t>(p.K, kb0 + p.k_per_group);
+  const int64_t span = ke0 > kb0 ? ke0 - kb0 : 0;
+  const int64_t sub = ((span + 15) / 16) * 4;  // k per wavefront, whole quads
+  const int64_t kb = kb0 + w * sub, ke = std::min<int64_t>(ke0, kb + sub);
+  const int64_t wl = w0 + 4 * c;
+  const bool w_ok = wl < p.W;  // W % 4 == 0: the float4 is wholly in or out
+  floatx4 acc[4][NBN];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) acc[c4][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int U = 4;  // k quads per batch; the next batch is in flight
+  auto load = [&](int64_t k4, float4 (&x)[U], float (&y)[U][NBN]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = k4 + 4 * u + q;
+      const bool kin = k < ke;
+      x[u] = kin && w_ok ? *reinterpret_cast<const float4*>(X + k * ldx + wl)
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) {
+        const int64_t n = 16 * nb + c;
+        y[u][nb] = kin && n < p.R ? Y[k * ldy + n] : 0.0f;
+      }
+    }
+  };
+  float4 x[U], xn[U];
+  float y[U][NBN], yn[U][NBN];
+  load(kb, x, y);
+  for (int64_t k4 = kb; k4 < ke; k4 += 4 * U) {
+    if (k4 + 4 * U < ke) load(k4 + 4 * U, xn, yn);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) {
+        acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, y[u][nb], acc[0][nb], 0, 0, 0);
+        acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, y[u][nb], acc[1][nb], 0, 0, 0);
+        acc[2][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, y[u][nb], acc[2][nb], 0, 0, 0);
+        acc[3][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, y[u][nb], acc[3][nb], 0, 0, 0);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      x[u] = xn[u];
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) y[u][nb] = yn[u][nb];
+    }
+  }
+  // Wavefront partials summed in order 0 + 1 + 2 + 3 through LDS.
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) {
+    __syncthreads();
+    if (w != 0)
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) red[w][nb][lane] = acc[c4][nb];
+    __syncthreads();
+    if (w == 0)
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb) {
+        acc[c4][nb] += red[1][nb][lane];
+        acc[c4][nb] += red[2][nb][lane];
+        acc[c4][nb] += red[3][nb][lane];
+      }
+  }
+  if (w != 0) return;
+  // Element i of acc[c4][nb] at lane (q, c): w = w0 + 4*(4q + i) + c4, n' = 16 nb + c.
+  // Partial layout: ws[g][w][n'].
+  float* part = p.ws + static_cast<int64_t>(g) * p.W * p.R;
+#pragma unroll
+  for (int nb = 0; nb < NBN; ++nb) {
+    const int64_t n = 16 * nb + c;
+    if (n >= p.R) continue;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t wi = w0 + 4 * (4 * q + i) + c4;
+        if (wi < p.W) part[wi * p.R + n] = acc[c4][nb][i];
+      }
+  }
+}
+
+// Sums the k-group partials in group order and writes C with the epilogue.
+// Thread t owns outputs 4t .. 4t + 3 of the [W, R] partial layout (R % 4 == 0
+// here, so they share one w); the group loads are issued four at a time.
+__global__ __launch_bounds__(kThreads) void skinny_colsum_finish(SkArgs p) {
+  const int64_t total = p.W * p.R, nq = total / 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < nq; t += stride) {
+    float4 s = *reinterpret_cast<const float4*>(p.ws + 4 * t);
+    int g = 1;
+    for (; g + 3 < p.groups; g += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = *reinterpret_cast<const float4*>(p.ws + static_cast<int64_t>(g + u) * total + 4 * t);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s.x += v[u].x;
+        s.y += v[u].y;
+        s.z += v[u].z;
+        s.w += v[u].w;
+      }
+    }
+    for (; g < p.groups; ++g) {
+      const float4 v = *reinterpret_cast<const float4*>(p.ws + static_cast<int64_t>(g) * total + 4 * t);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+    const int64_t wi = (4 * t) / p.R, n0 = (4 * t) % p.R;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t m = p.big_is_m ? wi : n0 + e, nn = p.big_is_m ? n0 + e : wi;
+      p.C[m * p.ldc + nn] = Epilogue(p, m, nn, sv[e]);
+    }
+  }
+}
+
+// Reference order of the group sum for R % 4 != 0: one output per thread.
+__global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
+  const int64_t total = p.W * p.R;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < total;
+       idx += stride) {
+    float s = p.ws[idx];
+    for (int g = 1; g < p.groups; ++g) s += p.ws[static_cast<int64_t>(g) * total + idx];
+    const int64_t wi = idx / p.R, n = idx % p.R;
+    const int64_t m = p.big_is_m ? wi : n, nn = p.big_is_m ? n : wi;
+    p.C[m * p.ldc + nn] = Epilogue(p, m, nn, s);
+  }
+}
+
+bool Vec4(const void* base, int64_t ld) { return aligned16(base) && ld % 4 == 0; }
+
+int64_t ColsumGroups(int64_t W, int64_t K) {
+  const int64_t wtiles = (W + kColW - 1) / kColW;
+  const int64_t want = std::max<int64_t>(1, (512 + wtiles - 1) / wtiles);
+  return std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(K / 128, 64)));
+}
+
+}  // namespace
+
+SkinnyKind SkinnyKindOf(const GemmDesc& d) {
+  if (d.batch != 1 || d.heads != 1 || d.causal != Causal::kNone || d.b_int8) return SkinnyKind::kNone;
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return SkinnyKind::kNone;
+  if (d.M > (int64_t{1} << 40) || d.N > (int64_t{1} << 40)) return SkinnyKind::kNone;
+  const float* A = static_cast<const float*>(d.A);
+  const float* B = static_cast<const float*>(d.B);
+  if (d.a_kc) {
+    const bool b_ok = !d.b_kc || Vec4(B, d.ldb);
+    if (!Vec4(A, d.lda) || d.K % 4 != 0 || !b_ok) return SkinnyKind::kNone;
+    // small K: the output C is the stream
+    if (d.K <= 64 && d.M >= 64 && d.N >= 64 && d.N % 4 == 0 && Vec4(d.C, d.ldc))
+      return SkinnyKind::kOuter;
+    // small N: A is the stream
+    if (d.N <= 64 && d.K >= 256 && d.M >= 64) return SkinnyKind::kRowDot;
+    return SkinnyKind::kNone;
+  }
+  if (!d.b_kc && d.K >= 256) {
+    // TN: A(m,k) = A[k*lda + m], B(k,n) = B[k*ldb + n]
+    if (d.N <= 64 && d.M >= 128 && d.M % 4 == 0 && Vec4(A, d.lda)) return SkinnyKind::kColSum;
+    if (d.M <= 64 && d.N >= 128 && d.N % 4 == 0 && Vec4(B, d.ldb)) return SkinnyKind::kColSum;
+  }
+  return SkinnyKind::kNone;
+}
+
+const char* SkinnyKindName(SkinnyKind k) {
+  switch (k) {
+    case SkinnyKind::kOuter: return "skinny/outer";
+    case SkinnyKind::kRowDot: return "skinny/rowdot";
+    case SkinnyKind::kColSum: return "skinny/colsum";
+    default: return "skinny/none";
+  }
+}
+
+size_t SkinnyWorkspace(const GemmDesc& d) {
+  if (SkinnyKindOf(d) != SkinnyKind::kColSum) return 0;
+  const bool big_m = d.N <= 64 && d.M >= 128;
+  const int64_t W = big_m ? d.M : d.N, R = big_m ? d.N : d.M;
+  return static_cast<size_t>(ColsumGroups(W, d.K)) * W * R * sizeof(float);
+}
+
+Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) {
+  const SkinnyKind kind = SkinnyKindOf(d);
+  if (kind == SkinnyKind::kNone) return Status::Fail(kUnitEngine, "Gemm: shape is not skinny");
+  SkArgs a{};
+  a.A = static_cast<const float*>(d.A);
+  a.B = static_cast<const float*>(d.B);
+  a.C = d.C;
+  a.ws = static_cast<float*>(ctx.ws);
+  a.M = d.M; a.N = d.N; a.K = d.K;
+  a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
+  a.alpha = d.alpha;
+  a.accumulate = d.accumulate ? 1 : 0;
+  a.bias = d.bias;
+  a.act = d.act;
+  a.b_kc = d.b_kc ? 1 : 0;
+  if (kind == SkinnyKind::kOuter) {
+    const int64_t gx = (d.M + kOuterRows - 1) / kOuterRows, gy = (d.N + kOuterN - 1) / kOuterN;
+    if (gx > 0x7FFFFFFF || gy > 65535) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+    switch ((d.K + 15) / 16) {
+      case 1: hipLaunchKernelGGL(skinny_outer<1>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+      case 2: hipLaunchKernelGGL(skinny_outer<2>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+      default: hipLaunchKernelGGL(skinny_outer<4>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+    }
+    return LaunchStatus("Gemm(skinny outer)");
+  }
+  if (kind == SkinnyKind::kRowDot) {
+    const int64_t gx = (d.M + kRowdotM - 1) / kRowdotM;
+    if (gx > 0x7FFFFFFF) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+    const dim3 grid(static_cast<unsigned>(gx)), block(64 * kRowdotWaves);
+    switch ((d.N + 15) / 16) {
+      case 1: hipLaunchKernelGGL(skinny_rowdot<1>, grid, block, 0, ctx.stream, a); break;
+      case 2: hipLaunchKernelGGL(skinny_rowdot<2>, grid, block, 0, ctx.stream, a); break;
+      default: hipLaunchKernelGGL(skinny_rowdot<4>, grid, block, 0, ctx.stream, a); break;
+    }
+    return LaunchStatus("Gemm(skinny rowdot)");
+  }
+  a.big_is_m = (d.N <= 64 && d.M >= 128) ? 1 : 0;
+  a.W = a.big_is_m ? d.M : d.N;
+  a.R = a.big_is_m ? d.N : d.M;
+  a.groups = static_cast<int>(ColsumGroups(a.W, d.K));
+  a.k_per_group = (d.K + a.groups - 1) / a.groups;
+  const size_t need = static_cast<size_t>(a.groups) * a.W * a.R * sizeof(float);
+  if (ctx.ws_bytes < need) return Status::Fail(kUnitEngine, "Gemm: workspace too small for skinny colsum");
+  const int64_t gx = (a.W + kColW - 1) / kColW;
+  if (gx > 0x7FFFFFFF) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(a.groups));
+  switch ((a.R + 15) / 16) {
+    case 1: hipLaunchKernelGGL(skinny_colsum<1>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+    case 2: hipLaunchKernelGGL(skinny_colsum<2>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+    default: hipLaunchKernelGGL(skinny_colsum<4>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+  }
+  if (Status s = LaunchStatus("Gemm(skinny colsum)"); !s) return s;
+  if (a.R % 4 == 0 && aligned16(ctx.ws))
+    hipLaunchKernelGGL(skinny_colsum_finish, dim3(grid_for(static_cast<size_t>(a.W * a.R / 4), kThreads, 4096)),
+                       dim3(kThreads), 0, ctx.stream, a);
+  else
+    hipLaunchKernelGGL(skinny_colsum_finish1, dim3(grid_for(static_cast<size_t>(a.W * a.R), kThreads, 4096)),
+                       dim3(kThreads), 0, ctx.stream, a);
+  return LaunchStatus("Gemm(skinny colsum finish)");
+}
+
+}  // namespace seeml_hip

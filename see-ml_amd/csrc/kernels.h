@@ -80,6 +80,18 @@ int GemmConfigCount();
 const char* GemmConfigName(int cfg);
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);
 
+// LoRA-shaped GEMMs (k_skinny.hip): one extent is the adapter rank. kOuter:
+// K <= 64 (the output is the HBM stream); kRowDot: N <= 64 with A
+// k-contiguous (A is the stream); kColSum: TN with min(M, N) <= 64 (the
+// large [K, W] operand is the stream; k-group partials in the workspace).
+enum class SkinnyKind : int { kNone = 0, kOuter = 1, kRowDot = 2, kColSum = 3 };
+SkinnyKind SkinnyKindOf(const GemmDesc& d);
+const char* SkinnyKindName(SkinnyKind k);
+size_t SkinnyWorkspace(const GemmDesc& d);
+Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx);
+// The plan index that selects the skinny kernels (one past the tile configs).
+int GemmSkinnyConfig();
+
 // Row-major convenience forms of the reference's GEMM family.
 GemmDesc GemmNNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
 GemmDesc GemmNTDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);

@@ -105,6 +105,59 @@ def test_gemm_every_tile_config_and_split(env, orc, layout):
             assert rel_err(env.H(out), want) <= TOL_STEP, (cfg, splits)
 
 
+# LoRA-shaped GEMMs take the skinny kernels (outer: K <= 64; rowdot: N <= 64
+# with A k-contiguous; colsum: TN with min(M, N) <= 64), chosen by the
+# planner's heuristic; the same shapes forced onto a generic tile config give
+# the reference for run-to-run and path-to-path agreement.
+SKINNY = [
+    (0, 1000, 520, 16), (0, 256, 2048, 64), (0, 300, 132, 8), (0, 129, 68, 4), (1, 1000, 520, 16),
+    (1, 200, 256, 64), (0, 1000, 16, 2048), (0, 130, 64, 1024), (0, 77, 8, 260), (1, 300, 40, 512),
+    (1, 1000, 16, 2048), (2, 520, 16, 1000), (2, 16, 520, 1000), (2, 64, 1024, 300),
+    (2, 1024, 64, 2048), (2, 8, 132, 256), (2, 2048, 16, 4096),
+]
+
+
+@pytest.mark.parametrize("layout,M,N,K", SKINNY)
+def test_gemm_skinny(env, orc, layout, M, N, K):
+    A = rnd(M * K, 31)
+    B = rnd(K * N, 32)
+    want = np.zeros(M * N, f32)
+    fn = ("seeml_hip_gemm_nn", "seeml_hip_gemm_nt", "seeml_hip_gemm_tn")[layout]
+    if layout == 0:
+        orc.gemm_nn(A, B, want, M, N, K, None, 0)
+    elif layout == 1:
+        orc.gemm_nt(A, B, want, M, N, K)
+    else:
+        orc.gemm_tn(A, B, want, M, N, K)
+    out = env.T(np.full(M * N, np.nan, f32))
+    args = (env.T(A), env.T(B), out, M, N, K) + ((None, 0) if layout == 0 else ())
+    env.call(fn, *args)
+    got = env.H(out)
+    assert rel_err(got, want) <= TOL_STEP
+    env.call(fn, *args)
+    assert same_bits(env.H(out), got), "run-to-run bits differ"
+    skinny = env.L.seeml_hip_gemm_config_count() - 1
+    assert env.L.seeml_hip_gemm_config_name(skinny).decode() == "skinny"
+    forced = env.T(np.full(M * N, np.nan, f32))
+    env.call("seeml_hip_gemm_forced", layout, env.T(A), env.T(B), forced, M, N, K, skinny, 1)
+    assert same_bits(env.H(forced), got)
+    generic = env.T(np.full(M * N, np.nan, f32))
+    env.call("seeml_hip_gemm_forced", layout, env.T(A), env.T(B), generic, M, N, K, 0, 1)
+    assert rel_err(env.H(generic), got) <= TOL_STEP
+
+
+def test_gemm_skinny_epilogue(env, orc):
+    """GemmNN's fused bias/act epilogue through the skinny outer kernel."""
+    M, N, K = 600, 264, 16
+    A, B, bias = rnd(M * K, 41), rnd(K * N, 42), rnd(N, 43)
+    for act in range(4):
+        want = np.zeros(M * N, f32)
+        orc.gemm_nn(A, B, want, M, N, K, bias, act)
+        out = env.T(np.full(M * N, np.nan, f32))
+        env.call("seeml_hip_gemm_nn", env.T(A), env.T(B), out, M, N, K, env.T(bias), act)
+        assert rel_err(env.H(out), want) <= TOL_STEP, act
+
+
 def test_gemm_acc_and_q8(env, orc):
     M, N, K = 70, 90, 110
     A, B, C0 = rnd(M * K, 21), rnd(K * N, 22), rnd(M * N, 23)
