@@ -94,7 +94,8 @@ template <int D>
 struct KvTile {
   static constexpr int kStride = D + 4;  // floats per LDS row
   static constexpr int kPer = kAttnK * D / 4 / kAttnThreads;
-  float4 r[kPer];
+  // Plain floats (not float4 members), so the staged tile stays in VGPRs.
+  float r[kPer][4];
   // Rows j0.. of a [S, ld] head view; rows past S are clamped onto row S-1
   // (their keys are masked for every valid query).
   __device__ __forceinline__ void load(const float* __restrict__ base, int64_t ld, int j0, int S) {
@@ -103,7 +104,11 @@ struct KvTile {
       const int vi = static_cast<int>(threadIdx.x) + i * kAttnThreads;
       const int row = vi / (D / 4), c4 = vi % (D / 4);
       const int j = min(j0 + row, S - 1);
-      r[i] = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(j) * ld + 4 * c4);
+      const float4 q = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(j) * ld + 4 * c4);
+      r[i][0] = q.x;
+      r[i][1] = q.y;
+      r[i][2] = q.z;
+      r[i][3] = q.w;
     }
   }
   __device__ __forceinline__ void store(float* __restrict__ lds) const {
@@ -111,7 +116,8 @@ struct KvTile {
     for (int i = 0; i < kPer; ++i) {
       const int vi = static_cast<int>(threadIdx.x) + i * kAttnThreads;
       const int row = vi / (D / 4), c4 = vi % (D / 4);
-      *reinterpret_cast<float4*>(lds + row * kStride + 4 * c4) = r[i];
+      *reinterpret_cast<float4*>(lds + row * kStride + 4 * c4) =
+          make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
     }
   }
 };
@@ -140,16 +146,78 @@ __device__ __forceinline__ floatx16 ScoreTile(const float* __restrict__ kt,
     a1[e] = 0.0f;
   }
   const float* row = kt + r * KvTile<D>::kStride + 4 * h;
+  // Fragment reads run one group ahead of the MFMAs that consume them.
+  float4 kf[2];
+  kf[0] = *reinterpret_cast<const float4*>(row);
 #pragma unroll
   for (int g = 0; g < D / 8; ++g) {
-    const float4 kf = *reinterpret_cast<const float4*>(row + 8 * g);
+    if (g + 1 < D / 8) kf[(g + 1) & 1] = *reinterpret_cast<const float4*>(row + 8 * (g + 1));
+    const float4 f = kf[g & 1];
     floatx16& acc = (g & 1) ? a1 : a0;
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[g].x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[g].y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[g].z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[g].w, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.x, qf[g].x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.y, qf[g].y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.z, qf[g].z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.w, qf[g].w, acc, 0, 0, 0);
   }
   return a0 + a1;
+}
+
+// acc^T += tile^T P^T over one 32-key tile: for k index e (key kk = 8*(e/4)
+// + 4h + e%4 of the tile) the B operand is the lane's p[e], and MFMA nb's A
+// operand at lane (h, r) is tile[kk][NB*r + nb], i.e. MFMA nb's row i is
+// feature NB*i + nb. The NB values of one e are contiguous, read as one
+// 8- or 16-byte LDS access, one e ahead of the MFMAs that use them.
+template <int D>
+struct Frag {
+  static constexpr int NB = D / 32;
+  float v[NB];
+};
+
+template <int D>
+__device__ __forceinline__ Frag<D> ReadFrag(const float* __restrict__ tile, int e, int h, int r) {
+  constexpr int NB = D / 32;
+  const float* p = tile + (8 * (e >> 2) + 4 * h + (e & 3)) * KvTile<D>::kStride + NB * r;
+  Frag<D> f;
+  if constexpr (NB == 4) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    f.v[0] = x.x; f.v[1] = x.y; f.v[2] = x.z; f.v[3] = x.w;
+  } else {
+    const float2 x = *reinterpret_cast<const float2*>(p);
+    f.v[0] = x.x; f.v[1] = x.y;
+  }
+  return f;
+}
+
+template <int D, typename PV>
+__device__ __forceinline__ void AccumulateTile(const float* __restrict__ tile, const PV& pv, int h,
+                                               int r, floatx16 (&acc)[D / 32]) {
+  constexpr int NB = D / 32;
+  Frag<D> f[2];
+  f[0] = ReadFrag<D>(tile, 0, h, r);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    if (e + 1 < 16) f[(e + 1) & 1] = ReadFrag<D>(tile, e + 1, h, r);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[e & 1].v[nb], pv[e], acc[nb], 0, 0, 0);
+  }
+}
+
+// Writes acc (as laid out by AccumulateTile) to row `out` of a [*, H*d] head
+// view: element e of acc[nb] at lane (h, r) is feature NB*i + nb with
+// i = 8*(e/4) + 4h + e%4, so the NB blocks of one e form one vector store.
+template <int D>
+__device__ __forceinline__ void StoreRow(float* __restrict__ out, const floatx16 (&acc)[D / 32],
+                                         int h) {
+  constexpr int NB = D / 32;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = 8 * (e >> 2) + 4 * h + (e & 3);
+    if constexpr (NB == 4)
+      *reinterpret_cast<float4*>(out + 4 * i) = make_float4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
+    else
+      *reinterpret_cast<float2*>(out + 2 * i) = make_float2(acc[0][e], acc[1][e]);
+  }
 }
 
 template <int D>
@@ -251,14 +319,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
           *reinterpret_cast<float4*>(prow + j) =
               make_float4(sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]);
       }
-      const float* vtile = vt[t & 1];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float* vrow = vtile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          oacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * nb], sc[e], oacc[nb], 0, 0, 0);
-      }
+      AccumulateTile<D>(vt[t & 1], sc, h, r, oacc);
     }
     if (t + 1 < tiles_wg) {
       ks.store(kt[(t + 1) & 1]);
@@ -267,17 +328,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     __syncthreads();
   }
 
-  if (row_ok) {
-    // O^T element e of block nb: feature 32*nb + 8*(e/4) + 4h + e%4 of query i.
-    float* orow = oh + static_cast<int64_t>(i) * ld;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
-            make_float4(oacc[nb][4 * q4], oacc[nb][4 * q4 + 1], oacc[nb][4 * q4 + 2],
-                        oacc[nb][4 * q4 + 3]);
-  }
+  if (row_ok) StoreRow<D>(oh + static_cast<int64_t>(i) * ld, oacc, h);
   // Causal tail: columns past this wavefront's diagonal tile are exact 0.
   const int zc = tiles_w * kAttnK;
   for (int rr = 0; rr < 32; ++rr) {
@@ -439,14 +490,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
           if (j > i) g[e] = 0.0f;
         }
       }
-      const float* ktile = kt[t & 1];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float* krow = ktile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[32 * nb], g[e], acc[nb], 0, 0, 0);
-      }
+      AccumulateTile<D>(kt[t & 1], g, h, r, acc);
     }
     if (t + 1 < tiles_wg) {
       ks.store(kt[(t + 1) & 1]);
@@ -455,16 +499,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
     }
     __syncthreads();
   }
-  if (row_ok) {
-    float* orow = oh + static_cast<int64_t>(i) * ld;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
-            make_float4(acc[nb][4 * q4], acc[nb][4 * q4 + 1], acc[nb][4 * q4 + 2],
-                        acc[nb][4 * q4 + 3]);
-  }
+  if (row_ok) StoreRow<D>(oh + static_cast<int64_t>(i) * ld, acc, h);
 }
 
 template <int D, bool SCALED>
@@ -521,14 +556,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dkv_fused(
 #pragma unroll
         for (int e = 0; e < 16; ++e) g[e] = g[e] * scale;
       }
-      const float* xtile = xt[(t - t0) & 1];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float* xrow = xtile + (8 * (e >> 2) + 4 * h + (e & 3)) * TS + r;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xrow[32 * nb], g[e], acc[nb], 0, 0, 0);
-      }
+      AccumulateTile<D>(xt[(t - t0) & 1], g, h, r, acc);
     }
     if (t + 1 < ntiles) {
       xs.store(xt[(t + 1 - t0) & 1]);
@@ -537,16 +565,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dkv_fused(
     }
     __syncthreads();
   }
-  if (col_ok) {
-    float* orow = oh + static_cast<int64_t>(j) * ld;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4*>(orow + 32 * nb + 8 * q4 + 4 * h) =
-            make_float4(acc[nb][4 * q4], acc[nb][4 * q4 + 1], acc[nb][4 * q4 + 2],
-                        acc[nb][4 * q4 + 3]);
-  }
+  if (col_ok) StoreRow<D>(oh + static_cast<int64_t>(j) * ld, acc, h);
 }
 
 // The fused kernels' shape gate: d in {64, 128}, S % 4 == 0 (16-byte P
