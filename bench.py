@@ -161,11 +161,13 @@ def main():
     # region) picks the dominant kernel: the (opcode, shape, tile) group with
     # the largest share of the step.
     ms = e.profile(PROGRAM_TRAIN, reps=args.profile_reps)
-    summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS)
+    variants = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(plan.train))]
+    summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS,
+                               variants=variants)
     rows = summ["rows"]
     groups = {}
     for i, r in enumerate(rows):
-        tile = e.gemm_choice(PROGRAM_TRAIN, i) if r["op"] in workmodel.GEMMS else ""
+        tile = variants[i]
         g = groups.setdefault((r["op"], tuple(r["shape"]), tile), [0.0, []])
         g[0] += r["ms"]
         g[1].append(i)

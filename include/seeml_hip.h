@@ -126,8 +126,10 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
  * within 3% of the best mean; picks are installed and graphs rebuilt.
  * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
-/* Describe the GEMM plan chosen for instruction `index` of `program`:
- * writes "cfg-name splits=S" into buf. */
+/* Describe the kernel variant chosen for instruction `index` of `program`:
+ * GEMMs "cfg-name splits=S" (or "skinny/<kind>"); SoftmaxRowsBwd "causal S=n"
+ * when its probabilities are proven AttnFwd/AttnDP outputs (only their causal
+ * half is read), else ""; other opcodes "". */
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap);
 

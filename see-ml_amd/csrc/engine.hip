@@ -147,12 +147,54 @@ class Engine {
     if (Status s = HipOk(hipHostMalloc(&h_scalars_, sizeof(StepScalars)), "pinned scalars"); !s)
       return s;
     if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
+    for (int p = 0; p < 3; ++p) PlanCausalRows(p);
     for (int p = 0; p < 3; ++p) plans_[p].assign(plan_.program[p].size(), GemmPlan{});
     for (int p = 0; p < 3; ++p)
       for (size_t i = 0; i < plan_.program[p].size(); ++i)
         if (IsGemmOp(plan_.program[p][i].opcode)) plans_[p][i] = PlanGemm(DescOf(plan_.program[p][i]));
     if (Status s = SetStep(0); !s) return s;
     return HipOk(hipStreamSynchronize(stream_), "open");
+  }
+
+  // SoftmaxRowsBwd whose probs are the latest AttnFwd output and whose dP is
+  // the latest AttnDP output, both of the same (B, H, S) with rows = B*H*S
+  // and cols = S: those kernels store exact +0 above the causal diagonal,
+  // so the row kernel may skip reading that half (kernels.h). Dataflow over
+  // the straight-line program: the most recent instruction before idx whose
+  // written bytes overlap an operand must be that producer, writing exactly
+  // that range.
+  void PlanCausalRows(int program) {
+    const auto& prog = plan_.program[program];
+    causal_rows_[program].assign(prog.size(), 0);
+    std::vector<std::vector<std::pair<uint64_t, uint64_t>>> writes(prog.size());
+    for (size_t i = 0; i < prog.size(); ++i) (void)WriteRangesOf(prog[i], &writes[i]);
+    auto last_writer = [&](size_t idx, uint64_t off, uint64_t bytes) -> long {
+      for (size_t j = idx; j-- > 0;)
+        for (const auto& w : writes[j])
+          if (w.first < off + bytes && off < w.first + w.second) return static_cast<long>(j);
+      return -1;
+    };
+    for (size_t i = 0; i < prog.size(); ++i) {
+      const UpdateInstruction& ins = prog[i];
+      if (static_cast<Op>(ins.opcode) != Op::kSoftmaxRowsBwd) continue;
+      if (IsRodataRef(ins.in[0]) || IsRodataRef(ins.in[1])) continue;
+      const uint64_t rows = Hi(ins.out[0]), cols = Lo(ins.out[0]);
+      const uint64_t bytes = rows * cols * sizeof(float);
+      const long wp = last_writer(i, RefOffset(ins.in[0]), bytes);
+      const long wd = last_writer(i, RefOffset(ins.in[1]), bytes);
+      if (wp < 0 || wd < 0) continue;
+      const UpdateInstruction& f = prog[static_cast<size_t>(wp)];
+      const UpdateInstruction& g = prog[static_cast<size_t>(wd)];
+      if (static_cast<Op>(f.opcode) != Op::kAttnFwd || static_cast<Op>(g.opcode) != Op::kAttnDP)
+        continue;
+      // AttnFwd: out[0] = probs, B<<32|S in out[1], H<<32|d in out[2];
+      // AttnDP: in[2] = dP, B<<32|S in out[0], H<<32|d in out[1].
+      if (f.out[0] != ins.in[0] || g.in[2] != ins.in[1]) continue;
+      if (f.out[1] != g.out[0] || Hi(f.out[2]) != Hi(g.out[1])) continue;
+      const uint64_t B = Hi(f.out[1]), S = Lo(f.out[1]), H = Hi(f.out[2]);
+      if (S != cols || B * H * S != rows) continue;
+      causal_rows_[program][i] = S;
+    }
   }
 
   // ---- instruction decode ------------------------------------------------
@@ -277,7 +319,8 @@ class Engine {
       case Op::kAttnDV:
         return AttnDV(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
       case Op::kSoftmaxRowsBwd:
-        return SoftmaxRowsBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), c);
+        return SoftmaxRowsBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), c,
+                              causal_rows_[program][idx]);
       case Op::kAttnDQ:
         return AttnDQ(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
       case Op::kAttnDK:
@@ -1001,6 +1044,10 @@ class Engine {
   }
 
   std::string GemmChoice(int program, size_t idx) const {
+    if (static_cast<Op>(plan_.program[program][idx].opcode) == Op::kSoftmaxRowsBwd)
+      return causal_rows_[program][idx] ? "causal S=" + std::to_string(causal_rows_[program][idx])
+                                        : std::string();
+    if (!IsGemmOp(plan_.program[program][idx].opcode)) return std::string();
     const GemmPlan& p = plans_[program][idx];
     if (p.cfg == GemmSkinnyConfig())
       return SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])));
@@ -1052,6 +1099,7 @@ class Engine {
   size_t argmax_cap_ = 0;
   uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
+  std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;
   struct Segment {

@@ -600,19 +600,25 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
   store_row<TPR, V>(dx + r * cols, nv, t, gv, nt);
 }
 
+// causal_s > 0: row r is query i = r % causal_s and the entries j > i of P
+// and dP are known exact +0 (see SoftmaxRowsBwd); only the float4s holding
+// j <= i are read, the rest of the row is written as (+0) * (0 - sum).
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __restrict__ p,
                                                                const float* __restrict__ dp,
                                                                float* __restrict__ ds,
-                                                               size_t rows, int cols, int nt) {
+                                                               size_t rows, int cols, int nt,
+                                                               int causal_s) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
+  // Float4s that hold any j <= i (the rest are known zeros when causal).
+  const int nread = causal_s > 0 ? static_cast<int>(r % causal_s) / 4 + 1 : nv;
   float4 pv[V], dv[V];
-  load_row<TPR, V>(p + r * cols, nv, t, pv, nt);
-  load_row<TPR, V>(dp + r * cols, nv, t, dv, nt);
+  load_row<TPR, V>(p + r * cols, nread, t, pv, nt);
+  load_row<TPR, V>(dp + r * cols, nread, t, dv, nt);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -626,6 +632,8 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __re
   for (int i = 0; i < V; ++i)
     dv[i] = make_float4(pv[i].x * (dv[i].x - sum), pv[i].y * (dv[i].y - sum),
                         pv[i].z * (dv[i].z - sum), pv[i].w * (dv[i].w - sum));
+  // Unread float4s were zero-filled, so their entries already equal
+  // (+0) * (0 - sum), the value the full read would give.
   store_row<TPR, V>(ds + r * cols, nv, t, dv, nt);
 }
 
@@ -897,14 +905,19 @@ Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const flo
 }
 
 Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
-                      const Ctx& c) {
+                      const Ctx& c, size_t causal_s) {
   if (rows == 0 || cols == 0) return Status::Ok();
   const int rc = RegCase(cols, {probs, dp, ds});
-  if (rc >= 0)
+  if (causal_s != 0 && (causal_s != cols || rows % causal_s != 0))
+    return Status::Fail(kUnitEngine, "SoftmaxRowsBwd: causal geometry does not match the rows");
+  if (rc >= 0) {
+    // Traffic: the causal form reads about half of P and dP.
+    const size_t traffic = causal_s ? 8 * rows * cols : 12 * rows * cols;
     REG_DISPATCH(softmax_rows_bwd_reg, rc, rows, probs, dp, ds, rows, static_cast<int>(cols),
-                 StreamPolicy(12 * rows * cols) ? 1 : 0);
-  else
+                 StreamPolicy(traffic) ? 1 : 0, static_cast<int>(causal_s));
+  } else {
     ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
+  }
   return LaunchStatus("SoftmaxRowsBwd");
 }
 

@@ -169,8 +169,13 @@ Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, siz
                   size_t cols, const Ctx& c);
 Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
                   float* dx, size_t rows, size_t cols, const Ctx& c);
+// causal_s > 0: the caller has proven that rows are (b, h, i) with i = row %
+// causal_s, cols == causal_s, and that probs and dp hold exact +0 at every
+// j > i (AttnFwd / AttnDP outputs). Those entries are then not read: their
+// dS is (+0) * (0 - rowsum), the reference's expression on those values, and
+// their +0 products leave the double rowsum's bits unchanged.
 Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
-                      const Ctx& c);
+                      const Ctx& c, size_t causal_s = 0);
 // Causal row softmax in place over raw scores (attention forward, step 2).
 Status AttnSoftmaxRows(float* p, size_t rows, size_t S, const Ctx& c);
 

@@ -272,6 +272,21 @@ bool OperandsOf(const UpdateInstruction& ins, Operand* ops, size_t* n) {
 
 }  // namespace
 
+bool WriteRangesOf(const UpdateInstruction& ins,
+                   std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
+  Operand ops[8];
+  size_t n = 0;
+  ranges->clear();
+  if (!OperandsOf(ins, ops, &n)) return false;
+  for (size_t i = 0; i < n; ++i) {
+    if (!ops[i].write || IsRodataRef(ops[i].ref)) continue;
+    uint64_t bytes = 0;
+    if (!MulOk(ops[i].elems, ops[i].elem_bytes, &bytes)) return false;
+    ranges->emplace_back(RefOffset(ops[i].ref), bytes);
+  }
+  return true;
+}
+
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,
                            uint64_t rodata_size, uint32_t plan_version) {
   const std::string op = std::to_string(ins.opcode);

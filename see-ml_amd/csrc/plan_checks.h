@@ -14,6 +14,7 @@
 
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "plan_abi.h"
@@ -48,6 +49,12 @@ inline bool RangeOk(uint64_t off, uint64_t bytes, uint64_t size) {
 // geometry), chunk digests folded in order, then the size.
 uint64_t ContentHash64(const uint8_t* data, size_t size);
 uint64_t PlanSelfHash(const uint8_t* plan, size_t size, size_t hash_offset);
+
+// Arena byte ranges [offset, offset + bytes) an instruction writes (rodata is
+// never written), from the validator's operand table; false when the dims
+// are malformed.
+bool WriteRangesOf(const UpdateInstruction& ins,
+                   std::vector<std::pair<uint64_t, uint64_t>>* ranges);
 
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,
                            uint64_t rodata_size, uint32_t plan_version);

@@ -111,7 +111,9 @@ def decoder_model(vocab, dim, layers, heads, ffn, seq, norm="rms", mlp="swiglu")
 
 def make(name: str) -> Workload:
     """Full-size BASELINE configs: c1..c5. Reduced parity variants: c2s,
-    c3s, c4s, c5s keep each config's op structure at CPU-checkable size."""
+    c3s, c4s, c5s keep each config's op structure at CPU-checkable size;
+    c3m, c4m do too with head widths 64 and 128 (the fused attention
+    kernels' shapes)."""
     if name == "c1":
         return Workload("c1", mlp_model(), UpdateConfig(
             batch=32, loss="xent", lora=LoraSpec(rank=8, alpha=16.0, seed=7), lr=1e-3,
@@ -132,6 +134,9 @@ def make(name: str) -> Workload:
         "c3s": (512, 64, 2, 4, 96, 32, 4, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),
         "c4s": (1000, 128, 2, 4, 256, 64, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
         "c5s": (1000, 128, 2, 4, 512, 64, 2, 16, (), 1e-3, "layer", "gelu"),
+        # head widths 64 and 128: the fused attention kernels' shapes
+        "c3m": (512, 128, 2, 2, 192, 64, 4, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),
+        "c4m": (1000, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
     }
     if name not in dec:
         raise KeyError(name)

@@ -2,7 +2,9 @@
 
 Bytes count each operand the reference kernel must read or write once, at
 4 B per f32/i32 element (1 B per int8 weight) — the traffic floor, not what
-a kernel happens to move. FLOPs count 2 per multiply-add of the
+a kernel happens to move — except where the engine has proven part of an
+operand's contents (a causal SoftmaxRowsBwd: the masked half of P and dP is
+exact +0), where they count only what must still be read. FLOPs count 2 per multiply-add of the
 contractions (causal attention counts only the j <= i half the kernels
 compute). These are the numbers `roofline.achieved` and the MFMA-utilisation
 / HBM-throughput figures divide by measured kernel time.
@@ -28,8 +30,12 @@ def _lo(w):
     return w & 0xFFFFFFFF
 
 
-def work(ins: dict) -> dict:
-    """{'op', 'flops', 'bytes', 'cls', 'shape'} for one decoded instruction."""
+def work(ins: dict, variant: str = "") -> dict:
+    """{'op', 'flops', 'bytes', 'cls', 'shape'} for one decoded instruction.
+
+    `variant` is the engine's kernel choice for it (seeml_hip_gemm_choice):
+    a causal SoftmaxRowsBwd reads only the float4s of P and dP that hold
+    j <= i, so its bytes are those reads plus the full dS write."""
     name = OP_NAME.get(ins["opcode"], str(ins["opcode"]))
     o = ins["out"]
     flops, nbytes, cls, shape = 0, 0, "hbm", ()
@@ -83,6 +89,9 @@ def work(ins: dict) -> dict:
     elif name == "SoftmaxRowsBwd":
         r, c = _hi(o[0]), _lo(o[0])
         nbytes, shape = 12 * r * c, (r, c)
+        if variant.startswith("causal") and c and r % c == 0:
+            read = sum(4 * (i // 4 + 1) for i in range(c)) * (r // c)
+            nbytes = 8 * read + 4 * r * c
     elif name == "EmbedFwd":
         T, D = o[0], _lo(o[1])
         nbytes, shape = 4 * T + 8 * T * D, (T, D)
@@ -108,9 +117,11 @@ def work(ins: dict) -> dict:
     return dict(op=name, flops=flops, bytes=nbytes, cls=cls, shape=shape)
 
 
-def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: float = 8000.0):
+def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: float = 8000.0,
+              variants: list = None):
     """Aggregate per-instruction timings into the BASELINE metric's parts."""
-    rows = [dict(work(ins), ms=t) for ins, t in zip(program, ms)]
+    variants = variants or [""] * len(program)
+    rows = [dict(work(ins, v), ms=t) for ins, t, v in zip(program, ms, variants)]
     dense = [r for r in rows if r["cls"] == "mfma"]
     gem_all = [r for r in rows if r["op"] in GEMMS]
     hbm = [r for r in rows if r["cls"] == "hbm" and r["op"] not in GEMMS]

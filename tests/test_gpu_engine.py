@@ -49,7 +49,8 @@ def drift_floor(plan, w, steps, orc):
     return a, b
 
 
-@pytest.mark.parametrize("name,steps", [("c1", 5), ("c2s", 3), ("c3s", 3), ("c4s", 3), ("c5s", 3)])
+@pytest.mark.parametrize("name,steps", [("c1", 5), ("c2s", 3), ("c3s", 3), ("c4s", 3), ("c5s", 3),
+                                        ("c3m", 3), ("c4m", 3)])
 def test_plan_parity_vs_oracle(torch_gpu, orc, name, steps):
     w, p = compile_workload(name)
     e = engine(p)
@@ -226,3 +227,37 @@ def test_c2_full_size_invariants(torch_gpu):
     e2 = engine(p)
     for i in range(5):
         assert np.float32(e2.train_step(x, y)).view(np.uint32) == np.float32(losses[i]).view(np.uint32)
+
+
+def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
+    """SoftmaxRowsBwd fed by AttnFwd / AttnDP reads only the causal half of P
+    and dP. Replaying the plan instruction by instruction up to it, P and dP
+    are exact +0 above the diagonal and the engine's dS equals the generic
+    full-row kernel's on the same P and dP, bit for bit."""
+    from seeml_amd import PROGRAM_TRAIN, _lib, planner
+    torch = torch_gpu
+    w, p = compile_workload("c4m")
+    e = engine(p, use_graph=False)
+    x, y = configs.batch(w, 0)
+    e.stage(x, y)
+    idx = next(i for i, ins in enumerate(p.train)
+               if ins["opcode"] == planner.OP["SoftmaxRowsBwd"])
+    for j in range(idx + 1):
+        e.time_instruction(PROGRAM_TRAIN, j, reps=1)
+    ins = p.train[idx]
+    rows, cols = ins["out"][0] >> 32, ins["out"][0] & 0xFFFFFFFF
+    P = e.read(ins["inp"][0], rows * cols).reshape(rows, cols)
+    dP = e.read(ins["inp"][1], rows * cols).reshape(rows, cols)
+    dS = e.read(ins["inp"][2], rows * cols)
+    upper = np.arange(cols)[None, :] > (np.arange(rows) % cols)[:, None]
+    assert np.all(P[upper].view(np.uint32) == 0) and np.all(dP[upper].view(np.uint32) == 0)
+    dev = torch.device("cuda:0")
+    out = torch.full((rows * cols,), float("nan"), device=dev)
+    tp, tdp = torch.from_numpy(P.ravel().copy()).to(dev), torch.from_numpy(dP.ravel().copy()).to(dev)
+    rc = _lib.lib().seeml_hip_softmax_rows_bwd(tp.data_ptr(), tdp.data_ptr(), out.data_ptr(), rows,
+                                               cols, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    want = out.cpu().numpy()
+    assert np.array_equal(dS.view(np.uint32), want.view(np.uint32))
+    e.close()

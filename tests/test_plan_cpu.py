@@ -78,7 +78,7 @@ def test_plan_hash_matches_reference(ref):
                 == ref.content_hash64(blob, n)), n
 
 
-@pytest.mark.parametrize("name", ["c1", "c2s", "c3s", "c4s", "c5s"])
+@pytest.mark.parametrize("name", ["c1", "c2s", "c3s", "c4s", "c5s", "c3m", "c4m"])
 def test_compiled_plans_verify_and_corruption_is_caught(name):
     w, p = compile_workload(name)
     assert verify_plan(p.blob) == (0, "")
@@ -143,7 +143,7 @@ def test_library_exports_every_declared_symbol():
     assert len(declared) == len(set(re.findall(r"\b(seeml_hip_\w+)\s*\(", text)))
 
 
-@pytest.mark.parametrize("name,steps", [("c1", 3), ("c3s", 2), ("c5s", 2), ("c2s", 2)])
+@pytest.mark.parametrize("name,steps", [("c1", 3), ("c3s", 2), ("c5s", 2), ("c2s", 2), ("c4m", 1)])
 def test_oracle_dispatch_bitwise_equals_reference_dispatch(orc, ref, name, steps):
     """orc_execute (the C restatement) and ref_execute (the reference's own
     kernels) run the same compiled plan for several steps: every arena byte
