@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "../../include/seeml_hip.h"
+#include "device_common.h"
 #include "kernels.h"
 #include "stager.h"
 #include "plan_checks.h"
@@ -444,6 +445,7 @@ class Engine {
         i = std::max(j, i + 1);
       }
     }
+    PlanChains(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -451,14 +453,117 @@ class Engine {
                  "fused AdamW table upload");
   }
 
+  // LoRA merge chains (kernels.h SkinnyChain): a GemmNN/NT on the skinny
+  // outer kernel, then Scale of its output and/or AddEW of that with
+  // another tensor, adjacent in the plan and none of them marked for timing.
+  // The chain runs as one kernel when its results are provably those of the
+  // three launches in order: the AddEW/Scale operands are exactly the
+  // preceding outputs, and no range the chain writes overlaps a range it
+  // reads (so no workgroup can see another's write). u's own write is
+  // skipped only when the AddEW output is exactly u's range (u is then dead
+  // and overwritten within the chain).
+  struct ChainRun {
+    size_t first = 0, count = 0;
+    SkinnyChain ch;
+  };
+
+  void PlanChains(int program) {
+    chains_[program].clear();
+    const auto& prog = plan_.program[program];
+    auto is_marked = [&](size_t i) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), i);
+    };
+    using Ranges = std::vector<std::pair<uint64_t, uint64_t>>;
+    auto overlap = [](const Ranges& a, const Ranges& b) {
+      for (const auto& x : a)
+        for (const auto& y : b)
+          if (x.first < y.first + y.second && y.first < x.first + x.second) return true;
+      return false;
+    };
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      const UpdateInstruction& g = prog[i];
+      const auto op = static_cast<Op>(g.opcode);
+      if ((op != Op::kGemmNN && op != Op::kGemmNT) || g.flags != 0 || is_marked(i)) continue;
+      if (plans_[program][i].cfg != GemmSkinnyConfig()) continue;
+      const GemmDesc d = DescOf(g);
+      if (SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N) continue;
+      const uint64_t n = g.out[0] * g.out[1];
+      const uint64_t u = g.in[2];
+      size_t k = i + 1;
+      SkinnyChain ch;
+      uint64_t v = u;  // the value the AddEW must consume
+      if (static_cast<Op>(prog[k].opcode) == Op::kScale && prog[k].in[0] == u &&
+          prog[k].out[0] == n && !is_marked(k) && k + 1 < prog.size()) {
+        ch.kind = 1;
+        ch.alpha = Bits(prog[k].in[2]);
+        v = prog[k].in[1];
+        ++k;
+      } else {
+        ch.kind = 2;
+      }
+      const UpdateInstruction& a = prog[k];
+      if (static_cast<Op>(a.opcode) != Op::kAddEW || a.out[0] != n || is_marked(k)) continue;
+      if (a.in[0] != v && a.in[1] != v) continue;
+      ch.y_first = a.in[1] == v;
+      const uint64_t y = ch.y_first ? a.in[0] : a.in[1];
+      if (IsRodataRef(y) || IsRodataRef(a.in[2])) continue;
+      const uint64_t bytes = n * sizeof(float);
+      ch.write_u = a.in[2] != u;
+      Ranges writes, reads, tmp;
+      if (ch.write_u) writes.emplace_back(RefOffset(u), bytes);
+      if (ch.kind == 1) writes.emplace_back(RefOffset(v), bytes);
+      writes.emplace_back(RefOffset(a.in[2]), bytes);
+      (void)ReadRangesOf(g, &reads);
+      reads.emplace_back(RefOffset(y), bytes);
+      if (overlap(writes, reads)) continue;
+      // Distinct written tensors must not partially overlap one another.
+      bool clash = false;
+      for (size_t x = 0; x < writes.size(); ++x)
+        for (size_t z = x + 1; z < writes.size(); ++z)
+          if (overlap(Ranges{writes[x]}, Ranges{writes[z]})) clash = true;
+      if (clash) continue;
+      ch.s = ch.kind == 1 ? WP(v) : nullptr;
+      ch.y = RP(y);
+      ch.yout = WP(a.in[2]);
+      if (!aligned16(ch.y) || !aligned16(ch.yout) || (ch.s && !aligned16(ch.s))) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = k - i + 1;
+      run.ch = ch;
+      chains_[program].push_back(run);
+      i = k;
+    }
+  }
+
+  // Algorithmic bytes of an instruction of a chain, for splitting the fused
+  // launch's measured time in the per-instruction profile.
+  double ChainBytes(const UpdateInstruction& ins) const {
+    const double M = ins.out[0], N = ins.out[1], K = ins.out[2];
+    switch (static_cast<Op>(ins.opcode)) {
+      case Op::kScale: return 8.0 * ins.out[0];
+      case Op::kAddEW: return 12.0 * ins.out[0];
+      default: return 4.0 * (M * K + K * N + M * N);
+    }
+  }
+
   // The captured launch sequence of instructions [begin, end): plan order,
-  // fused AdamW runs (wholly inside the range) as one launch each.
+  // fused AdamW runs and LoRA merge chains (wholly inside the range) as one
+  // launch each.
   Status RunFused(int program, size_t begin, size_t end) {
     const Ctx c = MakeCtx();
     const auto& runs = fused_runs_[program];
-    size_t r = 0;
+    const auto& chains = chains_[program];
+    size_t r = 0, q = 0;
     while (r < runs.size() && runs[r].first < begin) ++r;
+    while (q < chains.size() && chains[q].first < begin) ++q;
     for (size_t i = begin; i < end;) {
+      if (q < chains.size() && chains[q].first == i && i + chains[q].count <= end) {
+        if (Status s = LaunchSkinnyChain(DescOf(plan_.program[program][i]), chains[q].ch, c); !s)
+          return s;
+        i += chains[q].count;
+        ++q;
+        continue;
+      }
       if (r < runs.size() && runs[r].first == i && i + runs[r].count <= end) {
         if (Status s = AdamWMulti(fused_segs_[program] + runs[r].seg_offset, runs[r].count,
                                   runs[r].blocks, c);
@@ -973,11 +1078,21 @@ class Engine {
     std::vector<double> acc(n, 0.0);
     const Ctx c = MakeCtx();
     const auto& runs = use_graph_ ? fused_runs_[program] : std::vector<FusedRun>{};
+    const auto& chains = use_graph_ ? chains_[program] : std::vector<ChainRun>{};
     Status result = Status::Ok();
     for (int r = 0; r < reps && result; ++r) {
       (void)hipEventRecord(ev[0], stream_);
-      size_t fr = 0;
+      size_t fr = 0, fq = 0;
       for (size_t i = 0; i < n;) {
+        if (fq < chains.size() && chains[fq].first == i) {
+          if (Status s = LaunchSkinnyChain(DescOf(prog[i]), chains[fq].ch, c); !s) {
+            result = s;
+            break;
+          }
+          i += chains[fq++].count;
+          (void)hipEventRecord(ev[i], stream_);
+          continue;
+        }
         if (fr < runs.size() && runs[fr].first == i) {
           if (Status s = AdamWMulti(fused_segs_[program] + runs[fr].seg_offset, runs[fr].count,
                                     runs[fr].blocks, c);
@@ -995,7 +1110,19 @@ class Engine {
       if (!result) break;
       if (Status s = HipOk(hipEventSynchronize(ev[n]), "profile sync"); !s) { result = s; break; }
       fr = 0;
+      fq = 0;
       for (size_t i = 0; i < n;) {
+        if (fq < chains.size() && chains[fq].first == i) {
+          const ChainRun& run = chains[fq++];
+          float ms = 0.0f;
+          (void)hipEventElapsedTime(&ms, ev[i], ev[i + run.count]);
+          double total = 0.0;
+          for (size_t k = i; k < i + run.count; ++k) total += ChainBytes(prog[k]);
+          for (size_t k = i; k < i + run.count; ++k)
+            acc[k] += total > 0.0 ? ms * ChainBytes(prog[k]) / total : 0.0;
+          i += run.count;
+          continue;
+        }
         if (fr < runs.size() && runs[fr].first == i) {
           const FusedRun& run = runs[fr++];
           float ms = 0.0f;
@@ -1099,6 +1226,7 @@ class Engine {
   size_t argmax_cap_ = 0;
   uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
+  std::vector<ChainRun> chains_[3];
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;

@@ -55,6 +55,14 @@ struct SkArgs {
   int big_is_m;        // the large operand is A (W = M) or B (W = N)
   int groups;          // k-groups (partials)
   int64_t k_per_group;
+  // outer: chained Scale / AddEW epilogue (SkinnyChain)
+  int chain;
+  float chain_alpha;
+  float* S;
+  const float* Y;
+  float* Yout;
+  int write_u;
+  int y_first;
 };
 
 __device__ __forceinline__ float Epilogue(const SkArgs& p, int64_t m, int64_t n, float acc) {
@@ -98,7 +106,9 @@ __device__ __forceinline__ void OuterLoadB(const SkArgs& p, int64_t n, int q, fl
   }
 }
 
-template <int KG>
+// PLAIN: the GEMM epilogue is the identity (alpha == 1, no accumulate, bias or
+// activation: 1 * x == x exactly), so accumulators are stored as they are.
+template <int KG, bool CHAIN, bool PLAIN>
 __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int q = lane >> 4, c = lane & 15;
@@ -118,9 +128,24 @@ __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
   }
   const int64_t nend = std::min<int64_t>(p.N, n0 + kOuterWN);
   float4 bf[KG], bn[KG];
+  // Chain: the AddEW operand y of the current and next column steps, loaded
+  // a step ahead like B (rows past M and columns past N read row/col 0).
+  float4 yc[kOuterRB], yn[kOuterRB];
+  auto load_y = [&](int64_t nb, float4 (&yv)[kOuterRB]) {
+#pragma unroll
+    for (int rb = 0; rb < kOuterRB; ++rb) {
+      const int64_t mo = m0 + 16 * rb + c, n = nb + 4 * q;
+      const bool in = mo < p.M && n < p.N;
+      yv[rb] = *reinterpret_cast<const float4*>(p.Y + (in ? mo * p.N + n : 0));
+    }
+  };
   OuterLoadB<KG>(p, std::min<int64_t>(n0 + c, p.N - 1), q, bf);
+  if constexpr (CHAIN) load_y(n0, yc);
   for (int64_t nb = n0; nb < nend; nb += 16) {
-    if (nb + 16 < nend) OuterLoadB<KG>(p, std::min<int64_t>(nb + 16 + c, p.N - 1), q, bn);
+    if (nb + 16 < nend) {
+      OuterLoadB<KG>(p, std::min<int64_t>(nb + 16 + c, p.N - 1), q, bn);
+      if constexpr (CHAIN) load_y(nb + 16, yn);
+    }
     floatx4 acc[kOuterRB];
 #pragma unroll
     for (int rb = 0; rb < kOuterRB; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -138,14 +163,33 @@ __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
 #pragma unroll
       for (int rb = 0; rb < kOuterRB; ++rb) {
         const int64_t mo = m0 + 16 * rb + c;
-        if (mo < p.M)
-          *reinterpret_cast<float4*>(p.C + mo * p.ldc + n) =
-              make_float4(Epilogue(p, mo, n + 0, acc[rb][0]), Epilogue(p, mo, n + 1, acc[rb][1]),
-                          Epilogue(p, mo, n + 2, acc[rb][2]), Epilogue(p, mo, n + 3, acc[rb][3]));
+        if (mo >= p.M) continue;
+        const float4 u =
+            PLAIN ? make_float4(acc[rb][0], acc[rb][1], acc[rb][2], acc[rb][3])
+                  : make_float4(Epilogue(p, mo, n + 0, acc[rb][0]), Epilogue(p, mo, n + 1, acc[rb][1]),
+                                Epilogue(p, mo, n + 2, acc[rb][2]), Epilogue(p, mo, n + 3, acc[rb][3]));
+        if (p.write_u) *reinterpret_cast<float4*>(p.C + mo * p.ldc + n) = u;
+        if constexpr (CHAIN) {
+          // The Scale and AddEW element expressions, in plan order.
+          const int64_t at = mo * p.N + n;
+          float4 v = u;
+          if (p.chain == 1) {
+            v = make_float4(p.chain_alpha * u.x, p.chain_alpha * u.y, p.chain_alpha * u.z,
+                            p.chain_alpha * u.w);
+            *reinterpret_cast<float4*>(p.S + at) = v;
+          }
+          const float4 y = yc[rb];
+          *reinterpret_cast<float4*>(p.Yout + at) =
+              p.y_first ? make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w)
+                        : make_float4(v.x + y.x, v.y + y.y, v.z + y.z, v.w + y.w);
+        }
       }
     }
 #pragma unroll
     for (int g = 0; g < KG; ++g) bf[g] = bn[g];
+    if constexpr (CHAIN)
+#pragma unroll
+      for (int rb = 0; rb < kOuterRB; ++rb) yc[rb] = yn[rb];
   }
 }
 
@@ -444,10 +488,35 @@ size_t SkinnyWorkspace(const GemmDesc& d) {
   return static_cast<size_t>(ColsumGroups(W, d.K)) * W * R * sizeof(float);
 }
 
-Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) {
+namespace {
+Status LaunchSkinnyImpl(const GemmDesc& d, const SkinnyChain* ch, const Ctx& ctx);
+}
+
+Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) { return LaunchSkinnyImpl(d, nullptr, ctx); }
+
+Status LaunchSkinnyChain(const GemmDesc& d, const SkinnyChain& ch, const Ctx& ctx) {
+  if (SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N || (ch.kind != 1 && ch.kind != 2) ||
+      !ch.y || !ch.yout || (ch.kind == 1 && !ch.s) || !aligned16(ch.y) || !aligned16(ch.yout) ||
+      (ch.s && !aligned16(ch.s)))
+    return Status::Fail(kUnitEngine, "Gemm: chain does not fit the skinny outer kernel");
+  return LaunchSkinnyImpl(d, &ch, ctx);
+}
+
+namespace {
+Status LaunchSkinnyImpl(const GemmDesc& d, const SkinnyChain* ch, const Ctx& ctx) {
   const SkinnyKind kind = SkinnyKindOf(d);
   if (kind == SkinnyKind::kNone) return Status::Fail(kUnitEngine, "Gemm: shape is not skinny");
   SkArgs a{};
+  a.write_u = 1;
+  if (ch) {
+    a.chain = ch->kind;
+    a.chain_alpha = ch->alpha;
+    a.S = ch->s;
+    a.Y = ch->y;
+    a.Yout = ch->yout;
+    a.write_u = ch->write_u ? 1 : 0;
+    a.y_first = ch->y_first ? 1 : 0;
+  }
   a.A = static_cast<const float*>(d.A);
   a.B = static_cast<const float*>(d.B);
   a.C = d.C;
@@ -463,11 +532,22 @@ Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) {
     const int64_t gx = (d.M + kOuterRows - 1) / kOuterRows, gy = (d.N + kOuterN - 1) / kOuterN;
     if (gx > 0x7FFFFFFF || gy > 65535) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
     const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+    const bool plain = d.alpha == 1.0f && !d.accumulate && !d.bias && d.act == 0;
+#define SEEML_OUTER(KG_)                                                                      \
+  if (ch && plain)                                                                            \
+    hipLaunchKernelGGL((skinny_outer<KG_, true, true>), grid, dim3(kThreads), 0, ctx.stream, a);  \
+  else if (ch)                                                                                \
+    hipLaunchKernelGGL((skinny_outer<KG_, true, false>), grid, dim3(kThreads), 0, ctx.stream, a); \
+  else if (plain)                                                                             \
+    hipLaunchKernelGGL((skinny_outer<KG_, false, true>), grid, dim3(kThreads), 0, ctx.stream, a); \
+  else                                                                                        \
+    hipLaunchKernelGGL((skinny_outer<KG_, false, false>), grid, dim3(kThreads), 0, ctx.stream, a);
     switch ((d.K + 15) / 16) {
-      case 1: hipLaunchKernelGGL(skinny_outer<1>, grid, dim3(kThreads), 0, ctx.stream, a); break;
-      case 2: hipLaunchKernelGGL(skinny_outer<2>, grid, dim3(kThreads), 0, ctx.stream, a); break;
-      default: hipLaunchKernelGGL(skinny_outer<4>, grid, dim3(kThreads), 0, ctx.stream, a); break;
+      case 1: SEEML_OUTER(1) break;
+      case 2: SEEML_OUTER(2) break;
+      default: SEEML_OUTER(4) break;
     }
+#undef SEEML_OUTER
     return LaunchStatus("Gemm(skinny outer)");
   }
   if (kind == SkinnyKind::kRowDot) {
@@ -505,5 +585,7 @@ Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) {
                        dim3(kThreads), 0, ctx.stream, a);
   return LaunchStatus("Gemm(skinny colsum finish)");
 }
+
+}  // namespace
 
 }  // namespace seeml_hip

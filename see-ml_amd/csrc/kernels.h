@@ -92,6 +92,24 @@ Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx);
 // The plan index that selects the skinny kernels (one past the tile configs).
 int GemmSkinnyConfig();
 
+// A kOuter GEMM u = A B followed in the plan by Scale and/or AddEW of its
+// output, executed as one kernel (the engine proves the chain: exact operand
+// matches, and no written range overlapping a read one). kind 1: s = alpha * u
+// -> s, then yout = y (+) s; kind 2: yout = y (+) u. (+) keeps the AddEW's
+// operand order (y_first). u itself is written unless write_u is false (its
+// range is exactly yout's, overwritten by the chain). The flat [M*N] arrays
+// share C's indexing (ldc == N).
+struct SkinnyChain {
+  int kind = 0;
+  float alpha = 1.0f;
+  float* s = nullptr;
+  const float* y = nullptr;
+  float* yout = nullptr;
+  bool write_u = true;
+  bool y_first = true;
+};
+Status LaunchSkinnyChain(const GemmDesc& d, const SkinnyChain& ch, const Ctx& ctx);
+
 // Row-major convenience forms of the reference's GEMM family.
 GemmDesc GemmNNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
 GemmDesc GemmNTDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);

@@ -272,19 +272,33 @@ bool OperandsOf(const UpdateInstruction& ins, Operand* ops, size_t* n) {
 
 }  // namespace
 
-bool WriteRangesOf(const UpdateInstruction& ins,
-                   std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
+namespace {
+
+bool RangesOf(const UpdateInstruction& ins, bool writes,
+              std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
   Operand ops[8];
   size_t n = 0;
   ranges->clear();
   if (!OperandsOf(ins, ops, &n)) return false;
   for (size_t i = 0; i < n; ++i) {
-    if (!ops[i].write || IsRodataRef(ops[i].ref)) continue;
+    if (ops[i].write != writes || IsRodataRef(ops[i].ref)) continue;
     uint64_t bytes = 0;
     if (!MulOk(ops[i].elems, ops[i].elem_bytes, &bytes)) return false;
     ranges->emplace_back(RefOffset(ops[i].ref), bytes);
   }
   return true;
+}
+
+}  // namespace
+
+bool WriteRangesOf(const UpdateInstruction& ins,
+                   std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
+  return RangesOf(ins, true, ranges);
+}
+
+bool ReadRangesOf(const UpdateInstruction& ins,
+                  std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
+  return RangesOf(ins, false, ranges);
 }
 
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,

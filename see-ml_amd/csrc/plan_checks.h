@@ -55,6 +55,9 @@ uint64_t PlanSelfHash(const uint8_t* plan, size_t size, size_t hash_offset);
 // are malformed.
 bool WriteRangesOf(const UpdateInstruction& ins,
                    std::vector<std::pair<uint64_t, uint64_t>>* ranges);
+// The same for the arena ranges an instruction reads.
+bool ReadRangesOf(const UpdateInstruction& ins,
+                  std::vector<std::pair<uint64_t, uint64_t>>* ranges);
 
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,
                            uint64_t rodata_size, uint32_t plan_version);
