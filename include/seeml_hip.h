@@ -127,9 +127,11 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
  * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
 /* Describe the kernel variant chosen for instruction `index` of `program`:
- * GEMMs "cfg-name splits=S" (or "skinny/<kind>"); SoftmaxRowsBwd "causal S=n"
- * when its probabilities are proven AttnFwd/AttnDP outputs (only their causal
- * half is read), else ""; other opcodes "". */
+ * GEMMs "cfg-name splits=S" (or "skinny/<kind>"), with " +AddEW" when the
+ * AddEW after it runs in its epilogue (that AddEW then reads "in GEMM
+ * epilogue"); SoftmaxRowsBwd "causal S=n" when its probabilities are proven
+ * AttnFwd/AttnDP outputs (only their causal half is read), else ""; other
+ * opcodes "". Fusions are planned when the program's graph is built. */
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap);
 

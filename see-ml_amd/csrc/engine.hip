@@ -149,6 +149,7 @@ class Engine {
       return s;
     if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
     for (int p = 0; p < 3; ++p) PlanCausalRows(p);
+    PlanLiveness();
     for (int p = 0; p < 3; ++p) plans_[p].assign(plan_.program[p].size(), GemmPlan{});
     for (int p = 0; p < 3; ++p)
       for (size_t i = 0; i < plan_.program[p].size(); ++i)
@@ -196,6 +197,52 @@ class Engine {
       if (S != cols || B * H * S != rows) continue;
       causal_rows_[program][i] = S;
     }
+  }
+
+  // ---- liveness of transient values ---------------------------------------
+  // A fused launch may leave out the store of an intermediate value that
+  // nothing observes. The plan's transient segment is assigned by liveness
+  // within one program (arena_binder.cc:25-98; the values that must outlive
+  // it, the loss and the gradients, are pinned there), so a transient value
+  // never carries from one run of a program into another. Observed are the
+  // persistent segment, the I/O slots, the loss, the eval probabilities and
+  // the merge deltas the host reads back.
+  using Ranges = std::vector<std::pair<uint64_t, uint64_t>>;
+
+  static bool Overlaps(const Ranges& rs, uint64_t off, uint64_t bytes) {
+    for (const auto& r : rs)
+      if (r.first < off + bytes && off < r.first + r.second) return true;
+    return false;
+  }
+
+  void PlanLiveness() {
+    const PlanHeader& h = plan_.header;
+    observed_.clear();
+    observed_.emplace_back(0, h.persistent_size);
+    if (h.input_ref != kNullRef) observed_.emplace_back(RefOffset(h.input_ref), h.input_floats * 4);
+    if (h.label_ref != kNullRef) observed_.emplace_back(RefOffset(h.label_ref), h.label_bytes);
+    if (h.loss_ref != kNullRef) observed_.emplace_back(RefOffset(h.loss_ref), sizeof(float));
+    if (plan_.eval_probs_ref != kNullRef)
+      observed_.emplace_back(RefOffset(plan_.eval_probs_ref),
+                             plan_.eval_softmax_rows * plan_.eval_softmax_cols * sizeof(float));
+    for (const EmitEntry& e : plan_.emit) observed_.emplace_back(e.arena_offset, e.byte_size);
+    for (int p = 0; p < 3; ++p) {
+      const auto& prog = plan_.program[p];
+      depends_[p].assign(prog.size(), Ranges{});
+      for (size_t i = 0; i < prog.size(); ++i)
+        if (!DependRangesOf(prog[i], &depends_[p][i]))
+          depends_[p][i].assign(1, {0, ~uint64_t{0}});  // unknown: depends on everything
+    }
+  }
+
+  // True when the value instruction k of `program` leaves in the arena bytes
+  // [off, off + bytes) is observed by nothing: it is transient and no later
+  // instruction of the program depends on any of those bytes.
+  bool DeadAfter(int program, size_t k, uint64_t off, uint64_t bytes) const {
+    if (Overlaps(observed_, off, bytes)) return false;
+    for (size_t j = k + 1; j < depends_[program].size(); ++j)
+      if (Overlaps(depends_[program][j], off, bytes)) return false;
+    return true;
   }
 
   // ---- instruction decode ------------------------------------------------
@@ -453,18 +500,32 @@ class Engine {
                  "fused AdamW table upload");
   }
 
-  // LoRA merge chains (kernels.h SkinnyChain): a GemmNN/NT on the skinny
-  // outer kernel, then Scale of its output and/or AddEW of that with
-  // another tensor, adjacent in the plan and none of them marked for timing.
-  // The chain runs as one kernel when its results are provably those of the
-  // three launches in order: the AddEW/Scale operands are exactly the
-  // preceding outputs, and no range the chain writes overlaps a range it
-  // reads (so no workgroup can see another's write). u's own write is
-  // skipped only when the AddEW output is exactly u's range (u is then dead
-  // and overwritten within the chain).
+  // Fused chains, each launched as one kernel when its results are provably
+  // those of its instructions run in order. None of a chain's instructions
+  // may be marked for timing.
+  //
+  // Skinny chains (kernels.h SkinnyChain): a GemmNN/NT on the skinny outer
+  // kernel, then Scale of its output and/or AddEW of that with another
+  // tensor, adjacent in the plan (LoRA's u = t B, s = alpha u, y' = y + s).
+  // The AddEW/Scale operands are exactly the preceding outputs, and no range
+  // the chain writes overlaps a range it reads (so no workgroup can see
+  // another's write). u and s are stored unless dead: overwritten by the
+  // chain's own output, or observed by nothing afterwards (DeadAfter).
+  //
+  // Dense chains (GemmDesc::out): a GEMM on the tile kernels (batch 1, plain
+  // epilogue; with split-K the reduction applies it) and the AddEW right
+  // after it that consumes its output C, e.g. the base and LoRA parts of an
+  // input gradient. The epilogue forms the AddEW's sum from the value it
+  // would store, so the bits are the two launches'. C is stored unless dead
+  // or overwritten by the sum. The sum's output and C must not overlap the
+  // GEMM's operands (other workgroups are still reading them), and the
+  // AddEW's other operand must not overlap C, whose new value it would
+  // otherwise have read.
   struct ChainRun {
     size_t first = 0, count = 0;
-    SkinnyChain ch;
+    bool dense = false;
+    SkinnyChain ch;  // skinny
+    GemmDesc d;      // dense: the GEMM with its fused AddEW
   };
 
   void PlanChains(int program) {
@@ -473,22 +534,25 @@ class Engine {
     auto is_marked = [&](size_t i) {
       return std::binary_search(marked_[program].begin(), marked_[program].end(), i);
     };
-    using Ranges = std::vector<std::pair<uint64_t, uint64_t>>;
     auto overlap = [](const Ranges& a, const Ranges& b) {
       for (const auto& x : a)
-        for (const auto& y : b)
-          if (x.first < y.first + y.second && y.first < x.first + x.second) return true;
+        if (Overlaps(b, x.first, x.second)) return true;
       return false;
     };
     for (size_t i = 0; i + 1 < prog.size(); ++i) {
       const UpdateInstruction& g = prog[i];
       const auto op = static_cast<Op>(g.opcode);
-      if ((op != Op::kGemmNN && op != Op::kGemmNT) || g.flags != 0 || is_marked(i)) continue;
-      if (plans_[program][i].cfg != GemmSkinnyConfig()) continue;
+      if (op != Op::kGemmNN && op != Op::kGemmNT && op != Op::kGemmTN) continue;
+      if (g.flags != 0 || is_marked(i)) continue;
       const GemmDesc d = DescOf(g);
-      if (SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N) continue;
       const uint64_t n = g.out[0] * g.out[1];
+      const uint64_t bytes = n * sizeof(float);
       const uint64_t u = g.in[2];
+      if (plans_[program][i].cfg != GemmSkinnyConfig()) {
+        if (PlanDenseChain(program, i, d)) ++i;
+        continue;
+      }
+      if (op == Op::kGemmTN || SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N) continue;
       size_t k = i + 1;
       SkinnyChain ch;
       uint64_t v = u;  // the value the AddEW must consume
@@ -507,11 +571,15 @@ class Engine {
       ch.y_first = a.in[1] == v;
       const uint64_t y = ch.y_first ? a.in[0] : a.in[1];
       if (IsRodataRef(y) || IsRodataRef(a.in[2])) continue;
-      const uint64_t bytes = n * sizeof(float);
-      ch.write_u = a.in[2] != u;
-      Ranges writes, reads, tmp;
+      // y is read from memory; u and s exist only in registers until stored.
+      if (Overlaps(Ranges{{RefOffset(u), bytes}}, RefOffset(y), bytes) ||
+          (ch.kind == 1 && Overlaps(Ranges{{RefOffset(v), bytes}}, RefOffset(y), bytes)))
+        continue;
+      ch.write_u = a.in[2] != u && !DeadAfter(program, k, RefOffset(u), bytes);
+      const bool write_s = ch.kind == 1 && a.in[2] != v && !DeadAfter(program, k, RefOffset(v), bytes);
+      Ranges writes, reads;
       if (ch.write_u) writes.emplace_back(RefOffset(u), bytes);
-      if (ch.kind == 1) writes.emplace_back(RefOffset(v), bytes);
+      if (write_s) writes.emplace_back(RefOffset(v), bytes);
       writes.emplace_back(RefOffset(a.in[2]), bytes);
       (void)ReadRangesOf(g, &reads);
       reads.emplace_back(RefOffset(y), bytes);
@@ -522,7 +590,7 @@ class Engine {
         for (size_t z = x + 1; z < writes.size(); ++z)
           if (overlap(Ranges{writes[x]}, Ranges{writes[z]})) clash = true;
       if (clash) continue;
-      ch.s = ch.kind == 1 ? WP(v) : nullptr;
+      ch.s = write_s ? WP(v) : nullptr;
       ch.y = RP(y);
       ch.yout = WP(a.in[2]);
       if (!aligned16(ch.y) || !aligned16(ch.yout) || (ch.s && !aligned16(ch.s))) continue;
@@ -533,6 +601,61 @@ class Engine {
       chains_[program].push_back(run);
       i = k;
     }
+  }
+
+  // A dense chain at instruction i (the GEMM), if instruction i + 1 admits one.
+  bool PlanDenseChain(int program, size_t i, GemmDesc d) {
+    const auto& prog = plan_.program[program];
+    const UpdateInstruction& g = prog[i];
+    const UpdateInstruction& a = prog[i + 1];
+    if (static_cast<Op>(a.opcode) != Op::kAddEW ||
+        std::binary_search(marked_[program].begin(), marked_[program].end(), i + 1))
+      return false;
+    if (d.batch != 1 || d.ldc != d.N || d.causal != Causal::kNone ||
+        d.accumulate || d.bias || d.act != 0 || d.b_int8)
+      return false;
+    const uint64_t c = g.in[2], bytes = a.out[0] * sizeof(float);
+    if (a.out[0] != g.out[0] * g.out[1] || (a.in[0] != c && a.in[1] != c)) return false;
+    const bool addend_first = a.in[1] == c;
+    const uint64_t y = addend_first ? a.in[0] : a.in[1];
+    const uint64_t o = a.in[2];
+    if (y == c || IsRodataRef(o)) return false;
+    const bool write_c = o != c && !DeadAfter(program, i + 1, RefOffset(c), bytes);
+    Ranges writes{{RefOffset(o), bytes}};
+    if (write_c) writes.emplace_back(RefOffset(c), bytes);
+    Ranges reads;
+    (void)ReadRangesOf(g, &reads);
+    for (const auto& w : writes)
+      if (Overlaps(reads, w.first, w.second)) return false;
+    if (write_c && o != c && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(c), bytes))
+      return false;
+    if (!IsRodataRef(y)) {
+      if (Overlaps(Ranges{{RefOffset(c), bytes}}, RefOffset(y), bytes)) return false;
+      if (y != o && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(y), bytes)) return false;
+    }
+    d.addend = RP(y);
+    d.out = WP(o);
+    d.addend_first = addend_first;
+    d.write_c = write_c;
+    ChainRun run;
+    run.first = i;
+    run.count = 2;
+    run.dense = true;
+    run.d = d;
+    chains_[program].push_back(run);
+    return true;
+  }
+
+  // The chain instruction idx belongs to in the built program, or null.
+  const ChainRun* ChainAt(int program, size_t idx) const {
+    for (const ChainRun& run : chains_[program])
+      if (idx >= run.first && idx < run.first + run.count) return &run;
+    return nullptr;
+  }
+
+  Status LaunchChain(int program, const ChainRun& run, const Ctx& c) {
+    if (run.dense) return LaunchGemm(run.d, plans_[program][run.first], c);
+    return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
   }
 
   // Algorithmic bytes of an instruction of a chain, for splitting the fused
@@ -558,8 +681,7 @@ class Engine {
     while (q < chains.size() && chains[q].first < begin) ++q;
     for (size_t i = begin; i < end;) {
       if (q < chains.size() && chains[q].first == i && i + chains[q].count <= end) {
-        if (Status s = LaunchSkinnyChain(DescOf(plan_.program[program][i]), chains[q].ch, c); !s)
-          return s;
+        if (Status s = LaunchChain(program, chains[q], c); !s) return s;
         i += chains[q].count;
         ++q;
         continue;
@@ -1085,7 +1207,7 @@ class Engine {
       size_t fr = 0, fq = 0;
       for (size_t i = 0; i < n;) {
         if (fq < chains.size() && chains[fq].first == i) {
-          if (Status s = LaunchSkinnyChain(DescOf(prog[i]), chains[fq].ch, c); !s) {
+          if (Status s = LaunchChain(program, chains[fq], c); !s) {
             result = s;
             break;
           }
@@ -1116,6 +1238,11 @@ class Engine {
           const ChainRun& run = chains[fq++];
           float ms = 0.0f;
           (void)hipEventElapsedTime(&ms, ev[i], ev[i + run.count]);
+          if (run.dense) {  // MFMA-bound: the fused AddEW adds only epilogue traffic
+            acc[i] += ms;
+            i += run.count;
+            continue;
+          }
           double total = 0.0;
           for (size_t k = i; k < i + run.count; ++k) total += ChainBytes(prog[k]);
           for (size_t k = i; k < i + run.count; ++k)
@@ -1174,11 +1301,14 @@ class Engine {
     if (static_cast<Op>(plan_.program[program][idx].opcode) == Op::kSoftmaxRowsBwd)
       return causal_rows_[program][idx] ? "causal S=" + std::to_string(causal_rows_[program][idx])
                                         : std::string();
+    const ChainRun* run = ChainAt(program, idx);
+    if (run && run->dense && idx == run->first + 1) return "in GEMM epilogue";
     if (!IsGemmOp(plan_.program[program][idx].opcode)) return std::string();
     const GemmPlan& p = plans_[program][idx];
     if (p.cfg == GemmSkinnyConfig())
       return SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])));
-    return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits);
+    return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits) +
+           (run && run->dense ? " +AddEW" : "");
   }
 
   void Release() {
@@ -1227,6 +1357,8 @@ class Engine {
   uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
   std::vector<ChainRun> chains_[3];
+  std::vector<Ranges> depends_[3];  // per instruction: DependRangesOf
+  Ranges observed_;
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;

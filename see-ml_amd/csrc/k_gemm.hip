@@ -19,7 +19,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Sums split-K partials in slice order and applies the epilogue (batch 1).
+// Sums split-K partials in slice order and applies the epilogue, a fused
+// AddEW included (batch 1).
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(GemmKArgs p) {
   const int64_t total = p.M * p.N;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
@@ -32,7 +33,13 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(GemmKArgs p) {
     if (p.accumulate) val = p.C[m * p.ldc + n] + val;
     if (p.bias) val = val + p.bias[n];
     val = dev_act(p.act, val);
-    p.C[m * p.ldc + n] = val;
+    if (p.out) {
+      if (p.write_c) p.C[m * p.ldc + n] = val;
+      const float y = p.addend[idx];
+      p.out[idx] = p.addend_first ? y + val : val + y;
+    } else {
+      p.C[m * p.ldc + n] = val;
+    }
   }
 }
 
@@ -97,6 +104,7 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
   if (plan.cfg == kNumCfgs) {
+    if (d.out) return Status::Fail(kUnitEngine, "Gemm: the skinny kernels take no fused AddEW");
     if (ctx.ws_bytes < SkinnyWorkspace(d))
       return Status::Fail(kUnitEngine, "Gemm: workspace too small for the skinny kernel");
     return LaunchSkinny(d, ctx);
@@ -106,6 +114,11 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");
   if (plan.splits > 1 && ctx.ws_bytes < plan.ws_bytes)
     return Status::Fail(kUnitEngine, "Gemm: workspace too small for split-K");
+  if (d.out && (!d.addend || d.batch != 1 || d.ldc != d.N || d.causal != Causal::kNone ||
+                d.accumulate || d.bias))
+    return Status::Fail(kUnitEngine,
+                        "Gemm: a fused AddEW needs batch 1, ldc == N and a plain epilogue "
+                        "(no accumulate, bias or causal mode)");
   if (d.b_int8 && !d.a_kc)
     return Status::Fail(kUnitEngine, "Gemm: unsupported int8 operand layout");
   if (!d.a_kc && d.b_kc)
@@ -118,6 +131,16 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   const bool vec = !d.b_int8 && VecOk(d.A, d.lda, d.a_sb, d.a_sh, d.a_kc ? d.K : d.M) &&
                    VecOk(d.B, d.ldb, d.b_sb, d.b_sh, d.b_kc ? d.K : d.N) &&
                    d.lda < (int64_t{1} << 23) && d.ldb < (int64_t{1} << 23);
+  if (d.out && !vec) {
+    // The element-load form has no fused epilogue: the GEMM stores C (always
+    // safe: C's range is C's while the GEMM writes it), then the AddEW runs.
+    GemmDesc plain = d;
+    plain.addend = nullptr;
+    plain.out = nullptr;
+    if (Status s = LaunchGemm(plain, plan, ctx); !s) return s;
+    return d.addend_first ? AddEW(d.addend, d.C, d.out, static_cast<size_t>(d.M * d.N), ctx)
+                          : AddEW(d.C, d.addend, d.out, static_cast<size_t>(d.M * d.N), ctx);
+  }
   const int cfg = vec ? plan.cfg : gemm::kCfgSmall;
   const CfgInfo& c = kCfgs[cfg];
   const int64_t tm = CeilDiv(d.M, c.mt_m), tn = CeilDiv(d.N, c.mt_n);
@@ -145,6 +168,10 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
                       : d.K;
   a.tiles_m = static_cast<int>(tm);
   a.tiles_n = static_cast<int>(tn);
+  a.addend = d.addend;
+  a.out = d.out;
+  a.addend_first = d.addend_first ? 1 : 0;
+  a.write_c = d.write_c ? 1 : 0;
 
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                   static_cast<unsigned>(d.batch));

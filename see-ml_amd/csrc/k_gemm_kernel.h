@@ -89,6 +89,10 @@ struct GemmKArgs {
   int splits;
   int64_t k_per_split;
   int tiles_m, tiles_n;
+  const float* addend;  // fused AddEW (GemmDesc::addend): out = addend (+) c
+  float* out;
+  int addend_first;
+  int write_c;
 };
 
 // Tile configurations (the autotuner's arms).
@@ -246,7 +250,7 @@ __device__ __forceinline__ int64_t XcdLogical(int64_t lin, int64_t total) {
 }
 
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED>
+          bool VEC, bool SCHED, bool FUSED>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
   using BT = typename std::conditional<B_I8, int8_t, float>::type;
   constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -428,6 +432,42 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
     }
   }
 
+  // A fused AddEW (GemmKArgs::out; FUSED instantiations, launched with one
+  // slice and a plain epilogue). On a whole tile, each lane holds one base
+  // pointer per array; element (i, j, v) sits a compile-time number of rows
+  // and columns from it, so no per-element offsets stay live. The addends
+  // are loaded first, all in flight together, then the sums are stored.
+  // The value summed is the one the plain epilogue would store in C.
+  if constexpr (FUSED) {
+    if (p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
+      const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
+      const float* ya = p.addend + lm * p.N + ln;
+      float* oa = p.out + lm * p.N + ln;
+      float* ca = C + lm * p.ldc + ln;
+      float yv[BM][BN][16];
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            yv[i][j][v] = ya[(32 * i + 8 * (v >> 2) + (v & 3)) * p.N + 32 * j];
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = 32 * i + 8 * (v >> 2) + (v & 3);
+            const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
+            if (p.write_c) ca[row * p.ldc + 32 * j] = val;
+            const float y = yv[i][j][v];
+            oa[row * p.N + 32 * j] = p.addend_first ? y + val : val + y;
+          }
+      return;
+    }
+  }
+
   // Write-back. Lane (h, r) of the 32x32 block holds rows 8*(v/4) + 4*h + v%4
   // of column r in accumulator element v.
 #pragma unroll
@@ -449,22 +489,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
         if (p.bias) val = val + p.bias[n];
         val = dev_act(p.act, val);
         if (p.causal == static_cast<int>(Causal::kLowerOut) && n > m) val = 0.0f;
-        C[m * p.ldc + n] = val;
+        if constexpr (FUSED) {  // a partial tile
+          if (p.write_c) C[m * p.ldc + n] = val;
+          const float y = p.addend[m * p.N + n];
+          p.out[m * p.N + n] = p.addend_first ? y + val : val + y;
+        } else {
+          C[m * p.ldc + n] = val;
+        }
       }
 }
 
 // Launches config `cfg` of one operand-layout variant. The element-load
 // form (!VEC) exists only for the small tile; the host plans it as such.
-template <bool A_KC, bool B_KC, bool B_I8, bool VEC, bool SCHED = false>
+template <bool A_KC, bool B_KC, bool B_I8, bool VEC, bool SCHED = false, bool FUSED = false>
 void LaunchVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
   const dim3 block(kCfgs[cfg].threads);
 #define SEEML_GEMM_CASE(I, MM, NN, KK, WM_, WN_)                                                \
   case I:                                                                                     \
-    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, B_I8, VEC, SCHED>), grid, \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, B_I8, VEC, SCHED, FUSED>), grid, \
                        block, 0, s, a);                                                       \
     break;
   if constexpr (!VEC) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<64, 64, 32, 2, 2, A_KC, B_KC, B_I8, false, false>), grid,
+    hipLaunchKernelGGL((gemm_mfma_kernel<64, 64, 32, 2, 2, A_KC, B_KC, B_I8, false, false, false>), grid,
                        dim3(kCfgs[kCfgSmall].threads), 0, s, a);
   } else {
     switch (cfg) {

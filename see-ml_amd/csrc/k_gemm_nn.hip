@@ -5,7 +5,8 @@ namespace seeml_hip {
 namespace gemm {
 
 void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a) {
-  if (vec) LaunchVariant<true, false, false, true, true>(cfg, grid, s, a);
+  if (vec && a.out && a.splits == 1) LaunchVariant<true, false, false, true, true, true>(cfg, grid, s, a);
+  else if (vec) LaunchVariant<true, false, false, true, true>(cfg, grid, s, a);
   else LaunchVariant<true, false, false, false>(cfg, grid, s, a);
 }
 

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
           if (p.chain == 1) {
             v = make_float4(p.chain_alpha * u.x, p.chain_alpha * u.y, p.chain_alpha * u.z,
                             p.chain_alpha * u.w);
-            *reinterpret_cast<float4*>(p.S + at) = v;
+            if (p.S) *reinterpret_cast<float4*>(p.S + at) = v;
           }
           const float4 y = yc[rb];
           *reinterpret_cast<float4*>(p.Yout + at) =
@@ -496,7 +496,7 @@ Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx) { return LaunchSkinnyImpl
 
 Status LaunchSkinnyChain(const GemmDesc& d, const SkinnyChain& ch, const Ctx& ctx) {
   if (SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N || (ch.kind != 1 && ch.kind != 2) ||
-      !ch.y || !ch.yout || (ch.kind == 1 && !ch.s) || !aligned16(ch.y) || !aligned16(ch.yout) ||
+      !ch.y || !ch.yout || !aligned16(ch.y) || !aligned16(ch.yout) ||
       (ch.s && !aligned16(ch.s)))
     return Status::Fail(kUnitEngine, "Gemm: chain does not fit the skinny outer kernel");
   return LaunchSkinnyImpl(d, &ch, ctx);

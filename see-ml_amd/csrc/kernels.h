@@ -66,6 +66,14 @@ struct GemmDesc {
   const float* bias = nullptr;
   int act = 0;
   Causal causal = Causal::kNone;
+  // A following AddEW folded into the epilogue (tile kernels or their
+  // split-K reduction; batch 1, ldc == N): out[m*N+n] = addend[m*N+n] (+) c, where c is the
+  // value the GEMM stores at C(m, n) and (+) keeps the AddEW's operand order
+  // (addend_first). C itself is stored only when write_c.
+  const float* addend = nullptr;
+  float* out = nullptr;
+  bool addend_first = true;
+  bool write_c = true;
 };
 
 struct GemmPlan {
@@ -94,11 +102,12 @@ int GemmSkinnyConfig();
 
 // A kOuter GEMM u = A B followed in the plan by Scale and/or AddEW of its
 // output, executed as one kernel (the engine proves the chain: exact operand
-// matches, and no written range overlapping a read one). kind 1: s = alpha * u
-// -> s, then yout = y (+) s; kind 2: yout = y (+) u. (+) keeps the AddEW's
-// operand order (y_first). u itself is written unless write_u is false (its
-// range is exactly yout's, overwritten by the chain). The flat [M*N] arrays
-// share C's indexing (ldc == N).
+// matches, and no written range overlapping a read one). kind 1: s = alpha * u,
+// then yout = y (+) s; kind 2: yout = y (+) u. (+) keeps the AddEW's operand
+// order (y_first). u is stored unless write_u is false and s only where
+// s != nullptr: the engine drops a store when the value is dead (its range is
+// overwritten by the chain, or nothing observes it afterwards). The flat
+// [M*N] arrays share C's indexing (ldc == N).
 struct SkinnyChain {
   int kind = 0;
   float alpha = 1.0f;

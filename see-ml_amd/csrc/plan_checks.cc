@@ -301,6 +301,21 @@ bool ReadRangesOf(const UpdateInstruction& ins,
   return RangesOf(ins, false, ranges);
 }
 
+bool DependRangesOf(const UpdateInstruction& ins,
+                    std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
+  if (!RangesOf(ins, false, ranges)) return false;
+  switch (static_cast<Op>(ins.opcode)) {
+    case Op::kGemmAccNN: case Op::kClipNorm: case Op::kSgdStep: case Op::kAdamWStep: {
+      std::vector<std::pair<uint64_t, uint64_t>> w;
+      if (!RangesOf(ins, true, &w)) return false;
+      ranges->insert(ranges->end(), w.begin(), w.end());
+      break;
+    }
+    default: break;
+  }
+  return true;
+}
+
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,
                            uint64_t rodata_size, uint32_t plan_version) {
   const std::string op = std::to_string(ins.opcode);

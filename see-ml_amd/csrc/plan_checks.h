@@ -58,6 +58,12 @@ bool WriteRangesOf(const UpdateInstruction& ins,
 // The same for the arena ranges an instruction reads.
 bool ReadRangesOf(const UpdateInstruction& ins,
                   std::vector<std::pair<uint64_t, uint64_t>>* ranges);
+// Every arena range an instruction's results depend on: ReadRangesOf plus the
+// operands it updates in place (GemmAccNN's C, the optimizer steps'
+// parameters and moments, ClipNorm's tensor), which the operand table lists
+// as writes only.
+bool DependRangesOf(const UpdateInstruction& ins,
+                    std::vector<std::pair<uint64_t, uint64_t>>* ranges);
 
 Status ValidateInstruction(const UpdateInstruction& ins, uint64_t arena_size,
                            uint64_t rodata_size, uint32_t plan_version);

@@ -12,7 +12,8 @@ compute). These are the numbers `roofline.achieved` and the MFMA-utilisation
 Classes: "mfma" for GEMM-family contractions with min(M, N, K) >= 64 (dense,
 compute-bound on the matrix cores); "hbm" for skinny LoRA GEMMs (a dim = r)
 and every non-contraction kernel; "attn" for the attention contractions,
-judged by min(compute, bandwidth).
+judged by min(compute, bandwidth); "fused" for an instruction executed inside
+another's launch (no time, no bytes of its own).
 """
 from __future__ import annotations
 
@@ -35,7 +36,9 @@ def work(ins: dict, variant: str = "") -> dict:
 
     `variant` is the engine's kernel choice for it (seeml_hip_gemm_choice):
     a causal SoftmaxRowsBwd reads only the float4s of P and dP that hold
-    j <= i, so its bytes are those reads plus the full dS write."""
+    j <= i, so its bytes are those reads plus the full dS write; a GEMM with
+    the following AddEW in its epilogue ("+AddEW") also reads the addend and
+    writes the sum, and that AddEW (class "fused") has no launch of its own."""
     name = OP_NAME.get(ins["opcode"], str(ins["opcode"]))
     o = ins["out"]
     flops, nbytes, cls, shape = 0, 0, "hbm", ()
@@ -48,6 +51,8 @@ def work(ins: dict, variant: str = "") -> dict:
             nbytes += 4 * M * N
         if ins["flags"] & 1:
             nbytes += 4 * N
+        if variant.endswith("+AddEW"):
+            nbytes += 8 * M * N
         cls = "mfma" if min(M, N, K) >= 64 else "hbm"
         shape = (M, N, K)
     elif name in ATTN or name in ("RopeFwd", "RopeBwd"):
@@ -64,6 +69,8 @@ def work(ins: dict, variant: str = "") -> dict:
             flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
         else:  # DV / DQ / DK: read P-shaped + one activation, write one
             flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
+    elif name == "AddEW" and variant == "in GEMM epilogue":
+        cls, shape = "fused", (o[0],)
     elif name in ("AddEW", "MulEW", "ReluBwd", "GeluBwd", "SiluBwd"):
         nbytes, shape = 12 * o[0], (o[0],)
     elif name in ("Scale", "ReluFwd", "GeluFwd", "SiluFwd", "Copy"):

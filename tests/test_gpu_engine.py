@@ -276,3 +276,27 @@ def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
     want = out.cpu().numpy()
     assert np.array_equal(dS.view(np.uint32), want.view(np.uint32))
     e.close()
+
+
+def test_gemm_addew_chains_are_planned(torch_gpu):
+    """On a decoder the GEMM + AddEW fusion and the LoRA chains fire (so the
+    graph == eager bitwise test above compares fused against unfused
+    launches): every AddEW reported inside a GEMM epilogue directly follows
+    a GEMM reported "+AddEW"; an eager engine plans no fusion."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c4m")
+    x, y = configs.batch(w, 0)
+    e = engine(p)
+    e.train_step(x, y)
+    ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+    fused = [i for i, c in enumerate(ch) if c == "in GEMM epilogue"]
+    assert len(fused) >= 4, ch
+    assert all(ch[i - 1].endswith("+AddEW") for i in fused)
+    assert sum(c.endswith("+AddEW") for c in ch) == len(fused)
+    e.close()
+    e = engine(p, use_graph=False)
+    e.train_step(x, y)
+    assert not any("AddEW" in e.gemm_choice(PROGRAM_TRAIN, i) or
+                   e.gemm_choice(PROGRAM_TRAIN, i) == "in GEMM epilogue"
+                   for i in range(len(p.train)))
+    e.close()
