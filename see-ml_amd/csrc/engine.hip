@@ -229,19 +229,37 @@ class Engine {
     for (int p = 0; p < 3; ++p) {
       const auto& prog = plan_.program[p];
       depends_[p].assign(prog.size(), Ranges{});
-      for (size_t i = 0; i < prog.size(); ++i)
+      writes_[p].assign(prog.size(), Ranges{});
+      for (size_t i = 0; i < prog.size(); ++i) {
         if (!DependRangesOf(prog[i], &depends_[p][i]))
           depends_[p][i].assign(1, {0, ~uint64_t{0}});  // unknown: depends on everything
+        if (!WriteRangesOf(prog[i], &writes_[p][i])) writes_[p][i].clear();  // overwrites nothing
+      }
     }
   }
 
   // True when the value instruction k of `program` leaves in the arena bytes
-  // [off, off + bytes) is observed by nothing: it is transient and no later
-  // instruction of the program depends on any of those bytes.
+  // [off, off + bytes) is observed by nothing: it is transient, and walking
+  // the program from k + 1 every byte of it is overwritten before any later
+  // instruction depends on it (or the program ends).
   bool DeadAfter(int program, size_t k, uint64_t off, uint64_t bytes) const {
     if (Overlaps(observed_, off, bytes)) return false;
-    for (size_t j = k + 1; j < depends_[program].size(); ++j)
-      if (Overlaps(depends_[program][j], off, bytes)) return false;
+    Ranges live{{off, bytes}};  // the bytes still holding the value
+    for (size_t j = k + 1; j < depends_[program].size() && !live.empty(); ++j) {
+      for (const auto& r : live)
+        if (Overlaps(depends_[program][j], r.first, r.second)) return false;
+      for (const auto& w : writes_[program][j]) {
+        Ranges rest;
+        for (const auto& r : live) {
+          const uint64_t lo = r.first, hi = r.first + r.second;
+          const uint64_t wlo = w.first, whi = w.first + w.second;
+          if (whi <= lo || hi <= wlo) { rest.push_back(r); continue; }
+          if (lo < wlo) rest.emplace_back(lo, wlo - lo);
+          if (whi < hi) rest.emplace_back(whi, hi - whi);
+        }
+        live.swap(rest);
+      }
+    }
     return true;
   }
 
@@ -493,6 +511,7 @@ class Engine {
       }
     }
     PlanChains(program);
+    PlanPointwiseRuns(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -521,11 +540,16 @@ class Engine {
   // GEMM's operands (other workgroups are still reading them), and the
   // AddEW's other operand must not overlap C, whose new value it would
   // otherwise have read.
+  //
+  // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
+  enum class ChainKind { kSkinny, kDense, kPointwise };
   struct ChainRun {
     size_t first = 0, count = 0;
-    bool dense = false;
-    SkinnyChain ch;  // skinny
-    GemmDesc d;      // dense: the GEMM with its fused AddEW
+    ChainKind kind = ChainKind::kSkinny;
+    SkinnyChain ch;      // skinny
+    GemmDesc d;          // dense: the GEMM with its fused AddEW
+    PointwiseRun pw;     // pointwise
+    uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
   };
 
   void PlanChains(int program) {
@@ -598,9 +622,150 @@ class Engine {
       run.first = i;
       run.count = k - i + 1;
       run.ch = ch;
+      run.bytes = 4 * (d.M * d.K + d.K * d.N) + bytes * (1 + writes.size());  // t, B, y; stores
       chains_[program].push_back(run);
       i = k;
     }
+  }
+
+  // Pointwise runs: maximal stretches (up to kPwOps) of adjacent pointwise
+  // instructions of one element count n, outside the other fusions and not
+  // marked. Every arena operand range (4n bytes from its offset) must be
+  // identical to or disjoint from every other in the run, so element i of
+  // each instruction depends only on element i of earlier values: each
+  // thread then evaluates the run for its elements in registers, forwarding
+  // a result to later readers of the same range, and stores each written
+  // range's final value unless DeadAfter the run.
+  static bool PwOpOf(const UpdateInstruction& ins, PwOp* op, int* arity) {
+    *arity = 2;
+    switch (static_cast<Op>(ins.opcode)) {
+      case Op::kAddEW: *op = PwOp::kAdd; return true;
+      case Op::kMulEW: *op = PwOp::kMul; return true;
+      case Op::kReluBwd: *op = PwOp::kReluBwd; return true;
+      case Op::kGeluBwd: *op = PwOp::kGeluBwd; return true;
+      case Op::kSiluBwd: *op = PwOp::kSiluBwd; return true;
+      default: break;
+    }
+    *arity = 1;
+    switch (static_cast<Op>(ins.opcode)) {
+      case Op::kScale: *op = PwOp::kScale; return true;
+      case Op::kReluFwd: *op = PwOp::kRelu; return true;
+      case Op::kGeluFwd: *op = PwOp::kGelu; return true;
+      case Op::kSiluFwd: *op = PwOp::kSilu; return true;
+      case Op::kCopy: *op = PwOp::kCopy; return true;
+      default: return false;
+    }
+  }
+
+  void PlanPointwiseRuns(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    for (size_t i = 0; i < prog.size();) {
+      ChainRun run;
+      if (BuildPointwiseRun(program, i, taken, &run)) {
+        i += run.count;
+        chains_[program].push_back(run);
+      } else {
+        ++i;
+      }
+    }
+    std::sort(chains_[program].begin(), chains_[program].end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  bool BuildPointwiseRun(int program, size_t i, const std::vector<char>& taken, ChainRun* out) {
+    const auto& prog = plan_.program[program];
+    PointwiseRun pw;
+    PwStep steps[kPwOps];
+    uint64_t outs[kPwOps] = {};
+    int nin_after[kPwOps] = {};
+    std::vector<std::pair<uint64_t, int>> slot_of;  // ref -> slot of its current value
+    std::vector<uint64_t> offs;                     // arena operand offsets seen
+    uint64_t n = 0;
+    int nin = 0;
+    size_t j = i;
+    for (; j < prog.size() && j - i < static_cast<size_t>(kPwOps); ++j) {
+      const UpdateInstruction& ins = prog[j];
+      PwOp op;
+      int arity;
+      if (taken[j] || !PwOpOf(ins, &op, &arity)) break;
+      if (j == i) n = ins.out[0];
+      if (n == 0 || ins.out[0] != n) break;
+      const uint64_t bytes = n * sizeof(float);
+      const uint64_t a = ins.in[0], b = arity == 2 ? ins.in[1] : ins.in[0];
+      const uint64_t o = arity == 2 ? ins.in[2] : ins.in[1];
+      if (IsRodataRef(o)) break;
+      bool ok = true;
+      for (const uint64_t ref : {a, b, o}) {
+        if (IsRodataRef(ref)) continue;
+        const uint64_t off = RefOffset(ref);
+        for (const uint64_t x : offs)
+          if (x != off && x < off + bytes && off < x + bytes) ok = false;
+      }
+      if (!ok) break;
+      // Operand slots (inputs first read here are loaded by the kernel).
+      int next_nin = nin;
+      auto next_slots = slot_of;
+      const float* next_in[kPwIn];
+      std::copy(pw.in, pw.in + kPwIn, next_in);
+      auto slot = [&](uint64_t ref) -> int {
+        for (const auto& e : next_slots)
+          if (e.first == ref) return e.second;
+        if (next_nin == kPwIn) return -1;
+        next_in[next_nin] = RP(ref);
+        next_slots.emplace_back(ref, next_nin);
+        return next_nin++;
+      };
+      const int sa = slot(a), sb = slot(b);
+      if (sa < 0 || sb < 0) break;
+      const int step = static_cast<int>(j - i);
+      steps[step].op = op;
+      steps[step].a = sa;
+      steps[step].b = sb;
+      pw.alpha[step] = op == PwOp::kScale ? Bits(ins.in[2]) : 1.0f;
+      outs[step] = o;
+      bool replaced = false;
+      for (auto& e : next_slots)
+        if (e.first == o) e.second = kPwIn + step, replaced = true;
+      if (!replaced) next_slots.emplace_back(o, kPwIn + step);
+      nin = next_nin;
+      nin_after[step] = nin;
+      slot_of = next_slots;
+      std::copy(next_in, next_in + kPwIn, pw.in);
+      for (const uint64_t ref : {a, b, o})
+        if (!IsRodataRef(ref)) offs.push_back(RefOffset(ref));
+    }
+    // The longest prefix (two steps or more) that is a compiled program.
+    // Inputs are numbered in first-read order, so a prefix's are a prefix.
+    size_t count = j - i;
+    for (; count >= 2; --count)
+      if ((pw.program = PwProgramOf(nin_after[count - 1], steps, static_cast<int>(count))) >= 0)
+        break;
+    if (count < 2) return false;
+    const uint64_t bytes = n * sizeof(float);
+    pw.n = n;
+    int stored = 0;
+    for (size_t st = 0; st < count; ++st) {
+      // Step st's result is its range's final value unless a later step of
+      // the prefix writes the same range.
+      bool final_value = true;
+      for (size_t later = st + 1; later < count; ++later)
+        if (outs[later] == outs[st]) final_value = false;
+      if (!final_value || DeadAfter(program, i + count - 1, RefOffset(outs[st]), bytes)) continue;
+      pw.out[st] = WP(outs[st]);
+      ++stored;
+    }
+    out->first = i;
+    out->count = count;
+    out->kind = ChainKind::kPointwise;
+    out->pw = pw;
+    out->bytes = bytes * static_cast<uint64_t>(nin_after[count - 1] + stored);
+    return true;
   }
 
   // A dense chain at instruction i (the GEMM), if instruction i + 1 admits one.
@@ -640,7 +805,7 @@ class Engine {
     ChainRun run;
     run.first = i;
     run.count = 2;
-    run.dense = true;
+    run.kind = ChainKind::kDense;
     run.d = d;
     chains_[program].push_back(run);
     return true;
@@ -654,23 +819,15 @@ class Engine {
   }
 
   Status LaunchChain(int program, const ChainRun& run, const Ctx& c) {
-    if (run.dense) return LaunchGemm(run.d, plans_[program][run.first], c);
-    return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
-  }
-
-  // Algorithmic bytes of an instruction of a chain, for splitting the fused
-  // launch's measured time in the per-instruction profile.
-  double ChainBytes(const UpdateInstruction& ins) const {
-    const double M = ins.out[0], N = ins.out[1], K = ins.out[2];
-    switch (static_cast<Op>(ins.opcode)) {
-      case Op::kScale: return 8.0 * ins.out[0];
-      case Op::kAddEW: return 12.0 * ins.out[0];
-      default: return 4.0 * (M * K + K * N + M * N);
+    switch (run.kind) {
+      case ChainKind::kDense: return LaunchGemm(run.d, plans_[program][run.first], c);
+      case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
+      default: return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
     }
   }
 
   // The captured launch sequence of instructions [begin, end): plan order,
-  // fused AdamW runs and LoRA merge chains (wholly inside the range) as one
+  // fused AdamW runs and chains (wholly inside the range) as one
   // launch each.
   Status RunFused(int program, size_t begin, size_t end) {
     const Ctx c = MakeCtx();
@@ -1238,15 +1395,9 @@ class Engine {
           const ChainRun& run = chains[fq++];
           float ms = 0.0f;
           (void)hipEventElapsedTime(&ms, ev[i], ev[i + run.count]);
-          if (run.dense) {  // MFMA-bound: the fused AddEW adds only epilogue traffic
-            acc[i] += ms;
-            i += run.count;
-            continue;
-          }
-          double total = 0.0;
-          for (size_t k = i; k < i + run.count; ++k) total += ChainBytes(prog[k]);
-          for (size_t k = i; k < i + run.count; ++k)
-            acc[k] += total > 0.0 ? ms * ChainBytes(prog[k]) / total : 0.0;
+          // One launch: its time goes to the chain's first instruction (the
+          // others report "in ..." from GemmChoice).
+          acc[i] += ms;
           i += run.count;
           continue;
         }
@@ -1302,13 +1453,24 @@ class Engine {
       return causal_rows_[program][idx] ? "causal S=" + std::to_string(causal_rows_[program][idx])
                                         : std::string();
     const ChainRun* run = ChainAt(program, idx);
-    if (run && run->dense && idx == run->first + 1) return "in GEMM epilogue";
+    if (run && idx != run->first) {
+      switch (run->kind) {
+        case ChainKind::kDense: return "in GEMM epilogue";
+        case ChainKind::kPointwise: return "in pointwise run";
+        default: return "in chain";
+      }
+    }
+    if (run && run->kind == ChainKind::kPointwise)
+      return "pointwise run of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
     if (!IsGemmOp(plan_.program[program][idx].opcode)) return std::string();
     const GemmPlan& p = plans_[program][idx];
-    if (p.cfg == GemmSkinnyConfig())
-      return SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])));
+    if (p.cfg == GemmSkinnyConfig()) {
+      std::string k = SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])));
+      if (run) k += " chain of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
+      return k;
+    }
     return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits) +
-           (run && run->dense ? " +AddEW" : "");
+           (run ? " +AddEW" : "");
   }
 
   void Release() {
@@ -1358,6 +1520,7 @@ class Engine {
   std::vector<FusedRun> fused_runs_[3];
   std::vector<ChainRun> chains_[3];
   std::vector<Ranges> depends_[3];  // per instruction: DependRangesOf
+  std::vector<Ranges> writes_[3];   // per instruction: WriteRangesOf
   Ranges observed_;
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   StepScalars* h_scalars_ = nullptr;

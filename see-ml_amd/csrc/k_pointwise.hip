@@ -128,6 +128,107 @@ __global__ __launch_bounds__(kBlock) void ew_binary(const float* __restrict__ x,
   for (size_t i = nv * 4 + gid; i < n; i += tstride) out[i] = f(x[i], y[i]);
 }
 
+// ---- pointwise runs (kernels.h PointwiseRun) ------------------------------
+struct PwProg {
+  int nin, nops;
+  PwOp op[kPwOps];
+  int a[kPwOps], b[kPwOps];
+};
+// The programs compiled, one kernel each: the wirings of the instruction
+// runs the compiler emits (LoRA scaling, SwiGLU, residual-gradient sums).
+constexpr PwProg kPwProgs[] = {
+    // SwiGLU forward: s = silu(g); h = s * u
+    {2, 2, {PwOp::kSilu, PwOp::kMul}, {0, 4}, {0, 1}},
+    // SwiGLU backward: ds = dh * u; du = dh * s; dg = silu'(ds, g)
+    {4, 3, {PwOp::kMul, PwOp::kMul, PwOp::kSiluBwd}, {0, 0, 4}, {1, 2, 3}},
+    // a gradient sum, then its LoRA-scaled copy
+    {2, 2, {PwOp::kAdd, PwOp::kScale}, {0, 4}, {1, 4}},
+    // a gradient sum through an activation's backward, then scaled
+    {3, 3, {PwOp::kAdd, PwOp::kReluBwd, PwOp::kScale}, {0, 4, 5}, {1, 2, 5}},
+    {3, 3, {PwOp::kAdd, PwOp::kGeluBwd, PwOp::kScale}, {0, 4, 5}, {1, 2, 5}},
+    // LoRA branch scaled and added (when no skinny GEMM chain absorbed it)
+    {2, 2, {PwOp::kScale, PwOp::kAdd}, {0, 1}, {0, 4}},
+};
+constexpr int kNumPwProgs = sizeof(kPwProgs) / sizeof(kPwProgs[0]);
+
+template <PwOp OP>
+__device__ __forceinline__ float PwApply(float a, float b, float alpha) {
+  if constexpr (OP == PwOp::kAdd) return AddF()(a, b);
+  else if constexpr (OP == PwOp::kMul) return MulF()(a, b);
+  else if constexpr (OP == PwOp::kScale) return ScaleF{alpha}(a);
+  else if constexpr (OP == PwOp::kRelu) return ReluF()(a);
+  else if constexpr (OP == PwOp::kReluBwd) return ReluBwdF()(a, b);
+  else if constexpr (OP == PwOp::kGelu) return GeluF()(a);
+  else if constexpr (OP == PwOp::kGeluBwd) return GeluBwdF()(a, b);
+  else if constexpr (OP == PwOp::kSilu) return SiluF()(a);
+  else if constexpr (OP == PwOp::kSiluBwd) return SiluBwdF()(a, b);
+  else return a;  // kCopy
+}
+
+// Steps J.. of program P on one set of slot values (plain floats: arrays of
+// the float4 struct type are placed in scratch memory).
+template <int P, int J>
+__device__ __forceinline__ void PwSteps(float (&v)[kPwIn + kPwOps][4], const PointwiseRun& r) {
+  constexpr PwProg prog = kPwProgs[P];
+  if constexpr (J < prog.nops) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[kPwIn + J][e] = PwApply<prog.op[J]>(v[prog.a[J]][e], v[prog.b[J]][e], r.alpha[J]);
+    PwSteps<P, J + 1>(v, r);
+  }
+}
+
+template <int P, bool NT>
+__global__ __launch_bounds__(kBlock) void pw_run_kernel(PointwiseRun r, size_t nv) {
+  constexpr PwProg prog = kPwProgs[P];
+  constexpr int kUnroll = Unroll(NT);
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock * kUnroll;
+  for (size_t base = static_cast<size_t>(blockIdx.x) * kBlock * kUnroll + threadIdx.x; base < nv;
+       base += stride) {
+    float v[kUnroll][kPwIn + kPwOps][4];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+#pragma unroll
+      for (int k = 0; k < prog.nin; ++k) {
+        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < nv) q = ld4(r.in[k] + 4 * i, NT);
+        v[u][k][0] = q.x; v[u][k][1] = q.y; v[u][k][2] = q.z; v[u][k][3] = q.w;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const size_t i = base + static_cast<size_t>(u) * kBlock;
+      if (i >= nv) continue;
+      PwSteps<P, 0>(v[u], r);
+#pragma unroll
+      for (int j = 0; j < prog.nops; ++j)
+        if (r.out[j])
+          st4(r.out[j] + 4 * i,
+              make_float4(v[u][kPwIn + j][0], v[u][kPwIn + j][1], v[u][kPwIn + j][2],
+                          v[u][kPwIn + j][3]),
+              NT);
+    }
+  }
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const size_t tstride = static_cast<size_t>(gridDim.x) * kBlock;
+  for (size_t i = nv * 4 + gid; i < r.n; i += tstride) {
+    float v[kPwIn + kPwOps][4] = {};
+#pragma unroll
+    for (int k = 0; k < prog.nin; ++k) v[k][0] = r.in[k][i];
+    PwSteps<P, 0>(v, r);
+#pragma unroll
+    for (int j = 0; j < prog.nops; ++j)
+      if (r.out[j]) r.out[j][i] = v[kPwIn + j][0];
+  }
+}
+
+template <int P>
+void LaunchPw(const PointwiseRun& r, size_t nv, bool nt, dim3 grid, hipStream_t s) {
+  if (nt) hipLaunchKernelGGL((pw_run_kernel<P, true>), grid, dim3(kBlock), 0, s, r, nv);
+  else hipLaunchKernelGGL((pw_run_kernel<P, false>), grid, dim3(kBlock), 0, s, r, nv);
+}
+
 // Fill writes only: a separate kernel so no read of uninitialised memory.
 __global__ __launch_bounds__(kBlock) void fill_kernel(float* __restrict__ out, size_t n, size_t nv,
                                                       float v) {
@@ -513,6 +614,44 @@ Status Rope(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, fl
 }
 
 }  // namespace
+
+int PwProgramOf(int nin, const PwStep* steps, int nops) {
+  for (int p = 0; p < kNumPwProgs; ++p) {
+    const PwProg& g = kPwProgs[p];
+    if (g.nin != nin || g.nops != nops) continue;
+    bool same = true;
+    for (int j = 0; j < nops; ++j)
+      same = same && g.op[j] == steps[j].op && g.a[j] == steps[j].a && g.b[j] == steps[j].b;
+    if (same) return p;
+  }
+  return -1;
+}
+
+Status LaunchPointwiseRun(const PointwiseRun& r, const Ctx& c) {
+  if (r.program < 0 || r.program >= kNumPwProgs)
+    return Status::Fail(kUnitEngine, "pointwise run: no compiled program");
+  const PwProg& g = kPwProgs[r.program];
+  bool aligned = true;
+  int nout = 0;
+  for (int k = 0; k < g.nin; ++k) aligned = aligned && aligned16(r.in[k]);
+  for (int j = 0; j < g.nops; ++j)
+    if (r.out[j]) aligned = aligned && aligned16(r.out[j]), ++nout;
+  if (r.n == 0 || nout == 0) return Status::Ok();
+  const size_t nv = aligned ? r.n / 4 : 0;
+  const bool nt = StreamPolicy(4 * r.n * static_cast<size_t>(g.nin + nout));
+  const size_t work = nv ? (nv + Unroll(nt) - 1) / Unroll(nt) : r.n;
+  const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
+  switch (r.program) {
+    case 0: LaunchPw<0>(r, nv, nt, grid, c.stream); break;
+    case 1: LaunchPw<1>(r, nv, nt, grid, c.stream); break;
+    case 2: LaunchPw<2>(r, nv, nt, grid, c.stream); break;
+    case 3: LaunchPw<3>(r, nv, nt, grid, c.stream); break;
+    case 4: LaunchPw<4>(r, nv, nt, grid, c.stream); break;
+    default: LaunchPw<5>(r, nv, nt, grid, c.stream); break;
+  }
+  static_assert(kNumPwProgs == 6, "one launch case per program");
+  return LaunchStatus("pointwise run");
+}
 
 Status AddEW(const float* x, const float* y, float* out, size_t n, const Ctx& c) {
   return Binary(x, y, out, n, AddF{}, c, "AddEW");

@@ -125,6 +125,33 @@ GemmDesc GemmNTDesc(const float* A, const float* B, float* C, int64_t M, int64_t
 GemmDesc GemmTNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K);
 
 // ---- pointwise family (k_pointwise.hip) ---------------------------------
+// A run of adjacent pointwise instructions on n elements each, executed as
+// one kernel that evaluates them per element in registers. The engine proves
+// the run: every operand range is identical to or disjoint from every other,
+// so element i of each instruction depends only on element i of the run's
+// inputs and earlier results. Value slots: 0..nin-1 hold the inputs as
+// loaded, slot kPwIn + j step j's result (a unary step has b == a). Each step
+// is the standalone kernel's element expression, so the stored bits are the
+// run's. The kernels are compiled per program (PwProgramOf: the wirings the
+// compiler's lowering produces); out[j] receives step j's result, or nothing
+// when null (dead, or overwritten later in the run).
+enum class PwOp : int { kAdd, kMul, kScale, kRelu, kReluBwd, kGelu, kGeluBwd, kSilu, kSiluBwd, kCopy };
+inline constexpr int kPwIn = 4, kPwOps = 4;
+struct PwStep {
+  PwOp op = PwOp::kCopy;
+  int a = 0, b = 0;
+};
+struct PointwiseRun {
+  size_t n = 0;
+  int program = -1;  // PwProgramOf
+  const float* in[kPwIn] = {};
+  float alpha[kPwOps] = {1.0f, 1.0f, 1.0f, 1.0f};  // Scale steps
+  float* out[kPwOps] = {};
+};
+// Index of the compiled program for these steps over nin inputs, or -1.
+int PwProgramOf(int nin, const PwStep* steps, int nops);
+Status LaunchPointwiseRun(const PointwiseRun& run, const Ctx& c);
+
 Status AddEW(const float* x, const float* y, float* out, size_t n, const Ctx& c);
 Status MulEW(const float* x, const float* y, float* out, size_t n, const Ctx& c);
 Status AddBias(const float* x, const float* b, float* out, size_t rows, size_t cols, const Ctx& c);

@@ -38,8 +38,12 @@ def work(ins: dict, variant: str = "") -> dict:
     a causal SoftmaxRowsBwd reads only the float4s of P and dP that hold
     j <= i, so its bytes are those reads plus the full dS write; a GEMM with
     the following AddEW in its epilogue ("+AddEW") also reads the addend and
-    writes the sum, and that AddEW (class "fused") has no launch of its own."""
+    writes the sum. A fused launch (skinny chain, pointwise run) reports the
+    bytes it moves ("B=<n>") on its first instruction; the instructions
+    executed inside another's launch ("in ...") are class "fused"."""
     name = OP_NAME.get(ins["opcode"], str(ins["opcode"]))
+    if variant.startswith("in "):
+        return dict(op=name, flops=0, bytes=0, cls="fused", shape=())
     o = ins["out"]
     flops, nbytes, cls, shape = 0, 0, "hbm", ()
     if name in GEMMS:
@@ -69,8 +73,6 @@ def work(ins: dict, variant: str = "") -> dict:
             flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
         else:  # DV / DQ / DK: read P-shaped + one activation, write one
             flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
-    elif name == "AddEW" and variant == "in GEMM epilogue":
-        cls, shape = "fused", (o[0],)
     elif name in ("AddEW", "MulEW", "ReluBwd", "GeluBwd", "SiluBwd"):
         nbytes, shape = 12 * o[0], (o[0],)
     elif name in ("Scale", "ReluFwd", "GeluFwd", "SiluFwd", "Copy"):
@@ -121,6 +123,8 @@ def work(ins: dict, variant: str = "") -> dict:
     elif name in ("KLDistillBwd",):
         N, C = _hi(o[0]), _lo(o[0])
         nbytes, shape = 12 * N * C + 4, (N, C)
+    if " B=" in variant:
+        nbytes = int(variant.rsplit(" B=", 1)[1])
     return dict(op=name, flops=flops, bytes=nbytes, cls=cls, shape=shape)
 
 

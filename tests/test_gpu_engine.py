@@ -278,9 +278,9 @@ def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
     e.close()
 
 
-def test_gemm_addew_chains_are_planned(torch_gpu):
-    """On a decoder the GEMM + AddEW fusion and the LoRA chains fire (so the
-    graph == eager bitwise test above compares fused against unfused
+def test_fusions_are_planned(torch_gpu):
+    """On a decoder the GEMM + AddEW fusion and the pointwise runs fire (so
+    the graph == eager bitwise test above compares fused against unfused
     launches): every AddEW reported inside a GEMM epilogue directly follows
     a GEMM reported "+AddEW"; an eager engine plans no fusion."""
     from seeml_amd import PROGRAM_TRAIN
@@ -293,10 +293,17 @@ def test_gemm_addew_chains_are_planned(torch_gpu):
     assert len(fused) >= 4, ch
     assert all(ch[i - 1].endswith("+AddEW") for i in fused)
     assert sum(c.endswith("+AddEW") for c in ch) == len(fused)
+    # pointwise runs (the SwiGLU forward and backward): a head reporting its
+    # bytes, followed by its members
+    heads = [i for i, c in enumerate(ch) if c.startswith("pointwise run of ")]
+    assert len(heads) >= 4, ch
+    for i in heads:
+        k = int(ch[i].split()[3])
+        assert all(c == "in pointwise run" for c in ch[i + 1:i + k])
     e.close()
     e = engine(p, use_graph=False)
     e.train_step(x, y)
-    assert not any("AddEW" in e.gemm_choice(PROGRAM_TRAIN, i) or
-                   e.gemm_choice(PROGRAM_TRAIN, i) == "in GEMM epilogue"
-                   for i in range(len(p.train)))
+    for i in range(len(p.train)):
+        c = e.gemm_choice(PROGRAM_TRAIN, i)
+        assert not (c.startswith("in ") or "+AddEW" in c or "run of" in c or "chain of" in c), c
     e.close()
