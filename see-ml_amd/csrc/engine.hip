@@ -512,6 +512,7 @@ class Engine {
     }
     PlanChains(program);
     PlanPointwiseRuns(program);
+    PlanScaleFolds(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -542,7 +543,9 @@ class Engine {
   // otherwise have read.
   //
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
-  enum class ChainKind { kSkinny, kDense, kPointwise };
+  //
+  // Scale folds: see PlanScaleFolds.
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -550,6 +553,8 @@ class Engine {
     GemmDesc d;          // dense: the GEMM with its fused AddEW
     PointwiseRun pw;     // pointwise
     uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
+    const float* fold_x = nullptr;  // scale fold: the Scale's input and factor
+    float fold_alpha = 1.0f;
   };
 
   void PlanChains(int program) {
@@ -768,6 +773,66 @@ class Engine {
     return true;
   }
 
+  // Scale folds: a Scale s = alpha x whose only readers are the skinny
+  // rowdot / colsum GEMMs right after it, each streaming exactly s. Those
+  // kernels then read x and scale each element as loaded (the same float
+  // product), and the Scale launches nothing. Conditions: s is dead after the
+  // last of them; they write neither x nor s; x is 16-byte aligned like s.
+  void PlanScaleFolds(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      const UpdateInstruction& sc = prog[i];
+      if (taken[i] || static_cast<Op>(sc.opcode) != Op::kScale) continue;
+      const uint64_t x = sc.in[0], sref = sc.in[1];
+      const uint64_t bytes = sc.out[0] * sizeof(float);
+      if (IsRodataRef(sref) || !aligned16(RP(x))) continue;
+      size_t j = i + 1;
+      for (; j < prog.size() && !taken[j] && IsGemmOp(prog[j].opcode); ++j) {
+        if (plans_[program][j].cfg != GemmSkinnyConfig()) break;
+        const GemmDesc d = DescOf(prog[j]);
+        int64_t elems = 0;
+        const void* stream = SkinnyStream(d, &elems);
+        if (stream != WP(sref) || static_cast<uint64_t>(elems) != sc.out[0]) break;
+        if ((d.A == stream ? d.B : d.A) == WP(sref)) break;  // s as the small operand too
+        bool clash = false;
+        for (const auto& w : writes_[program][j])
+          if (Overlaps(Ranges{w}, RefOffset(sref), bytes) ||
+              (!IsRodataRef(x) && Overlaps(Ranges{w}, RefOffset(x), bytes)))
+            clash = true;
+        if (clash) break;
+      }
+      if (j == i + 1 || !DeadAfter(program, j - 1, RefOffset(sref), bytes)) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = j - i;
+      run.kind = ChainKind::kScaleFold;
+      run.fold_x = RP(x);
+      run.fold_alpha = Bits(sc.in[2]);
+      chains_[program].push_back(run);
+      i = j - 1;
+    }
+    std::sort(chains_[program].begin(), chains_[program].end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  // Consumer idx of a scale fold, reading x with the factor applied.
+  Status LaunchFolded(int program, const ChainRun& run, size_t idx, const Ctx& c) {
+    GemmDesc d = DescOf(plan_.program[program][idx]);
+    int64_t elems = 0;
+    const void* stream = SkinnyStream(d, &elems);
+    if (d.A == stream) d.A = run.fold_x;
+    else d.B = run.fold_x;
+    d.scale_stream = true;
+    d.stream_scale = run.fold_alpha;
+    return LaunchGemm(d, plans_[program][idx], c);
+  }
+
   // A dense chain at instruction i (the GEMM), if instruction i + 1 admits one.
   bool PlanDenseChain(int program, size_t i, GemmDesc d) {
     const auto& prog = plan_.program[program];
@@ -822,6 +887,10 @@ class Engine {
     switch (run.kind) {
       case ChainKind::kDense: return LaunchGemm(run.d, plans_[program][run.first], c);
       case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
+      case ChainKind::kScaleFold:
+        for (size_t k = run.first + 1; k < run.first + run.count; ++k)
+          if (Status s = LaunchFolded(program, run, k, c); !s) return s;
+        return Status::Ok();
       default: return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
     }
   }
@@ -1364,11 +1433,22 @@ class Engine {
       size_t fr = 0, fq = 0;
       for (size_t i = 0; i < n;) {
         if (fq < chains.size() && chains[fq].first == i) {
-          if (Status s = LaunchChain(program, chains[fq], c); !s) {
+          const ChainRun& run = chains[fq++];
+          if (run.kind == ChainKind::kScaleFold) {  // timed launch by launch
+            (void)hipEventRecord(ev[i + 1], stream_);  // the Scale launches nothing
+            for (size_t k = i + 1; k < i + run.count && result; ++k) {
+              result = LaunchFolded(program, run, k, c);
+              (void)hipEventRecord(ev[k + 1], stream_);
+            }
+            if (!result) break;
+            i += run.count;
+            continue;
+          }
+          if (Status s = LaunchChain(program, run, c); !s) {
             result = s;
             break;
           }
-          i += chains[fq++].count;
+          i += run.count;
           (void)hipEventRecord(ev[i], stream_);
           continue;
         }
@@ -1393,6 +1473,15 @@ class Engine {
       for (size_t i = 0; i < n;) {
         if (fq < chains.size() && chains[fq].first == i) {
           const ChainRun& run = chains[fq++];
+          if (run.kind == ChainKind::kScaleFold) {
+            for (size_t k = i; k < i + run.count; ++k) {
+              float ms = 0.0f;
+              (void)hipEventElapsedTime(&ms, ev[k], ev[k + 1]);
+              acc[k] += ms;
+            }
+            i += run.count;
+            continue;
+          }
           float ms = 0.0f;
           (void)hipEventElapsedTime(&ms, ev[i], ev[i + run.count]);
           // One launch: its time goes to the chain's first instruction (the
@@ -1453,6 +1542,11 @@ class Engine {
       return causal_rows_[program][idx] ? "causal S=" + std::to_string(causal_rows_[program][idx])
                                         : std::string();
     const ChainRun* run = ChainAt(program, idx);
+    if (run && run->kind == ChainKind::kScaleFold) {
+      if (idx == run->first) return "in the next GEMMs' loads";
+      return std::string(SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])))) +
+             " scaled loads";
+    }
     if (run && idx != run->first) {
       switch (run->kind) {
         case ChainKind::kDense: return "in GEMM epilogue";

@@ -103,6 +103,8 @@ GemmPlan PlanGemm(const GemmDesc& d) { return PlanGemmWith(d, -1, -1); }
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
+  if (d.scale_stream && plan.cfg != kNumCfgs)
+    return Status::Fail(kUnitEngine, "Gemm: a scaled stream needs the skinny kernels");
   if (plan.cfg == kNumCfgs) {
     if (d.out) return Status::Fail(kUnitEngine, "Gemm: the skinny kernels take no fused AddEW");
     if (ctx.ws_bytes < SkinnyWorkspace(d))

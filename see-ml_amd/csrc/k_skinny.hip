@@ -63,7 +63,18 @@ struct SkArgs {
   float* Yout;
   int write_u;
   int y_first;
+  // rowdot / colsum: the streamed operand is scaled as loaded (GemmDesc::
+  // stream_scale), each element fl(stream_scale * x) as the folded Scale
+  // would have stored it.
+  int scale_stream;
+  float stream_scale;
 };
+
+__device__ __forceinline__ float4 ScaleLoaded(const SkArgs& p, float4 v) {
+  if (!p.scale_stream) return v;
+  return make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
+                     p.stream_scale * v.w);
+}
 
 __device__ __forceinline__ float Epilogue(const SkArgs& p, int64_t m, int64_t n, float acc) {
   float val = p.alpha * acc;
@@ -80,28 +91,37 @@ __device__ __forceinline__ float Epilogue(const SkArgs& p, int64_t m, int64_t n,
 // cover 64 contiguous bytes, so every store instruction writes 16 rows x 64 B
 // (32-byte runs measured ~30% slower on this write-bound shape). A wavefront
 // owns kOuterRB row blocks of 16 (their A fragments stay in registers) and
-// walks 16-column steps, each B fragment serving all its row blocks; the next
-// step's B fragment is loaded while the current one computes. A workgroup is
-// 4 wavefronts side by side in n: 16 * kOuterRB rows x 4 * kOuterWN columns.
+// walks 16-column steps, each B fragment serving all its row blocks. A
+// workgroup is 4 wavefronts side by side in n: 16 * kOuterRB rows x
+// 4 * kOuterWN columns.
 
 constexpr int kOuterRB = 4;     // row blocks of 16 per wavefront
 constexpr int kOuterWN = 128;   // columns per wavefront
 constexpr int kOuterRows = 16 * kOuterRB;
 constexpr int kOuterN = 4 * kOuterWN;
 
+constexpr int kOuterSteps = kOuterWN / 16;  // 16-column steps per wavefront
+// Loads issued ahead of their step: every B fragment at kernel entry when K
+// fits one k group (8 float4 per lane), else two steps ahead; the chain's y
+// operand two steps ahead. The step loop is unrolled, so each step's values
+// are distinct registers and the loads stay in flight across steps (with one
+// step ahead, the per-step latency of these small loads set the pace).
+template <int KG>
+constexpr int OuterBAhead() { return KG == 1 ? kOuterSteps : 2; }
+constexpr int kOuterYAhead = 2;
+
 template <int KG>  // k groups of 16: ceil(K / 16)
-__device__ __forceinline__ void OuterLoadB(const SkArgs& p, int64_t n, int q, float4 (&bf)[KG]) {
+__device__ __forceinline__ void OuterLoadB(const SkArgs& p, int64_t n, int q, float (&bf)[KG][4]) {
 #pragma unroll
   for (int g = 0; g < KG; ++g) {
     const int64_t k0 = 16 * g + 4 * q;
     if (p.b_kc) {
-      bf[g] = k0 < p.K ? *reinterpret_cast<const float4*>(p.B + n * p.ldb + k0)
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      const float4 v = k0 < p.K ? *reinterpret_cast<const float4*>(p.B + n * p.ldb + k0)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      bf[g][0] = v.x; bf[g][1] = v.y; bf[g][2] = v.z; bf[g][3] = v.w;
     } else {
-      bf[g].x = k0 + 0 < p.K ? p.B[(k0 + 0) * p.ldb + n] : 0.0f;
-      bf[g].y = k0 + 1 < p.K ? p.B[(k0 + 1) * p.ldb + n] : 0.0f;
-      bf[g].z = k0 + 2 < p.K ? p.B[(k0 + 2) * p.ldb + n] : 0.0f;
-      bf[g].w = k0 + 3 < p.K ? p.B[(k0 + 3) * p.ldb + n] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[g][j] = k0 + j < p.K ? p.B[(k0 + j) * p.ldb + n] : 0.0f;
     }
   }
 }
@@ -110,54 +130,62 @@ __device__ __forceinline__ void OuterLoadB(const SkArgs& p, int64_t n, int q, fl
 // activation: 1 * x == x exactly), so accumulators are stored as they are.
 template <int KG, bool CHAIN, bool PLAIN>
 __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
+  constexpr int kBA = OuterBAhead<KG>();
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int q = lane >> 4, c = lane & 15;
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kOuterRows;
   const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kOuterN + w * kOuterWN;
   if (n0 >= p.N) return;
-  float4 af[kOuterRB][KG];
+  float af[kOuterRB][KG][4];
 #pragma unroll
   for (int rb = 0; rb < kOuterRB; ++rb) {
     const int64_t m = std::min<int64_t>(m0 + 16 * rb + c, p.M - 1);
 #pragma unroll
     for (int g = 0; g < KG; ++g) {
       const int64_t k0 = 16 * g + 4 * q;
-      af[rb][g] = k0 < p.K ? *reinterpret_cast<const float4*>(p.A + m * p.lda + k0)
-                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      const float4 v = k0 < p.K ? *reinterpret_cast<const float4*>(p.A + m * p.lda + k0)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      af[rb][g][0] = v.x; af[rb][g][1] = v.y; af[rb][g][2] = v.z; af[rb][g][3] = v.w;
     }
   }
-  const int64_t nend = std::min<int64_t>(p.N, n0 + kOuterWN);
-  float4 bf[KG], bn[KG];
-  // Chain: the AddEW operand y of the current and next column steps, loaded
-  // a step ahead like B (rows past M and columns past N read row/col 0).
-  float4 yc[kOuterRB], yn[kOuterRB];
-  auto load_y = [&](int64_t nb, float4 (&yv)[kOuterRB]) {
+  // Per step: B fragments and (chain) the AddEW operand y. Columns past N
+  // read column N-1, rows past M read row 0; neither is stored.
+  float bf[kOuterSteps][KG][4];
+  float yv[kOuterSteps][kOuterRB][4];
+  auto load_b = [&](int st) {
+    OuterLoadB<KG>(p, std::min<int64_t>(n0 + 16 * st + c, p.N - 1), q, bf[st]);
+  };
+  auto load_y = [&](int st) {
 #pragma unroll
     for (int rb = 0; rb < kOuterRB; ++rb) {
-      const int64_t mo = m0 + 16 * rb + c, n = nb + 4 * q;
+      const int64_t mo = m0 + 16 * rb + c, n = n0 + 16 * st + 4 * q;
       const bool in = mo < p.M && n < p.N;
-      yv[rb] = *reinterpret_cast<const float4*>(p.Y + (in ? mo * p.N + n : 0));
+      const float4 v = *reinterpret_cast<const float4*>(p.Y + (in ? mo * p.N + n : 0));
+      yv[st][rb][0] = v.x; yv[st][rb][1] = v.y; yv[st][rb][2] = v.z; yv[st][rb][3] = v.w;
     }
   };
-  OuterLoadB<KG>(p, std::min<int64_t>(n0 + c, p.N - 1), q, bf);
-  if constexpr (CHAIN) load_y(n0, yc);
-  for (int64_t nb = n0; nb < nend; nb += 16) {
-    if (nb + 16 < nend) {
-      OuterLoadB<KG>(p, std::min<int64_t>(nb + 16 + c, p.N - 1), q, bn);
-      if constexpr (CHAIN) load_y(nb + 16, yn);
-    }
+#pragma unroll
+  for (int st = 0; st < kBA && st < kOuterSteps; ++st) load_b(st);
+  if constexpr (CHAIN)
+#pragma unroll
+    for (int st = 0; st < kOuterYAhead && st < kOuterSteps; ++st) load_y(st);
+#pragma unroll
+  for (int st = 0; st < kOuterSteps; ++st) {
+    const int64_t nb = n0 + 16 * st;
+    if (nb >= p.N) break;
+    if (st + kBA < kOuterSteps) load_b(st + kBA);
+    if constexpr (CHAIN)
+      if (st + kOuterYAhead < kOuterSteps) load_y(st + kOuterYAhead);
     floatx4 acc[kOuterRB];
 #pragma unroll
     for (int rb = 0; rb < kOuterRB; ++rb) acc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int g = 0; g < KG; ++g)
 #pragma unroll
-      for (int rb = 0; rb < kOuterRB; ++rb) {
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].x, af[rb][g].x, acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].y, af[rb][g].y, acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].z, af[rb][g].z, acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[g].w, af[rb][g].w, acc[rb], 0, 0, 0);
-      }
+      for (int rb = 0; rb < kOuterRB; ++rb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[st][g][j], af[rb][g][j], acc[rb], 0, 0, 0);
     const int64_t n = nb + 4 * q;
     if (n < p.N) {
 #pragma unroll
@@ -178,18 +206,13 @@ __global__ __launch_bounds__(kThreads) void skinny_outer(SkArgs p) {
                             p.chain_alpha * u.w);
             if (p.S) *reinterpret_cast<float4*>(p.S + at) = v;
           }
-          const float4 y = yc[rb];
+          const float* y = yv[st][rb];
           *reinterpret_cast<float4*>(p.Yout + at) =
-              p.y_first ? make_float4(y.x + v.x, y.y + v.y, y.z + v.z, y.w + v.w)
-                        : make_float4(v.x + y.x, v.y + y.y, v.z + y.z, v.w + y.w);
+              p.y_first ? make_float4(y[0] + v.x, y[1] + v.y, y[2] + v.z, y[3] + v.w)
+                        : make_float4(v.x + y[0], v.y + y[1], v.z + y[2], v.w + y[3]);
         }
       }
     }
-#pragma unroll
-    for (int g = 0; g < KG; ++g) bf[g] = bn[g];
-    if constexpr (CHAIN)
-#pragma unroll
-      for (int rb = 0; rb < kOuterRB; ++rb) yc[rb] = yn[rb];
   }
 }
 
@@ -223,7 +246,8 @@ __global__ __launch_bounds__(64 * kRowdotWaves) void skinny_rowdot(SkArgs p) {
   auto load = [&](int64_t g, float4& a, float4 (&b)[NB]) {
     const int64_t k0 = 16 * g + 4 * q;
     const bool in = g < ge && k0 < p.K;  // K % 4 == 0: a float4 is wholly in or out
-    a = in ? *reinterpret_cast<const float4*>(arow + k0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    a = in ? ScaleLoaded(p, *reinterpret_cast<const float4*>(arow + k0))
+           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if (p.b_kc) {
@@ -321,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum(SkArgs p) {
     for (int u = 0; u < U; ++u) {
       const int64_t k = k4 + 4 * u + q;
       const bool kin = k < ke;
-      x[u] = kin && w_ok ? *reinterpret_cast<const float4*>(X + k * ldx + wl)
+      x[u] = kin && w_ok ? ScaleLoaded(p, *reinterpret_cast<const float4*>(X + k * ldx + wl))
                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb) {
@@ -448,6 +472,22 @@ int64_t ColsumGroups(int64_t W, int64_t K) {
 
 }  // namespace
 
+const void* SkinnyStream(const GemmDesc& d, int64_t* elems) {
+  switch (SkinnyKindOf(d)) {
+    case SkinnyKind::kRowDot:
+      *elems = d.M * d.K;
+      return d.A;
+    case SkinnyKind::kColSum: {
+      const bool big_is_m = d.N <= 64 && d.M >= 128;  // as LaunchSkinnyImpl
+      *elems = d.K * (big_is_m ? d.M : d.N);
+      return big_is_m ? d.A : d.B;
+    }
+    default:
+      *elems = 0;
+      return nullptr;
+  }
+}
+
 SkinnyKind SkinnyKindOf(const GemmDesc& d) {
   if (d.batch != 1 || d.heads != 1 || d.causal != Causal::kNone || d.b_int8) return SkinnyKind::kNone;
   if (d.M <= 0 || d.N <= 0 || d.K <= 0) return SkinnyKind::kNone;
@@ -517,6 +557,10 @@ Status LaunchSkinnyImpl(const GemmDesc& d, const SkinnyChain* ch, const Ctx& ctx
     a.write_u = ch->write_u ? 1 : 0;
     a.y_first = ch->y_first ? 1 : 0;
   }
+  a.scale_stream = d.scale_stream ? 1 : 0;
+  a.stream_scale = d.stream_scale;
+  if (d.scale_stream && kind != SkinnyKind::kRowDot && kind != SkinnyKind::kColSum)
+    return Status::Fail(kUnitEngine, "Gemm: only the rowdot and colsum kernels scale their stream");
   a.A = static_cast<const float*>(d.A);
   a.B = static_cast<const float*>(d.B);
   a.C = d.C;

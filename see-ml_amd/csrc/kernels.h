@@ -74,6 +74,11 @@ struct GemmDesc {
   float* out = nullptr;
   bool addend_first = true;
   bool write_c = true;
+  // A Scale folded into the skinny rowdot / colsum kernels: their streamed
+  // operand (rowdot: A; colsum: the [K, W] one) is read as
+  // fl(stream_scale * x), element by element, as the Scale would have stored it.
+  bool scale_stream = false;
+  float stream_scale = 1.0f;
 };
 
 struct GemmPlan {
@@ -96,6 +101,9 @@ enum class SkinnyKind : int { kNone = 0, kOuter = 1, kRowDot = 2, kColSum = 3 };
 SkinnyKind SkinnyKindOf(const GemmDesc& d);
 const char* SkinnyKindName(SkinnyKind k);
 size_t SkinnyWorkspace(const GemmDesc& d);
+// The operand a rowdot / colsum kernel streams (and its element count), or
+// null for other shapes: the one GemmDesc::scale_stream applies to.
+const void* SkinnyStream(const GemmDesc& d, int64_t* elems);
 Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx);
 // The plan index that selects the skinny kernels (one past the tile configs).
 int GemmSkinnyConfig();

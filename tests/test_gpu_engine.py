@@ -279,10 +279,11 @@ def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
 
 
 def test_fusions_are_planned(torch_gpu):
-    """On a decoder the GEMM + AddEW fusion and the pointwise runs fire (so
-    the graph == eager bitwise test above compares fused against unfused
-    launches): every AddEW reported inside a GEMM epilogue directly follows
-    a GEMM reported "+AddEW"; an eager engine plans no fusion."""
+    """On a decoder the GEMM + AddEW fusion, the pointwise runs and the Scale
+    folds fire (so the graph == eager bitwise test above compares fused
+    against unfused launches): every AddEW reported inside a GEMM epilogue
+    directly follows a GEMM reported "+AddEW"; an eager engine plans no
+    fusion."""
     from seeml_amd import PROGRAM_TRAIN
     w, p = compile_workload("c4m")
     x, y = configs.batch(w, 0)
@@ -300,6 +301,10 @@ def test_fusions_are_planned(torch_gpu):
     for i in heads:
         k = int(ch[i].split()[3])
         assert all(c == "in pointwise run" for c in ch[i + 1:i + k])
+    # Scales folded into the skinny GEMMs that stream their output
+    folds = [i for i, c in enumerate(ch) if c == "in the next GEMMs' loads"]
+    assert folds, ch
+    assert all(ch[i + 1].endswith("scaled loads") for i in folds)
     e.close()
     e = engine(p, use_graph=False)
     e.train_step(x, y)
