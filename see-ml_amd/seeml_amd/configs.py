@@ -113,19 +113,23 @@ def make(name: str) -> Workload:
     """Full-size BASELINE configs: c1..c5. Reduced parity variants: c2s,
     c3s, c4s, c5s keep each config's op structure at CPU-checkable size;
     c3m, c4m do too with head widths 64 and 128 (the fused attention
-    kernels' shapes)."""
+    kernels' shapes). c2dx (c2sdx reduced) is C2 with the input's dX, the
+    interior-layer stream BASELINE's C2 text describes."""
     if name == "c1":
         return Workload("c1", mlp_model(), UpdateConfig(
             batch=32, loss="xent", lora=LoraSpec(rank=8, alpha=16.0, seed=7), lr=1e-3,
             weight_decay=0.01, default_steps=1000), classes=256, in_dim=256,
             description="MLP 256->512->256 + bias/ReLU, xent over 256, LoRA r8 a16, batch 32")
-    if name in ("c2", "c2s"):
-        d, b = (4096, 8192) if name == "c2" else (512, 1024)
+    if name in ("c2", "c2s", "c2dx", "c2sdx"):
+        d, b = (4096, 8192) if name in ("c2", "c2dx") else (512, 1024)
         r = 16
+        dx = name.endswith("dx")
         return Workload(name, linear_model(d), UpdateConfig(
-            batch=b, loss="mse", lora=LoraSpec(rank=r, alpha=32.0, seed=7), lr=1e-3),
+            batch=b, loss="mse", lora=LoraSpec(rank=r, alpha=32.0, seed=7), lr=1e-3,
+            input_grad=dx),
             out_dim=d, in_dim=d,
-            description=f"LoRA linear X[{b},{d}] W[{d},{d}] r{r} a32, MSE")
+            description=f"LoRA linear X[{b},{d}] W[{d},{d}] r{r} a32, MSE" +
+                        (", with dX (BASELINE's forward, dX, dA, dB)" if dx else ""))
     dec = {
         # name: vocab, dim, layers, heads, ffn, seq, batch_seqs, rank, targets, lr, norm, mlp
         "c3": (8192, 512, 4, 8, 1376, 256, 16, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),

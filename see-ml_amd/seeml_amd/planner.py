@@ -338,10 +338,12 @@ def graft_lora(block: Block, spec: LoraSpec) -> list:
 
 # -------------------------------------------------------------- autodiff ----
 
-def autodiff(block: Block, loss: Value, trainables: list) -> dict:
+def autodiff(block: Block, loss: Value, trainables: list, extra: tuple = ()) -> dict:
     """TrainableAutodiff::Run (autodiff.cc:362-444) with the VJP rules of
-    autodiff.cc:66-358, emission order included."""
-    needs = set(id(p) for p in trainables)
+    autodiff.cc:66-358, emission order included. `extra` values are treated
+    as needing a gradient too (their gradients are returned with the
+    trainables'); the reference prunes them (autodiff.cc:76-82)."""
+    needs = set(id(p) for p in trainables) | set(id(v) for v in extra)
     for op in block.ops:
         if any(id(o) in needs for o in op.operands):
             for r in op.results:
@@ -456,7 +458,7 @@ def autodiff(block: Block, loss: Value, trainables: list) -> dict:
         else:
             raise ValueError(f"no VJP rule for '{mn}'")
     grads = {}
-    for p in trainables:
+    for p in list(trainables) + list(extra):
         if id(p) not in adj:
             raise ValueError(f"no gradient reached '{p.id}'")
         grads[id(p)] = adj[id(p)]
@@ -727,6 +729,10 @@ class UpdateConfig:
     min_lr_factor: float = 0.0
     token_input: bool = False
     weight_seed: int = 7
+    # Benchmark variant: also compute the input's gradient dX, as for an
+    # interior layer (the compiler prunes it for the input layer,
+    # autodiff.cc:76-82). dX is pinned like the loss, so it keeps a slot.
+    input_grad: bool = False
 
 
 @dataclass
@@ -798,7 +804,9 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     adapters = graft_lora(block, cfg.lora)
     trainables = [v for ad in adapters for v in (ad.A, ad.B)]
     primal_ops = list(block.ops)
-    grads = autodiff(block, loss, trainables)
+    if cfg.input_grad and cfg.token_input:
+        raise ValueError("input_grad needs a float input")
+    grads = autodiff(block, loss, trainables, (inp,) if cfg.input_grad else ())
     synthesize_adamw(block, trainables, grads)
     merge_block, aliases, merge_outputs = build_merge(adapters)
 

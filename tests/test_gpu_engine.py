@@ -49,8 +49,8 @@ def drift_floor(plan, w, steps, orc):
     return a, b
 
 
-@pytest.mark.parametrize("name,steps", [("c1", 5), ("c2s", 3), ("c3s", 3), ("c4s", 3), ("c5s", 3),
-                                        ("c3m", 3), ("c4m", 3)])
+@pytest.mark.parametrize("name,steps", [("c1", 5), ("c2s", 3), ("c2sdx", 3), ("c3s", 3), ("c4s", 3),
+                                        ("c5s", 3), ("c3m", 3), ("c4m", 3)])
 def test_plan_parity_vs_oracle(torch_gpu, orc, name, steps):
     w, p = compile_workload(name)
     e = engine(p)

@@ -69,6 +69,22 @@ def test_c2_gemm_shapes_match_appendix():
                      ("GemmTN", (16, 4096, 8192)), ("GemmTN", (4096, 16, 8192))]
 
 
+def test_c2_dx_stream_adds_the_interior_layer_gradient():
+    """C2 with the input's dX (BASELINE's "forward, dX, dA, dB"): the pruned
+    stream plus GemmNT 8192x4096x16 (dX through the LoRA branch), GemmNT
+    8192x4096x4096 (dX through W) and their AddEW: 17 instructions."""
+    w = configs.make("c2dx")
+    p = planner.compile_update(w.model, w.cfg, materialize=False)
+    base = planner.compile_update(configs.make("c2").model, configs.make("c2").cfg,
+                                  materialize=False)
+    assert len(base.train) == 14 and len(p.train) == 17
+    extra = collections.Counter((planner.OP_NAME[i["opcode"]], tuple(i["out"])) for i in p.train)
+    extra.subtract((planner.OP_NAME[i["opcode"]], tuple(i["out"])) for i in base.train)
+    assert +extra == collections.Counter({("GemmNT", (8192, 4096, 16)): 1,
+                                          ("GemmNT", (8192, 4096, 4096)): 1,
+                                          ("AddEW", (8192 * 4096, 0, 0)): 1})
+
+
 def test_plan_hash_matches_reference(ref):
     for n in (0, 1, 7, 64, (1 << 20) - 1, 1 << 20, (1 << 20) * 3 + 5, 300 * (1 << 20) + 3):
         blob = np.random.default_rng(n).integers(0, 256, n).astype(np.uint8)
@@ -78,7 +94,7 @@ def test_plan_hash_matches_reference(ref):
                 == ref.content_hash64(blob, n)), n
 
 
-@pytest.mark.parametrize("name", ["c1", "c2s", "c3s", "c4s", "c5s", "c3m", "c4m"])
+@pytest.mark.parametrize("name", ["c1", "c2s", "c2sdx", "c3s", "c4s", "c5s", "c3m", "c4m"])
 def test_compiled_plans_verify_and_corruption_is_caught(name):
     w, p = compile_workload(name)
     assert verify_plan(p.blob) == (0, "")
@@ -143,7 +159,8 @@ def test_library_exports_every_declared_symbol():
     assert len(declared) == len(set(re.findall(r"\b(seeml_hip_\w+)\s*\(", text)))
 
 
-@pytest.mark.parametrize("name,steps", [("c1", 3), ("c3s", 2), ("c5s", 2), ("c2s", 2), ("c4m", 1)])
+@pytest.mark.parametrize("name,steps", [("c1", 3), ("c3s", 2), ("c5s", 2), ("c2s", 2), ("c2sdx", 2),
+                                        ("c4m", 1)])
 def test_oracle_dispatch_bitwise_equals_reference_dispatch(orc, ref, name, steps):
     """orc_execute (the C restatement) and ref_execute (the reference's own
     kernels) run the same compiled plan for several steps: every arena byte
