@@ -684,6 +684,35 @@ Status Copy(const float* src, float* dst, size_t n, const Ctx& c) {
   return Unary(src, dst, n, CopyF{}, c, "Copy");
 }
 
+// 32x32 tiles through LDS (padded a column against bank conflicts): reads
+// and writes are both row-contiguous 128-byte runs.
+constexpr int kTr = 32;
+__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ src,
+                                                        float* __restrict__ dst, int64_t rows,
+                                                        int64_t cols) {
+  __shared__ float tile[kTr][kTr + 1];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTr, c0 = static_cast<int64_t>(blockIdx.x) * kTr;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+  for (int k = ty; k < kTr; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) tile[k][tx] = src[r * cols + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < kTr; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (r < rows && c < cols) dst[c * rows + r] = tile[tx][k];
+  }
+}
+
+Status Transpose(const float* src, float* dst, int64_t rows, int64_t cols, const Ctx& c) {
+  if (rows <= 0 || cols <= 0) return Status::Ok();
+  const int64_t gx = (cols + kTr - 1) / kTr, gy = (rows + kTr - 1) / kTr;
+  if (gx > 0x7FFFFFFF || gy > 65535) return Status::Fail(kUnitEngine, "Transpose: grid exceeds launch limits");
+  hipLaunchKernelGGL(transpose_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
+                     dim3(256), 0, c.stream, src, dst, rows, cols);
+  return LaunchStatus("Transpose");
+}
+
 Status Fill(float* dst, float value, size_t n, const Ctx& c) {
   if (n == 0) return Status::Ok();
   const size_t nv = aligned16(dst) ? n / 4 : 0;

@@ -172,6 +172,9 @@ Status SiluFwd(const float* x, float* out, size_t n, const Ctx& c);
 Status SiluBwd(const float* dy, const float* x, float* dx, size_t n, const Ctx& c);
 Status Fill(float* dst, float value, size_t n, const Ctx& c);
 Status Copy(const float* src, float* dst, size_t n, const Ctx& c);
+// dst[c * rows + r] = src[r * cols + c]: a [rows, cols] matrix transposed
+// (the engine's k-contiguous copies of frozen GEMM weights).
+Status Transpose(const float* src, float* dst, int64_t rows, int64_t cols, const Ctx& c);
 Status EmbedFwd(const int32_t* tokens, const float* table, float* out, size_t rows, size_t dim,
                 size_t vocab, const Ctx& c);
 Status ReduceRows(const float* dy, float* db, size_t rows, size_t cols, const Ctx& c);

@@ -105,6 +105,24 @@ def test_gemm_every_tile_config_and_split(env, orc, layout):
             assert rel_err(env.H(out), want) <= TOL_STEP, (cfg, splits)
 
 
+@pytest.mark.parametrize("M,N,K", [(200, 136, 520), (256, 192, 128), (130, 68, 96)])
+def test_gemm_nn_equals_nt_on_the_transposed_operand_bitwise(env, M, N, K):
+    """The engine runs a GemmNN on a frozen weight as GemmNT on a transposed
+    copy: every tile config and split gives the same bits both ways (the
+    per-output k order does not depend on the operand layout)."""
+    A = rnd(M * K, 21)
+    B = rnd(K * N, 22)
+    Bt = np.ascontiguousarray(B.reshape(K, N).T).ravel()
+    ncfg = env.L.seeml_hip_gemm_config_count()
+    for cfg in range(ncfg):
+        for splits in (1, 3):
+            nn = env.T(np.full(M * N, np.nan, f32))
+            nt = env.T(np.full(M * N, np.nan, f32))
+            env.call("seeml_hip_gemm_forced", 0, env.T(A), env.T(B), nn, M, N, K, cfg, splits)
+            env.call("seeml_hip_gemm_forced", 1, env.T(A), env.T(Bt), nt, M, N, K, cfg, splits)
+            assert same_bits(env.H(nn), env.H(nt)), (cfg, splits)
+
+
 # LoRA-shaped GEMMs take the skinny kernels (outer: K <= 64; rowdot: N <= 64
 # with A k-contiguous; colsum: TN with min(M, N) <= 64), chosen by the
 # planner's heuristic; the same shapes forced onto a generic tile config give
