@@ -158,6 +158,7 @@ class Engine {
       return s;
     if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
     if (Status s = MakeWeightCopies(); !s) return s;
+    if (Status s = MakeRopeTables(); !s) return s;
     for (int p = 0; p < 3; ++p) PlanCausalRows(p);
     PlanLiveness();
     for (int p = 0; p < 3; ++p) plans_[p].assign(plan_.program[p].size(), GemmPlan{});
@@ -254,6 +255,50 @@ class Engine {
         return s;
     }
     return Status::Ok();
+  }
+
+  // RoPE angle tables, one per distinct (S, d, base) of the plan's RoPE
+  // instructions with d % 4 == 0 (kernels.h RopeTable: the same bits).
+  struct RopeTab {
+    uint64_t S = 0, d = 0, base_bits = 0;
+    float* t = nullptr;
+  };
+
+  Status MakeRopeTables() {
+    ropetabs_.clear();
+    size_t total = 0;
+    for (int p = 0; p < 3; ++p)
+      for (const UpdateInstruction& ins : plan_.program[p]) {
+        const auto op = static_cast<Op>(ins.opcode);
+        if (op != Op::kRopeFwd && op != Op::kRopeBwd) continue;
+        const uint64_t S = Lo(ins.out[0]), d = Lo(ins.out[1]);
+        if (S == 0 || d == 0 || d % 4 != 0 || S * d > 0xFFFFFFFFu) continue;
+        bool seen = false;
+        for (const RopeTab& r : ropetabs_) seen = seen || (r.S == S && r.d == d && r.base_bits == ins.out[2]);
+        if (seen) continue;
+        RopeTab r;
+        r.S = S;
+        r.d = d;
+        r.base_bits = ins.out[2];
+        r.t = reinterpret_cast<float*>(total);  // offset for now
+        total += Round64(RopeTableFloats(S, d) * sizeof(float));
+        ropetabs_.push_back(r);
+      }
+    if (ropetabs_.empty()) return Status::Ok();
+    if (Status s = HipOk(hipMalloc(&ropetab_buf_, total), "RoPE tables allocation failed"); !s)
+      return s;
+    const Ctx c = MakeCtx();
+    for (RopeTab& r : ropetabs_) {
+      r.t = reinterpret_cast<float*>(ropetab_buf_ + reinterpret_cast<uintptr_t>(r.t));
+      if (Status s = RopeTable(r.t, r.S, r.d, Bits(r.base_bits), c); !s) return s;
+    }
+    return Status::Ok();
+  }
+
+  const float* RopeTableOf(uint64_t S, uint64_t d, uint64_t base_bits) const {
+    for (const RopeTab& r : ropetabs_)
+      if (r.S == S && r.d == d && r.base_bits == base_bits) return r.t;
+    return nullptr;
   }
 
   const float* WeightCopyOf(uint64_t ref, int64_t K, int64_t N) const {
@@ -441,9 +486,17 @@ class Engine {
         return RmsNormBwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), RP(ins.out[0]),
                           WP(ins.in[3]), Hi(d1), Lo(d1), c);
       case Op::kRopeFwd:
-        return RopeFwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), Bits(d2), c);
-      case Op::kRopeBwd:
-        return RopeBwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), Bits(d2), c);
+      case Op::kRopeBwd: {
+        const int dir = static_cast<Op>(ins.opcode) == Op::kRopeFwd ? 1 : -1;
+        if (const float* t = RopeTableOf(Lo(d0), Lo(d1), d2); t && aligned16(RP(ins.in[0])) &&
+            aligned16(WP(ins.in[1])))
+          return RopeWithTable(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), t,
+                               dir, c);
+        return dir > 0 ? RopeFwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1),
+                                 Bits(d2), c)
+                       : RopeBwd(RP(ins.in[0]), WP(ins.in[1]), Hi(d0), Lo(d0), Hi(d1), Lo(d1),
+                                 Bits(d2), c);
+      }
       case Op::kAttnFwd:
         return AttnFwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]),
                        WP(ins.out[0]), Hi(d1), Lo(d1), Hi(d2), Lo(d2), c);
@@ -1644,6 +1697,9 @@ class Engine {
     if (wcopy_buf_) (void)hipFree(wcopy_buf_);
     wcopy_buf_ = nullptr;
     wcopies_.clear();
+    if (ropetab_buf_) (void)hipFree(ropetab_buf_);
+    ropetab_buf_ = nullptr;
+    ropetabs_.clear();
     if (ws_) (void)hipFree(ws_);
     if (d_scalars_) (void)hipFree(d_scalars_);
     for (int p = 0; p < 3; ++p) {
@@ -1675,6 +1731,8 @@ class Engine {
   uint8_t* rodata_ = nullptr;
   uint8_t* wcopy_buf_ = nullptr;  // transposed frozen weights (MakeWeightCopies)
   std::vector<WeightCopy> wcopies_;
+  uint8_t* ropetab_buf_ = nullptr;  // RoPE angle tables (MakeRopeTables)
+  std::vector<RopeTab> ropetabs_;
   size_t rodata_bytes_ = 0;
   void* ws_ = nullptr;
   size_t ws_bytes_ = 0;

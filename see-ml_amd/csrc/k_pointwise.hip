@@ -559,6 +559,65 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(const float* __restri
   }
 }
 
+// The angle table: one thread per (position, pair), the same expressions as
+// rope_rows_kernel's LDS table.
+__global__ __launch_bounds__(kBlock) void rope_angle_table_kernel(float* __restrict__ table,
+                                                                  uint32_t S, uint32_t half_d,
+                                                                  float step) {
+  const uint32_t e = blockIdx.x * kBlock + threadIdx.x;
+  if (e >= S * half_d) return;
+  const uint32_t c = e % half_d, sp = e / half_d;
+  float f = 1.0f;
+  for (uint32_t i = 0; i < c; ++i) f *= step;
+  const float theta = static_cast<float>(sp) * f;
+  table[2 * e] = cosf(theta);
+  table[2 * e + 1] = sinf(theta);
+}
+
+// RoPE through the angle table: each float4 of x is two pairs of one
+// position; its cos/sin are one float4 of the (cache-resident) table.
+template <int DIR, bool NT>
+__global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y,
+                                                            const float* __restrict__ table,
+                                                            uint32_t nv_row, uint32_t total4,
+                                                            uint32_t S, uint32_t d) {
+  constexpr int kU = Unroll(NT);
+  const uint32_t stride = gridDim.x * kBlock * kU;
+  for (uint32_t base = blockIdx.x * kBlock * kU + threadIdx.x; base < total4; base += stride) {
+    float4 v[kU], t[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t i = base + u * kBlock;
+      if (i >= total4) continue;
+      const uint32_t row = i / nv_row, col4 = i - row * nv_row;
+      const uint32_t c2 = ((4 * col4) % d) / 2;  // even: the float4 below is aligned
+      v[u] = ld4(x + 4 * static_cast<size_t>(i), NT);
+      t[u] = *reinterpret_cast<const float4*>(table + 2 * ((row % S) * (d / 2) + c2));
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t i = base + u * kBlock;
+      if (i >= total4) continue;
+      const float c0 = t[u].x, s0 = t[u].y, c1 = t[u].z, s1 = t[u].w;
+      const float4 w = v[u];
+      float4 o;
+      if constexpr (DIR > 0) {
+        o.x = w.x * c0 - w.y * s0;
+        o.y = w.x * s0 + w.y * c0;
+        o.z = w.z * c1 - w.w * s1;
+        o.w = w.z * s1 + w.w * c1;
+      } else {
+        o.x = w.x * c0 + w.y * s0;
+        o.y = -w.x * s0 + w.y * c0;
+        o.z = w.z * c1 + w.w * s1;
+        o.w = -w.z * s1 + w.w * c1;
+      }
+      st4(y + 4 * static_cast<size_t>(i), o, NT);
+    }
+  }
+}
+
 // General form: one thread per pair.
 __global__ __launch_bounds__(kBlock) void rope_kernel(const float* __restrict__ x,
                                                       float* __restrict__ y, size_t pairs,
@@ -814,6 +873,42 @@ Status AdamWStep(float* p, const float* g, float* m, float* v, size_t n, const C
   hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(nv ? nv : n, kBlock, kGridCap)), dim3(kBlock),
                      0, c.stream, p, g, m, v, n, nv, c.scalars);
   return LaunchStatus("AdamWStep");
+}
+
+size_t RopeTableFloats(size_t S, size_t d) { return S * d; }
+
+Status RopeTable(float* table, size_t S, size_t d, float base, const Ctx& c) {
+  if (d % 2 != 0 || S * (d / 2) > 0xFFFFFFFFu) return Status::Fail(kUnitEngine, "RopeTable: bad shape");
+  if (S == 0 || d == 0) return Status::Ok();
+  const float step = ::powf(base, -2.0f / static_cast<float>(d));  // as Rope
+  const size_t n = S * (d / 2);
+  hipLaunchKernelGGL(rope_angle_table_kernel, dim3(static_cast<unsigned>((n + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, c.stream, table, static_cast<uint32_t>(S),
+                     static_cast<uint32_t>(d / 2), step);
+  return LaunchStatus("RopeTable");
+}
+
+Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
+                     const float* table, int dir, const Ctx& c) {
+  const size_t rows = B * S, width = H * d;
+  if (rows == 0 || width == 0) return Status::Ok();
+  if (d % 4 != 0 || S == 0 || !aligned16(x) || !aligned16(y) || !aligned16(table) ||
+      rows * width / 4 > 0xFFFFFFFFu || S * d > 0xFFFFFFFFu)
+    return Status::Fail(kUnitEngine, "Rope: the table form needs d % 4 == 0 and aligned operands");
+  const uint32_t total4 = static_cast<uint32_t>(rows * width / 4);
+  const bool nt = StreamPolicy(8 * rows * width);
+  const size_t work = (total4 + Unroll(nt) - 1) / Unroll(nt);
+  const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
+  const uint32_t nv_row = static_cast<uint32_t>(width / 4), S32 = static_cast<uint32_t>(S),
+                 d32 = static_cast<uint32_t>(d);
+  if (dir > 0) {
+    if (nt) hipLaunchKernelGGL((rope_table_kernel<1, true>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+    else hipLaunchKernelGGL((rope_table_kernel<1, false>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+  } else {
+    if (nt) hipLaunchKernelGGL((rope_table_kernel<-1, true>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+    else hipLaunchKernelGGL((rope_table_kernel<-1, false>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+  }
+  return LaunchStatus(dir > 0 ? "RopeFwd" : "RopeBwd");
 }
 
 Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d, float base,

@@ -214,6 +214,16 @@ Status RopeFwd(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
                const Ctx& c);
 Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t d, float base,
                const Ctx& c);
+// RoPE's angles for (S, d, base), precomputed: table[2 (s d/2 + c) + {0, 1}] =
+// (cos t, sin t), t = s * base^(-2c/d) by the reference's recurrence: the
+// values RopeFwd/Bwd compute on the fly, so results through the table are
+// the same bits. RopeTableFloats(S, d) = S * d.
+size_t RopeTableFloats(size_t S, size_t d);
+Status RopeTable(float* table, size_t S, size_t d, float base, const Ctx& c);
+// RopeFwd (dir +1) / RopeBwd (dir -1) reading a RopeTable: a pure stream
+// (d % 4 == 0; x, y and the table 16-byte aligned).
+Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
+                     const float* table, int dir, const Ctx& c);
 
 // ---- row / reduction family (k_rows.hip) ----------------------------------
 size_t MseFwdWorkspace(size_t n);

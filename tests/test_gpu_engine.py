@@ -312,3 +312,37 @@ def test_fusions_are_planned(torch_gpu):
         c = e.gemm_choice(PROGRAM_TRAIN, i)
         assert not (c.startswith("in ") or "+AddEW" in c or "run of" in c or "chain of" in c), c
     e.close()
+
+
+def test_rope_through_the_angle_table_is_the_standalone_kernel(torch_gpu):
+    """The engine runs RoPE from an angle table built at open; replaying the
+    plan up to the first RopeFwd and the first RopeBwd, each output equals
+    the standalone kernel's (which evaluates the angles itself) bit for bit."""
+    from seeml_amd import PROGRAM_TRAIN, _lib, planner
+    torch = torch_gpu
+    w, p = compile_workload("c4m")
+    e = engine(p, use_graph=False)
+    x, y = configs.batch(w, 0)
+    e.stage(x, y)
+    dev = torch.device("cuda:0")
+    done = -1
+    for opname, fn in (("RopeFwd", "seeml_hip_rope_fwd"), ("RopeBwd", "seeml_hip_rope_bwd")):
+        idx = next(i for i, ins in enumerate(p.train) if ins["opcode"] == planner.OP[opname])
+        for j in range(done + 1, idx + 1):
+            e.time_instruction(PROGRAM_TRAIN, j, reps=1)
+        done = idx
+        ins = p.train[idx]
+        B, S = ins["out"][0] >> 32, ins["out"][0] & 0xFFFFFFFF
+        H, d = ins["out"][1] >> 32, ins["out"][1] & 0xFFFFFFFF
+        base = np.array([ins["out"][2]], np.uint32).view(np.float32)[0]
+        n = B * S * H * d
+        src = e.read(ins["inp"][0], n)
+        got = e.read(ins["inp"][1], n)
+        t = torch.from_numpy(src.copy()).to(dev)
+        out = torch.full((n,), float("nan"), device=dev)
+        rc = getattr(_lib.lib(), fn)(t.data_ptr(), out.data_ptr(), B, S, H, d, float(base),
+                                     torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert rc == 0
+        assert np.array_equal(got.view(np.uint32), out.cpu().numpy().view(np.uint32)), opname
+    e.close()
