@@ -132,8 +132,11 @@ int seeml_hip_autotune(seeml_hip_engine* e, int budget);
  * GEMMs "cfg-name splits=S" (or "skinny/<kind>"), with " +AddEW" when the
  * AddEW after it runs in its epilogue (that AddEW then reads "in GEMM
  * epilogue"); SoftmaxRowsBwd "causal S=n" when its probabilities are proven
- * AttnFwd/AttnDP outputs (only their causal half is read), else ""; other
- * opcodes "". Fusions are planned when the program's graph is built. */
+ * AttnFwd/AttnDP outputs (only their causal half is read), else ""; AttnFwd,
+ * AttnDP and a causal SoftmaxRowsBwd add "no zero tail" when no reader looks
+ * past the diagonal tiles (those zeros are not stored), AttnFwd "P unused"
+ * when P has no reader; other opcodes "". Fusions are planned when the
+ * program's graph is built. */
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap);
 

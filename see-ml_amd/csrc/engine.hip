@@ -161,6 +161,7 @@ class Engine {
     if (Status s = MakeRopeTables(); !s) return s;
     for (int p = 0; p < 3; ++p) PlanCausalRows(p);
     PlanLiveness();
+    for (int p = 0; p < 3; ++p) PlanCausalTails(p);
     for (int p = 0; p < 3; ++p) plans_[p].assign(plan_.program[p].size(), GemmPlan{});
     for (int p = 0; p < 3; ++p)
       for (size_t i = 0; i < plan_.program[p].size(); ++i)
@@ -372,6 +373,85 @@ class Engine {
     return true;
   }
 
+  // ---- causal tails ---------------------------------------------------------
+  // P (AttnFwd), dP (AttnDP) and dS (a causal SoftmaxRowsBwd) hold exact
+  // zeros above each row's diagonal. Past each 32-row block's diagonal tile
+  // those zeros are read only by whole-row readers: the fused DV/DQ/DK
+  // kernels and the causal SoftmaxRowsBwd never look there (they stop at the
+  // diagonal tile and mask j > i themselves). So a producer skips that tail
+  // when every reader of its output, up to the output's full overwrite, is
+  // one of those on exactly that tensor and geometry; an AttnFwd whose P has
+  // no reader at all (the eval program) stores no P. A transient that nobody
+  // reads is never observed (see liveness): only the bytes change, not a
+  // result.
+  void PlanCausalTails(int program) {
+    const auto& prog = plan_.program[program];
+    tails_[program].assign(prog.size(), static_cast<uint8_t>(kAttnStoreP | kAttnStoreTail));
+    for (size_t k = 0; k < prog.size(); ++k) {
+      const UpdateInstruction& ins = prog[k];
+      const auto op = static_cast<Op>(ins.opcode);
+      uint64_t ref = kNullRef, bs = 0, hd = 0;  // the produced tensor and its (B|S, H|d)
+      if (op == Op::kAttnFwd) {
+        bs = ins.out[1], hd = ins.out[2], ref = ins.out[0];
+        if (!AttnFusedPath({RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]), WP(ref)},
+                           Hi(bs), Lo(bs), Hi(hd), Lo(hd)))
+          continue;
+      } else if (op == Op::kAttnDP) {
+        bs = ins.out[0], hd = ins.out[1], ref = ins.in[2];
+        if (!AttnFusedPath({RP(ins.in[0]), RP(ins.in[1]), WP(ref)}, Hi(bs), Lo(bs), Hi(hd), Lo(hd)))
+          continue;
+      } else if (op == Op::kSoftmaxRowsBwd && causal_rows_[program][k]) {
+        ref = ins.in[2];
+        if (!SoftmaxRowsBwdCausalForm(RP(ins.in[0]), RP(ins.in[1]), WP(ref), Lo(ins.out[0])))
+          continue;
+      } else {
+        continue;
+      }
+      if (IsRodataRef(ref)) continue;
+      const uint64_t rows = op == Op::kSoftmaxRowsBwd ? Hi(ins.out[0]) : 0;
+      const uint64_t S = op == Op::kSoftmaxRowsBwd ? Lo(ins.out[0]) : Lo(bs);
+      const uint64_t bytes = (op == Op::kSoftmaxRowsBwd ? rows : Hi(bs) * Hi(hd) * S) * S * 4;
+      // Whether reader j takes the tensor through a tail-blind path.
+      auto blind = [&](size_t j) {
+        const UpdateInstruction& r = prog[j];
+        const auto rop = static_cast<Op>(r.opcode);
+        if (rop == Op::kSoftmaxRowsBwd)
+          return causal_rows_[program][j] != 0 && (r.in[0] == ref || r.in[1] == ref) &&
+                 r.in[2] != ref &&
+                 SoftmaxRowsBwdCausalForm(RP(r.in[0]), RP(r.in[1]), WP(r.in[2]), Lo(r.out[0]));
+        if (rop != Op::kAttnDV && rop != Op::kAttnDQ && rop != Op::kAttnDK) return false;
+        if (r.in[0] != ref || r.in[1] == ref || r.in[2] == ref) return false;
+        const uint64_t rB = Hi(r.out[0]), rS = Lo(r.out[0]), rH = Hi(r.out[1]), rd = Lo(r.out[1]);
+        const bool same = op == Op::kSoftmaxRowsBwd ? (rS == S && rB * rH * rS == rows)
+                                                    : (r.out[0] == bs && r.out[1] == hd);
+        return same && AttnFusedPath({RP(r.in[0]), RP(r.in[1]), WP(r.in[2])}, rB, rS, rH, rd);
+      };
+      bool tail = Overlaps(observed_, RefOffset(ref), bytes), read = tail;
+      Ranges live{{RefOffset(ref), bytes}};
+      for (size_t j = k + 1; j < prog.size() && !live.empty() && !tail; ++j) {
+        bool touches = false;
+        for (const auto& l : live) touches = touches || Overlaps(depends_[program][j], l.first, l.second);
+        if (touches) {
+          read = true;
+          if (!blind(j)) tail = true;
+        }
+        for (const auto& w : writes_[program][j]) {
+          Ranges rest;
+          for (const auto& l : live) {
+            const uint64_t lo = l.first, hi = l.first + l.second, wlo = w.first, whi = w.first + w.second;
+            if (whi <= lo || hi <= wlo) { rest.push_back(l); continue; }
+            if (lo < wlo) rest.emplace_back(lo, wlo - lo);
+            if (whi < hi) rest.emplace_back(whi, hi - whi);
+          }
+          live.swap(rest);
+        }
+      }
+      uint8_t f = static_cast<uint8_t>(kAttnStoreP | (tail ? kAttnStoreTail : 0));
+      if (op == Op::kAttnFwd && !read) f = 0;  // P is read by nothing
+      tails_[program][k] = f;
+    }
+  }
+
   // ---- instruction decode ------------------------------------------------
   const float* RP(uint64_t ref) const {
     return reinterpret_cast<const float*>((IsRodataRef(ref) ? rodata_ : arena_) + RefOffset(ref));
@@ -499,14 +579,16 @@ class Engine {
       }
       case Op::kAttnFwd:
         return AttnFwd(RP(ins.in[0]), RP(ins.in[1]), RP(ins.in[2]), WP(ins.in[3]),
-                       WP(ins.out[0]), Hi(d1), Lo(d1), Hi(d2), Lo(d2), c);
+                       WP(ins.out[0]), Hi(d1), Lo(d1), Hi(d2), Lo(d2), c, tails_[program][idx]);
       case Op::kAttnDP:
-        return AttnDP(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
+        return AttnDP(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c,
+                      (tails_[program][idx] & kAttnStoreTail) != 0);
       case Op::kAttnDV:
         return AttnDV(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
       case Op::kSoftmaxRowsBwd:
         return SoftmaxRowsBwd(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), c,
-                              causal_rows_[program][idx]);
+                              causal_rows_[program][idx],
+                              (tails_[program][idx] & kAttnStoreTail) != 0);
       case Op::kAttnDQ:
         return AttnDQ(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), Hi(d0), Lo(d0), Hi(d1), Lo(d1), c);
       case Op::kAttnDK:
@@ -1660,9 +1742,16 @@ class Engine {
   }
 
   std::string GemmChoice(int program, size_t idx) const {
-    if (static_cast<Op>(plan_.program[program][idx].opcode) == Op::kSoftmaxRowsBwd)
-      return causal_rows_[program][idx] ? "causal S=" + std::to_string(causal_rows_[program][idx])
-                                        : std::string();
+    const auto op = static_cast<Op>(plan_.program[program][idx].opcode);
+    const uint8_t tf = tails_[program][idx];
+    const char* no_tail = (tf & kAttnStoreTail) ? "" : "no zero tail";
+    if (op == Op::kSoftmaxRowsBwd)
+      return causal_rows_[program][idx]
+                 ? "causal S=" + std::to_string(causal_rows_[program][idx]) +
+                       (*no_tail ? std::string(", ") + no_tail : std::string())
+                 : std::string();
+    if (op == Op::kAttnFwd) return tf == 0 ? "P unused" : no_tail;
+    if (op == Op::kAttnDP) return no_tail;
     const ChainRun* run = ChainAt(program, idx);
     if (run && run->kind == ChainKind::kScaleFold) {
       if (idx == run->first) return "in the next GEMMs' loads";
@@ -1749,6 +1838,7 @@ class Engine {
   std::vector<Ranges> writes_[3];   // per instruction: WriteRangesOf
   Ranges observed_;
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
+  std::vector<uint8_t> tails_[3];         // per instruction: kAttnStore* (PlanCausalTails)
   StepScalars* h_scalars_ = nullptr;
   float* h_loss_ = nullptr;
   struct Segment {

@@ -223,7 +223,8 @@ __device__ __forceinline__ void StoreRow(float* __restrict__ out, const floatx16
 template <int D>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d) {
+    float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d,
+    int pstore) {
   constexpr int TS = KvTile<D>::kStride;
   constexpr int NB = D / 32;
   __shared__ __align__(16) float kt[2][kAttnK * TS];
@@ -301,6 +302,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   vs.store(vt[0]);
   __syncthreads();
   const bool row_ok = i < S;
+  const bool store_p = (pstore & kAttnStoreP) != 0;
   float* prow = ph + static_cast<int64_t>(ic) * S;
   for (int t = 0; t < tiles_wg; ++t) {
     if (t + 1 < tiles_wg) {
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int j = t * kAttnK + 8 * q4 + 4 * h;
-        if (row_ok && j < S)
+        if (store_p && row_ok && j < S)
           *reinterpret_cast<float4*>(prow + j) =
               make_float4(sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]);
       }
@@ -330,6 +332,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
 
   if (row_ok) StoreRow<D>(oh + static_cast<int64_t>(i) * ld, oacc, h);
   // Causal tail: columns past this wavefront's diagonal tile are exact 0.
+  if (!(pstore & kAttnStoreTail)) return;
   const int zc = tiles_w * kAttnK;
   for (int rr = 0; rr < 32; ++rr) {
     const int row = qw + rr;
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
 template <int D>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_dp_fused(
     const float* __restrict__ dout, const float* __restrict__ v, float* __restrict__ dp, int B,
-    int S, int H) {
+    int S, int H, int tail) {
   __shared__ __align__(16) float vt[2][kAttnK * KvTile<D>::kStride];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h = lane >> 5, r = lane & 31;
@@ -411,6 +414,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dp_fused(
     if (t + 1 < tiles_wg) vs.store(vt[(t + 1) & 1]);
     __syncthreads();
   }
+  if (!tail) return;
   const int zc = tiles_w * kAttnK;
   for (int rr = 0; rr < 32; ++rr) {
     const int row = qw + rr;
@@ -589,8 +593,13 @@ unsigned FusedBlocks(size_t B, size_t S, size_t H) {
 
 size_t AttnWorkspace(size_t, size_t, size_t, size_t) { return 0; }
 
+bool AttnFusedPath(std::initializer_list<const float*> ptrs, size_t B, size_t S, size_t H,
+                   size_t d) {
+  return FusedEligible(ptrs, B, S, H, d);
+}
+
 Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* probs, size_t B,
-               size_t S, size_t H, size_t d, const Ctx& c) {
+               size_t S, size_t H, size_t d, const Ctx& c, int pstore) {
   if (B * S * H * d == 0) return Status::Ok();
   if (FusedEligible({q, k, v, o, probs}, B, S, H, d)) {
     const unsigned blocks = FusedBlocks(B, S, H);
@@ -598,11 +607,11 @@ Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* 
     if (d == 128)
       hipLaunchKernelGGL(attn_fwd_fused<128>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
                          v, o, probs, static_cast<int>(B), static_cast<int>(S),
-                         static_cast<int>(H), inv);
+                         static_cast<int>(H), inv, pstore);
     else
       hipLaunchKernelGGL(attn_fwd_fused<64>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
                          v, o, probs, static_cast<int>(B), static_cast<int>(S),
-                         static_cast<int>(H), inv);
+                         static_cast<int>(H), inv, pstore);
     return LaunchStatus("AttnFwd");
   }
   const Geo g = MakeGeo(B, S, H, d);
@@ -634,16 +643,16 @@ Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* 
 }
 
 Status AttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S, size_t H,
-              size_t d, const Ctx& c) {
+              size_t d, const Ctx& c, bool tail) {
   if (B * S * H * d == 0) return Status::Ok();
   if (FusedEligible({dout, v, dp}, B, S, H, d)) {
     const int iB = static_cast<int>(B), iS = static_cast<int>(S), iH = static_cast<int>(H);
     if (d == 128)
       hipLaunchKernelGGL(attn_dp_fused<128>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
-                         c.stream, dout, v, dp, iB, iS, iH);
+                         c.stream, dout, v, dp, iB, iS, iH, tail ? 1 : 0);
     else
       hipLaunchKernelGGL(attn_dp_fused<64>, dim3(FusedBlocks(B, S, H)), dim3(kAttnThreads), 0,
-                         c.stream, dout, v, dp, iB, iS, iH);
+                         c.stream, dout, v, dp, iB, iS, iH, tail ? 1 : 0);
     return LaunchStatus("AttnDP");
   }
   const Geo g = MakeGeo(B, S, H, d);

@@ -608,7 +608,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __re
                                                                const float* __restrict__ dp,
                                                                float* __restrict__ ds,
                                                                size_t rows, int cols, int nt,
-                                                               int causal_s) {
+                                                               int causal_s, int tail) {
   __shared__ double dscratch[kBlock / kWave];
   size_t r;
   int t;
@@ -633,8 +633,10 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_bwd_reg(const float* __re
     dv[i] = make_float4(pv[i].x * (dv[i].x - sum), pv[i].y * (dv[i].y - sum),
                         pv[i].z * (dv[i].z - sum), pv[i].w * (dv[i].w - sum));
   // Unread float4s were zero-filled, so their entries already equal
-  // (+0) * (0 - sum), the value the full read would give.
-  store_row<TPR, V>(ds + r * cols, nv, t, dv, nt);
+  // (+0) * (0 - sum), the value the full read would give. Without `tail`
+  // only the float4s read are stored (the caller's readers never look
+  // past them).
+  store_row<TPR, V>(ds + r * cols, tail ? nv : nread, t, dv, nt);
 }
 
 // Causal row softmax in place (attention.cc:106-125): row u = (b, h, i) holds
@@ -904,8 +906,12 @@ Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const flo
   return LaunchStatus("RmsNormBwd");
 }
 
+bool SoftmaxRowsBwdCausalForm(const float* probs, const float* dp, const float* ds, size_t cols) {
+  return RegCase(cols, {probs, dp, ds}) >= 0;
+}
+
 Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
-                      const Ctx& c, size_t causal_s) {
+                      const Ctx& c, size_t causal_s, bool tail) {
   if (rows == 0 || cols == 0) return Status::Ok();
   const int rc = RegCase(cols, {probs, dp, ds});
   if (causal_s != 0 && (causal_s != cols || rows % causal_s != 0))
@@ -914,7 +920,8 @@ Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t row
     // Traffic: the causal form reads about half of P and dP.
     const size_t traffic = causal_s ? 8 * rows * cols : 12 * rows * cols;
     REG_DISPATCH(softmax_rows_bwd_reg, rc, rows, probs, dp, ds, rows, static_cast<int>(cols),
-                 StreamPolicy(traffic) ? 1 : 0, static_cast<int>(causal_s));
+                 StreamPolicy(traffic) ? 1 : 0, static_cast<int>(causal_s),
+                 causal_s == 0 || tail ? 1 : 0);
   } else {
     ROWS_DISPATCH(softmax_rows_bwd_kernel, rows, cols, probs, dp, ds, rows, cols);
   }

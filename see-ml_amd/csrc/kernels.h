@@ -12,6 +12,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <initializer_list>
 
 #include "plan_checks.h"
 
@@ -249,17 +250,33 @@ Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const flo
 // j > i (AttnFwd / AttnDP outputs). Those entries are then not read: their
 // dS is (+0) * (0 - rowsum), the reference's expression on those values, and
 // their +0 products leave the double rowsum's bits unchanged.
+// Without `tail` (causal form only) a row stores only the float4s it read,
+// for callers whose readers never look past them. SoftmaxRowsBwdCausalForm:
+// whether the causal form applies to these operands (register-resident rows;
+// the fallback reads and writes whole rows).
 Status SoftmaxRowsBwd(const float* probs, const float* dp, float* ds, size_t rows, size_t cols,
-                      const Ctx& c, size_t causal_s = 0);
+                      const Ctx& c, size_t causal_s = 0, bool tail = true);
+bool SoftmaxRowsBwdCausalForm(const float* probs, const float* dp, const float* ds, size_t cols);
 // Causal row softmax in place over raw scores (attention forward, step 2).
 Status AttnSoftmaxRows(float* p, size_t rows, size_t S, const Ctx& c);
 
 // ---- attention family (k_attention.hip): GEMM-engine compositions -------
 size_t AttnWorkspace(size_t B, size_t S, size_t H, size_t d);
+// What the fused forward stores of P (the GEMM-engine form always stores it
+// all): the rows up to each 32-query block's diagonal tile (kAttnStoreP) and
+// the exact-zero tail beyond it (kAttnStoreTail). The engine leaves out
+// what it proves no reader looks at; AttnDP's `tail` likewise.
+inline constexpr int kAttnStoreP = 1, kAttnStoreTail = 2;
 Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* probs, size_t B,
-               size_t S, size_t H, size_t d, const Ctx& c);
+               size_t S, size_t H, size_t d, const Ctx& c,
+               int pstore = kAttnStoreP | kAttnStoreTail);
 Status AttnDP(const float* dout, const float* v, float* dp, size_t B, size_t S, size_t H,
-              size_t d, const Ctx& c);
+              size_t d, const Ctx& c, bool tail = true);
+// Whether these operands take the fused kernels (d in {64, 128}, S % 4 == 0,
+// 16-byte aligned): those read P / dS only at and below each 32-row block's
+// diagonal tile, masking j > i.
+bool AttnFusedPath(std::initializer_list<const float*> ptrs, size_t B, size_t S, size_t H,
+                   size_t d);
 Status AttnDV(const float* probs, const float* dout, float* dv, size_t B, size_t S, size_t H,
               size_t d, const Ctx& c);
 Status AttnDQ(const float* ds, const float* k, float* dq, size_t B, size_t S, size_t H, size_t d,

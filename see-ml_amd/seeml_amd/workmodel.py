@@ -36,7 +36,10 @@ def work(ins: dict, variant: str = "") -> dict:
 
     `variant` is the engine's kernel choice for it (seeml_hip_gemm_choice):
     a causal SoftmaxRowsBwd reads only the float4s of P and dP that hold
-    j <= i, so its bytes are those reads plus the full dS write; a GEMM with
+    j <= i, so its bytes are those reads plus the dS write (only those
+    float4s with "no zero tail"; AttnFwd/AttnDP with "no zero tail" store
+    each 32-row block's P/dP only up to its diagonal tile, and "P unused"
+    none of it); a GEMM with
     the following AddEW in its epilogue ("+AddEW") also reads the addend and
     writes the sum. A fused launch (skinny chain, pointwise run) reports the
     bytes it moves ("B=<n>") on its first instruction; the instructions
@@ -65,12 +68,18 @@ def work(ins: dict, variant: str = "") -> dict:
         TD, P = B * S * H * d, B * H * S * S
         half = B * H * d * S * (S + 1)  # 2 flops x S(S+1)/2 causal pairs x d
         shape = (B, S, H, d)
+        # P-shaped stores without the zero tail: each 32-row block up to its
+        # diagonal tile.
+        nblk = (S + 31) // 32
+        P_head = B * H * sum(32 * min(S, 32 * (w + 1)) for w in range(nblk)) if S else 0
+        P_st = P if "no zero tail" not in variant else min(P, P_head)
         if name in ("RopeFwd", "RopeBwd"):
             nbytes = 8 * TD
         elif name == "AttnFwd":
-            flops, nbytes, cls = 2 * half, 4 * (4 * TD + P), "attn"
+            P_st = 0 if variant == "P unused" else P_st
+            flops, nbytes, cls = 2 * half, 4 * (4 * TD + P_st), "attn"
         elif name == "AttnDP":
-            flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
+            flops, nbytes, cls = half, 4 * (2 * TD + P_st), "attn"
         else:  # DV / DQ / DK: read P-shaped + one activation, write one
             flops, nbytes, cls = half, 4 * (2 * TD + P), "attn"
     elif name in ("AddEW", "MulEW", "ReluBwd", "GeluBwd", "SiluBwd"):
@@ -100,7 +109,7 @@ def work(ins: dict, variant: str = "") -> dict:
         nbytes, shape = 12 * r * c, (r, c)
         if variant.startswith("causal") and c and r % c == 0:
             read = sum(4 * (i // 4 + 1) for i in range(c)) * (r // c)
-            nbytes = 8 * read + 4 * r * c
+            nbytes = 8 * read + 4 * (read if "no zero tail" in variant else r * c)
     elif name == "EmbedFwd":
         T, D = o[0], _lo(o[1])
         nbytes, shape = 4 * T + 8 * T * D, (T, D)

@@ -246,9 +246,11 @@ def test_c2_full_size_invariants(torch_gpu):
 
 def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
     """SoftmaxRowsBwd fed by AttnFwd / AttnDP reads only the causal half of P
-    and dP. Replaying the plan instruction by instruction up to it, P and dP
-    are exact +0 above the diagonal and the engine's dS equals the generic
-    full-row kernel's on the same P and dP, bit for bit."""
+    and dP; with no reader looking past the diagonal tiles, the producers
+    store no zero tail and it stores only the float4s it read. Replaying the
+    plan up to it: P and dP are exact +0 above the diagonal inside each
+    row's diagonal tile, and every stored dS float4 equals the generic
+    full-row kernel's on P and dP with everything above the diagonal +0."""
     from seeml_amd import PROGRAM_TRAIN, _lib, planner
     torch = torch_gpu
     w, p = compile_workload("c4m")
@@ -257,24 +259,35 @@ def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
     e.stage(x, y)
     idx = next(i for i, ins in enumerate(p.train)
                if ins["opcode"] == planner.OP["SoftmaxRowsBwd"])
+    assert e.gemm_choice(PROGRAM_TRAIN, idx) == "causal S=128, no zero tail"
+    for name in ("AttnFwd", "AttnDP"):
+        k = max(i for i, ins in enumerate(p.train[:idx]) if ins["opcode"] == planner.OP[name])
+        assert e.gemm_choice(PROGRAM_TRAIN, k) == "no zero tail", name
     for j in range(idx + 1):
         e.time_instruction(PROGRAM_TRAIN, j, reps=1)
     ins = p.train[idx]
     rows, cols = ins["out"][0] >> 32, ins["out"][0] & 0xFFFFFFFF
     P = e.read(ins["inp"][0], rows * cols).reshape(rows, cols)
     dP = e.read(ins["inp"][1], rows * cols).reshape(rows, cols)
-    dS = e.read(ins["inp"][2], rows * cols)
-    upper = np.arange(cols)[None, :] > (np.arange(rows) % cols)[:, None]
-    assert np.all(P[upper].view(np.uint32) == 0) and np.all(dP[upper].view(np.uint32) == 0)
+    dS = e.read(ins["inp"][2], rows * cols).reshape(rows, cols)
+    i = np.arange(rows) % cols
+    j = np.arange(cols)[None, :]
+    upper = j > i[:, None]
+    inside = upper & (j < ((i // 32 + 1) * 32)[:, None])
+    assert np.all(P[inside].view(np.uint32) == 0) and np.all(dP[inside].view(np.uint32) == 0)
+    P0, dP0 = P.copy(), dP.copy()
+    P0[upper] = 0.0
+    dP0[upper] = 0.0
     dev = torch.device("cuda:0")
     out = torch.full((rows * cols,), float("nan"), device=dev)
-    tp, tdp = torch.from_numpy(P.ravel().copy()).to(dev), torch.from_numpy(dP.ravel().copy()).to(dev)
+    tp, tdp = torch.from_numpy(P0.ravel()).to(dev), torch.from_numpy(dP0.ravel()).to(dev)
     rc = _lib.lib().seeml_hip_softmax_rows_bwd(tp.data_ptr(), tdp.data_ptr(), out.data_ptr(), rows,
                                                cols, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rc == 0
-    want = out.cpu().numpy()
-    assert np.array_equal(dS.view(np.uint32), want.view(np.uint32))
+    want = out.cpu().numpy().reshape(rows, cols)
+    stored = j < (4 * (i // 4) + 4)[:, None]
+    assert np.array_equal(dS[stored].view(np.uint32), want[stored].view(np.uint32))
     e.close()
 
 
