@@ -122,10 +122,12 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
 /* GEMM tile autotuning (compiler/backend/tuner/bandit.cc:14-53,
  * autotuner.cc:21-80 retargeted to GPU tiles): for every distinct GEMM shape
  * of the train program, a deterministic UCB1 bandit over tile/split-K arms,
- * reward = measured fraction of fp32 MFMA peak. The split-K count (it
- * changes the bits) is the lowest arm's within 3% of the best mean, so it is
- * the same every run; the tile config at that split (bit-neutral) is the
- * fastest within 0.5%. Picks are installed and graphs rebuilt.
+ * reward = measured fraction of fp32 MFMA peak. The summation order (the
+ * split-K count, or skinny against tile kernel: both change the bits) is the
+ * lowest arm's within 3% of the best mean, so it is the same every run; the
+ * tile config within that order (bit-neutral) is the lowest arm's within
+ * 1.5%. A skinny hint ranks after the tile configs. Picks are installed and
+ * graphs rebuilt.
  * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
 /* Describe the kernel variant chosen for instruction `index` of `program`:

@@ -63,12 +63,14 @@ bool IsGemmOp(uint16_t op) {
 // ---- UCB1 bandit (compiler/backend/tuner/bandit.cc:14-53) -----------------
 // Deterministic: untried arms first in index order, score ties to the lowest
 // index, no RNG.
-// Autotune picks: the split-K count (which changes the bits) resolves ties
-// inside a 3% band to the lowest arm (the planner's hint first, then the
-// fixed config order), so it comes out the same every run; the tile config
-// at that split (bit-neutral) is the fastest, within a 0.5% noise guard.
+// Autotune picks: the summation order (split-K count, or skinny kernel
+// against tile kernel: both change the bits) resolves ties inside a 3% band
+// to the lowest arm (the planner's hint first, then the fixed config order),
+// so it comes out the same every run; the tile config within that order
+// (bit-neutral) resolves ties inside a 1.5% band the same way: standalone
+// timings that close do not rank the tiles inside the step's graph.
 constexpr double kAutotuneTolerance = 0.03;
-constexpr double kAutotuneTileTolerance = 0.005;
+constexpr double kAutotuneTileTolerance = 0.015;
 constexpr double kPeakFp32MfmaFlops = 157.3e12;  // MI355X dense fp32 matrix peak
 
 class Ucb1 {
@@ -780,7 +782,7 @@ class Engine {
       const uint64_t bytes = n * sizeof(float);
       const uint64_t u = g.in[2];
       if (plans_[program][i].cfg != GemmSkinnyConfig()) {
-        if (PlanDenseChain(program, i, d)) ++i;
+        if (const size_t len = PlanDenseChain(program, i, d)) i += len - 1;
         continue;
       }
       if (op == Op::kGemmTN || SkinnyKindOf(d) != SkinnyKind::kOuter || d.ldc != d.N) continue;
@@ -1035,47 +1037,78 @@ class Engine {
     return LaunchGemm(d, plans_[program][idx], c);
   }
 
-  // A dense chain at instruction i (the GEMM), if instruction i + 1 admits one.
-  bool PlanDenseChain(int program, size_t i, GemmDesc d) {
+  // A dense chain at instruction i (the GEMM): the AddEW at i + 1, or a
+  // Scale at i + 1 feeding the AddEW at i + 2, folded into the GEMM's
+  // epilogue. Returns the chain's length (0: none). The GEMM's output c and
+  // the Scale's output v are stored only while a later instruction reads
+  // them (at most one of the two: the epilogue has one extra store).
+  size_t PlanDenseChain(int program, size_t i, GemmDesc d) {
     const auto& prog = plan_.program[program];
-    const UpdateInstruction& g = prog[i];
-    const UpdateInstruction& a = prog[i + 1];
-    if (static_cast<Op>(a.opcode) != Op::kAddEW ||
-        std::binary_search(marked_[program].begin(), marked_[program].end(), i + 1))
-      return false;
+    auto marked = [&](size_t k) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), k);
+    };
     if (d.batch != 1 || d.ldc != d.N || d.causal != Causal::kNone ||
         d.accumulate || d.bias || d.act != 0 || d.b_int8)
-      return false;
-    const uint64_t c = g.in[2], bytes = a.out[0] * sizeof(float);
-    if (a.out[0] != g.out[0] * g.out[1] || (a.in[0] != c && a.in[1] != c)) return false;
-    const bool addend_first = a.in[1] == c;
+      return 0;
+    const UpdateInstruction& g = prog[i];
+    const uint64_t c = g.in[2], n = g.out[0] * g.out[1], bytes = n * sizeof(float);
+    size_t k = i + 1;
+    uint64_t v = c;  // the value the AddEW consumes
+    bool scaled = false;
+    float scale = 1.0f;
+    if (static_cast<Op>(prog[k].opcode) == Op::kScale && prog[k].in[0] == c &&
+        prog[k].out[0] == n && !marked(k) && k + 1 < prog.size() && GemmVecForm(d)) {
+      scaled = true;
+      scale = Bits(prog[k].in[2]);
+      v = prog[k].in[1];
+      if (IsRodataRef(v)) return 0;
+      ++k;
+    }
+    const UpdateInstruction& a = prog[k];
+    if (static_cast<Op>(a.opcode) != Op::kAddEW || marked(k) || a.out[0] != n) return 0;
+    if (a.in[0] != v && a.in[1] != v) return 0;
+    const bool addend_first = a.in[1] == v;
     const uint64_t y = addend_first ? a.in[0] : a.in[1];
     const uint64_t o = a.in[2];
-    if (y == c || IsRodataRef(o)) return false;
-    const bool write_c = o != c && !DeadAfter(program, i + 1, RefOffset(c), bytes);
+    if (y == v || y == c || IsRodataRef(o)) return 0;
+    // c and v hold the GEMM's and the Scale's results only in registers:
+    // nothing may read them from memory, and v may not partially cover c.
+    if (!IsRodataRef(y) && (Overlaps(Ranges{{RefOffset(c), bytes}}, RefOffset(y), bytes) ||
+                            (scaled && Overlaps(Ranges{{RefOffset(v), bytes}}, RefOffset(y), bytes))))
+      return 0;
+    if (scaled && v != c && Overlaps(Ranges{{RefOffset(c), bytes}}, RefOffset(v), bytes)) return 0;
+    // Values live after the AddEW: c (unless overwritten by v or o) and v.
+    const bool c_live = c != o && c != v && !DeadAfter(program, k, RefOffset(c), bytes);
+    const bool v_live = scaled && v != o && !DeadAfter(program, k, RefOffset(v), bytes);
+    if (c_live && v_live) return 0;
+    uint64_t cdst = c;  // where the C store goes (with write_c)
+    if (v_live) cdst = v;
+    const bool write_c = c_live || v_live;
     Ranges writes{{RefOffset(o), bytes}};
-    if (write_c) writes.emplace_back(RefOffset(c), bytes);
+    if (write_c) writes.emplace_back(RefOffset(cdst), bytes);
     Ranges reads;
     (void)ReadRangesOf(g, &reads);
     for (const auto& w : writes)
-      if (Overlaps(reads, w.first, w.second)) return false;
-    if (write_c && o != c && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(c), bytes))
-      return false;
-    if (!IsRodataRef(y)) {
-      if (Overlaps(Ranges{{RefOffset(c), bytes}}, RefOffset(y), bytes)) return false;
-      if (y != o && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(y), bytes)) return false;
-    }
+      if (Overlaps(reads, w.first, w.second)) return 0;
+    if (write_c && cdst != o && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(cdst), bytes))
+      return 0;
+    if (!IsRodataRef(y) && y != o && Overlaps(Ranges{{RefOffset(o), bytes}}, RefOffset(y), bytes))
+      return 0;
+    d.C = WP(cdst);
     d.addend = RP(y);
     d.out = WP(o);
     d.addend_first = addend_first;
     d.write_c = write_c;
+    d.out_scaled = scaled;
+    d.out_scale = scale;
+    d.c_gets_scaled = v_live;
     ChainRun run;
     run.first = i;
-    run.count = 2;
+    run.count = k - i + 1;
     run.kind = ChainKind::kDense;
     run.d = d;
     chains_[program].push_back(run);
-    return true;
+    return run.count;
   }
 
   // The chain instruction idx belongs to in the built program, or null.
@@ -1559,7 +1592,10 @@ class Engine {
       const GemmPlan hint = plans_[program][first];
       // Arms: the heuristic hint and its neighbourhood — every other tile
       // shape at the hint's split, and the hint's tile at half/double split.
-      std::vector<GemmPlan> arms{hint};
+      // A skinny hint goes after the tile configs: near-ties then resolve to
+      // a tile kernel, whose epilogue also takes a following Scale + AddEW.
+      std::vector<GemmPlan> arms;
+      if (hint.cfg != GemmSkinnyConfig()) arms.push_back(hint);
       auto add = [&](int cfg, int splits) {
         GemmPlan p = PlanGemmWith(d, cfg, splits);
         for (const auto& a : arms)
@@ -1600,9 +1636,13 @@ class Engine {
         bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
       }
       if (!result) break;
-      const int splits = arms[bandit.Best(kAutotuneTolerance)].splits;
+      // Summation-order class: the split count of a tile kernel (any tile
+      // shape gives the same bits at one split count), or the skinny
+      // kernels' own order (0).
+      auto order = [&](size_t a) { return arms[a].cfg == GemmSkinnyConfig() ? 0 : arms[a].splits; };
+      const int cls = order(bandit.Best(kAutotuneTolerance));
       const GemmPlan best =
-          arms[bandit.Best(kAutotuneTileTolerance, [&](size_t a) { return arms[a].splits == splits; })];
+          arms[bandit.Best(kAutotuneTileTolerance, [&](size_t a) { return order(a) == cls; })];
       for (size_t i : idxs) plans_[program][i] = best;
     }
     (void)hipEventDestroy(t0);
@@ -1775,7 +1815,7 @@ class Engine {
       return k;
     }
     return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits) +
-           (run ? " +AddEW" : "");
+           (run ? (run->count == 3 ? " +Scale+AddEW" : " +AddEW") : "");
   }
 
   void Release() {

@@ -34,9 +34,10 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(GemmKArgs p) {
     if (p.bias) val = val + p.bias[n];
     val = dev_act(p.act, val);
     if (p.out) {
-      if (p.write_c) p.C[m * p.ldc + n] = val;
+      const float sv = p.out_scaled ? p.out_scale * val : val;
+      if (p.write_c) p.C[m * p.ldc + n] = p.c_scaled ? sv : val;
       const float y = p.addend[idx];
-      p.out[idx] = p.addend_first ? y + val : val + y;
+      p.out[idx] = p.addend_first ? y + sv : sv + y;
     } else {
       p.C[m * p.ldc + n] = val;
     }
@@ -100,6 +101,12 @@ GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
 
 GemmPlan PlanGemm(const GemmDesc& d) { return PlanGemmWith(d, -1, -1); }
 
+bool GemmVecForm(const GemmDesc& d) {
+  return !d.b_int8 && VecOk(d.A, d.lda, d.a_sb, d.a_sh, d.a_kc ? d.K : d.M) &&
+         VecOk(d.B, d.ldb, d.b_sb, d.b_sh, d.b_kc ? d.K : d.N) &&
+         d.lda < (int64_t{1} << 23) && d.ldb < (int64_t{1} << 23);
+}
+
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
@@ -130,9 +137,9 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   // contiguous extent that is a multiple of 4 (a float4 is then wholly in or
   // out of range); per-lane offsets within a tile must fit 32 bits. Other
   // GEMMs (int8 B, odd shapes) take the element-load form of the small tile.
-  const bool vec = !d.b_int8 && VecOk(d.A, d.lda, d.a_sb, d.a_sh, d.a_kc ? d.K : d.M) &&
-                   VecOk(d.B, d.ldb, d.b_sb, d.b_sh, d.b_kc ? d.K : d.N) &&
-                   d.lda < (int64_t{1} << 23) && d.ldb < (int64_t{1} << 23);
+  const bool vec = GemmVecForm(d);
+  if (d.out_scaled && (!d.out || !vec))
+    return Status::Fail(kUnitEngine, "Gemm: a fused Scale + AddEW needs the 16-byte-load kernels");
   if (d.out && !vec) {
     // The element-load form has no fused epilogue: the GEMM stores C (always
     // safe: C's range is C's while the GEMM writes it), then the AddEW runs.
@@ -146,7 +153,9 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   const int cfg = vec ? plan.cfg : gemm::kCfgSmall;
   const CfgInfo& c = kCfgs[cfg];
   const int64_t tm = CeilDiv(d.M, c.mt_m), tn = CeilDiv(d.N, c.mt_n);
-  if (tm * tn > 0x7FFFFFFF || d.batch > 65535 || plan.splits > 65535)
+  // The kernel decomposes its linear workgroup id in 32 bits.
+  if (tm * tn > 0x7FFFFFFF || d.batch > 65535 || plan.splits > 65535 ||
+      tm * tn * c.threads > 0xFFFFFFFF || tm * tn * plan.splits * d.batch > 0xFFFFFFFF)
     return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
 
   GemmKArgs a{};
@@ -156,7 +165,8 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   a.ws = static_cast<float*>(ctx.ws);
   a.M = d.M; a.N = d.N; a.K = d.K;
   a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
-  a.heads = d.heads; a.batch = d.batch;
+  a.heads = std::min(d.heads, d.batch);  // same (z / heads, z % heads) for z < batch; fits 32 bits
+  a.batch = d.batch;
   a.a_sb = d.a_sb; a.a_sh = d.a_sh; a.b_sb = d.b_sb; a.b_sh = d.b_sh;
   a.c_sb = d.c_sb; a.c_sh = d.c_sh;
   a.alpha = d.alpha;
@@ -174,6 +184,9 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   a.out = d.out;
   a.addend_first = d.addend_first ? 1 : 0;
   a.write_c = d.write_c ? 1 : 0;
+  a.out_scale = d.out_scale;
+  a.out_scaled = d.out_scaled ? 1 : 0;
+  a.c_scaled = d.c_gets_scaled ? 1 : 0;
 
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                   static_cast<unsigned>(d.batch));

@@ -93,6 +93,9 @@ struct GemmKArgs {
   float* out;
   int addend_first;
   int write_c;
+  float out_scale;  // GemmDesc::out_scaled: the AddEW consumes fl(out_scale * c)
+  int out_scaled;
+  int c_scaled;     // GemmDesc::c_gets_scaled: the C store is the scaled value
 };
 
 // Tile configurations (the autotuner's arms).
@@ -243,9 +246,12 @@ __device__ __forceinline__ void ReadFrags(const float* __restrict__ lds, int w0,
 
 // Linear workgroup id -> logical id such that XCD x (= lin % 8) holds the
 // contiguous logical range of its share. A bijection on [0, total).
-__device__ __forceinline__ int64_t XcdLogical(int64_t lin, int64_t total) {
-  const int64_t per = total / kXcds, rem = total % kXcds;
-  const int64_t x = lin % kXcds, idx = lin / kXcds;
+// Workgroup counts fit 32 bits (a grid holds at most 2^32 - 1 workgroups),
+// and 32-bit divisions are a few instructions where 64-bit ones are a long
+// scalar routine run by every workgroup before its first load.
+__device__ __forceinline__ uint32_t XcdLogical(uint32_t lin, uint32_t total) {
+  const uint32_t per = total / kXcds, rem = total % kXcds;
+  const uint32_t x = lin % kXcds, idx = lin / kXcds;
   return x < rem ? x * (per + 1) + idx : rem * (per + 1) + (x - rem) * per + idx;
 }
 
@@ -266,21 +272,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
 
   // Logical work item of this workgroup: (tile, split slice, batch z).
-  const int64_t tiles = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-  const int64_t lin = blockIdx.x + static_cast<int64_t>(gridDim.x) *
-                                       (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
-  int64_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
-  const int64_t t_id = L % tiles;
+  const uint32_t tiles = static_cast<uint32_t>(p.tiles_m) * static_cast<uint32_t>(p.tiles_n);
+  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  uint32_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
+  const uint32_t t_id = L % tiles;
   L /= tiles;
   const int slice = static_cast<int>(L % gridDim.y);
-  const int64_t z = L / gridDim.y;
-  const int64_t grp = t_id / (kGroupRows * p.tiles_n);
-  const int64_t first = grp * kGroupRows;
-  const int64_t gm = std::min<int64_t>(kGroupRows, p.tiles_m - first);
-  const int64_t in_grp = t_id - grp * kGroupRows * p.tiles_n;
+  const uint32_t z = L / gridDim.y;
+  const uint32_t grp = t_id / (kGroupRows * static_cast<uint32_t>(p.tiles_n));
+  const uint32_t first = grp * kGroupRows;
+  const uint32_t gm = std::min<uint32_t>(kGroupRows, static_cast<uint32_t>(p.tiles_m) - first);
+  const uint32_t in_grp = t_id - grp * kGroupRows * static_cast<uint32_t>(p.tiles_n);
   const int64_t tm = first + in_grp % gm, tn = in_grp / gm;
   const int64_t m0 = tm * MT_M, n0 = tn * MT_N;
-  const int64_t zb = z / p.heads, zh = z % p.heads;
+  const uint32_t heads = static_cast<uint32_t>(p.heads);
+  const int64_t zb = z / heads, zh = z % heads;
 
   const float* A = static_cast<const float*>(p.A) + zb * p.a_sb + zh * p.a_sh;
   const BT* B = static_cast<const BT*>(p.B) + zb * p.b_sb + zh * p.b_sh;
@@ -460,10 +466,36 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
           for (int v = 0; v < 16; ++v) {
             const int64_t row = 32 * i + 8 * (v >> 2) + (v & 3);
             const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
-            if (p.write_c) ca[row * p.ldc + 32 * j] = val;
+            const float sv = p.out_scaled ? p.out_scale * val : val;
+            if (p.write_c) ca[row * p.ldc + 32 * j] = p.c_scaled ? sv : val;
             const float y = yv[i][j][v];
-            oa[row * p.N + 32 * j] = p.addend_first ? y + val : val + y;
+            oa[row * p.N + 32 * j] = p.addend_first ? y + sv : sv + y;
           }
+      return;
+    }
+  }
+
+  // A whole tile with the plain epilogue (one slice, no accumulate, bias,
+  // activation or causal zeroing): one base pointer per lane, every element
+  // a compile-time number of rows and columns from it, no per-element bounds
+  // or epilogue branches. Stores what the general write-back below stores.
+  // The 128x128x32/w2x2 tile keeps the general write-back: two of its
+  // workgroups share a CU, the other's k loop hides this one's write-back,
+  // and the back-to-back stores measured ~1% slower on it in the C4 step.
+  constexpr bool kPlainFast =
+      VEC && !FUSED && !(MT_M == 128 && MT_N == 128 && KT == 32 && WAVES_M == 2 && WAVES_N == 2);
+  if constexpr (kPlainFast) {
+    if (p.splits == 1 && !p.accumulate && !p.bias && p.act == 0 &&
+        p.causal != static_cast<int>(Causal::kLowerOut) && m0 + MT_M <= p.M &&
+        n0 + MT_N <= p.N) {
+      float* ca = C + (m0 + wm0 + 4 * h) * p.ldc + n0 + wn0 + r;
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            ca[(32 * i + 8 * (v >> 2) + (v & 3)) * p.ldc + 32 * j] = p.alpha * acc[i][j][v];
       return;
     }
   }
@@ -490,9 +522,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
         val = dev_act(p.act, val);
         if (p.causal == static_cast<int>(Causal::kLowerOut) && n > m) val = 0.0f;
         if constexpr (FUSED) {  // a partial tile
-          if (p.write_c) C[m * p.ldc + n] = val;
+          const float sv = p.out_scaled ? p.out_scale * val : val;
+          if (p.write_c) C[m * p.ldc + n] = p.c_scaled ? sv : val;
           const float y = p.addend[m * p.N + n];
-          p.out[m * p.N + n] = p.addend_first ? y + val : val + y;
+          p.out[m * p.N + n] = p.addend_first ? y + sv : sv + y;
         } else {
           C[m * p.ldc + n] = val;
         }

@@ -71,10 +71,17 @@ struct GemmDesc {
   // split-K reduction; batch 1, ldc == N): out[m*N+n] = addend[m*N+n] (+) c, where c is the
   // value the GEMM stores at C(m, n) and (+) keeps the AddEW's operand order
   // (addend_first). C itself is stored only when write_c.
+  // out_scaled: a Scale sits between the GEMM and the AddEW, so the AddEW
+  // consumes fl(out_scale * c) (the Scale's stored value) instead of c, and
+  // with c_gets_scaled the C store receives that scaled value (C then names
+  // the Scale's output). Needs the 16-byte-load tile kernels (GemmVecForm).
   const float* addend = nullptr;
   float* out = nullptr;
   bool addend_first = true;
   bool write_c = true;
+  bool out_scaled = false;
+  float out_scale = 1.0f;
+  bool c_gets_scaled = false;
   // A Scale folded into the skinny rowdot / colsum kernels: their streamed
   // operand (rowdot: A; colsum: the [K, W] one) is read as
   // fl(stream_scale * x), element by element, as the Scale would have stored it.
@@ -93,6 +100,9 @@ GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits);
 int GemmConfigCount();
 const char* GemmConfigName(int cfg);
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);
+// True when a tile-kernel launch of d takes the 16-byte-load form, whose
+// epilogue can apply a fused Scale + AddEW (GemmDesc::out_scaled).
+bool GemmVecForm(const GemmDesc& d);
 
 // LoRA-shaped GEMMs (k_skinny.hip): one extent is the adapter rank. kOuter:
 // K <= 64 (the output is the HBM stream); kRowDot: N <= 64 with A

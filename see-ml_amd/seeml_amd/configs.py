@@ -113,7 +113,7 @@ def make(name: str) -> Workload:
     """Full-size BASELINE configs: c1..c5. Reduced parity variants: c2s,
     c3s, c4s, c5s keep each config's op structure at CPU-checkable size;
     c3m, c4m do too with head widths 64 and 128 (the fused attention
-    kernels' shapes). c2dx (c2sdx reduced) is C2 with the input's dX, the
+    kernels' shapes); c4mr is c4m at LoRA rank 128. c2dx (c2sdx reduced) is C2 with the input's dX, the
     interior-layer stream BASELINE's C2 text describes."""
     if name == "c1":
         return Workload("c1", mlp_model(), UpdateConfig(
@@ -141,6 +141,9 @@ def make(name: str) -> Workload:
         # head widths 64 and 128: the fused attention kernels' shapes
         "c3m": (512, 128, 2, 2, 192, 64, 4, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),
         "c4m": (1000, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
+        # c4m at rank 128: the LoRA up-projections are dense tile GEMMs
+        # (rank > 64) with the Scale and the residual AddEW in their epilogue
+        "c4mr": (1000, 256, 2, 2, 512, 128, 2, 128, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
     }
     if name not in dec:
         raise KeyError(name)

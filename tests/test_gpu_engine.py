@@ -50,7 +50,7 @@ def drift_floor(plan, w, steps, orc):
 
 
 @pytest.mark.parametrize("name,steps", [("c1", 5), ("c2s", 3), ("c2sdx", 3), ("c3s", 3), ("c4s", 3),
-                                        ("c5s", 3), ("c3m", 3), ("c4m", 3)])
+                                        ("c5s", 3), ("c3m", 3), ("c4m", 3), ("c4mr", 2)])
 def test_plan_parity_vs_oracle(torch_gpu, orc, name, steps):
     w, p = compile_workload(name)
     e = engine(p)
@@ -101,7 +101,7 @@ def test_fused_attention_decoder_100_steps_tolerance(torch_gpu, orc):
     e.close()
 
 
-@pytest.mark.parametrize("name", ["c1", "c3s", "c4m"])
+@pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr"])
 def test_bitwise_determinism_and_graph_equals_eager(torch_gpu, name):
     w, p = compile_workload(name)
     runs = []
@@ -291,6 +291,34 @@ def test_causal_softmax_rows_bwd_is_the_generic_kernel(torch_gpu):
     e.close()
 
 
+def _check_dense_chains(ch, scaled=False):
+    """Every GEMM reported "+AddEW" ("+Scale+AddEW") is followed by its one
+    (two) members reported inside its epilogue, and nothing else is."""
+    heads = [i for i, c in enumerate(ch) if c.endswith("+AddEW")]
+    assert len(heads) >= 4, ch
+    members = set()
+    for i in heads:
+        k = 2 if ch[i].endswith("+Scale+AddEW") else 1
+        assert all(c == "in GEMM epilogue" for c in ch[i + 1:i + 1 + k]), ch[i:i + 1 + k]
+        members.update(range(i + 1, i + 1 + k))
+    assert members == {i for i, c in enumerate(ch) if c == "in GEMM epilogue"}
+    if scaled:
+        assert sum(c.endswith("+Scale+AddEW") for c in ch) >= 4, ch
+
+
+def test_dense_scale_chains_are_planned(torch_gpu):
+    """At LoRA rank 128 the up-projection GEMM, its Scale and the residual
+    AddEW run as one tile-kernel launch (the graph == eager and parity tests
+    run this workload fused against unfused and against the oracle)."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c4mr")
+    x, y = configs.batch(w, 0)
+    e = engine(p)
+    e.train_step(x, y)
+    _check_dense_chains([e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))], True)
+    e.close()
+
+
 def test_fusions_are_planned(torch_gpu):
     """On a decoder the GEMM + AddEW fusion, the pointwise runs and the Scale
     folds fire (so the graph == eager bitwise test above compares fused
@@ -303,10 +331,7 @@ def test_fusions_are_planned(torch_gpu):
     e = engine(p)
     e.train_step(x, y)
     ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
-    fused = [i for i, c in enumerate(ch) if c == "in GEMM epilogue"]
-    assert len(fused) >= 4, ch
-    assert all(ch[i - 1].endswith("+AddEW") for i in fused)
-    assert sum(c.endswith("+AddEW") for c in ch) == len(fused)
+    _check_dense_chains(ch)
     # pointwise runs (the SwiGLU forward and backward): a head reporting its
     # bytes, followed by its members
     heads = [i for i, c in enumerate(ch) if c.startswith("pointwise run of ")]

@@ -94,7 +94,7 @@ def test_plan_hash_matches_reference(ref):
                 == ref.content_hash64(blob, n)), n
 
 
-@pytest.mark.parametrize("name", ["c1", "c2s", "c2sdx", "c3s", "c4s", "c5s", "c3m", "c4m"])
+@pytest.mark.parametrize("name", ["c1", "c2s", "c2sdx", "c3s", "c4s", "c5s", "c3m", "c4m", "c4mr"])
 def test_compiled_plans_verify_and_corruption_is_caught(name):
     w, p = compile_workload(name)
     assert verify_plan(p.blob) == (0, "")
