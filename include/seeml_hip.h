@@ -126,12 +126,14 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
  * split-K count, or skinny against tile kernel: both change the bits) is the
  * lowest arm's within 3% of the best mean, so it is the same every run; the
  * tile config within that order (bit-neutral) is the lowest arm's within
- * 1.5%. A skinny hint ranks after the tile configs. Picks are installed and
- * graphs rebuilt.
+ * 1.5%. A skinny hint ranks after the tile configs. Column-split arms (whole
+ * rounds of 256x128 tiles, the remainder on smaller tiles) join the tile
+ * arms. Picks are installed and graphs rebuilt.
  * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
 /* Describe the kernel variant chosen for instruction `index` of `program`:
- * GEMMs "cfg-name splits=S" (or "skinny/<kind>"), with " +AddEW" when the
+ * GEMMs "cfg-name splits=S" (or "skinny/<kind>"; a column split reads
+ * "cfg|tail-cfg@n_split splits=1"), with " +AddEW" when the
  * AddEW after it runs in its epilogue (that AddEW then reads "in GEMM
  * epilogue"); SoftmaxRowsBwd "causal S=n" when its probabilities are proven
  * AttnFwd/AttnDP outputs (only their causal half is read), else ""; AttnFwd,
@@ -266,6 +268,12 @@ int seeml_hip_gemm_nt_q8(const float* A, const int8_t* B, float* C, uint64_t M, 
 /* GEMM with an explicit tile config / split count (autotuner arms, tests). */
 int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, uint64_t M,
                           uint64_t N, uint64_t K, int cfg, int splits, void* stream);
+/* GEMM as two launches over column ranges (tests): columns [0, n_split) on
+ * tile config `cfg`, the rest on `tail_cfg` (both one split); with `out`,
+ * the fused AddEW out = addend + C. n_split = 0: one launch of `cfg`. */
+int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
+                                uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
+                                const float* addend, float* out, void* stream);
 int seeml_hip_gemm_config_count(void);
 /* Name of tile config `cfg` ("MTMxMTNxKT/wWMxWN"), "?" when out of range. */
 const char* seeml_hip_gemm_config_name(int cfg);

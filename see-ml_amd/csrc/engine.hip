@@ -1605,6 +1605,12 @@ class Engine {
       for (int cfg = 0; cfg < GemmConfigCount(); ++cfg) add(cfg, hint.splits);
       if (hint.splits > 1) add(hint.cfg, std::max(1, hint.splits / 2));
       add(hint.cfg, std::min(64, hint.splits * 2));
+      // Column splits: whole rounds of 256x128 tiles, the remainder on
+      // 128x128 or 128x64 tiles (same order class as one split).
+      for (int tail : {0, 4}) {
+        const GemmPlan sp = PlanGemmSplit(d, 2, tail);
+        if (sp.n_split > 0) arms.push_back(sp);
+      }
       size_t need = 0;
       for (const auto& a : arms) need = std::max(need, a.ws_bytes);
       if (need > ws_bytes_) {
@@ -1814,7 +1820,11 @@ class Engine {
       if (run) k += " chain of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
       return k;
     }
-    return std::string(GemmConfigName(p.cfg)) + " splits=" + std::to_string(p.splits) +
+    const std::string tiles =
+        p.n_split > 0 ? std::string(GemmConfigName(p.cfg)) + "|" + GemmConfigName(p.tail_cfg) + "@" +
+                            std::to_string(p.n_split)
+                      : std::string(GemmConfigName(p.cfg));
+    return tiles + " splits=" + std::to_string(p.splits) +
            (run ? (run->count == 3 ? " +Scale+AddEW" : " +AddEW") : "");
   }
 
@@ -2186,6 +2196,26 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
                           : layout == 2 ? seeml_hip::GemmTNDesc(A, B, C, M, N, K)
                                         : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
   return RunGemm(d, stream, cfg, splits);
+}
+int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
+                                uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
+                                const float* addend, float* out, void* stream) {
+  seeml_hip::GemmDesc d = layout == 1   ? seeml_hip::GemmNTDesc(A, B, C, M, N, K)
+                          : layout == 2 ? seeml_hip::GemmTNDesc(A, B, C, M, N, K)
+                                        : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
+  if (addend || out) {
+    d.addend = addend;
+    d.out = out;
+  }
+  const seeml_hip::GemmPlan plan =
+      n_split > 0 ? seeml_hip::PlanGemmSplit(d, cfg, tail_cfg, static_cast<int64_t>(n_split))
+                  : seeml_hip::PlanGemmWith(d, cfg, 1);
+  if (n_split > 0 && plan.n_split != static_cast<int64_t>(n_split)) {
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
+                                                     "Gemm: the column split does not apply to this GEMM"));
+  }
+  SEEML_CTX(plan.ws_bytes);
+  return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
 }
 int seeml_hip_gemm_config_count(void) { return seeml_hip::GemmConfigCount(); }
 const char* seeml_hip_gemm_config_name(int cfg) { return seeml_hip::GemmConfigName(cfg); }

@@ -36,8 +36,8 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(GemmKArgs p) {
     if (p.out) {
       const float sv = p.out_scaled ? p.out_scale * val : val;
       if (p.write_c) p.C[m * p.ldc + n] = p.c_scaled ? sv : val;
-      const float y = p.addend[idx];
-      p.out[idx] = p.addend_first ? y + sv : sv + y;
+      const float y = p.addend[m * p.ldo + n];
+      p.out[m * p.ldo + n] = p.addend_first ? y + sv : sv + y;
     } else {
       p.C[m * p.ldc + n] = val;
     }
@@ -101,6 +101,44 @@ GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
 
 GemmPlan PlanGemm(const GemmDesc& d) { return PlanGemmWith(d, -1, -1); }
 
+namespace {
+// Compute units of the current device (cached per device).
+int DeviceCUs() {
+  static int cus[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cus[dev] = v;
+  }
+  return cus[dev];
+}
+}  // namespace
+
+// Only the 256x128 tile, whose 108 KB of LDS holds one workgroup per CU, so
+// a round of the chip is exactly one tile per CU.
+GemmPlan PlanGemmSplit(const GemmDesc& d, int cfg, int tail_cfg, int64_t n_split) {
+  GemmPlan plan = PlanGemmWith(d, cfg, 1);
+  if (d.batch != 1 || d.causal != Causal::kNone || d.b_int8 || cfg < 0 || cfg >= kNumCfgs ||
+      tail_cfg < 0 || tail_cfg >= kNumCfgs || plan.splits != 1 || !GemmVecForm(d))
+    return plan;
+  if (n_split <= 0) {
+    if (cfg != 2) return plan;
+    const CfgInfo& c = kCfgs[cfg];
+    const int64_t cus = DeviceCUs();
+    const int64_t tm = CeilDiv(d.M, c.mt_m), bands = CeilDiv(d.N, c.mt_n);
+    if (cus <= 0 || (tm * bands) % cus == 0) return plan;
+    int64_t b = bands - 1;
+    while (b > 0 && (tm * b) % cus != 0) --b;
+    if (b == 0) return plan;
+    n_split = b * c.mt_n;
+  }
+  if (n_split >= d.N || n_split % 4 != 0) return plan;
+  plan.tail_cfg = tail_cfg;
+  plan.n_split = n_split;
+  return plan;
+}
+
 bool GemmVecForm(const GemmDesc& d) {
   return !d.b_int8 && VecOk(d.A, d.lda, d.a_sb, d.a_sh, d.a_kc ? d.K : d.M) &&
          VecOk(d.B, d.ldb, d.b_sb, d.b_sh, d.b_kc ? d.K : d.N) &&
@@ -110,6 +148,33 @@ bool GemmVecForm(const GemmDesc& d) {
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
+  if (plan.n_split > 0) {
+    if (plan.n_split >= d.N || plan.n_split % 4 != 0 || plan.splits != 1 || d.batch != 1 ||
+        d.causal != Causal::kNone || d.b_int8 || plan.cfg < 0 || plan.cfg >= kNumCfgs ||
+        plan.tail_cfg < 0 || plan.tail_cfg >= kNumCfgs)
+      return Status::Fail(kUnitEngine, "Gemm: unsupported column split");
+    // Two launches over column ranges of the same operands: C, B's columns,
+    // bias and the fused AddEW's arrays are offset views with the full row
+    // strides.
+    const int64_t n1 = plan.n_split;
+    GemmDesc left = d, right = d;
+    left.N = n1;
+    right.N = d.N - n1;
+    const float* B = static_cast<const float*>(d.B);
+    right.B = d.b_kc ? B + n1 * d.ldb : B + n1;
+    right.C = d.C + n1;
+    if (d.bias) right.bias = d.bias + n1;
+    if (d.out) {
+      left.ldo = right.ldo = d.ldo ? d.ldo : d.N;
+      right.addend = d.addend + n1;
+      right.out = d.out + n1;
+    }
+    GemmPlan pl, pr;
+    pl.cfg = plan.cfg;
+    pr.cfg = plan.tail_cfg;
+    if (Status s = LaunchGemm(left, pl, ctx); !s) return s;
+    return LaunchGemm(right, pr, ctx);
+  }
   if (d.scale_stream && plan.cfg != kNumCfgs)
     return Status::Fail(kUnitEngine, "Gemm: a scaled stream needs the skinny kernels");
   if (plan.cfg == kNumCfgs) {
@@ -123,7 +188,7 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");
   if (plan.splits > 1 && ctx.ws_bytes < plan.ws_bytes)
     return Status::Fail(kUnitEngine, "Gemm: workspace too small for split-K");
-  if (d.out && (!d.addend || d.batch != 1 || d.ldc != d.N || d.causal != Causal::kNone ||
+  if (d.out && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
                 d.accumulate || d.bias))
     return Status::Fail(kUnitEngine,
                         "Gemm: a fused AddEW needs batch 1, ldc == N and a plain epilogue "
@@ -140,6 +205,8 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   const bool vec = GemmVecForm(d);
   if (d.out_scaled && (!d.out || !vec))
     return Status::Fail(kUnitEngine, "Gemm: a fused Scale + AddEW needs the 16-byte-load kernels");
+  if (d.out && !vec && d.ldo && d.ldo != d.N)
+    return Status::Fail(kUnitEngine, "Gemm: a column view's fused AddEW needs the 16-byte-load kernels");
   if (d.out && !vec) {
     // The element-load form has no fused epilogue: the GEMM stores C (always
     // safe: C's range is C's while the GEMM writes it), then the AddEW runs.
@@ -187,6 +254,7 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   a.out_scale = d.out_scale;
   a.out_scaled = d.out_scaled ? 1 : 0;
   a.c_scaled = d.c_gets_scaled ? 1 : 0;
+  a.ldo = d.ldo ? d.ldo : d.N;
 
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                   static_cast<unsigned>(d.batch));

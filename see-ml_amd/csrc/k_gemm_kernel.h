@@ -96,6 +96,7 @@ struct GemmKArgs {
   float out_scale;  // GemmDesc::out_scaled: the AddEW consumes fl(out_scale * c)
   int out_scaled;
   int c_scaled;     // GemmDesc::c_gets_scaled: the C store is the scaled value
+  int64_t ldo;      // row stride of addend and out
 };
 
 // Tile configurations (the autotuner's arms).
@@ -447,8 +448,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   if constexpr (FUSED) {
     if (p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
       const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
-      const float* ya = p.addend + lm * p.N + ln;
-      float* oa = p.out + lm * p.N + ln;
+      const float* ya = p.addend + lm * p.ldo + ln;
+      float* oa = p.out + lm * p.ldo + ln;
       float* ca = C + lm * p.ldc + ln;
       float yv[BM][BN][16];
 #pragma unroll
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
         for (int j = 0; j < BN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            yv[i][j][v] = ya[(32 * i + 8 * (v >> 2) + (v & 3)) * p.N + 32 * j];
+            yv[i][j][v] = ya[(32 * i + 8 * (v >> 2) + (v & 3)) * p.ldo + 32 * j];
 #pragma unroll
       for (int i = 0; i < BM; ++i)
 #pragma unroll
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
             const float sv = p.out_scaled ? p.out_scale * val : val;
             if (p.write_c) ca[row * p.ldc + 32 * j] = p.c_scaled ? sv : val;
             const float y = yv[i][j][v];
-            oa[row * p.N + 32 * j] = p.addend_first ? y + sv : sv + y;
+            oa[row * p.ldo + 32 * j] = p.addend_first ? y + sv : sv + y;
           }
       return;
     }
@@ -524,8 +525,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
         if constexpr (FUSED) {  // a partial tile
           const float sv = p.out_scaled ? p.out_scale * val : val;
           if (p.write_c) C[m * p.ldc + n] = p.c_scaled ? sv : val;
-          const float y = p.addend[m * p.N + n];
-          p.out[m * p.N + n] = p.addend_first ? y + sv : sv + y;
+          const float y = p.addend[m * p.ldo + n];
+          p.out[m * p.ldo + n] = p.addend_first ? y + sv : sv + y;
         } else {
           C[m * p.ldc + n] = val;
         }

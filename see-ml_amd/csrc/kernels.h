@@ -82,6 +82,7 @@ struct GemmDesc {
   bool out_scaled = false;
   float out_scale = 1.0f;
   bool c_gets_scaled = false;
+  int64_t ldo = 0;  // row stride of addend and out (0: N, the fused-AddEW default)
   // A Scale folded into the skinny rowdot / colsum kernels: their streamed
   // operand (rowdot: A; colsum: the [K, W] one) is read as
   // fl(stream_scale * x), element by element, as the Scale would have stored it.
@@ -93,10 +94,21 @@ struct GemmPlan {
   int cfg = 0;      // tile configuration index
   int splits = 1;   // deterministic split-K slices
   size_t ws_bytes = 0;
+  // Column split (one slice only): columns [0, n_split) run on `cfg`, the
+  // rest on `tail_cfg`, as two launches. With cfg's tiles over [0, n_split)
+  // a whole number of rounds of the chip, the last partial round runs on
+  // smaller tiles. Every output keeps its k order: the bits are unchanged.
+  int tail_cfg = -1;
+  int64_t n_split = 0;
 };
 GemmPlan PlanGemm(const GemmDesc& d);
 // `forced_cfg`/`forced_splits` >= 0 override the heuristic (autotuner arms).
 GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits);
+// The column-split plan of `cfg` with `tail_cfg` on the remainder (or, with
+// n_split > 0, at that column): n_split = 0 in the result when none fits
+// (batched, causal or int8 GEMMs; tiles over the columns already a whole
+// number of rounds; no whole-round prefix).
+GemmPlan PlanGemmSplit(const GemmDesc& d, int cfg, int tail_cfg, int64_t n_split = 0);
 int GemmConfigCount();
 const char* GemmConfigName(int cfg);
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);

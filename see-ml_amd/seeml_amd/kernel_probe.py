@@ -25,6 +25,9 @@ def main(argv=None):
     ap.add_argument("--k", type=int, required=True)
     ap.add_argument("--cfg", required=True, help="tile config name, e.g. 128x64x32/w4x1")
     ap.add_argument("--splits", type=int, default=1)
+    ap.add_argument("--tail-cfg", default=None,
+                    help="column split: tile config of columns [n-split, n) (two launches)")
+    ap.add_argument("--n-split", type=int, default=0)
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=1024)
     a = ap.parse_args(argv)
@@ -46,9 +49,16 @@ def main(argv=None):
     B = torch.randn(K * N, device=dev, generator=g)
     Cm = torch.empty(M * N, device=dev)
     s = torch.cuda.current_stream().cuda_stream
+    if a.tail_cfg is not None and a.tail_cfg not in names:
+        sys.exit(f"kernel_probe: unknown tile config {a.tail_cfg!r}; have {sorted(names)}")
     for _ in range(a.reps):
-        rc = L.seeml_hip_gemm_forced(LAYOUTS[a.layout], A.data_ptr(), B.data_ptr(), Cm.data_ptr(),
-                                     M, N, K, cfg, a.splits, s)
+        if a.tail_cfg is not None:
+            rc = L.seeml_hip_gemm_forced_split(LAYOUTS[a.layout], A.data_ptr(), B.data_ptr(),
+                                               Cm.data_ptr(), M, N, K, cfg, names[a.tail_cfg],
+                                               a.n_split, None, None, s)
+        else:
+            rc = L.seeml_hip_gemm_forced(LAYOUTS[a.layout], A.data_ptr(), B.data_ptr(), Cm.data_ptr(),
+                                         M, N, K, cfg, a.splits, s)
         if rc != 0:
             sys.exit(f"kernel_probe: {_lib.kernel_error()}")
     n = a.copy_mib * (1 << 20) // 4
@@ -59,7 +69,8 @@ def main(argv=None):
         if rc != 0:
             sys.exit(f"kernel_probe: {_lib.kernel_error()}")
     torch.cuda.synchronize()
-    print(f"kernel_probe: {a.layout} {M}x{N}x{K} {a.cfg} x{a.reps}, copy {a.copy_mib} MiB x{a.reps}",
+    tail = f" | {a.tail_cfg} @ {a.n_split}" if a.tail_cfg is not None else ""
+    print(f"kernel_probe: {a.layout} {M}x{N}x{K} {a.cfg}{tail} x{a.reps}, copy {a.copy_mib} MiB x{a.reps}",
           flush=True)
 
 

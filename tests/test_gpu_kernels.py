@@ -164,6 +164,34 @@ def test_gemm_skinny(env, orc, layout, M, N, K):
     assert rel_err(env.H(generic), got) <= TOL_STEP
 
 
+@pytest.mark.parametrize("layout,M,N,K,tail,n_split", [
+    (1, 512, 1000, 256, 0, 768), (0, 300, 520, 128, 4, 384), (2, 256, 640, 96, 0, 512),
+    (1, 256, 5504, 64, 4, 5120)])
+def test_gemm_column_split_is_bitwise_one_launch(env, layout, M, N, K, tail, n_split):
+    """A column-split plan (256x128 tiles on [0, n_split), smaller tiles on
+    the rest) gives every output the same k order as one launch: bit-equal
+    C, and bit-equal fused-AddEW output through the offset column views."""
+    A, B, Y = rnd(M * K, 61), rnd(K * N, 62), rnd(M * N, 63)
+    whole, split = (env.T(np.full(M * N, np.nan, f32)) for _ in range(2))
+    env.call("seeml_hip_gemm_forced_split", layout, env.T(A), env.T(B), whole, M, N, K, 2, 0, 0, None, None)
+    env.call("seeml_hip_gemm_forced_split", layout, env.T(A), env.T(B), split, M, N, K, 2, tail, n_split,
+             None, None)
+    assert same_bits(env.H(split), env.H(whole))
+    a = A.reshape((K, M) if layout == 2 else (M, K)).astype(np.float64)
+    b = B.reshape((N, K) if layout == 1 else (K, N)).astype(np.float64)
+    want = (a.T if layout == 2 else a) @ (b.T if layout == 1 else b)
+    assert rel_err(env.H(whole), want.reshape(-1).astype(f32)) <= TOL_STEP
+    outs = []
+    for ns, tl in ((0, 0), (n_split, tail)):
+        c, o = env.T(np.full(M * N, np.nan, f32)), env.T(np.full(M * N, np.nan, f32))
+        env.call("seeml_hip_gemm_forced_split", layout, env.T(A), env.T(B), c, M, N, K, 2, tl, ns,
+                 env.T(Y), o)
+        outs.append((env.H(c), env.H(o)))
+    assert same_bits(outs[0][0], env.H(whole)) and same_bits(outs[1][0], env.H(whole))
+    assert same_bits(outs[1][1], outs[0][1])
+    assert same_bits(outs[0][1], (Y + env.H(whole)).astype(f32))
+
+
 def test_gemm_skinny_epilogue(env, orc):
     """GemmNN's fused bias/act epilogue through the skinny outer kernel."""
     M, N, K = 600, 264, 16
