@@ -259,34 +259,61 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   for (int g = 0; g < D / 8; ++g)
     qf[g] = *reinterpret_cast<const float4*>(qh + static_cast<int64_t>(ic) * ld + 8 * g + 4 * h);
 
+  // Both passes are software-pipelined by one key tile: iteration t stages
+  // K(t+1) (and in pass 2 V(t)) into LDS, then issues the score MFMAs of
+  // tile t+1 in the same basic block as the VALU work on tile t (the
+  // softmax statistics; the probabilities, their stores and P V), so the
+  // matrix cores run while the vector ALU works. The values and their order
+  // of evaluation are the unpipelined loop's: the results are the same bits.
+  // LDS: kt[(t+1) & 1] was last read by the scores of tile t-1 (iteration
+  // t-2), vt[t & 1] by P V of tile t-2; the barrier of iteration t-1 orders
+  // both before the stores of iteration t.
+
   // ---- pass 1: row maximum and exp-sum ----
   float m = -__builtin_inff(), l = 0.0f;
+  auto stats = [&](floatx16 sc, int t, bool diag) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = sc[e] * c2;
+    if (diag) MaskDiagonal(sc, t, i, h, -__builtin_inff());
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mn = fmaxf(m, tmax);
+    const float alpha = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+    float ssum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ssum += __builtin_amdgcn_exp2f(sc[e] - mn);
+    ssum += __shfl_xor(ssum, 32, 64);
+    l = l * alpha + ssum;
+    m = mn;
+  };
   KvTile<D> ks, vs;
+  floatx16 sc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
   ks.load(kh, ld, 0, S);
   ks.store(kt[0]);
   __syncthreads();
+  if (tiles_w > 0) sc = ScoreTile<D>(kt[0], qf, h, r);
+  if (tiles_wg > 1) ks.load(kh, ld, kAttnK, S);
   for (int t = 0; t < tiles_wg; ++t) {
-    if (t + 1 < tiles_wg) ks.load(kh, ld, (t + 1) * kAttnK, S);
-    if (t < tiles_w) {
-      floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = sc[e] * c2;
-      if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, -__builtin_inff());
-      float tmax = -__builtin_inff();
-#pragma unroll
-      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mn = fmaxf(m, tmax);
-      const float alpha = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-      float ssum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ssum += __builtin_amdgcn_exp2f(sc[e] - mn);
-      ssum += __shfl_xor(ssum, 32, 64);
-      l = l * alpha + ssum;
-      m = mn;
-    }
     if (t + 1 < tiles_wg) ks.store(kt[(t + 1) & 1]);
     __syncthreads();
+    if (t + 2 < tiles_wg) ks.load(kh, ld, (t + 2) * kAttnK, S);
+    if (t + 1 < tiles_w) {
+      const floatx16 sn = ScoreTile<D>(kt[(t + 1) & 1], qf, h, r);
+      stats(sc, t, false);
+      sc = sn;
+      // One VALU op of tile t's statistics after each score MFMA of tile t+1.
+#pragma unroll
+      for (int x = 0; x < 2 * D / 4; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+      }
+    } else if (t < tiles_w) {
+      stats(sc, t, true);
+    }
   }
 
   // ---- pass 2: probabilities, P, O ----
@@ -296,38 +323,52 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[nb][e] = 0.0f;
+  const bool row_ok = i < S;
+  const bool store_p = (pstore & kAttnStoreP) != 0;
+  // Every row of the wavefront exists: its stores before the diagonal tile
+  // need no per-lane test.
+  const bool rows_ok = qw + 31 < S;
+  float* prow = ph + static_cast<int64_t>(ic) * S;
+  // Tile t's probabilities from its scores (in place), and their stores to P.
+  auto to_probs = [&](floatx16& p, int t, bool diag) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) p[e] = __builtin_amdgcn_exp2f(p[e] * c2 - m) * inv_l;
+    if (diag) MaskDiagonal(p, t, i, h, 0.0f);
+  };
+  auto store_row = [&](const floatx16& p, int t, bool checked) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int j = t * kAttnK + 8 * q4 + 4 * h;
+      if (!checked || (row_ok && j < S))
+        *reinterpret_cast<float4*>(prow + j) = make_float4(p[4 * q4], p[4 * q4 + 1], p[4 * q4 + 2], p[4 * q4 + 3]);
+    }
+  };
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
   ks.load(kh, ld, 0, S);
   vs.load(vh, ld, 0, S);
   ks.store(kt[0]);
-  vs.store(vt[0]);
   __syncthreads();
-  const bool row_ok = i < S;
-  const bool store_p = (pstore & kAttnStoreP) != 0;
-  float* prow = ph + static_cast<int64_t>(ic) * S;
+  if (tiles_w > 0) sc = ScoreTile<D>(kt[0], qf, h, r);
+  if (tiles_wg > 1) ks.load(kh, ld, kAttnK, S);
   for (int t = 0; t < tiles_wg; ++t) {
-    if (t + 1 < tiles_wg) {
-      ks.load(kh, ld, (t + 1) * kAttnK, S);
-      vs.load(vh, ld, (t + 1) * kAttnK, S);
-    }
-    if (t < tiles_w) {
-      floatx16 sc = ScoreTile<D>(kt[t & 1], qf, h, r);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(sc[e] * c2 - m) * inv_l;
-      if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, 0.0f);
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int j = t * kAttnK + 8 * q4 + 4 * h;
-        if (store_p && row_ok && j < S)
-          *reinterpret_cast<float4*>(prow + j) =
-              make_float4(sc[4 * q4], sc[4 * q4 + 1], sc[4 * q4 + 2], sc[4 * q4 + 3]);
-      }
+    if (t + 1 < tiles_wg) ks.store(kt[(t + 1) & 1]);
+    vs.store(vt[t & 1]);
+    __syncthreads();
+    if (t + 2 < tiles_wg) ks.load(kh, ld, (t + 2) * kAttnK, S);
+    if (t + 1 < tiles_wg) vs.load(vh, ld, (t + 1) * kAttnK, S);
+    if (t + 1 < tiles_w) {
+      // Tile t lies wholly below the diagonal (j < i for every lane).
+      const floatx16 sn = ScoreTile<D>(kt[(t + 1) & 1], qf, h, r);
+      to_probs(sc, t, false);
+      if (store_p) store_row(sc, t, !rows_ok);
+      AccumulateTile<D>(vt[t & 1], sc, h, r, oacc);
+      sc = sn;
+    } else if (t < tiles_w) {
+      to_probs(sc, t, true);
+      if (store_p) store_row(sc, t, true);
       AccumulateTile<D>(vt[t & 1], sc, h, r, oacc);
     }
-    if (t + 1 < tiles_wg) {
-      ks.store(kt[(t + 1) & 1]);
-      vs.store(vt[(t + 1) & 1]);
-    }
-    __syncthreads();
   }
 
   if (row_ok) StoreRow<D>(oh + static_cast<int64_t>(i) * ld, oacc, h);
