@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from helpers import TOL_100, TOL_STEP, HostPlanRunner, compile_workload, rel_err
-from seeml_amd import configs
+from seeml_amd import configs, planner
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,33 @@ def test_plan_parity_vs_oracle(torch_gpu, orc, name, steps):
             floor = rel_err(b.read(ref, cnt), a.read(ref, cnt))
             err = rel_err(e.read(ref, cnt), r.read(ref, cnt))
             assert err <= max(TOL_STEP, 4 * floor), (base, ref, err, floor)
+    e.close()
+
+
+@pytest.mark.parametrize("name", ["c2s", "c4mr"])
+def test_autotuned_engine_parity(torch_gpu, orc, name):
+    """The bench runs autotuned plans: after seeml_hip_autotune (tile and
+    split-K arms, skinny against tile kernels, column splits) the engine
+    still matches the oracle and every GEMM reports a known variant."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload(name)
+    e = engine(p)
+    e.autotune(8)
+    r = HostPlanRunner(p, orc)
+    losses = []
+    for s in range(2):
+        x, y = configs.batch(w, s)
+        lg = e.train_step(x, y)
+        lr = r.train_step(x, y)
+        assert abs(lg - lr) <= TOL_STEP * max(abs(lr), 1e-3), (s, lg, lr)
+        losses.append(lg)
+    assert rel_err(persistent(e, p), persistent(r, p)) <= TOL_STEP
+    names = {e._L.seeml_hip_gemm_config_name(i).decode() for i in range(e._L.seeml_hip_gemm_config_count())}
+    ops = {planner.OP[k]: k for k in ("GemmNN", "GemmNT", "GemmTN")}
+    for i, ins in enumerate(p.train):
+        if ins["opcode"] in ops:
+            c = e.gemm_choice(PROGRAM_TRAIN, i)
+            assert c.startswith("in ") or c.split()[0].split("|")[0] in names or c.startswith("skinny/"), c
     e.close()
 
 
