@@ -143,6 +143,10 @@ int seeml_hip_autotune(seeml_hip_engine* e, int budget);
  * program's graph is built. */
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap);
+/* Test hook: forces instruction `index`'s GEMM plan to tile config `cfg`
+ * (seeml_hip_gemm_config_count() - 1 is the skinny kernels) with `splits`
+ * slices; the program's graph and fusions are re-planned on its next run. */
+int seeml_hip_set_gemm_plan(seeml_hip_engine* e, int program, uint64_t index, int cfg, int splits);
 
 /* ---- Feeder (replaces runtime/feeder/dataset.h:39-177) --------------------
  * A host dataset of fixed-shape samples: feature rows (f32) with class (i32)
@@ -274,6 +278,14 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
 int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
                                 uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
                                 const float* addend, float* out, void* stream);
+/* GEMM (NN or NT, tile config `cfg`: 2, or 0 for NT) with a LoRA
+ * up-projection in its epilogue (tests): out = y (+) s where y = A B,
+ * u = t bl (t [M, r] row-major, bl [r, N] row-major, r a multiple of 8, in
+ * the k order of a tile GEMM), s = scale * u when `scaled` (else u), and
+ * y_first selects the sum's operand order. Only `out` is written. */
+int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float* out, uint64_t M,
+                               uint64_t N, uint64_t K, int cfg, const float* t, const float* bl,
+                               uint64_t r, int scaled, float scale, int y_first, void* stream);
 int seeml_hip_gemm_config_count(void);
 /* Name of tile config `cfg` ("MTMxMTNxKT/wWMxWN"), "?" when out of range. */
 const char* seeml_hip_gemm_config_name(int cfg);

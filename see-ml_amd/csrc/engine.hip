@@ -749,7 +749,7 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -781,6 +781,10 @@ class Engine {
       const uint64_t n = g.out[0] * g.out[1];
       const uint64_t bytes = n * sizeof(float);
       const uint64_t u = g.in[2];
+      if (const size_t len = PlanLoraBase(program, i)) {
+        i += len - 1;
+        continue;
+      }
       if (plans_[program][i].cfg != GemmSkinnyConfig()) {
         if (const size_t len = PlanDenseChain(program, i, d)) i += len - 1;
         continue;
@@ -1037,6 +1041,103 @@ class Engine {
     return LaunchGemm(d, plans_[program][idx], c);
   }
 
+  // A LoRA'd projection as one run: the base GEMM y = x W at i, the rank-r
+  // down-projection t = x A at i + 1, the up-projection u = t B at i + 2, an
+  // optional Scale s = a u at i + 3, and the AddEW of y and s. The run
+  // launches the down-projection first, then the base GEMM with u, the Scale
+  // and the AddEW in its epilogue (GemmDesc::lora_t): y, u and s never reach
+  // memory. The up-projection must run on a tile plan with one slice, so the
+  // epilogue's u (the tile kernels' k order) has its bits; y, u and s must be
+  // dead after the AddEW. Returns the run's length (0: none).
+  size_t PlanLoraBase(int program, size_t i) {
+    const auto& prog = plan_.program[program];
+    auto marked = [&](size_t k) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), k);
+    };
+    if (i + 4 >= prog.size()) return 0;
+    const UpdateInstruction& g0 = prog[i];
+    const UpdateInstruction& g1 = prog[i + 1];
+    const UpdateInstruction& g2 = prog[i + 2];
+    const auto op0 = static_cast<Op>(g0.opcode), op2 = static_cast<Op>(g2.opcode);
+    if ((op0 != Op::kGemmNN && op0 != Op::kGemmNT) || op2 != Op::kGemmNN || !IsGemmOp(g1.opcode) ||
+        static_cast<Op>(g1.opcode) == Op::kGemmAccNN)
+      return 0;
+    for (size_t k = i; k < i + 3; ++k)
+      if (marked(k)) return 0;
+    GemmDesc d = DescOf(g0);
+    const GemmPlan& p0 = plans_[program][i];
+    const GemmPlan& p2 = plans_[program][i + 2];
+    if (d.batch != 1 || d.causal != Causal::kNone || d.accumulate || d.bias || d.b_int8 ||
+        !d.a_kc || d.ldc != d.N || p0.splits != 1)
+      return 0;
+    auto lora_cfg_ok = [&](int cfg) { return cfg == 2 || (cfg == 0 && d.b_kc); };
+    if (!lora_cfg_ok(p0.cfg) || (p0.n_split > 0 && !lora_cfg_ok(p0.tail_cfg))) return 0;
+    // up-projection u = t B: M x N over K = r, t the down-projection's output
+    const GemmDesc du = DescOf(g2);
+    const uint64_t t = g1.in[2];
+    if (g2.in[0] != t || du.M != d.M || du.N != d.N || du.K % 8 != 0 || du.K > 256 ||
+        p2.cfg == GemmSkinnyConfig() || p2.splits != 1 || du.batch != 1 || du.accumulate ||
+        du.bias || du.act != 0 || du.alpha != 1.0f || du.b_int8 || !du.a_kc || du.b_kc)
+      return 0;
+    const uint64_t n = static_cast<uint64_t>(d.M) * d.N, bytes = n * sizeof(float);
+    const uint64_t y = g0.in[2], uref = g2.in[2];
+    size_t k = i + 3;
+    uint64_t v = uref;
+    bool scaled = false;
+    float scale = 1.0f;
+    if (static_cast<Op>(prog[k].opcode) == Op::kScale && prog[k].in[0] == uref &&
+        prog[k].out[0] == n && !marked(k) && k + 1 < prog.size()) {
+      scaled = true;
+      scale = Bits(prog[k].in[2]);
+      v = prog[k].in[1];
+      ++k;
+    }
+    const UpdateInstruction& a = prog[k];
+    if (static_cast<Op>(a.opcode) != Op::kAddEW || marked(k) || a.out[0] != n) return 0;
+    if (!((a.in[0] == y && a.in[1] == v) || (a.in[0] == v && a.in[1] == y))) return 0;
+    const bool y_first = a.in[0] == y;
+    const uint64_t o = a.in[2];
+    if (IsRodataRef(o) || IsRodataRef(y) || IsRodataRef(uref) || IsRodataRef(v) || IsRodataRef(t)) return 0;
+    // y, u and s exist only in registers: each dead after the AddEW (or
+    // overwritten by its output), and the down-projection does not touch y.
+    for (uint64_t ref : {y, uref, v})
+      if (ref != o && !DeadAfter(program, k, RefOffset(ref), bytes)) return 0;
+    Ranges w1;
+    (void)WriteRangesOf(g1, &w1);
+    if (Overlaps(w1, RefOffset(y), bytes)) return 0;
+    // The fused launch reads x, W, t and B while it writes o; the
+    // down-projection reads x and A: none of them may overlap o, and the
+    // base GEMM's operands may not overlap t.
+    Ranges reads;
+    (void)ReadRangesOf(g0, &reads);
+    (void)ReadRangesOf(g2, &reads);
+    (void)ReadRangesOf(g1, &reads);
+    if (Overlaps(reads, RefOffset(o), bytes)) return 0;
+    Ranges r0;
+    (void)ReadRangesOf(g0, &r0);
+    for (const auto& wr : w1)
+      if (Overlaps(r0, wr.first, wr.second)) return 0;
+    if (!aligned16(du.A) || du.lda % 4 != 0 || !aligned16(WP(o))) return 0;
+    d.out = WP(o);
+    d.write_c = false;
+    d.out_scaled = scaled;
+    d.out_scale = scale;
+    d.lora_t = static_cast<const float*>(du.A);
+    d.lora_b = static_cast<const float*>(du.B);
+    d.lora_ldt = du.lda;
+    d.lora_ldb = du.ldb;
+    d.lora_r = static_cast<int>(du.K);
+    d.lora_y_first = y_first;
+    if (!GemmVecForm(d)) return 0;
+    ChainRun run;
+    run.first = i;
+    run.count = k - i + 1;
+    run.kind = ChainKind::kLoraBase;
+    run.d = d;
+    chains_[program].push_back(run);
+    return run.count;
+  }
+
   // A dense chain at instruction i (the GEMM): the AddEW at i + 1, or a
   // Scale at i + 1 feeding the AddEW at i + 2, folded into the GEMM's
   // epilogue. Returns the chain's length (0: none). The GEMM's output c and
@@ -1121,6 +1222,12 @@ class Engine {
   Status LaunchChain(int program, const ChainRun& run, const Ctx& c) {
     switch (run.kind) {
       case ChainKind::kDense: return LaunchGemm(run.d, plans_[program][run.first], c);
+      case ChainKind::kLoraBase: {
+        const size_t i1 = run.first + 1;
+        if (Status s = LaunchGemm(DescOf(plan_.program[program][i1]), plans_[program][i1], c); !s)
+          return s;
+        return LaunchGemm(run.d, plans_[program][run.first], c);
+      }
       case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
       case ChainKind::kScaleFold:
         for (size_t k = run.first + 1; k < run.first + run.count; ++k)
@@ -1568,6 +1675,17 @@ class Engine {
                  "probe copy");
   }
 
+  // Test hook: one GEMM instruction's plan, forced; the graph is rebuilt (and
+  // its fusions re-planned) on the program's next run.
+  Status SetGemmPlan(int program, size_t index, int cfg, int splits) {
+    if (program < 0 || program > 2 || index >= plan_.program[program].size() ||
+        !IsGemmOp(plan_.program[program][index].opcode) || cfg < 0 || cfg >= GemmConfigCount())
+      return Status::Fail(kUnitEngine, "set_gemm_plan: not a GEMM instruction or config");
+    plans_[program][index] = PlanGemmWith(DescOf(plan_.program[program][index]), cfg, splits);
+    DropGraph(program);
+    return Status::Ok();
+  }
+
   // ---- GEMM tile autotuning ------------------------------------------------
   Status Autotune(int budget) {
     const int program = static_cast<int>(Program::kTrain);
@@ -1807,6 +1925,8 @@ class Engine {
     if (run && idx != run->first) {
       switch (run->kind) {
         case ChainKind::kDense: return "in GEMM epilogue";
+        case ChainKind::kLoraBase:
+          return idx == run->first + 1 ? "in LoRA run (launched first)" : "in LoRA epilogue";
         case ChainKind::kPointwise: return "in pointwise run";
         default: return "in chain";
       }
@@ -1824,6 +1944,9 @@ class Engine {
         p.n_split > 0 ? std::string(GemmConfigName(p.cfg)) + "|" + GemmConfigName(p.tail_cfg) + "@" +
                             std::to_string(p.n_split)
                       : std::string(GemmConfigName(p.cfg));
+    if (run && run->kind == ChainKind::kLoraBase)
+      return tiles + " splits=" + std::to_string(p.splits) + " +LoRA" +
+             (run->count == 5 ? " +Scale" : "") + " +AddEW";
     return tiles + " splits=" + std::to_string(p.splits) +
            (run ? (run->count == 3 ? " +Scale+AddEW" : " +AddEW") : "");
   }
@@ -2074,6 +2197,10 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e) { return e->impl.w
 
 int seeml_hip_autotune(seeml_hip_engine* e, int budget) { return Ret(e, e->impl.Autotune(budget)); }
 
+int seeml_hip_set_gemm_plan(seeml_hip_engine* e, int program, uint64_t index, int cfg, int splits) {
+  return Ret(e, e->impl.SetGemmPlan(program, index, cfg, splits));
+}
+
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap) {
   if (program < 0 || program > 2 || index >= e->impl.plans_[program].size())
@@ -2214,6 +2341,25 @@ int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, floa
     return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
                                                      "Gemm: the column split does not apply to this GEMM"));
   }
+  SEEML_CTX(plan.ws_bytes);
+  return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
+}
+int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float* out, uint64_t M,
+                               uint64_t N, uint64_t K, int cfg, const float* t, const float* bl,
+                               uint64_t r, int scaled, float scale, int y_first, void* stream) {
+  seeml_hip::GemmDesc d = layout == 1 ? seeml_hip::GemmNTDesc(A, B, out, M, N, K)
+                                      : seeml_hip::GemmNNDesc(A, B, out, M, N, K);
+  d.out = out;
+  d.write_c = false;
+  d.out_scaled = scaled != 0;
+  d.out_scale = scale;
+  d.lora_t = t;
+  d.lora_b = bl;
+  d.lora_ldt = static_cast<int64_t>(r);
+  d.lora_ldb = static_cast<int64_t>(N);
+  d.lora_r = static_cast<int>(r);
+  d.lora_y_first = y_first != 0;
+  const seeml_hip::GemmPlan plan = seeml_hip::PlanGemmWith(d, cfg, 1);
   SEEML_CTX(plan.ws_bytes);
   return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
 }

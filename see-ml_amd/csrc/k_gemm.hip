@@ -178,9 +178,10 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     if (d.bias) right.bias = d.bias + n1;
     if (d.out) {
       left.ldo = right.ldo = d.ldo ? d.ldo : d.N;
-      right.addend = d.addend + n1;
+      if (d.addend) right.addend = d.addend + n1;
       right.out = d.out + n1;
     }
+    if (d.lora_t) right.lora_b = d.lora_b + n1;
     GemmPlan pl, pr;
     pl.cfg = plan.cfg;
     pr.cfg = plan.tail_cfg;
@@ -200,7 +201,12 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");
   if (plan.splits > 1 && ctx.ws_bytes < plan.ws_bytes)
     return Status::Fail(kUnitEngine, "Gemm: workspace too small for split-K");
-  if (d.out && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
+  if (d.lora_t && (!d.out || d.addend || d.lora_r <= 0 || d.lora_r % 8 != 0 || !d.lora_b ||
+                   !aligned16(d.lora_t) || d.lora_ldt % 4 != 0 || plan.splits != 1 ||
+                   (plan.cfg != 2 && !(plan.cfg == 0 && d.b_kc)) || !d.a_kc || d.b_int8 || d.batch != 1 ||
+                   d.causal != Causal::kNone || d.accumulate || d.bias || !GemmVecForm(d)))
+    return Status::Fail(kUnitEngine, "Gemm: unsupported LoRA epilogue");
+  if (d.out && !d.lora_t && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
                 d.accumulate || d.bias))
     return Status::Fail(kUnitEngine,
                         "Gemm: a fused AddEW needs batch 1, ldc == N and a plain epilogue "
@@ -267,6 +273,12 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   a.out_scaled = d.out_scaled ? 1 : 0;
   a.c_scaled = d.c_gets_scaled ? 1 : 0;
   a.ldo = d.ldo ? d.ldo : d.N;
+  a.lora_t = d.lora_t;
+  a.lora_b = d.lora_b;
+  a.lora_ldt = d.lora_ldt;
+  a.lora_ldb = d.lora_ldb;
+  a.lora_r = d.lora_r;
+  a.lora_y_first = d.lora_y_first ? 1 : 0;
 
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                   static_cast<unsigned>(d.batch));

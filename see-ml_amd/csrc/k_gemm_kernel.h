@@ -97,6 +97,15 @@ struct GemmKArgs {
   int out_scaled;
   int c_scaled;     // GemmDesc::c_gets_scaled: the C store is the scaled value
   int64_t ldo;      // row stride of addend and out
+  // LoRA up-projection in the epilogue (GemmDesc::lora_t): with lora_t set,
+  // out = c (+) fl(out_scale * u) where u = T B' over lora_r (T [M, lora_r]
+  // row-major, B' [lora_r, N] row-major), the same MFMA k order as a tile
+  // GEMM of u; addend unused. lora_y_first: c is the AddEW's first operand.
+  const float* lora_t;
+  const float* lora_b;
+  int64_t lora_ldt, lora_ldb;
+  int lora_r;
+  int lora_y_first;
 };
 
 // Tile configurations (the autotuner's arms).
@@ -257,7 +266,7 @@ __device__ __forceinline__ uint32_t XcdLogical(uint32_t lin, uint32_t total) {
 }
 
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED>
+          bool VEC, bool SCHED, bool FUSED, bool LORA = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
   using BT = typename std::conditional<B_I8, int8_t, float>::type;
   constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -445,6 +454,48 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   // and columns from it, so no per-element offsets stay live. The addends
   // are loaded first, all in flight together, then the sums are stored.
   // The value summed is the one the plain epilogue would store in C.
+  if constexpr (LORA) {
+    {
+      // One 32x32 block at a time: u's fragments come straight from T and B'
+      // (k = 8g + 4h + j for MFMA j of group g, as in the k loop above), and
+      // the block's outputs are stored before the next one starts. (Stores
+      // from one base pointer per lane, with no per-element bounds, measured
+      // 5% slower here: the per-element form spreads them between the next
+      // block's MFMAs.)
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j) {
+          const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
+          const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
+          floatx16 u;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) u[v] = 0.0f;
+          for (int g = 0; g < p.lora_r / KG; ++g) {
+            const int k0 = g * KG + 4 * h;
+            const float4 ta = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
+            const float tb0 = p.lora_b[(k0 + 0) * p.lora_ldb + col];
+            const float tb1 = p.lora_b[(k0 + 1) * p.lora_ldb + col];
+            const float tb2 = p.lora_b[(k0 + 2) * p.lora_ldb + col];
+            const float tb3 = p.lora_b[(k0 + 3) * p.lora_ldb + col];
+            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.x, tb0, u, 0, 0, 0);
+            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.y, tb1, u, 0, 0, 0);
+            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.z, tb2, u, 0, 0, 0);
+            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.w, tb3, u, 0, 0, 0);
+          }
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t m = m0 + wm0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int64_t n = n0 + wn0 + 32 * j + r;
+            if (m >= p.M || n >= p.N) continue;
+            const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
+            const float sv = p.out_scaled ? p.out_scale * u[v] : u[v];
+            p.out[m * p.ldo + n] = p.lora_y_first ? val + sv : sv + val;
+          }
+        }
+      return;
+    }
+  }
   if constexpr (FUSED) {
     if (p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
       const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
@@ -564,6 +615,24 @@ void LaunchVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
     }
   }
 #undef SEEML_GEMM_CASE
+}
+
+// The LoRA-epilogue instantiations (GemmKArgs::lora_t): the tiles the base
+// projection GEMMs run on. Returns false for any other config.
+template <bool A_KC, bool B_KC>
+bool LaunchLoraVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+  switch (cfg) {
+    case 0:
+      hipLaunchKernelGGL((gemm_mfma_kernel<128, 128, 32, 2, 2, A_KC, B_KC, false, true, true, true, true>),
+                         grid, dim3(kCfgs[0].threads), 0, s, a);
+      return true;
+    case 2:
+      hipLaunchKernelGGL((gemm_mfma_kernel<256, 128, 32, 4, 2, A_KC, B_KC, false, true, true, true, true>),
+                         grid, dim3(kCfgs[2].threads), 0, s, a);
+      return true;
+    default:
+      return false;
+  }
 }
 
 // Per-layout entry points, one instantiation unit each (built in parallel).

@@ -5,6 +5,10 @@ namespace seeml_hip {
 namespace gemm {
 
 void LaunchNT(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+  if (a.lora_t) {  // the host admits only vec, one slice and configs 0 / 2
+    (void)LaunchLoraVariant<true, true>(cfg, grid, s, a);
+    return;
+  }
   if (vec && a.out && a.splits == 1) LaunchVariant<true, true, false, true, true, true>(cfg, grid, s, a);
   else if (vec) LaunchVariant<true, true, false, true, true>(cfg, grid, s, a);
   else LaunchVariant<true, true, false, false>(cfg, grid, s, a);

@@ -83,6 +83,18 @@ struct GemmDesc {
   float out_scale = 1.0f;
   bool c_gets_scaled = false;
   int64_t ldo = 0;  // row stride of addend and out (0: N, the fused-AddEW default)
+  // A LoRA up-projection folded into the epilogue (with out; addend unused):
+  // out = c (+) fl(out_scale * u) (out_scale only when out_scaled), where
+  // u = T B' over lora_r (a multiple of 8; T [M, lora_r] with row stride
+  // lora_ldt, 16-byte rows; B' [lora_r, N] with row stride lora_ldb), in
+  // the k order of a tile GEMM of u, so u has that GEMM's bits. lora_y_first:
+  // c is the AddEW's first operand. Tile configs 0 and 2, one slice, A
+  // k-contiguous.
+  const float* lora_t = nullptr;
+  const float* lora_b = nullptr;
+  int64_t lora_ldt = 0, lora_ldb = 0;
+  int lora_r = 0;
+  bool lora_y_first = true;
   // A Scale folded into the skinny rowdot / colsum kernels: their streamed
   // operand (rowdot: A; colsum: the [K, W] one) is read as
   // fl(stream_scale * x), element by element, as the Scale would have stored it.

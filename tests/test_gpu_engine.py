@@ -333,6 +333,46 @@ def _check_dense_chains(ch, scaled=False):
         assert sum(c.endswith("+Scale+AddEW") for c in ch) >= 4, ch
 
 
+def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
+    """With the projection GEMMs on the 256x128 tile (forced here; the C4
+    autotuner picks it), each base GEMM, its LoRA down-projection,
+    up-projection, Scale and residual AddEW run as one LoRA run: the
+    down-projection first, then the base GEMM with u, the Scale and the sum
+    in its epilogue. The fused graph equals the eager engine bit for bit and
+    the oracle to tolerance."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c4mr")
+    ops = {planner.OP[k] for k in ("GemmNN", "GemmNT")}
+    D = 256
+    base = [i for i, ins in enumerate(p.train)
+            if ins["opcode"] in ops and list(ins["out"][:3]) == [w.cfg.batch, D, D]]
+    assert base
+    runs = []
+    for use_graph in (True, False):
+        e = engine(p, use_graph=use_graph)
+        for i in base:
+            assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 2, 1) == 0
+        losses = []
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+        if use_graph:
+            ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+            heads = [c for c in ch if "+LoRA" in c]
+            assert len(heads) >= 4, ch
+            assert sum(c == "in LoRA run (launched first)" for c in ch) == len(heads)
+        runs.append((np.array(losses, np.float32), persistent(e, p)))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    r = HostPlanRunner(p, orc)
+    for s in range(2):
+        x, y = configs.batch(w, s)
+        lr = r.train_step(x, y)
+        assert abs(runs[0][0][s] - lr) <= TOL_STEP * max(abs(lr), 1e-3), (s, runs[0][0][s], lr)
+    assert rel_err(runs[0][1], persistent(r, p)) <= TOL_STEP
+
+
 def test_dense_scale_chains_are_planned(torch_gpu):
     """At LoRA rank 128 the up-projection GEMM, its Scale and the residual
     AddEW run as one tile-kernel launch (the graph == eager and parity tests

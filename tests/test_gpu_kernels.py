@@ -192,6 +192,29 @@ def test_gemm_column_split_is_bitwise_one_launch(env, layout, M, N, K, tail, n_s
     assert same_bits(outs[0][1], (Y + env.H(whole)).astype(f32))
 
 
+@pytest.mark.parametrize("layout,M,N,K,r,cfg", [(1, 512, 384, 256, 16, 2), (0, 300, 200, 96, 16, 2),
+                                                 (1, 256, 512, 128, 128, 0), (1, 260, 130, 64, 8, 0)])
+def test_gemm_lora_epilogue_is_bitwise_the_unfused_chain(env, layout, M, N, K, r, cfg):
+    """The base GEMM with the LoRA up-projection, Scale and AddEW in its
+    epilogue equals, bit for bit, the base GEMM, the up-projection as a tile
+    GEMM (one slice), the Scale and the AddEW run one by one."""
+    A, B = rnd(M * K, 71), rnd(K * N, 72)
+    t, bl = rnd(M * r, 73), rnd(r * N, 74)
+    scale = f32(0.37)
+    y = env.T(np.full(M * N, np.nan, f32))
+    env.call("seeml_hip_gemm_forced", layout, env.T(A), env.T(B), y, M, N, K, cfg, 1)
+    u = env.T(np.full(M * N, np.nan, f32))
+    env.call("seeml_hip_gemm_forced", 0, env.T(t), env.T(bl), u, M, N, r, 5, 1)
+    yh, uh = env.H(y), env.H(u)
+    for scaled, y_first in ((1, 1), (1, 0), (0, 1)):
+        s = (scale * uh).astype(f32) if scaled else uh
+        want = (yh + s) if y_first else (s + yh)
+        out = env.T(np.full(M * N, np.nan, f32))
+        env.call("seeml_hip_gemm_forced_lora", layout, env.T(A), env.T(B), out, M, N, K, cfg,
+                 env.T(t), env.T(bl), r, scaled, scale, y_first)
+        assert same_bits(env.H(out), want.astype(f32)), (scaled, y_first)
+
+
 def test_gemm_skinny_epilogue(env, orc):
     """GemmNN's fused bias/act epilogue through the skinny outer kernel."""
     M, N, K = 600, 264, 16
