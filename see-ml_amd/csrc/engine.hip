@@ -1075,7 +1075,10 @@ class Engine {
     // up-projection u = t B: M x N over K = r, t the down-projection's output
     const GemmDesc du = DescOf(g2);
     const uint64_t t = g1.in[2];
-    if (g2.in[0] != t || du.M != d.M || du.N != d.N || du.K % 8 != 0 || du.K > 256 ||
+    // Rank 16 or less: the epilogue's u costs r/8 MFMA groups and r scalar
+    // B' loads per 32x32 block, with nothing to hide them; at rank 64 (C5)
+    // that cost exceeded the unfused chain's (C5 step 469.6 -> 474.1 ms).
+    if (g2.in[0] != t || du.M != d.M || du.N != d.N || du.K % 8 != 0 || du.K > 16 ||
         p2.cfg == GemmSkinnyConfig() || p2.splits != 1 || du.batch != 1 || du.accumulate ||
         du.bias || du.act != 0 || du.alpha != 1.0f || du.b_int8 || !du.a_kc || du.b_kc)
       return 0;

@@ -334,24 +334,28 @@ def _check_dense_chains(ch, scaled=False):
 
 
 def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
-    """With the projection GEMMs on the 256x128 tile (forced here; the C4
-    autotuner picks it), each base GEMM, its LoRA down-projection,
-    up-projection, Scale and residual AddEW run as one LoRA run: the
-    down-projection first, then the base GEMM with u, the Scale and the sum
-    in its epilogue. The fused graph equals the eager engine bit for bit and
-    the oracle to tolerance."""
+    """With the projection GEMMs on the 256x128 tile and the rank-16
+    up-projections on a tile plan (both forced here; the C4 autotuner picks
+    them), each base GEMM, its LoRA down-projection, up-projection, Scale and
+    residual AddEW run as one LoRA run: the down-projection first, then the
+    base GEMM with u, the Scale and the sum in its epilogue. The fused graph
+    equals the eager engine bit for bit and the oracle to tolerance."""
     from seeml_amd import PROGRAM_TRAIN
-    w, p = compile_workload("c4mr")
+    w, p = compile_workload("c4m")
     ops = {planner.OP[k] for k in ("GemmNN", "GemmNT")}
-    D = 256
+    D, r = 256, w.cfg.lora.rank
     base = [i for i, ins in enumerate(p.train)
             if ins["opcode"] in ops and list(ins["out"][:3]) == [w.cfg.batch, D, D]]
-    assert base
+    up = [i for i, ins in enumerate(p.train)
+          if ins["opcode"] == planner.OP["GemmNN"] and list(ins["out"][:3]) == [w.cfg.batch, D, r]]
+    assert base and up
     runs = []
     for use_graph in (True, False):
         e = engine(p, use_graph=use_graph)
         for i in base:
             assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 2, 1) == 0
+        for i in up:
+            assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 5, 1) == 0
         losses = []
         for s in range(2):
             x, y = configs.batch(w, s)
