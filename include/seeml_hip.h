@@ -280,7 +280,7 @@ int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, floa
                                 const float* addend, float* out, void* stream);
 /* GEMM (NN or NT, tile config `cfg`: 2, or 0 for NT) with a LoRA
  * up-projection in its epilogue (tests): out = y (+) s where y = A B,
- * u = t bl (t [M, r] row-major, bl [r, N] row-major, r a multiple of 8, in
+ * u = t bl (t [M, r] row-major, bl [r, N] row-major, r = 8 or 16, in
  * the k order of a tile GEMM), s = scale * u when `scaled` (else u), and
  * y_first selects the sum's operand order. Only `out` is written. */
 int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float* out, uint64_t M,

@@ -201,7 +201,7 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");
   if (plan.splits > 1 && ctx.ws_bytes < plan.ws_bytes)
     return Status::Fail(kUnitEngine, "Gemm: workspace too small for split-K");
-  if (d.lora_t && (!d.out || d.addend || d.lora_r <= 0 || d.lora_r % 8 != 0 || !d.lora_b ||
+  if (d.lora_t && (!d.out || d.addend || d.lora_r <= 0 || d.lora_r % 8 != 0 || d.lora_r > 16 || !d.lora_b ||
                    !aligned16(d.lora_t) || d.lora_ldt % 4 != 0 || plan.splits != 1 ||
                    (plan.cfg != 2 && !(plan.cfg == 0 && d.b_kc)) || !d.a_kc || d.b_int8 || d.batch != 1 ||
                    d.causal != Causal::kNone || d.accumulate || d.bias || !GemmVecForm(d)))

@@ -455,46 +455,60 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   // are loaded first, all in flight together, then the sums are stored.
   // The value summed is the one the plain epilogue would store in C.
   if constexpr (LORA) {
-    {
-      // One 32x32 block at a time: u's fragments come straight from T and B'
-      // (k = 8g + 4h + j for MFMA j of group g, as in the k loop above), and
-      // the block's outputs are stored before the next one starts. (Stores
-      // from one base pointer per lane, with no per-element bounds, measured
-      // 5% slower here: the per-element form spreads them between the next
-      // block's MFMAs.)
+    // u = T B' block by block (k = 8g + 4h + j for MFMA j of group g, as in
+    // the k loop above). Up to rank 16 every fragment of the wavefront's
+    // blocks is loaded at once, before any MFMA, so their latencies overlap;
+    // each block's outputs are stored right after its MFMAs (stores from one
+    // base pointer per lane, with no per-element bounds, measured 5% slower:
+    // the per-element form spreads them between the next block's MFMAs).
+    constexpr int kLoraG = 2;  // k groups held at once: rank <= 16
+    float ta[BM][kLoraG][4], tb[BN][kLoraG][4];
+    const int ng = p.lora_r / KG;
 #pragma unroll
-      for (int i = 0; i < BM; ++i)
+    for (int i = 0; i < BM; ++i) {
+      const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
 #pragma unroll
-        for (int j = 0; j < BN; ++j) {
-          const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
-          const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
-          floatx16 u;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) u[v] = 0.0f;
-          for (int g = 0; g < p.lora_r / KG; ++g) {
-            const int k0 = g * KG + 4 * h;
-            const float4 ta = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
-            const float tb0 = p.lora_b[(k0 + 0) * p.lora_ldb + col];
-            const float tb1 = p.lora_b[(k0 + 1) * p.lora_ldb + col];
-            const float tb2 = p.lora_b[(k0 + 2) * p.lora_ldb + col];
-            const float tb3 = p.lora_b[(k0 + 3) * p.lora_ldb + col];
-            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.x, tb0, u, 0, 0, 0);
-            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.y, tb1, u, 0, 0, 0);
-            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.z, tb2, u, 0, 0, 0);
-            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta.w, tb3, u, 0, 0, 0);
-          }
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int64_t m = m0 + wm0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
-            const int64_t n = n0 + wn0 + 32 * j + r;
-            if (m >= p.M || n >= p.N) continue;
-            const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
-            const float sv = p.out_scaled ? p.out_scale * u[v] : u[v];
-            p.out[m * p.ldo + n] = p.lora_y_first ? val + sv : sv + val;
-          }
-        }
-      return;
+      for (int g = 0; g < kLoraG; ++g) {
+        const int k0 = g * KG + 4 * h;
+        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (g < ng) q = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
+        ta[i][g][0] = q.x; ta[i][g][1] = q.y; ta[i][g][2] = q.z; ta[i][g][3] = q.w;
+      }
     }
+#pragma unroll
+    for (int j = 0; j < BN; ++j) {
+      const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
+#pragma unroll
+      for (int g = 0; g < kLoraG; ++g)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          tb[j][g][jj] = g < ng ? p.lora_b[(g * KG + 4 * h + jj) * p.lora_ldb + col] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+      for (int j = 0; j < BN; ++j) {
+        floatx16 u;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) u[v] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kLoraG; ++g) {
+          if (g >= ng) break;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            u = __builtin_amdgcn_mfma_f32_32x32x2f32(ta[i][g][jj], tb[j][g][jj], u, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = m0 + wm0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+          const int64_t n = n0 + wn0 + 32 * j + r;
+          if (m >= p.M || n >= p.N) continue;
+          const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
+          const float sv = p.out_scaled ? p.out_scale * u[v] : u[v];
+          p.out[m * p.ldo + n] = p.lora_y_first ? val + sv : sv + val;
+        }
+      }
+    return;
   }
   if constexpr (FUSED) {
     if (p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {

@@ -85,7 +85,7 @@ struct GemmDesc {
   int64_t ldo = 0;  // row stride of addend and out (0: N, the fused-AddEW default)
   // A LoRA up-projection folded into the epilogue (with out; addend unused):
   // out = c (+) fl(out_scale * u) (out_scale only when out_scaled), where
-  // u = T B' over lora_r (a multiple of 8; T [M, lora_r] with row stride
+  // u = T B' over lora_r (8 or 16; T [M, lora_r] with row stride
   // lora_ldt, 16-byte rows; B' [lora_r, N] with row stride lora_ldb), in
   // the k order of a tile GEMM of u, so u has that GEMM's bits. lora_y_first:
   // c is the AddEW's first operand. Tile configs 0 and 2, one slice, A

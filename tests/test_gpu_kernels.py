@@ -193,7 +193,7 @@ def test_gemm_column_split_is_bitwise_one_launch(env, layout, M, N, K, tail, n_s
 
 
 @pytest.mark.parametrize("layout,M,N,K,r,cfg", [(1, 512, 384, 256, 16, 2), (0, 300, 200, 96, 16, 2),
-                                                 (1, 256, 512, 128, 128, 0), (1, 260, 130, 64, 8, 0)])
+                                                 (1, 256, 512, 128, 16, 0), (1, 260, 130, 64, 8, 0)])
 def test_gemm_lora_epilogue_is_bitwise_the_unfused_chain(env, layout, M, N, K, r, cfg):
     """The base GEMM with the LoRA up-projection, Scale and AddEW in its
     epilogue equals, bit for bit, the base GEMM, the up-projection as a tile
