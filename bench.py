@@ -175,8 +175,12 @@ def main():
     log("top (op, shape, tile) groups by step share:")
     for (op, shape, tile), (tot, idx) in sorted(groups.items(), key=lambda kv: -kv[1][0])[:40]:
         r0 = rows[idx[0]]
-        rate = (f"{r0['flops'] * len(idx) / (tot * 1e-3) / 1e12:7.1f} TFLOP/s" if r0["flops"]
-                else f"{r0['bytes'] * len(idx) / (tot * 1e-3) / 1e9:7.0f} GB/s")
+        if tot <= 0.0:  # fused into another launch: no time of its own
+            rate = "      -"
+        elif r0["flops"]:
+            rate = f"{r0['flops'] * len(idx) / (tot * 1e-3) / 1e12:7.1f} TFLOP/s"
+        else:
+            rate = f"{r0['bytes'] * len(idx) / (tot * 1e-3) / 1e9:7.0f} GB/s"
         log(f"  {tot:8.3f} ms  x{len(idx):<4d} {op:15s} {'x'.join(map(str, shape)):22s} {tile:28s} {rate}")
     dom_row = rows[dom_idx[0]]
     # Its launches get event-record nodes in the train graph, timed live in
