@@ -121,16 +121,33 @@ uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e);
 
 /* GEMM tile autotuning (compiler/backend/tuner/bandit.cc:14-53,
  * autotuner.cc:21-80 retargeted to GPU tiles): for every distinct GEMM shape
- * of the train program, a deterministic UCB1 bandit over tile/split-K arms,
- * reward = measured fraction of fp32 MFMA peak. The summation order (the
- * split-K count, or skinny against tile kernel: both change the bits) is the
- * lowest arm's within 3% of the best mean, so it is the same every run; the
- * tile config within that order (bit-neutral) is the lowest arm's within
- * 1.5%. A skinny hint ranks after the tile configs. Column-split arms (whole
- * rounds of 256x128 tiles, the remainder on smaller tiles) join the tile
- * arms. Picks are installed and graphs rebuilt.
+ * of the train program, a deterministic UCB1 bandit over tile arms, reward =
+ * measured fraction of fp32 MFMA peak. Every arm keeps the summation order
+ * the shape fixes (the split-K count, or the skinny kernels' order): arms
+ * differ only in tile config or column split (whole rounds of 256x128 tiles,
+ * the rest on smaller tiles), which change no bits, so an autotuned run has
+ * the same bits as an untuned one whatever the timings. The pick is the
+ * lowest arm within 1.5% of the best mean (arm 0 = the heuristic plan).
+ * Picks are installed and graphs rebuilt.
  * budget = launches per shape (at least twice the number of arms). */
 int seeml_hip_autotune(seeml_hip_engine* e, int budget);
+/* seeml_hip_autotune with injected rewards (the reference's injected reward
+ * closure, test/compiler/backend/tuner_test.cc:130-145): each pull's reward
+ * is reward(ctx, group, arm, cfg, splits, n_split) for the group-th GEMM
+ * shape (in the tuner's order) and its arm-th arm; nothing is launched. */
+typedef double (*seeml_hip_tune_reward_fn)(void* ctx, uint64_t group, uint64_t arm, int cfg,
+                                           int splits, uint64_t n_split);
+int seeml_hip_autotune_injected(seeml_hip_engine* e, int budget, seeml_hip_tune_reward_fn reward,
+                                void* ctx);
+/* The engine's UCB1 bandit driven like AutotuneGemmTiling
+ * (compiler/backend/tuner/autotuner.cc:57-80, bandit.cc:14-53):
+ * max(trials, arms) pulls, each rewarded by reward(ctx, arm); picks[t] is
+ * the t-th selected arm, pulls/means the per-arm statistics and best_arm
+ * BestArm(). Host only. */
+typedef double (*seeml_hip_arm_reward_fn)(void* ctx, uint64_t arm);
+int seeml_hip_ucb1_run(uint64_t arms, double exploration, uint64_t trials,
+                       seeml_hip_arm_reward_fn reward, void* ctx, uint64_t* picks,
+                       uint64_t* pulls, double* means, uint64_t* best_arm);
 /* Describe the kernel variant chosen for instruction `index` of `program`:
  * GEMMs "cfg-name splits=S" (or "skinny/<kind>"; a column split reads
  * "cfg|tail-cfg@n_split splits=1"), with " +AddEW" when the
@@ -282,10 +299,13 @@ int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, floa
  * up-projection in its epilogue (tests): out = y (+) s where y = A B,
  * u = t bl (t [M, r] row-major, bl [r, N] row-major, r = 8 or 16, in
  * the k order of a tile GEMM), s = scale * u when `scaled` (else u), and
- * y_first selects the sum's operand order. Only `out` is written. */
+ * y_first selects the sum's operand order. Only `out` is written. With
+ * n_split > 0 the GEMM runs as a column split: [0, n_split) on `cfg`, the
+ * rest on `tail_cfg` (bl's columns offset like B's). */
 int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float* out, uint64_t M,
-                               uint64_t N, uint64_t K, int cfg, const float* t, const float* bl,
-                               uint64_t r, int scaled, float scale, int y_first, void* stream);
+                               uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
+                               const float* t, const float* bl, uint64_t r, int scaled,
+                               float scale, int y_first, void* stream);
 int seeml_hip_gemm_config_count(void);
 /* Name of tile config `cfg` ("MTMxMTNxKT/wWMxWN"), "?" when out of range. */
 const char* seeml_hip_gemm_config_name(int cfg);

@@ -83,6 +83,7 @@ _REF_ONLY = {
     "threads": ([], _Z),
     "plan_self_hash": ([_P, _Z, _Z], _U64),
     "content_hash64": ([_P, _Z], _U64),
+    "ucb1_run": ([_U64, C.c_double, _U64, _P, _P, _P, _P, _P, _P], None),
 }
 
 

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstring>
 
+#include "compiler/backend/tuner/bandit.h"
 #include "runtime/executor/update_kernels.h"
 #include "source/identity/hash.h"
 #include "source/parallel/parallel_for.h"
@@ -30,6 +31,27 @@ uint64_t ref_plan_self_hash(const uint8_t* plan, size_t size, size_t at) {
 }
 uint64_t ref_content_hash64(const uint8_t* data, size_t size) {
   return up::ContentHash64(data, size);
+}
+
+// The reference's Ucb1Bandit (compiler/backend/tuner/bandit.cc) driven the
+// way AutotuneGemmTiling drives it (autotuner.cc:57-80): max(trials, arms)
+// pulls, each rewarded by reward(ctx, arm). picks[t] is the t-th selection.
+typedef double (*ref_arm_reward_fn)(void* ctx, uint64_t arm);
+void ref_ucb1_run(uint64_t arms, double exploration, uint64_t trials, ref_arm_reward_fn reward,
+                  void* ctx, uint64_t* picks, uint64_t* pulls, double* means,
+                  uint64_t* best_arm) {
+  up::Ucb1Bandit bandit(arms, exploration);
+  const uint64_t budget = trials > arms ? trials : arms;
+  for (uint64_t t = 0; t < budget; ++t) {
+    const size_t arm = bandit.Select();
+    picks[t] = arm;
+    bandit.Update(arm, reward(ctx, arm));
+  }
+  for (uint64_t i = 0; i < arms; ++i) {
+    pulls[i] = bandit.pulls(i);
+    means[i] = bandit.meanReward(i);
+  }
+  *best_arm = bandit.BestArm();
 }
 
 void ref_gemm_nn(const float* A, const float* B, float* C, size_t M, size_t N,

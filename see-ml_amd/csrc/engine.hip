@@ -63,19 +63,20 @@ bool IsGemmOp(uint16_t op) {
 // ---- UCB1 bandit (compiler/backend/tuner/bandit.cc:14-53) -----------------
 // Deterministic: untried arms first in index order, score ties to the lowest
 // index, no RNG.
-// Autotune picks: the summation order (split-K count, or skinny kernel
-// against tile kernel: both change the bits) resolves ties inside a 3% band
-// to the lowest arm (the planner's hint first, then the fixed config order),
-// so it comes out the same every run; the tile config within that order
-// (bit-neutral) resolves ties inside a 1.5% band the same way: standalone
-// timings that close do not rank the tiles inside the step's graph.
-constexpr double kAutotuneTolerance = 0.03;
+// Autotune arms never change a result's bits: every arm of a GEMM keeps the
+// summation order GemmOrderOf fixes from its shape (the split-K count, or
+// the skinny kernels' order), and differs only in tile config or column
+// split. The pick is the lowest-index arm within 1.5% of the best mean:
+// standalone timings that close do not rank the tiles inside the step's
+// graph, so near-ties keep the planner's hint (arm 0) or the earlier config.
 constexpr double kAutotuneTileTolerance = 0.015;
 constexpr double kPeakFp32MfmaFlops = 157.3e12;  // MI355X dense fp32 matrix peak
 
 class Ucb1 {
  public:
   explicit Ucb1(size_t arms, double c = 1.0) : pulls_(arms, 0), mean_(arms, 0.0), c_(c) {}
+  uint64_t pulls(size_t arm) const { return pulls_[arm]; }
+  double mean(size_t arm) const { return mean_[arm]; }
   size_t Select() const {
     for (size_t i = 0; i < pulls_.size(); ++i)
       if (pulls_[i] == 0) return i;
@@ -98,20 +99,16 @@ class Ucb1 {
     mean_[arm] += (reward - mean_[arm]) / static_cast<double>(pulls_[arm]);
   }
   // The lowest-index pulled arm whose mean is within `tol` (relative) of the
-  // best mean among the arms `in` admits: arms closer than timing noise
-  // resolve the same way every run.
-  template <typename In>
-  size_t Best(double tol, In in) const {
+  // best mean: arms closer than timing noise resolve the same way every run.
+  // At tol = 0 this is the reference's BestArm (the first strict maximum).
+  size_t Best(double tol = 0.0) const {
     size_t best = pulls_.size();
     for (size_t i = 0; i < pulls_.size(); ++i)
-      if (pulls_[i] > 0 && in(i) && (best == pulls_.size() || mean_[i] > mean_[best])) best = i;
+      if (pulls_[i] > 0 && (best == pulls_.size() || mean_[i] > mean_[best])) best = i;
     if (best == pulls_.size()) return 0;
     for (size_t i = 0; i < best; ++i)
-      if (pulls_[i] > 0 && in(i) && mean_[i] >= (1.0 - tol) * mean_[best]) return i;
+      if (pulls_[i] > 0 && mean_[i] >= (1.0 - tol) * mean_[best]) return i;
     return best;
-  }
-  size_t Best(double tol = 0.0) const {
-    return Best(tol, [](size_t) { return true; });
   }
 
  private:
@@ -156,8 +153,11 @@ class Engine {
           !s)
         return s;
     if (Status s = HipOk(hipMalloc(&d_scalars_, sizeof(StepScalars)), "scalars"); !s) return s;
-    if (Status s = HipOk(hipHostMalloc(&h_scalars_, sizeof(StepScalars)), "pinned scalars"); !s)
+    if (Status s = HipOk(hipHostMalloc(&h_scalars_, 2 * sizeof(StepScalars)), "pinned scalars"); !s)
       return s;
+    for (hipEvent_t& ev : scalar_ev_)
+      if (Status s = HipOk(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "scalar event"); !s)
+        return s;
     if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
     if (Status s = MakeWeightCopies(); !s) return s;
     if (Status s = MakeRopeTables(); !s) return s;
@@ -1108,6 +1108,18 @@ class Engine {
     Ranges w1;
     (void)WriteRangesOf(g1, &w1);
     if (Overlaps(w1, RefOffset(y), bytes)) return 0;
+    // Unfused, the down- and up-projections run after y is stored and the
+    // AddEW after u and s are: none of them may read y from memory, u and s
+    // may not land on y, and s either is u (an in-place Scale) or is apart
+    // from it. Fused, y, u and s never reach memory.
+    Ranges r12;
+    (void)ReadRangesOf(g1, &r12);
+    (void)ReadRangesOf(g2, &r12);
+    if (Overlaps(r12, RefOffset(y), bytes)) return 0;
+    const Ranges yr{{RefOffset(y), bytes}};
+    if (Overlaps(yr, RefOffset(uref), bytes) || Overlaps(yr, RefOffset(v), bytes)) return 0;
+    if (scaled && v != uref && Overlaps(Ranges{{RefOffset(uref), bytes}}, RefOffset(v), bytes))
+      return 0;
     // The fused launch reads x, W, t and B while it writes o; the
     // down-projection reads x and A: none of them may overlap o, and the
     // base GEMM's operands may not overlap t.
@@ -1388,12 +1400,20 @@ class Engine {
     return Status::Ok();
   }
 
+  // Two pinned scalar slots used in turn: a slot is rewritten only after
+  // the upload that last read it has completed (its event), so back-to-back
+  // steps never overwrite bytes a pending copy still reads.
   Status SetStep(uint64_t step) {
+    const int slot = scalar_slot_ ^= 1;
+    if (Status s = HipOk(hipEventSynchronize(scalar_ev_[slot]), "scalar slot wait"); !s) return s;
+    h_scalars_[slot] = MakeStepScalars(plan_.header, step == 0 ? 1 : step);
+    if (Status s = HipOk(hipMemcpyAsync(d_scalars_, &h_scalars_[slot], sizeof(StepScalars),
+                                        hipMemcpyHostToDevice, stream_),
+                         "step scalars upload");
+        !s)
+      return s;
     step_ = step;
-    *h_scalars_ = MakeStepScalars(plan_.header, step == 0 ? 1 : step);
-    return HipOk(hipMemcpyAsync(d_scalars_, h_scalars_, sizeof(StepScalars),
-                                hipMemcpyHostToDevice, stream_),
-                 "step scalars upload");
+    return HipOk(hipEventRecord(scalar_ev_[slot], stream_), "scalar slot event");
   }
 
   // The feeder contract's bounds (contract.cc:173-207) on host-staged ids.
@@ -1455,10 +1475,13 @@ class Engine {
     return Status::Ok();
   }
 
+  // The batch is validated and staged before step_ advances: a rejected
+  // batch leaves the step counter (AdamW bias correction, LR schedule) as
+  // it was.
   Status TrainStep(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
                    bool on_device, float* loss) {
-    if (Status s = SetStep(step_ + 1); !s) return s;
     if (Status s = Stage(input, input_bytes, labels, label_bytes, on_device); !s) return s;
+    if (Status s = SetStep(step_ + 1); !s) return s;
     if (Status s = Run(static_cast<int>(Program::kTrain)); !s) return s;
     float l = 0.0f;
     if (Status s = Loss(&l); !s) return s;
@@ -1690,7 +1713,11 @@ class Engine {
   }
 
   // ---- GEMM tile autotuning ------------------------------------------------
-  Status Autotune(int budget) {
+  // With `inject`, each pull's reward comes from inject(ctx, group, arm, cfg,
+  // splits, n_split) instead of a timed launch, and nothing is launched (the
+  // reference's injected reward closure, test/compiler/backend/tuner_test.cc:130-145).
+  using RewardFn = double (*)(void*, uint64_t, uint64_t, int, int, uint64_t);
+  Status Autotune(int budget, RewardFn inject = nullptr, void* inject_ctx = nullptr) {
     const int program = static_cast<int>(Program::kTrain);
     const auto& prog = plan_.program[program];
     const uint64_t persist = plan_.header.persistent_size;
@@ -1707,30 +1734,53 @@ class Engine {
     if (Status s = HipOk(hipEventCreate(&t0), "event"); !s) return s;
     if (Status s = HipOk(hipEventCreate(&t1), "event"); !s) return s;
     Status result = Status::Ok();
+    uint64_t group = 0;
     for (auto& [key, idxs] : groups) {
       const size_t first = idxs.front();
       const GemmDesc d = DescOf(prog[first]);
-      const GemmPlan hint = plans_[program][first];
-      // Arms: the heuristic hint and its neighbourhood — every other tile
-      // shape at the hint's split, and the hint's tile at half/double split.
-      // A skinny hint goes after the tile configs: near-ties then resolve to
-      // a tile kernel, whose epilogue also takes a following Scale + AddEW.
-      std::vector<GemmPlan> arms;
-      if (hint.cfg != GemmSkinnyConfig()) arms.push_back(hint);
-      auto add = [&](int cfg, int splits) {
-        GemmPlan p = PlanGemmWith(d, cfg, splits);
+      const GemmOrder order = GemmOrderOf(d);
+      // Arm 0 is the heuristic plan; the others are every tile config at
+      // the order's split count and, at one split, the column splits (whole
+      // rounds of 256x128 tiles, the rest on 128x128 or 128x64 tiles). The
+      // skinny kernels' order has one kernel: nothing to tune.
+      const GemmPlan hint = PlanGemm(d);
+      const uint64_t gid = group++;
+      if (order.skinny) {
+        for (size_t i : idxs) plans_[program][i] = hint;
+        continue;
+      }
+      std::vector<GemmPlan> arms{hint};
+      auto add = [&](const GemmPlan& p) {
         for (const auto& a : arms)
-          if (a.cfg == p.cfg && a.splits == p.splits) return;
+          if (a.cfg == p.cfg && a.splits == p.splits && a.n_split == p.n_split &&
+              a.tail_cfg == p.tail_cfg)
+            return;
         arms.push_back(p);
       };
-      for (int cfg = 0; cfg < GemmConfigCount(); ++cfg) add(cfg, hint.splits);
-      if (hint.splits > 1) add(hint.cfg, std::max(1, hint.splits / 2));
-      add(hint.cfg, std::min(64, hint.splits * 2));
-      // Column splits: whole rounds of 256x128 tiles, the remainder on
-      // 128x128 or 128x64 tiles (same order class as one split).
-      for (int tail : {0, 4}) {
-        const GemmPlan sp = PlanGemmSplit(d, 2, tail);
-        if (sp.n_split > 0) arms.push_back(sp);
+      for (int cfg = 0; cfg < GemmSkinnyConfig(); ++cfg) add(PlanGemmWith(d, cfg, order.splits));
+      if (order.splits == 1)
+        for (int tail : {0, 4}) {
+          const GemmPlan sp = PlanGemmSplit(d, 2, tail);
+          if (sp.n_split > 0) add(sp);
+        }
+      for (const auto& a : arms)
+        if (!GemmPlanKeepsOrder(d, a)) {
+          result = Status::Fail(kUnitEngine, "autotune: an arm would change the summation order");
+          break;
+        }
+      if (!result) break;
+      if (inject) {
+        Ucb1 bandit(arms.size());
+        const int trials = std::max<int>(budget, 2 * static_cast<int>(arms.size()));
+        for (int t = 0; t < trials; ++t) {
+          const size_t arm = bandit.Select();
+          const GemmPlan& a = arms[arm];
+          bandit.Update(arm, inject(inject_ctx, gid, arm, a.cfg, a.splits,
+                                    static_cast<uint64_t>(a.n_split)));
+        }
+        const GemmPlan best = arms[bandit.Best(kAutotuneTileTolerance)];
+        for (size_t i : idxs) plans_[program][i] = best;
+        continue;
       }
       size_t need = 0;
       for (const auto& a : arms) need = std::max(need, a.ws_bytes);
@@ -1763,13 +1813,7 @@ class Engine {
         bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
       }
       if (!result) break;
-      // Summation-order class: the split count of a tile kernel (any tile
-      // shape gives the same bits at one split count), or the skinny
-      // kernels' own order (0).
-      auto order = [&](size_t a) { return arms[a].cfg == GemmSkinnyConfig() ? 0 : arms[a].splits; };
-      const int cls = order(bandit.Best(kAutotuneTolerance));
-      const GemmPlan best =
-          arms[bandit.Best(kAutotuneTileTolerance, [&](size_t a) { return order(a) == cls; })];
+      const GemmPlan best = arms[bandit.Best(kAutotuneTileTolerance)];
       for (size_t i : idxs) plans_[program][i] = best;
     }
     (void)hipEventDestroy(t0);
@@ -1978,6 +2022,10 @@ class Engine {
     if (h_count_) (void)hipHostFree(h_count_);
     h_count_ = nullptr;
     if (h_scalars_) (void)hipHostFree(h_scalars_);
+    for (hipEvent_t& ev : scalar_ev_) {
+      if (ev) (void)hipEventDestroy(ev);
+      ev = nullptr;
+    }
     if (h_loss_) (void)hipHostFree(h_loss_);
     if (stream_) (void)hipStreamDestroy(stream_);
     arena_ = rodata_ = nullptr;
@@ -2015,7 +2063,9 @@ class Engine {
   Ranges observed_;
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   std::vector<uint8_t> tails_[3];         // per instruction: kAttnStore* (PlanCausalTails)
-  StepScalars* h_scalars_ = nullptr;
+  StepScalars* h_scalars_ = nullptr;  // two pinned slots (SetStep)
+  hipEvent_t scalar_ev_[2] = {nullptr, nullptr};
+  int scalar_slot_ = 0;
   float* h_loss_ = nullptr;
   struct Segment {
     hipGraph_t graph = nullptr;
@@ -2049,6 +2099,13 @@ int Report(const Status& s) {
   g_kernel_error = s.error;
   return SEEML_HIP_ERROR;
 }
+}  // namespace
+
+// The standalone entry points' status: the message is kept for
+// seeml_hip_kernel_error() on this thread.
+int ReportStandalone(const Status& s) { return Report(s); }
+
+namespace {
 
 Status StandaloneCtx(void* stream, size_t ws_need, Ctx* out) {
   int dev = 0;
@@ -2199,6 +2256,30 @@ void* seeml_hip_stream(seeml_hip_engine* e) { return e->impl.stream_; }
 uint64_t seeml_hip_workspace_bytes(const seeml_hip_engine* e) { return e->impl.ws_bytes_; }
 
 int seeml_hip_autotune(seeml_hip_engine* e, int budget) { return Ret(e, e->impl.Autotune(budget)); }
+int seeml_hip_autotune_injected(seeml_hip_engine* e, int budget, seeml_hip_tune_reward_fn reward,
+                                void* ctx) {
+  if (!reward) return Ret(e, Status::Fail(seeml_hip::kUnitEngine, "autotune: no reward function"));
+  return Ret(e, e->impl.Autotune(budget, reward, ctx));
+}
+
+int seeml_hip_ucb1_run(uint64_t arms, double exploration, uint64_t trials,
+                       seeml_hip_arm_reward_fn reward, void* ctx, uint64_t* picks,
+                       uint64_t* pulls, double* means, uint64_t* best_arm) {
+  if (arms == 0 || !reward) return SEEML_HIP_ERROR;
+  seeml_hip::Ucb1 bandit(arms, exploration);
+  const uint64_t budget = std::max(trials, arms);
+  for (uint64_t t = 0; t < budget; ++t) {
+    const size_t arm = bandit.Select();
+    if (picks) picks[t] = arm;
+    bandit.Update(arm, reward(ctx, arm));
+  }
+  for (uint64_t i = 0; i < arms; ++i) {
+    if (pulls) pulls[i] = bandit.pulls(i);
+    if (means) means[i] = bandit.mean(i);
+  }
+  if (best_arm) *best_arm = bandit.Best();
+  return SEEML_HIP_OK;
+}
 
 int seeml_hip_set_gemm_plan(seeml_hip_engine* e, int program, uint64_t index, int cfg, int splits) {
   return Ret(e, e->impl.SetGemmPlan(program, index, cfg, splits));
@@ -2348,8 +2429,9 @@ int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, floa
   return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
 }
 int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float* out, uint64_t M,
-                               uint64_t N, uint64_t K, int cfg, const float* t, const float* bl,
-                               uint64_t r, int scaled, float scale, int y_first, void* stream) {
+                               uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
+                               const float* t, const float* bl, uint64_t r, int scaled, float scale,
+                               int y_first, void* stream) {
   seeml_hip::GemmDesc d = layout == 1 ? seeml_hip::GemmNTDesc(A, B, out, M, N, K)
                                       : seeml_hip::GemmNNDesc(A, B, out, M, N, K);
   d.out = out;
@@ -2362,7 +2444,12 @@ int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float
   d.lora_ldb = static_cast<int64_t>(N);
   d.lora_r = static_cast<int>(r);
   d.lora_y_first = y_first != 0;
-  const seeml_hip::GemmPlan plan = seeml_hip::PlanGemmWith(d, cfg, 1);
+  const seeml_hip::GemmPlan plan =
+      n_split > 0 ? seeml_hip::PlanGemmSplit(d, cfg, tail_cfg, static_cast<int64_t>(n_split))
+                  : seeml_hip::PlanGemmWith(d, cfg, 1);
+  if (n_split > 0 && plan.n_split != static_cast<int64_t>(n_split))
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
+                                                     "Gemm: the column split does not apply to this GEMM"));
   SEEML_CTX(plan.ws_bytes);
   return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
 }

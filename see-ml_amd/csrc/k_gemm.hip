@@ -61,10 +61,19 @@ const char* GemmConfigName(int cfg) {
   return cfg >= 0 && cfg < kNumCfgs ? kCfgs[cfg].name : "?";
 }
 
+// The heuristic takes the skinny kernels only for the shapes that stream a
+// rank-wide operand through a reduction over the token rows (rowdot: N is
+// the rank; colsum: a weight gradient). A rank-K outer product (K <= 64)
+// runs on the tile kernels: they time within 1% of the skinny outer kernel
+// alone and their epilogue takes a following Scale + AddEW or a whole LoRA
+// run. A forced skinny config still selects the outer kernel (tests).
 GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
   GemmPlan plan;
-  const bool skinny = SkinnyKindOf(d) != SkinnyKind::kNone;
-  if (skinny && (forced_cfg == kNumCfgs || forced_cfg < 0)) {
+  const SkinnyKind kind = SkinnyKindOf(d);
+  const bool skinny = forced_cfg == kNumCfgs
+                          ? kind != SkinnyKind::kNone
+                          : forced_cfg < 0 && (kind == SkinnyKind::kRowDot || kind == SkinnyKind::kColSum);
+  if (skinny) {
     plan.cfg = kNumCfgs;
     plan.splits = 1;
     plan.ws_bytes = SkinnyWorkspace(d);
@@ -112,6 +121,20 @@ int DeviceCUs() {
   return cus[dev];
 }
 }  // namespace
+
+GemmOrder GemmOrderOf(const GemmDesc& d) {
+  const GemmPlan h = PlanGemmWith(d, -1, -1);
+  GemmOrder o;
+  o.skinny = h.cfg == kNumCfgs;
+  o.splits = o.skinny ? 1 : h.splits;
+  return o;
+}
+
+bool GemmPlanKeepsOrder(const GemmDesc& d, const GemmPlan& p) {
+  const GemmOrder o = GemmOrderOf(d);
+  if (o.skinny) return p.cfg == kNumCfgs;
+  return p.cfg >= 0 && p.cfg < kNumCfgs && p.splits == o.splits && (p.n_split == 0 || p.splits == 1);
+}
 
 // The heuristic plan, and for large GEMMs whose 256x128 tiles leave a
 // partial last round, the column split of at least two whole rounds with

@@ -43,6 +43,10 @@ struct Ctx {
   const StepScalars* scalars = nullptr;
 };
 
+// SEEML_HIP_OK / SEEML_HIP_ERROR for a standalone C-ABI entry point; a
+// failure's message is what seeml_hip_kernel_error() returns on this thread.
+int ReportStandalone(const Status& s);
+
 // ---- GEMM engine (k_gemm.hip) -------------------------------------------
 enum class Causal : int {
   kNone = 0,
@@ -116,6 +120,18 @@ struct GemmPlan {
 GemmPlan PlanGemm(const GemmDesc& d);
 // `forced_cfg`/`forced_splits` >= 0 override the heuristic (autotuner arms).
 GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits);
+// A GEMM's summation order: the skinny kernels' own order, or the tile
+// kernels' per-output k order at `splits` deterministic split-K slices (any
+// tile config and any column split at one slice give the same bits). It is
+// a pure function of the shape, layout and operand alignment — the
+// heuristic's — so no timing can change a result's bits.
+struct GemmOrder {
+  bool skinny = false;
+  int splits = 1;
+};
+GemmOrder GemmOrderOf(const GemmDesc& d);
+// True when plan `p` keeps GemmOrderOf(d).
+bool GemmPlanKeepsOrder(const GemmDesc& d, const GemmPlan& p);
 // The column-split plan of `cfg` with `tail_cfg` on the remainder (or, with
 // n_split > 0, at that column): n_split = 0 in the result when none fits
 // (batched, causal or int8 GEMMs; tiles over the columns already a whole

@@ -23,6 +23,9 @@ _TYPES = {
     "uint32_t": C.c_uint32,
     "int32_t": C.c_int32,
     "double": C.c_double,
+    # callback typedefs: passed as a ctypes CFUNCTYPE object cast to c_void_p
+    "seeml_hip_tune_reward_fn": C.c_void_p,
+    "seeml_hip_arm_reward_fn": C.c_void_p,
 }
 
 
@@ -73,6 +76,17 @@ def lib():
             raise FileNotFoundError(
                 f"{LIB_PATH} is not built — run __graft_entry__.build() "
                 "(hipcc for gfx950); the backend has no CPU fallback")
+        # torch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
+        # libamdhip64.so.7, linked by that file name). Loaded first, it is
+        # the one this library's libamdhip64.so.7 dependency binds to; loaded
+        # after this library, torch would bring a second runtime into the
+        # process, and this library's HIP calls then fail. The tests and the
+        # bench hand this library torch tensors, so torch's runtime goes in
+        # first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = C.CDLL(LIB_PATH)
         for name, (rtype, argtypes) in parse_header().items():
             fn = getattr(handle, name)

@@ -102,6 +102,80 @@ def test_autotuned_engine_parity(torch_gpu, orc, name):
     e.close()
 
 
+def _gemm_orders(e, p):
+    """instruction index -> the summation order the engine reports for every
+    GEMM of the train program ("splits=S" or "skinny/<kind>"); read from an
+    eager engine, which reports each GEMM's own plan (no fusion)."""
+    import re
+    from seeml_amd import PROGRAM_TRAIN
+    ops = {planner.OP[k] for k in ("GemmNN", "GemmNT", "GemmTN")}
+    out = {}
+    for i, ins in enumerate(p.train):
+        if ins["opcode"] in ops:
+            c = e.gemm_choice(PROGRAM_TRAIN, i)
+            m = re.search(r"splits=(\d+)", c)
+            out[i] = c.split()[0] if c.startswith("skinny/") else f"splits={m.group(1)}"
+    return out
+
+
+def _tile_picks(e, p):
+    from seeml_amd import PROGRAM_TRAIN
+    ops = {planner.OP[k] for k in ("GemmNN", "GemmNT", "GemmTN")}
+    return {i: e.gemm_choice(PROGRAM_TRAIN, i) for i, ins in enumerate(p.train) if ins["opcode"] in ops}
+
+
+@pytest.mark.parametrize("name", ["c2sdx", "c4m", "c3s"])
+def test_autotune_cannot_change_the_summation_order(torch_gpu, name):
+    """Whatever the rewards — one arm far ahead, arms within the 1.5% band of
+    each other on either side of it, rewards that invert the config order —
+    the autotuner installs only plans with the summation order the shape
+    fixes (the untuned engine's split count or skinny kernel), so the
+    trained bits equal the untuned engine's. The reference's tuner cannot
+    change bits either: its k grouping is fixed (gemm.cc:33-93)."""
+    import ctypes as C
+    w, p = compile_workload(name)
+    REWARD = C.CFUNCTYPE(C.c_double, C.c_void_p, C.c_uint64, C.c_uint64, C.c_int, C.c_int,
+                         C.c_uint64)
+    schemes = {
+        "last wins": lambda g, a, cfg, s, n: 1.0 if a == 7 else 0.1,
+        "within band, rising": lambda g, a, cfg, s, n: 1.0 + 0.001 * a,
+        "outside band, rising": lambda g, a, cfg, s, n: 1.0 + 0.02 * a,
+        "outside band, falling": lambda g, a, cfg, s, n: 1.0 - 0.02 * a,
+        "by config, inverted": lambda g, a, cfg, s, n: 1.0 / (1 + cfg) + (0.5 if n else 0.0),
+    }
+
+    def train(e, steps=2):
+        losses = []
+        for s in range(steps):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+        return np.array(losses, np.float32), persistent(e, p)
+
+    base_eager = engine(p, use_graph=False)
+    base_orders = _gemm_orders(base_eager, p)
+    base_eager.close()
+    base = engine(p)
+    base_bits = train(base)
+    base.close()
+    picks = set()
+    for label, fn in schemes.items():
+        cb = REWARD(lambda ctx, g, a, cfg, s, n, fn=fn: fn(g, a, cfg, s, n))
+        runs = []
+        for use_graph in (False, True):
+            e = engine(p, use_graph=use_graph)
+            assert e._L.seeml_hip_autotune_injected(e._h, 16, C.cast(cb, C.c_void_p), None) == 0, \
+                e._L.seeml_hip_last_error(e._h)
+            if not use_graph:
+                assert _gemm_orders(e, p) == base_orders, label
+                picks.add(tuple(sorted(_tile_picks(e, p).items())))
+            runs.append(train(e))
+            e.close()
+        for got in runs:
+            assert np.array_equal(got[0].view(np.uint32), base_bits[0].view(np.uint32)), label
+            assert np.array_equal(got[1].view(np.uint32), base_bits[1].view(np.uint32)), label
+    assert len(picks) >= 2, "the schemes never moved a tile pick: the test would be vacuous"
+
+
 def test_c1_many_steps_tolerance(torch_gpu, orc):
     w, p = compile_workload("c1")
     e = engine(p)
