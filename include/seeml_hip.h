@@ -280,6 +280,17 @@ int seeml_hip_gemm_nt(const float* A, const float* B, float* C, uint64_t M, uint
                       uint64_t K, void* stream);
 int seeml_hip_gemm_tn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
                       uint64_t K, void* stream);
+/* seeml_hip_gemm_tn without allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same plan,
+ * kernels and bits as seeml_hip_gemm_tn, but its scratch is a fixed device
+ * array of SEEML_HIP_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends; a shape needing more is rejected with an error before any launch.
+ * It calls no hipMalloc/hipFree. Calls that overlap on one GPU race on the
+ * shared array. */
+#define SEEML_HIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int seeml_hip_gemm_tn_noalloc(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
+                              uint64_t K, void* stream);
 int seeml_hip_gemm_acc_nn(const float* A, const float* B, float* C, uint64_t M, uint64_t N,
                           uint64_t K, float alpha, void* stream);
 int seeml_hip_gemm_nn_q8(const float* A, const int8_t* B, float* C, uint64_t M, uint64_t N,
