@@ -29,6 +29,7 @@ class Workload:
     name: str
     model: Model
     cfg: UpdateConfig
+    teacher: Model | None = None  # distillation losses
     vocab: int = 0            # token models
     classes: int = 0          # xent width
     seq: int = 0
@@ -48,6 +49,31 @@ def mlp_model(d_in=256, hidden=512, d_out=256) -> Model:
         SmfOp("Relu", ["h1b"], "a1"),
         SmfOp("MatMul", ["a1", "w2"], "h2"), SmfOp("AddBias", ["h2", "b2"], "logits"),
     ])
+
+
+def mlp3_model(d_in, h1, h2, d_out, acts=("relu", "gelu", None), biases=(True, True, True)) -> Model:
+    """A three-layer MLP: each layer MatMul, optional AddBias, optional
+    activation (Relu/Gelu/Silu); weights ~N(0, 1/fan_in)."""
+    dims = [(d_in, h1), (h1, h2), (h2, d_out)]
+    T = [Tensor("x", (-1, d_in), const=False)]
+    ops = []
+    prev = "x"
+    for i, ((k, n), act, bias) in enumerate(zip(dims, acts, biases), start=1):
+        sd = 1.0 / math.sqrt(k)
+        T.append(Tensor(f"w{i}", (k, n), std=sd))
+        out = "logits" if i == 3 and not bias and act is None else f"h{i}"
+        ops.append(SmfOp("MatMul", [prev, f"w{i}"], out))
+        prev = out
+        if bias:
+            T.append(Tensor(f"b{i}", (n,), std=sd))
+            out = "logits" if i == 3 and act is None else f"h{i}b"
+            ops.append(SmfOp("AddBias", [prev, f"b{i}"], out))
+            prev = out
+        if act is not None:
+            out = "logits" if i == 3 else f"a{i}"
+            ops.append(SmfOp(act.capitalize(), [prev], out))
+            prev = out
+    return Model("x", "logits", 0, T, ops)
 
 
 def linear_model(d=4096) -> Model:
@@ -120,6 +146,39 @@ def make(name: str) -> Workload:
             batch=32, loss="xent", lora=LoraSpec(rank=8, alpha=16.0, seed=7), lr=1e-3,
             weight_decay=0.01, default_steps=1000), classes=256, in_dim=256,
             description="MLP 256->512->256 + bias/ReLU, xent over 256, LoRA r8 a16, batch 32")
+    # Plans carrying the ABI's remaining instruction kinds, compiled the way
+    # the reference compiler emits them (source/plan/config.h:56-81):
+    #   f1  fused GEMM epilogues (bias+ReLU, GELU alone), per-tensor ClipNorm,
+    #       AdamW under the warmup + cosine LR schedule
+    #   f2  fused bias+SiLU and bias-only epilogues, SGD with ClipNorm
+    #   q1  int8 frozen weights (GemmNNQ8 with a fused SiLU, GemmNNQ8,
+    #       GemmNTQ8 for the input gradient)
+    #   k1  KL distillation against a frozen teacher (KLDistillFwd/Bwd)
+    #   k2  (1-w)*xent + w*KL, with an int8 teacher and student
+    abi = {
+        "f1": dict(acts=("relu", "gelu", None), biases=(True, False, True), targets=("w3",),
+                   cfg=dict(clip_norm=0.05, lr=1e-2, lr_schedule=1, warmup_steps=3,
+                            default_steps=12, min_lr_factor=0.1)),
+        "f2": dict(acts=("silu", None, None), biases=(True, True, True), targets=("w3",),
+                   cfg=dict(optimizer="sgd", clip_norm=0.05, lr=5e-2)),
+        "q1": dict(acts=("silu", "gelu", None), biases=(False, True, True), targets=("w2", "w3"),
+                   cfg=dict(quantize_base=True)),
+        "k1": dict(acts=("relu", "gelu", None), biases=(True, True, True), targets=(),
+                   cfg=dict(loss="kl", temperature=2.0), teacher=True),
+        "k2": dict(acts=("gelu", "silu", None), biases=(True, False, True), targets=(),
+                   cfg=dict(loss="xent_kl", distill_weight=0.3, temperature=1.5,
+                            quantize_base=True), teacher=True),
+    }
+    if name in abi:
+        a = abi[name]
+        d_in, h1, h2, d_out, b = 128, 256, 192, 96, 64
+        model = mlp3_model(d_in, h1, h2, d_out, a["acts"], a["biases"])
+        teacher = mlp3_model(d_in, h1, h2, d_out, ("gelu", "relu", None), (True, True, True)) \
+            if a.get("teacher") else None
+        cfg = UpdateConfig(batch=b, lora=LoraSpec(rank=8, alpha=16.0, seed=7, targets=a["targets"]),
+                           **{"loss": "xent", "default_steps": 100, **a["cfg"]})
+        return Workload(name, model, cfg, teacher=teacher, classes=d_out, in_dim=d_in,
+                        description=f"MLP {d_in}->{h1}->{h2}->{d_out} {a['acts']} {a['cfg']}")
     if name in ("c2", "c2s", "c2dx", "c2sdx"):
         d, b = (4096, 8192) if name in ("c2", "c2dx") else (512, 1024)
         r = 16
@@ -178,6 +237,8 @@ def batch(w: Workload, step: int = 0, seed: int = 7):
     x = rng.standard_normal((b, w.in_dim), dtype=np.float32)
     if w.cfg.loss == "mse":
         y = rng.standard_normal((b, w.out_dim), dtype=np.float32)
+    elif w.cfg.loss == "kl":
+        return x.reshape(-1), None  # no label slot: the teacher is the target
     else:
         y = rng.integers(0, w.classes, b).astype(np.int32)
     return x.reshape(-1), y.reshape(-1)

@@ -197,10 +197,12 @@ class Model:
         return None
 
 
-def build_forward(block: Block, model: Model, inp: Value, weights: dict) -> Value:
+def build_forward(block: Block, model: Model, inp: Value, weights: dict, prefix: str = "") -> Value:
     """BuildForward (parser.cc:12-253): one SIR op per model op in order; a
     constant tensor is declared (sc_mem.weight) at its first use
-    (value_resolver.cc:26-47)."""
+    (value_resolver.cc:26-47). `prefix` names a second graph sharing the
+    input (the distillation teacher, "t::", update_compiler.cc:118): every
+    value and weight id it declares carries it."""
     env = {model.input_name: inp}
 
     def resolve(name):
@@ -210,8 +212,8 @@ def build_forward(block: Block, model: Model, inp: Value, weights: dict) -> Valu
         if t is None or not t.const:
             raise ValueError(f"'{name}' is not a constant tensor in the model")
         op = block.append("sc_mem.weight")
-        v = op.add_result(name, t.dims)
-        weights[name] = (v, t)
+        v = op.add_result(prefix + name, t.dims)
+        weights[prefix + name] = (v, t)
         env[name] = v
         return v
 
@@ -220,40 +222,40 @@ def build_forward(block: Block, model: Model, inp: Value, weights: dict) -> Valu
         k = o.kind
         if k == "MatMul":
             op = block.append("sc_high.matmul", ins)
-            env[o.output] = op.add_result(o.output, (ins[0].shape[0], ins[1].shape[1]))
+            env[o.output] = op.add_result(prefix + o.output, (ins[0].shape[0], ins[1].shape[1]))
         elif k == "AddBias":
             op = block.append("sc_high.add_bias", ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
         elif k in ("Relu", "Gelu", "Silu"):
             op = block.append("sc_high." + k.lower(), ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
         elif k == "Mul":
             op = block.append("sc_high.mul", ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
         elif k == "Embedding":
             op = block.append("sc_high.embedding", ins)
-            env[o.output] = op.add_result(o.output, (ins[0].shape[0], ins[1].shape[1]))
+            env[o.output] = op.add_result(prefix + o.output, (ins[0].shape[0], ins[1].shape[1]))
         elif k == "Add":
             op = block.append("sc_high.add", ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
         elif k == "RmsNorm":
             op = block.append("sc_high.rms_norm", ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
-            op.add_result(o.output + ".rstd", (ins[0].shape[0],))
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
+            op.add_result(prefix + o.output + ".rstd", (ins[0].shape[0],))
         elif k == "Rope":
             op = block.append("sc_high.rope", ins, {"heads": o.attr0, "seq": model.seq_len})
-            env[o.output] = op.add_result(o.output, ins[0].shape)
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
         elif k == "Attention":
             rows = ins[0].shape[0]
             op = block.append("sc_high.attention", ins, {"heads": o.attr0, "seq": model.seq_len})
-            env[o.output] = op.add_result(o.output, ins[0].shape)
-            op.add_result(o.output + ".probs", (rows * o.attr0, model.seq_len))
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
+            op.add_result(prefix + o.output + ".probs", (rows * o.attr0, model.seq_len))
         elif k == "LayerNorm":
             rows = ins[0].shape[0]
             op = block.append("sc_high.layer_norm", ins)
-            env[o.output] = op.add_result(o.output, ins[0].shape)
-            op.add_result(o.output + ".mean", (rows,))
-            op.add_result(o.output + ".rstd", (rows,))
+            env[o.output] = op.add_result(prefix + o.output, ins[0].shape)
+            op.add_result(prefix + o.output + ".mean", (rows,))
+            op.add_result(prefix + o.output + ".rstd", (rows,))
         else:
             raise ValueError(f"unknown model op kind {k}")
     return env[model.output_name]
@@ -286,6 +288,9 @@ def graft_lora(block: Block, spec: LoraSpec) -> list:
             continue
         w = op.operands[1]
         if w.op is None or w.op.mn != "sc_mem.weight":
+            continue
+        # the student graph only (lora_grafter.cc:16-18,38)
+        if w.id.startswith("t::") or op.results[0].id.startswith("t::"):
             continue
         if any(u.mn != "sc_high.matmul" or len(u.operands) != 2 or u.operands[1] is not w
                or u.operands[0] is w for u in block.users(w)):
@@ -455,6 +460,15 @@ def autodiff(block: Block, loss: Value, trainables: list, extra: tuple = ()) -> 
                 raise ValueError("d/dtarget unsupported")
             if N(pred):
                 accumulate(pred, emit1("sc_low.mse_grad", [pred, target, g], pred))
+        elif mn == "sc_high.kl_distill":
+            # dstudent = seed * (p_s - p_t) / (N * T); the teacher is frozen
+            # (autodiff.cc:331-353)
+            s_logits, t_logits = op.operands
+            if N(t_logits):
+                raise ValueError("d/dteacher unsupported")
+            if N(s_logits):
+                accumulate(s_logits, emit1("sc_low.kl_grad", [op.results[1], op.results[2], g],
+                                           s_logits, {"temperature": op.attrs["temperature"]}))
         else:
             raise ValueError(f"no VJP rule for '{mn}'")
     grads = {}
@@ -465,16 +479,140 @@ def autodiff(block: Block, loss: Value, trainables: list, extra: tuple = ()) -> 
     return grads
 
 
-def synthesize_adamw(block: Block, trainables: list, grads: dict) -> None:
-    """OptimizerSynthesizer::Run for AdamW (optimizer.cc:12-57): params in
-    ascending id order, each with zero-init m/v state then the fused step."""
+def synthesize_optimizer(block: Block, trainables: list, grads: dict, kind: str = "adamw",
+                         clip_norm: float = 0.0) -> None:
+    """OptimizerSynthesizer::Run (compiler/analysis/calculus/optimizer.cc:
+    12-57): params in ascending id order; per parameter an optional
+    per-tensor ClipNorm of its gradient, then the SGD step, or AdamW's
+    zero-init m/v state and the fused step."""
     for p in sorted(trainables, key=lambda v: v.id.encode()):
         g = grads[id(p)]
+        if clip_norm > 0.0:
+            block.append("sc_low.clip_norm", [g], {"max_norm": float(np.float32(clip_norm))})
+        if kind == "sgd":
+            block.append("sc_low.sgd_step", [p, g])
+            continue
         m = block.append("sc_mem.param", [], {"trainable": 0, "init": "zeros"}).add_result(
             p.id + ".adam_m", p.shape)
         v = block.append("sc_mem.param", [], {"trainable": 0, "init": "zeros"}).add_result(
             p.id + ".adam_v", p.shape)
         block.append("sc_low.adamw_step", [p, g, m, v])
+
+
+# ------------------------------------------------- quantization + fusion ---
+
+_WEIGHT_SWEEP_GRAIN = 65536  # kWeightSweepGrain (reviewer/quantization.h:26)
+
+
+def quant_scale(values: np.ndarray):
+    """SelectQuantizedWeights' per-tensor scale (reviewer/quantization.cc:
+    29-52): max|w| / 127 in f32 (1 for an all-zero tensor), or None when the
+    scale is not a normal float (such a tensor stays f32)."""
+    max_abs = np.float32(np.max(np.abs(values))) if values.size else np.float32(0.0)
+    scale = np.float32(max_abs / np.float32(127.0)) if max_abs > 0 else np.float32(1.0)
+    if not np.isfinite(scale) or scale < np.finfo(np.float32).tiny:
+        return None
+    return scale
+
+
+def quantize_int8(values: np.ndarray, scale) -> np.ndarray:
+    """The binder's int8 pack (arena_binder.cc:135-160): clamp(round(w /
+    scale), -127, 127), with the quotient rounded to f32 and std::round's
+    halves away from zero."""
+    q = (values.astype(np.float32) / np.float32(scale)).astype(np.float64)
+    r = np.sign(q) * np.floor(np.abs(q) + 0.5)
+    return np.clip(r, -127.0, 127.0).astype(np.int8)
+
+
+def select_quantized(block: Block) -> list:
+    """The weights SelectQuantizedWeights considers (quantization.cc:13-28):
+    every frozen weight whose every reader is a forward or input-gradient
+    GEMM taking it as the right operand only."""
+    out = []
+    for op in block.ops:
+        if op.mn != "sc_mem.weight":
+            continue
+        v = op.results[0]
+        users = block.users(v)
+        if all(u.mn in ("sc_high.matmul", "sc_low.matmul_nt") and len(u.operands) == 2
+               and u.operands[1] is v and u.operands[0] is not v for u in users):
+            out.append(v)
+    return out
+
+
+_EPILOGUE_ACT = {"sc_high.relu": "relu", "sc_high.gelu": "gelu", "sc_high.silu": "silu"}
+
+
+def _uses(block: Block, v: Value) -> int:
+    return sum(1 for op in block.ops for o in op.operands if o is v)
+
+
+def _replace_uses(block: Block, old: Value, new: Value) -> None:
+    for op in block.ops:
+        op.operands = [new if o is old else o for o in op.operands]
+
+
+def fuse_epilogues(block: Block, quantized: set, protected: set) -> list:
+    """GemmEpilogueFuser::Run (algebra/epilogue_fuser.cc:36-118): a forward
+    GEMM whose only reader is an AddBias (and that one's only reader an
+    activation), or an activation, absorbs them into its epilogue; the
+    orphaned ops are returned for the DCE sweep. A bias declared after the
+    GEMM moves before it; a bias never rides a quantized GEMM."""
+    fused_away = []
+    for gemm in list(block.ops):
+        if gemm.mn != "sc_high.matmul" or len(gemm.operands) != 2 or len(gemm.results) != 1:
+            continue
+        c = gemm.results[0]
+        if _uses(block, c) != 1 or id(c) in protected:
+            continue
+        user = next(op for op in block.ops if any(o is c for o in op.operands))
+        if (user.mn == "sc_high.add_bias" and len(user.operands) == 2 and user.operands[0] is c
+                and len(user.results) == 1 and id(gemm.operands[1]) not in quantized):
+            y, bias = user.results[0], user.operands[1]
+            bdef = bias.op
+            if bdef is not None and block.ops.index(bdef) > block.ops.index(gemm):
+                if not bdef.mn.startswith("sc_mem."):
+                    continue
+                block.ops.remove(bdef)
+                block.ops.insert(block.ops.index(gemm), bdef)
+            act = None
+            if _uses(block, y) == 1:
+                act = next(op for op in block.ops if any(o is y for o in op.operands))
+            name = (_EPILOGUE_ACT.get(act.mn) if act is not None and len(act.operands) == 1
+                    and len(act.results) == 1 else None)
+            if name and id(y) not in protected and id(act.results[0]) not in protected:
+                gemm.operands.append(bias)
+                gemm.attrs["epilogue_act"] = name
+                _replace_uses(block, act.results[0], c)
+                fused_away += [user, act]
+            elif id(y) not in protected:
+                gemm.operands.append(bias)
+                _replace_uses(block, y, c)
+                fused_away.append(user)
+        elif (user.mn in _EPILOGUE_ACT and len(user.operands) == 1 and len(user.results) == 1
+              and id(user.results[0]) not in protected):
+            gemm.attrs["epilogue_act"] = _EPILOGUE_ACT[user.mn]
+            _replace_uses(block, user.results[0], c)
+            fused_away.append(user)
+    return fused_away
+
+
+_EFFECTFUL = ("sc_low.clip_norm", "sc_low.sgd_step", "sc_low.adamw_step", "sc_low.gemm_acc")
+
+
+def dead_code_elimination(block: Block, roots: set) -> int:
+    """DeadCodeElimination::Run (updater/dce.cc:23-45): a backward sweep
+    removing every op whose results nothing reads and no root names;
+    storage declarations and in-place updates are kept."""
+    removed = 0
+    for op in reversed(list(block.ops)):
+        if op.mn.startswith("sc_mem.") or op.mn in _EFFECTFUL:
+            continue
+        if any(_uses(block, r) or id(r) in roots for r in op.results):
+            continue
+        block.ops.remove(op)
+        removed += 1
+    return removed
 
 
 def build_merge(adapters: list):
@@ -540,8 +678,14 @@ def linear_scan(block: Block, base: int, bound: dict, pinned: set, refs: dict) -
 
 # --------------------------------------------------------------- lowering ---
 
-def lower(ops: list, ref) -> list:
-    """LowerOps (instruction_lowering.cc:18-350): one 64-byte word per op."""
+_ACT_CODE = {"relu": 1, "gelu": 2, "silu": 3}  # EpilogueAct (instruction.h:124)
+
+
+def lower(ops: list, ref, quant: dict | None = None) -> list:
+    """LowerOps (instruction_lowering.cc:18-350): one 64-byte word per op.
+    `quant` maps a quantized weight's value id to its dequant scale: GEMMs
+    reading it as B take the q8 opcodes with the scale in in[3]."""
+    quant = quant or {}
     words = []
     for op in ops:
         mn = op.mn
@@ -561,11 +705,26 @@ def lower(ops: list, ref) -> list:
 
         if mn in ("sc_high.matmul", "sc_low.matmul_nt", "sc_low.matmul_tn"):
             a = op.operands[0]
-            ins["opcode"] = {"sc_high.matmul": OP["GemmNN"], "sc_low.matmul_nt": OP["GemmNT"],
-                             "sc_low.matmul_tn": OP["GemmTN"]}[mn]
+            scale = quant.get(id(op.operands[1])) if mn != "sc_low.matmul_tn" else None
+            if scale is None:
+                ins["opcode"] = {"sc_high.matmul": OP["GemmNN"], "sc_low.matmul_nt": OP["GemmNT"],
+                                 "sc_low.matmul_tn": OP["GemmTN"]}[mn]
+            else:
+                ins["opcode"] = OP["GemmNNQ8"] if mn == "sc_high.matmul" else OP["GemmNTQ8"]
+                i[3] = f32_bits(scale)
             i[0], i[1], i[2] = ref(a), ref(op.operands[1]), ref(R[0])
             o[0], o[1] = R[0].shape
             o[2] = a.shape[0] if mn == "sc_low.matmul_tn" else a.shape[1]
+            # fused epilogue (plan v5): a third operand is the bias, riding
+            # in[3]; "epilogue_act" sets the activation bits
+            # (instruction_lowering.cc:79-103)
+            bias = mn == "sc_high.matmul" and len(op.operands) == 3
+            if bias and scale is not None:
+                raise ValueError(f"fused bias on a quantized GEMM ('{R[0].id}')")
+            if bias:
+                i[3] = ref(op.operands[2])
+            act = _ACT_CODE.get(op.attrs.get("epilogue_act"), 0)
+            ins["flags"] = (1 if bias else 0) | (act << 1)
         elif mn == "sc_low.gemm_acc":
             a, b = op.operands[0], op.operands[1]
             ins["opcode"] = OP["GemmAccNN"]
@@ -663,6 +822,26 @@ def lower(ops: list, ref) -> list:
             ins["opcode"] = OP["MseBwd"]
             i[0], i[1], i[2], i[3] = ref(op.operands[0]), ref(op.operands[1]), ref(op.operands[2]), ref(R[0])
             o[0] = R[0].volume
+        elif mn == "sc_high.kl_distill":
+            s_logits = op.operands[0]
+            ins["opcode"] = OP["KLDistillFwd"]
+            i[0], i[1], i[2], i[3] = ref(s_logits), ref(op.operands[1]), ref(R[0]), ref(R[1])
+            o[0], o[1] = ref(R[2]), pack32(*s_logits.shape)
+            o[2] = f32_bits(op.attrs.get("temperature", 1.0))
+        elif mn == "sc_low.kl_grad":
+            ins["opcode"] = OP["KLDistillBwd"]
+            for j in range(3):
+                i[j] = ref(op.operands[j])
+            i[3] = ref(R[0])
+            o[0], o[1] = pack32(*R[0].shape), f32_bits(op.attrs.get("temperature", 1.0))
+        elif mn == "sc_low.clip_norm":
+            ins["opcode"] = OP["ClipNorm"]
+            i[0], i[1] = ref(op.operands[0]), f32_bits(op.attrs.get("max_norm", 0.0))
+            o[0] = op.operands[0].volume
+        elif mn == "sc_low.sgd_step":
+            ins["opcode"] = OP["SgdStep"]
+            i[0], i[1] = ref(op.operands[0]), ref(op.operands[1])
+            o[0] = op.operands[0].volume
         elif mn == "sc_low.adamw_step":
             ins["opcode"] = OP["AdamWStep"]
             for j in range(4):
@@ -733,6 +912,15 @@ class UpdateConfig:
     # interior layer (the compiler prunes it for the input layer,
     # autodiff.cc:76-82). dX is pinned like the loss, so it keeps a slot.
     input_grad: bool = False
+    # source/plan/config.h:25-81: optimizer kind and per-tensor gradient
+    # clipping, distillation (loss "kl" or "xent_kl" against a teacher
+    # model), int8 frozen weights, GEMM epilogue fusion.
+    optimizer: str = "adamw"      # adamw | sgd
+    clip_norm: float = 0.0
+    temperature: float = 2.0
+    distill_weight: float = 0.5
+    quantize_base: bool = False
+    fuse_epilogues: bool = True
 
 
 @dataclass
@@ -773,8 +961,21 @@ def _fill_weights(out: np.ndarray, t: Tensor, seed: int, index: int, pool) -> li
     return [pool.submit(fill, c) for c in range(n_chunks)]
 
 
-def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: bool = True) -> CompiledPlan:
+def _fill_now(out: np.ndarray, t: Tensor, seed: int, index: int) -> None:
+    """_fill_weights run synchronously (the same values, chunk by chunk)."""
+    class _Now:
+        def submit(self, fn, *a):
+            fn(*a)
+            return None
+    _fill_weights(out, t, seed, index, _Now())
+
+
+def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: bool = True,
+                   teacher: Model | None = None) -> CompiledPlan:
     """UpdateCompiler::CompileImpl restated (update_compiler.cc:43-602)."""
+    wants_teacher = cfg.loss in ("kl", "xent_kl")
+    if wants_teacher and teacher is None:
+        raise ValueError("the selected loss requires a teacher model")
     block = Block()
     batch = cfg.batch
     if cfg.token_input:
@@ -787,18 +988,48 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     weights = {}
     out = build_forward(block, model, inp, weights)
     out_dim = out.shape[1]
+    t_out = None
+    if wants_teacher:
+        t_out = build_forward(block, teacher, inp, weights, prefix="t::")
+        if t_out.shape[1] != out_dim:
+            raise ValueError("teacher output dimensionality mismatch")
     # --- loss graft (update_compiler.cc:132-199)
-    if cfg.loss == "xent":
-        labels = block.add_argument((batch,), "i32")
-        label_kind, label_bytes = 1, batch * 4
-        op = block.append("sc_high.softmax_xent", [out, labels])
-        loss = op.add_result("loss.xent", ())
+    labels, label_kind, label_bytes = None, 0, 0
+
+    def make_xent():
+        lab = block.add_argument((batch,), "i32")
+        op = block.append("sc_high.softmax_xent", [out, lab])
+        l = op.add_result("loss.xent", ())
         op.add_result("loss.xent_probs", (batch, out_dim))
+        return lab, l
+
+    def make_kl():
+        op = block.append("sc_high.kl_distill", [out, t_out],
+                          {"temperature": float(np.float32(cfg.temperature))})
+        l = op.add_result("loss.kl", ())
+        op.add_result("loss.kl_ps", (batch, out_dim))
+        op.add_result("loss.kl_pt", (batch, out_dim))
+        return l
+
+    if cfg.loss == "xent":
+        labels, loss = make_xent()
+        label_kind, label_bytes = 1, batch * 4
     elif cfg.loss == "mse":
         labels = block.add_argument((batch, out_dim), "f32")
         label_kind, label_bytes = 2, batch * out_dim * 4
         op = block.append("sc_high.mse", [out, labels])
         loss = op.add_result("loss.mse", ())
+    elif cfg.loss == "kl":
+        loss = make_kl()
+    elif cfg.loss == "xent_kl":
+        labels, xent = make_xent()
+        label_kind, label_bytes = 1, batch * 4
+        kl = make_kl()
+        w = np.float32(cfg.distill_weight)
+        wx = block.append("sc_high.scale", [xent], {"alpha": float(np.float32(1.0) - w)}).add_result(
+            "loss.xent_w", ())
+        wk = block.append("sc_high.scale", [kl], {"alpha": float(w)}).add_result("loss.kl_w", ())
+        loss = block.append("sc_high.add", [wx, wk]).add_result("loss.total", ())
     else:
         raise ValueError(cfg.loss)
     adapters = graft_lora(block, cfg.lora)
@@ -807,8 +1038,31 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     if cfg.input_grad and cfg.token_input:
         raise ValueError("input_grad needs a float input")
     grads = autodiff(block, loss, trainables, (inp,) if cfg.input_grad else ())
-    synthesize_adamw(block, trainables, grads)
+    synthesize_optimizer(block, trainables, grads, cfg.optimizer, cfg.clip_norm)
     merge_block, aliases, merge_outputs = build_merge(adapters)
+
+    # --- frozen-weight quantization (update_compiler.cc:272-285): the
+    # selected weights' values are drawn here, because the scale the q8
+    # GEMMs carry is their max |w| / 127.
+    weight_index = {name: k for k, name in enumerate(weights)}
+    quant, packed = {}, {}
+    if cfg.quantize_base:
+        for v in select_quantized(block):
+            vals = np.empty(v.volume, np.float32)
+            _fill_now(vals, weights[v.id][1], cfg.weight_seed, weight_index[v.id])
+            sc = quant_scale(vals)
+            if sc is not None:
+                quant[id(v)] = sc
+                packed[v.id] = quantize_int8(vals, sc)
+    # --- epilogue fusion, then the DCE sweep (update_compiler.cc:287-336)
+    protected = {id(loss)} | {id(g) for g in grads.values()}
+    if cfg.fuse_epilogues:
+        fused_away = fuse_epilogues(block, set(quant), protected)
+        if fused_away:
+            dead = {id(op) for op in fused_away}
+            primal_ops = [op for op in primal_ops if id(op) not in dead]
+    roots = set(protected) | {id(r) for op in primal_ops for r in op.results}
+    dead_code_elimination(block, roots)
 
     # --- segmented arena binding (arena_binder.cc:102-185)
     refs = {}
@@ -833,7 +1087,8 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
             off = align_up(rodata_size)
             rodata_offsets[v.id] = off
             refs[id(v)] = off | RODATA_BIT
-            rodata_size = off + v.nbytes
+            # a quantized weight packs as int8: one byte per element
+            rodata_size = off + (v.volume if v.id in packed else v.nbytes)
     pinned = {id(loss)} | {id(g) for g in grads.values()}
     arena = linear_scan(block, align_up(io_end), refs, pinned, refs)
     merge_refs = {mid: refs[id(orig)] for mid, orig in aliases.items()}
@@ -847,8 +1102,8 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     def ref_merge(v):
         return merge_refs[id(v)]
 
-    train_words = lower(block.ops, ref_train)
-    eval_words = lower(primal_ops, ref_train)
+    train_words = lower(block.ops, ref_train, quant)
+    eval_words = lower(primal_ops, ref_train, quant)
     merge_words = lower(merge_block.ops, ref_merge)
 
     # --- persistent image (update_compiler.cc:415-442)
@@ -861,6 +1116,8 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     # --- rodata layout (values are written straight into the blob below)
     smf_offsets, smf_cursor = {}, 0
     for name, (v, t) in weights.items():
+        if name.startswith("t::"):
+            continue  # the teacher's weights live in its own model file
         smf_offsets[name] = smf_cursor
         smf_cursor = align_up(smf_cursor + v.nbytes)
 
@@ -875,8 +1132,10 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     h.update(magic=0x55454553, version=7, arena_size=align_up(arena),
              persistent_size=persistent_size, input_ref=refs[id(inp)],
              input_floats=batch if cfg.token_input else batch * inp.shape[1],
-             label_ref=refs[id(labels)], label_bytes=label_bytes, label_kind=label_kind,
-             optimizer_kind=1, loss_ref=refs[id(loss)], lr=cfg.lr, beta1=cfg.beta1,
+             label_ref=refs[id(labels)] if labels is not None else NULL_REF,
+             label_bytes=label_bytes, label_kind=label_kind,
+             optimizer_kind=0 if cfg.optimizer == "sgd" else 1, clip_norm=cfg.clip_norm,
+             loss_ref=refs[id(loss)], lr=cfg.lr, beta1=cfg.beta1,
              beta2=cfg.beta2, eps=cfg.eps, weight_decay=cfg.weight_decay, batch=batch,
              default_steps=cfg.default_steps, lr_schedule=cfg.lr_schedule,
              warmup_steps=cfg.warmup_steps, min_lr_factor=cfg.min_lr_factor,
@@ -922,6 +1181,9 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
         futs = []
         for index, (name, (v, t)) in enumerate(weights.items()):
             off0 = h["rodata_offset"] + rodata_offsets[name]
+            if name in packed:
+                view[off0:off0 + v.volume] = packed[name].view(np.uint8)
+                continue
             futs += _fill_weights(view[off0:off0 + v.nbytes].view(np.float32), t,
                                   cfg.weight_seed, index, pool)
         for f in futs:

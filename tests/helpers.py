@@ -53,7 +53,37 @@ def verify_plan(blob: bytes):
 
 def compile_workload(name: str, hash_fn=None):
     w = configs.make(name)
-    return w, planner.compile_update(w.model, w.cfg, hash_fn=hash_fn)
+    return w, planner.compile_update(w.model, w.cfg, hash_fn=hash_fn, teacher=w.teacher)
+
+
+def append_train_instructions(plan, words: list, extra_arena: int = 0):
+    """A copy of compiled `plan` with the 64-byte instruction words `words`
+    appended to its train program and the arena grown by `extra_arena`
+    bytes (room for their outputs), re-sealed. Returns (blob, header)."""
+    h = dict(plan.header)
+    n = len(words)
+    old = bytes(plan.blob)
+    t_end = h["train_instr_offset"] + 64 * h["train_instr_count"]
+    blob = bytearray(old[:t_end] + b"".join(words) + old[t_end:])
+    for k in ("merge_instr_offset", "eval_instr_offset", "rodata_offset", "persist_init_offset",
+              "emit_table_offset"):
+        h[k] += 64 * n
+    h["train_instr_count"] += n
+    h["arena_size"] = planner.align_up(h["arena_size"] + extra_arena)
+    h["plan_hash"] = 0
+    planner.HEADER.pack_into(blob, 0, *[h[k] for k, _ in planner.HEADER_FIELDS])
+    buf = (C.c_uint8 * len(blob)).from_buffer(blob)
+    h["plan_hash"] = _lib.lib().seeml_hip_plan_self_hash(buf, len(blob), planner.PLAN_HASH_OFFSET)
+    del buf
+    struct.pack_into("<Q", blob, planner.PLAN_HASH_OFFSET, h["plan_hash"])
+    return blob, h
+
+
+class PlanView:
+    """The fields HostPlanRunner reads from a compiled plan, for a raw blob."""
+
+    def __init__(self, blob, header):
+        self.blob, self.header = blob, header
 
 
 class HostPlanRunner:

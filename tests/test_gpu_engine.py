@@ -529,3 +529,98 @@ def test_rope_through_the_angle_table_is_the_standalone_kernel(torch_gpu):
         assert rc == 0
         assert np.array_equal(got.view(np.uint32), out.cpu().numpy().view(np.uint32)), opname
     e.close()
+
+
+# ---- plans carrying the ABI's remaining instruction kinds -----------------
+
+ABI_PLANS = [("f1", 14), ("f2", 4), ("q1", 3), ("k1", 3), ("k2", 3)]
+
+
+@pytest.mark.parametrize("name,steps", ABI_PLANS)
+def test_abi_plan_parity_vs_oracle(torch_gpu, orc, name, steps):
+    """Plans whose instructions the five BASELINE configs never emit run
+    through the engine's dispatch: GemmNN with fused bias/activation flags
+    (instruction.h:106-134, gemm.cc:145-169), GemmNNQ8/NTQ8 on int8 rodata
+    (gemm.cc:211-228), ClipNorm and SGD (optimizer.cc:17-42), KL
+    distillation (loss.cc:99-140) and the warmup + cosine LR schedule
+    (update_engine.cc:515-534; f1's 14 steps cross the warmup, the cosine
+    decay and the floor). Losses per step, the trained state, the eval loss
+    and the merge deltas agree with the oracle running the same plan bytes;
+    the graph equals eager dispatch bit for bit."""
+    import struct
+    from seeml_amd import PROGRAM_EVAL
+    w, p = compile_workload(name)
+    r = HostPlanRunner(p, orc)
+    runs = []
+    for use_graph in (True, False):
+        e = engine(p, use_graph=use_graph)
+        losses = []
+        for s in range(steps):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+            if use_graph:
+                lr = r.train_step(x, y)
+                assert abs(losses[-1] - lr) <= TOL_STEP * max(abs(lr), 1e-3), (s, losses[-1], lr)
+        state = persistent(e, p)
+        if use_graph:
+            tol = TOL_STEP if steps <= 5 else TOL_100
+            assert rel_err(state, persistent(r, p)) <= tol
+            x, y = configs.batch(w, 99)
+            e.stage(x, y)
+            e.run(PROGRAM_EVAL)
+            r.stage(x, y)
+            r.run(2)
+            assert abs(e.loss() - r.loss()) <= TOL_STEP * max(abs(r.loss()), 1e-3)
+            e.run_merge()
+            r.run(1)
+            h = p.header
+            for i in range(h["emit_count"]):
+                _, nbytes, off = struct.unpack_from("<3Q", p.blob, h["emit_table_offset"] + 24 * i)
+                got, want = e.read(off, nbytes // 4), r.read(off, nbytes // 4)
+                assert rel_err(got, want) <= (TOL_STEP if steps <= 5 else TOL_100), i
+        runs.append((np.array(losses, np.float32), state))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+
+
+def test_nop_copy_reduce_rows_fill_through_the_engine(torch_gpu, orc):
+    """Nop, Copy, ReduceRows and Fill (elementwise.cc:55-78) appended to a
+    compiled plan's train program, reading the trained LoRA A and writing
+    past the compiled arena: the engine's outputs equal the oracle's bit for
+    bit (the kernels round per element / sum rows in the reference's order)."""
+    from helpers import PlanView, append_train_instructions, instr
+    w, p = compile_workload("f2")
+    _, aref, _, (K, M), _ = p.adapters[0]
+    rank = w.cfg.lora.rank
+    base = planner.align_up(p.header["arena_size"])
+    n = K * rank
+    copy_out, rows_out, fill_out = base, planner.align_up(base + 4 * n), planner.align_up(base + 4 * n) + 256
+    words = [instr(planner.OP["Nop"]),
+             instr(planner.OP["Copy"], (aref, copy_out), (n,)),
+             instr(planner.OP["ReduceRows"], (aref, rows_out), (K, rank)),
+             instr(planner.OP["Fill"], (fill_out, planner.f32_bits(2.5)), (37,))]
+    blob, h = append_train_instructions(p, words, extra_arena=4 * n + 256 + 256)
+    view = PlanView(blob, h)
+    from seeml_amd import DeviceUpdateEngine
+    r = HostPlanRunner(view, orc)
+    for use_graph in (True, False):
+        e = DeviceUpdateEngine(blob, use_graph=use_graph)
+        rr = HostPlanRunner(view, orc)
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            lg, lr = e.train_step(x, y), rr.train_step(x, y)
+            assert abs(lg - lr) <= TOL_STEP * max(abs(lr), 1e-3)
+        a_got = e.read(aref, n)
+        for ref, cnt in ((copy_out, n), (rows_out, rank), (fill_out, 37)):
+            got, mine = e.read(ref, cnt), None
+            if ref == copy_out:
+                mine = a_got
+            elif ref == rows_out:
+                mine = np.zeros(rank, np.float32)
+                orc.reduce_rows(np.ascontiguousarray(a_got), mine, K, rank)
+            else:
+                mine = np.full(37, 2.5, np.float32)
+            assert np.array_equal(got.view(np.uint32), mine.view(np.uint32)), (use_graph, ref)
+        e.close()
+    del r

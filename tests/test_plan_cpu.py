@@ -160,7 +160,8 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("name,steps", [("c1", 3), ("c3s", 2), ("c5s", 2), ("c2s", 2), ("c2sdx", 2),
-                                        ("c4m", 1)])
+                                        ("c4m", 1), ("f1", 14), ("f2", 3), ("q1", 3), ("k1", 2),
+                                        ("k2", 2)])
 def test_oracle_dispatch_bitwise_equals_reference_dispatch(orc, ref, name, steps):
     """orc_execute (the C restatement) and ref_execute (the reference's own
     kernels) run the same compiled plan for several steps: every arena byte
@@ -190,3 +191,117 @@ def test_lora_init_matches_counter_randn_statistics():
     assert abs(float(a.mean())) < 0.01 and abs(float(a.std()) - 1.0) < 0.01
     # element j depends only on (seed, j): a prefix is stable
     assert np.array_equal(planner.counter_randn(7, 100), a[:100])
+
+
+# ---- plans carrying the ABI's remaining instruction kinds -----------------
+
+def _kinds(p):
+    out = collections.Counter()
+    for prog in (p.train, p.eval, p.merge):
+        for ins in prog:
+            out[(planner.OP_NAME[ins["opcode"]], ins["flags"])] += 1
+    return out
+
+
+def test_abi_workloads_carry_every_remaining_instruction_kind():
+    """The compiler restatement emits what the reference compiler emits for
+    these configs (source/plan/config.h:56-81): fused GEMM epilogues with
+    every bias/activation combination the fuser forms (epilogue_fuser.cc:
+    55-112; flags per instruction.h:106-134), q8 GEMMs with the scale in
+    in[3] and an activation-only epilogue, ClipNorm before each optimizer
+    step, SGD, the KL-distillation pair, and the LR schedule header."""
+    seen = collections.Counter()
+    for n in ("f1", "f2", "q1", "k1", "k2"):
+        w, p = compile_workload(n)
+        assert verify_plan(bytes(p.blob)) == (0, ""), n
+        seen.update(_kinds(p))
+    for flags in (1, 3, 4, 5, 7):   # bias; bias+relu; gelu; bias+gelu; bias+silu
+        assert seen[("GemmNN", flags)] > 0, flags
+    assert seen[("GemmNNQ8", 6)] > 0 and seen[("GemmNNQ8", 0)] > 0 and seen[("GemmNTQ8", 0)] > 0
+    for op in ("ClipNorm", "SgdStep", "KLDistillFwd", "KLDistillBwd"):
+        assert seen[(op, 0)] > 0, op
+    w, p = compile_workload("f1")
+    assert (p.header["lr_schedule"], p.header["warmup_steps"], p.header["default_steps"]) == (1, 3, 12)
+    # ClipNorm precedes each parameter's optimizer step (optimizer.cc:24-30)
+    names = [planner.OP_NAME[i["opcode"]] for i in p.train]
+    steps = [k for k, nm in enumerate(names) if nm == "AdamWStep"]
+    assert all(names[k - 1] == "ClipNorm" for k in steps)
+    w, p = compile_workload("f2")
+    assert p.header["optimizer_kind"] == 0
+    w, p = compile_workload("k1")
+    assert p.header["label_kind"] == 0 and p.header["label_ref"] == NULL
+
+
+def test_fused_epilogue_plans_equal_the_unfused_plan_bitwise(orc):
+    """Fusion changes memory traffic, never bits (instruction.h:106-112): the
+    same model compiled with and without fuse_epilogues trains to the same
+    loss and adapter bits on the oracle."""
+    for n in ("f1", "f2"):
+        w = configs.make(n)
+        fused = planner.compile_update(w.model, w.cfg)
+        cfg = planner.UpdateConfig(**{**w.cfg.__dict__, "fuse_epilogues": False})
+        plain = planner.compile_update(w.model, cfg)
+        assert len(fused.train) < len(plain.train)
+        a, b = HostPlanRunner(fused, orc), HostPlanRunner(plain, orc)
+        for s in range(4):
+            x, y = configs.batch(w, s)
+            la, lb = a.train_step(x, y), b.train_step(x, y)
+            assert np.float32(la).view(np.uint32) == np.float32(lb).view(np.uint32)
+        n_p = fused.header["persistent_size"] // 4
+        assert np.array_equal(a.read(0, n_p).view(np.uint32), b.read(0, n_p).view(np.uint32))
+
+
+def test_int8_pack_known_answers():
+    """The binder's per-tensor symmetric pack (arena_binder.cc:135-160) and
+    the quantizer's scale (reviewer/quantization.cc:29-52): halves round
+    away from zero (std::round), values clamp to [-127, 127], an all-zero
+    tensor takes scale 1, and a subnormal scale deselects the tensor."""
+    vals = np.array([0.0, 1.27, -1.27, 0.005, -0.005, 0.015, 0.6349999, 2.0], np.float32)
+    sc = planner.quant_scale(vals)
+    assert sc == np.float32(np.float32(2.0) / np.float32(127.0))
+    q = planner.quantize_int8(vals, np.float32(0.01))
+    assert list(q) == [0, 127, -127, 1, -1, 2, 63, 127]
+    assert planner.quant_scale(np.zeros(5, np.float32)) == np.float32(1.0)
+    assert planner.quant_scale(np.full(3, 1e-37, np.float32)) is None
+    # a q8 plan's int8 rodata dequantizes back within half a step
+    w, p = compile_workload("q1")
+    INV = {v: k for k, v in planner.OP.items()}
+    q8 = [i for i in p.train if INV[i["opcode"]] == "GemmNNQ8"]
+    assert q8 and all(np.array([i["inp"][3]], np.uint64).astype(np.uint32).view(np.float32)[0] > 0
+                      for i in q8)
+
+
+@pytest.mark.parametrize("lr,warmup,horizon,floor", [(0.1, 10, 100, 0.1), (1e-2, 3, 12, 0.1),
+                                                     (1e-3, 0, 50, 0.0), (5e-4, 20, 10, 0.25)])
+def test_backend_effective_lr_equals_the_oracle(orc, lr, warmup, horizon, floor):
+    """seeml_hip_effective_lr (the scalar the engine uploads each step) reads
+    the schedule from a plan header and equals the oracle's restatement of
+    UpdateEngine::EffectiveLr (update_engine.cc:515-534) bit for bit at every
+    step, with the reference's boundary behaviour (update_engine_test.cc:
+    811-841): the warmup ramp, exactly lr at the warmup boundary, monotone
+    cosine decay, the floor at the horizon and beyond."""
+    import ctypes as C
+    h = dict((n, 0) for n, _ in planner.HEADER_FIELDS)
+    h.update(lr=lr, lr_schedule=1, warmup_steps=warmup, default_steps=horizon,
+             min_lr_factor=floor)
+    raw = planner.HEADER.pack(*[h[n] for n, _ in planner.HEADER_FIELDS])
+    buf = (C.c_uint8 * len(raw)).from_buffer_copy(raw)
+    L = _lib.lib()
+    got = np.array([L.seeml_hip_effective_lr(buf, s) for s in range(1, 3 * horizon + 30)],
+                   np.float32)
+    want = np.array([orc.effective_lr(lr, 1, warmup, horizon, floor, s)
+                     for s in range(1, 3 * horizon + 30)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    base, fl = np.float32(lr), np.float32(lr) * np.float32(floor)
+    if warmup:
+        assert got[0] == np.float32(base * np.float32(1) / np.float32(warmup))
+        assert got[warmup - 1] == base
+    if horizon > warmup:
+        decay = got[warmup:horizon - 1]
+        assert np.all(np.diff(decay) <= 0) and np.all(decay < base) and np.all(decay > fl)
+        assert got[horizon - 1] == fl
+    assert np.all(got[max(horizon, warmup):] == fl)
+    h["lr_schedule"] = 0
+    raw0 = planner.HEADER.pack(*[h[n] for n, _ in planner.HEADER_FIELDS])
+    buf0 = (C.c_uint8 * len(raw0)).from_buffer_copy(raw0)
+    assert L.seeml_hip_effective_lr(buf0, 7) == np.float32(lr)
