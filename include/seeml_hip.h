@@ -96,6 +96,11 @@ uint64_t seeml_hip_get_step(const seeml_hip_engine* e);
 /* Replays a program (Execute / ExecuteTrainProgram, update_engine.cc:278-304)
  * asynchronously on the engine stream. */
 int seeml_hip_run(seeml_hip_engine* e, int program);
+/* ExecuteRange (update_engine.cc:306-509): instructions [begin, end) of
+ * `program`, each dispatched exactly once, eagerly (no fusion), in plan
+ * order on the engine stream. Instruction-by-instruction replay for
+ * per-instruction checks and probes. */
+int seeml_hip_run_range(seeml_hip_engine* e, int program, uint64_t begin, uint64_t end);
 int seeml_hip_sync(seeml_hip_engine* e);
 /* LossValue (update_engine.cc:511-513): synchronizes, then reads the f32 at
  * the plan's loss_ref. */

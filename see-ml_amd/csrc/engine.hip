@@ -649,6 +649,19 @@ class Engine {
     return Status::Ok();
   }
 
+  // ExecuteRange (update_engine.cc:306-509) over instructions [begin, end)
+  // of `program`: each dispatched once, eagerly (no fusion), in plan order
+  // on the engine stream.
+  Status RunRange(int program, size_t begin, size_t end) {
+    if (program < 0 || program > 2 || begin > end || end > plan_.program[program].size())
+      return Status::Fail(kUnitEngine, "instruction range out of bounds");
+    if (Status s = EnsureWorkspace(program); !s) return s;
+    const Ctx c = MakeCtx();
+    for (size_t i = begin; i < end; ++i)
+      if (Status s = Dispatch(program, i, c); !s) return s;
+    return Status::Ok();
+  }
+
   // Runs of consecutive AdamWStep instructions whose operands are pairwise
   // disjoint (one per LoRA tensor, optimizer.cc:15-20) launch as one
   // multi-tensor kernel in the captured graph. Order-independent by
@@ -2229,6 +2242,9 @@ int seeml_hip_set_step(seeml_hip_engine* e, uint64_t step) { return Ret(e, e->im
 uint64_t seeml_hip_get_step(const seeml_hip_engine* e) { return e->impl.step_; }
 
 int seeml_hip_run(seeml_hip_engine* e, int program) { return Ret(e, e->impl.Run(program)); }
+int seeml_hip_run_range(seeml_hip_engine* e, int program, uint64_t begin, uint64_t end) {
+  return Ret(e, e->impl.RunRange(program, begin, end));
+}
 
 int seeml_hip_sync(seeml_hip_engine* e) {
   return Ret(e, seeml_hip::HipOk(hipStreamSynchronize(e->impl.stream_), "sync"));

@@ -93,6 +93,10 @@ class DeviceUpdateEngine:
     def run(self, program: int = PROGRAM_TRAIN):
         self._check(self._L.seeml_hip_run(self._h, program), "run")
 
+    def run_range(self, program: int, begin: int, end: int):
+        """Instructions [begin, end) of `program`, each once, eagerly."""
+        self._check(self._L.seeml_hip_run_range(self._h, program, begin, end), "run_range")
+
     def sync(self):
         self._check(self._L.seeml_hip_sync(self._h), "sync")
 

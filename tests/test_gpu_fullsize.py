@@ -1,0 +1,82 @@
+"""The BASELINE configs at their own size on the GPU.
+
+C3 (vocab 8192, d_model 512, 4 layers, S = 256, 16 sequences, LoRA r8 on
+q/v) runs two whole steps against the reference's own executor kernels
+(oracle/_ref, ParallelFor on the host's cores): losses and the trained
+state within the north star's per-step bar.
+
+C4 and C5 are too large for a CPU step, so each is checked the way the bench
+runs it and then instruction by instruction:
+  1. the plan is opened and autotuned exactly as bench.py does, and one
+     step runs through the fused hipGraph (LoRA runs, GEMM epilogue chains,
+     pointwise runs, Scale folds, causal tails, column splits);
+  2. the persistent state is put back to the plan's initial image and the
+     same step is replayed eagerly, one instruction at a time; the first
+     instruction of every (opcode, shape) group is checked against the
+     oracle on the inputs the device held (instr_check.py);
+  3. the replay's loss and trained state equal the graph step's bit for bit.
+So every kernel variant the bench times is pinned: the eager replay uses
+the same autotuned plans, and the graph differs from it only by fusions
+that must give the same bits."""
+import os
+
+import numpy as np
+import pytest
+
+from helpers import TOL_STEP, HostPlanRunner, compile_workload, rel_err
+from instr_check import CHECKED, OPN, replay_and_check
+from seeml_amd import configs
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def _host_threads() -> int:
+    # the GPU box's CPU share is 16 cores per GPU, whatever os.cpu_count says
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def test_c3_full_size_parity_vs_reference_kernels(torch_gpu, ref):
+    from seeml_amd import DeviceUpdateEngine
+    ref.set_threads(_host_threads())
+    w, p = compile_workload("c3")
+    e = DeviceUpdateEngine(p.blob)
+    r = HostPlanRunner(p, ref)
+    for s in range(2):
+        x, y = configs.batch(w, s)
+        lg, lr = e.train_step(x, y), r.train_step(x, y)
+        assert abs(lg - lr) <= TOL_STEP * abs(lr), (s, lg, lr)
+    n = p.header["persistent_size"] // 4
+    assert rel_err(e.read(0, n), r.read(0, n)) <= TOL_STEP
+    e.close()
+
+
+@pytest.mark.parametrize("name", ["c4", "c5"])
+def test_full_size_graph_step_equals_the_checked_eager_replay(torch_gpu, orc, name):
+    from seeml_amd import DeviceUpdateEngine
+    w, p = compile_workload(name)
+    h = p.header
+    n = h["persistent_size"] // 4
+    p0 = h["persist_init_offset"]
+    initial = np.frombuffer(p.blob, np.float32, count=n, offset=p0).copy()
+    e = DeviceUpdateEngine(p.blob)
+    e.autotune(16)  # as bench.py
+    x, y = configs.batch(w, 0)
+    loss_graph = e.train_step(x, y)
+    state_graph = e.read(0, n)
+    assert np.isfinite(loss_graph)
+    e.write(0, initial)
+    checked = replay_and_check(e, p, orc, p.train, x, y, step=1)
+    loss_eager = e.loss()
+    assert np.float32(loss_eager).view(np.uint32) == np.float32(loss_graph).view(np.uint32)
+    assert np.array_equal(e.read(0, n).view(np.uint32), state_graph.view(np.uint32))
+    in_plan = {OPN[i["opcode"]] for i in p.train} & CHECKED
+    assert {k[0] for k in checked} == in_plan
+    e.close()
