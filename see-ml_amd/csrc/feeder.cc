@@ -1,53 +1,105 @@
-// feeder.cc — the batch feeder's dataset (runtime/feeder/dataset.cc), host.
+// feeder.cc — the batch feeder's dataset, host side.
+//
+// A corpus is held exactly as the .sds sample section lays it out: one
+// fixed-size record per sample — a feature row's f32 input followed by its
+// label bytes, or a token record's seq + 1 i32 ids. Loading and saving are
+// then one bulk transfer each, a validation split is a cut of one buffer,
+// and one copy loop serves both kinds: a record's first input_dim * 4 bytes
+// are the served input, and its label bytes sit right after them (feature
+// rows) or one id further on (token records: the shifted next-token view).
+//
+// Serving walks a cursor over the records, through this epoch's permutation
+// when shuffled. The permutation is the reference's (runtime/feeder/
+// dataset.cc:344-417): Fisher–Yates from the identity, i = n-1 .. 1, each j
+// the next splitmix64 draw mod (i + 1), a fresh one at every wrap. A
+// splitmix64 state advances by the golden-ratio increment per draw and one
+// permutation takes n - 1 draws, so epoch e's permutation starts at
+// origin + e (n - 1) increments: any epoch is drawn directly, and restoring
+// a serving position costs one permutation, not a replay of every epoch.
 #include "feeder.h"
 
 #include <algorithm>
-#include <cstdio>
+#include <cstdint>
 #include <cstring>
 #include <fstream>
+#include <numeric>
 #include <utility>
 
 namespace seeml_hip {
 
 namespace {
 
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ULL;  // splitmix64's state increment
 constexpr uint64_t kSdsHeaderBytes = 40;
-constexpr uint64_t kChunkBudget = 256 * 1024;  // bounded record staging for file I/O
 
 Status Fail(const std::string& m) { return Status::Fail(kUnitDataset, m); }
+
+// The .sds header (40 bytes, little-endian).
+struct SdsHeader {
+  uint32_t magic, version;
+  uint64_t num_samples, input_dim;
+  uint32_t label_kind, input_kind;
+  uint64_t label_dim;
+};
+static_assert(sizeof(SdsHeader) == kSdsHeaderBytes, "the .sds header is 40 bytes");
+
+// Label bytes of one served sample (token records: one class id per
+// position, the shifted view).
+uint64_t ServedLabelBytes(uint32_t input_kind, uint32_t label_kind, uint64_t input_dim,
+                          uint64_t label_dim) {
+  if (input_kind == 1) return input_dim * sizeof(int32_t);
+  if (label_kind == 1) return sizeof(int32_t);
+  if (label_kind == 2) return label_dim * sizeof(float);
+  return 0;
+}
+
+// A record's size, overflow-checked: token records are seq + 1 ids; a
+// feature record is the input row followed by its label bytes.
+bool RecordBytes(uint32_t input_kind, uint64_t input_dim, uint64_t label_bytes, uint64_t* out) {
+  if (input_kind == 1) return input_dim < UINT64_MAX && MulOk(input_dim + 1, sizeof(int32_t), out);
+  uint64_t in = 0;
+  if (!MulOk(input_dim, sizeof(float), &in) || in > UINT64_MAX - label_bytes) return false;
+  *out = in + label_bytes;
+  return true;
+}
+
+int32_t IdAt(const uint8_t* p) {
+  int32_t v;
+  std::memcpy(&v, p, sizeof v);
+  return v;
+}
 
 }  // namespace
 
 uint64_t SplitMix64(uint64_t* state) {
-  uint64_t z = (*state += 0x9E3779B97F4A7C15ULL);
+  uint64_t z = (*state += kGolden);
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
   return z ^ (z >> 31);
 }
 
 uint64_t Dataset::label_bytes_per_sample() const {
-  // A token record derives one class id per position (dataset.cc:23-33).
-  if (input_kind_ == 1) return input_dim_ * sizeof(int32_t);
-  if (label_kind_ == 1) return sizeof(int32_t);
-  if (label_kind_ == 2) return label_dim_ * sizeof(float);
-  return 0;
+  return ServedLabelBytes(input_kind_, label_kind_, input_dim_, label_dim_);
 }
 
 Status Dataset::FromTokens(const int32_t* tokens, uint64_t count, uint64_t num_records,
                            uint64_t seq, Dataset* out) {
   if (num_records == 0) return Fail("zero samples");
   if (seq == 0) return Fail("zero input dim");
-  uint64_t want = 0;
-  if (seq == UINT64_MAX || !MulOk(num_records, seq + 1, &want) || count != want)
+  uint64_t ids = 0;
+  if (seq == UINT64_MAX || !MulOk(num_records, seq + 1, &ids) || count != ids)
     return Fail("token buffer size mismatch");
-  for (uint64_t i = 0; i < want; ++i)
-    if (tokens[i] < 0) return Fail("negative token id at position " + std::to_string(i));
+  const int32_t* neg = std::find_if(tokens, tokens + ids, [](int32_t t) { return t < 0; });
+  if (neg != tokens + ids)
+    return Fail("negative token id at position " + std::to_string(neg - tokens));
   Dataset d;
   d.input_kind_ = 1;
   d.label_kind_ = 1;
   d.num_samples_ = num_records;
   d.input_dim_ = seq;
-  d.tokens_.assign(tokens, tokens + want);
+  d.record_bytes_ = (seq + 1) * sizeof(int32_t);
+  const uint8_t* bytes = reinterpret_cast<const uint8_t*>(tokens);
+  d.records_.assign(bytes, bytes + ids * sizeof(int32_t));
   *out = std::move(d);
   return Status::Ok();
 }
@@ -55,103 +107,78 @@ Status Dataset::FromTokens(const int32_t* tokens, uint64_t count, uint64_t num_r
 Status Dataset::FromMemory(const float* inputs, uint64_t input_count, const uint8_t* labels,
                            uint64_t label_bytes, uint64_t num_samples, uint64_t input_dim,
                            uint32_t label_kind, uint64_t label_dim, Dataset* out) {
-  Dataset d;
-  d.num_samples_ = num_samples;
-  d.input_dim_ = input_dim;
-  d.label_kind_ = label_kind;
-  d.label_dim_ = label_dim;
   if (num_samples == 0) return Fail("zero samples");
   if (input_dim == 0) return Fail("zero input dim");
   if (label_kind > 2) return Fail("unknown label kind");
   if (label_kind == 2 && (label_dim == 0 || label_dim > UINT64_MAX / sizeof(float)))
     return Fail("label dim out of range");
-  uint64_t want_inputs = 0, want_labels = 0;
-  if (!MulOk(num_samples, input_dim, &want_inputs) || input_count != want_inputs)
+  const uint64_t lb = ServedLabelBytes(0, label_kind, input_dim, label_dim);
+  uint64_t floats = 0, lab_total = 0, rec = 0, total = 0;
+  if (!MulOk(num_samples, input_dim, &floats) || input_count != floats)
     return Fail("input buffer size mismatch");
-  if (!MulOk(num_samples, d.label_bytes_per_sample(), &want_labels) || label_bytes != want_labels)
+  if (!MulOk(num_samples, lb, &lab_total) || label_bytes != lab_total)
     return Fail("label buffer size mismatch");
-  d.inputs_.assign(inputs, inputs + want_inputs);
-  if (want_labels) d.labels_.assign(labels, labels + want_labels);
-  *out = std::move(d);
-  return Status::Ok();
-}
-
-Status Dataset::LoadFromFile(const std::string& path, Dataset* out) {
-  std::ifstream f(path, std::ios::binary);
-  if (!f) return Fail("cannot open '" + path + "'");
-  f.seekg(0, std::ios::end);
-  const std::streamoff end_pos = f.tellg();
-  if (end_pos < 0) return Fail("cannot stat '" + path + "'");
-  const uint64_t file_size = static_cast<uint64_t>(end_pos);
-  f.seekg(0);
-  auto read = [&](void* dst, uint64_t n) {
-    f.read(static_cast<char*>(dst), static_cast<std::streamsize>(n));
-    return static_cast<bool>(f);
-  };
-
-  uint32_t magic = 0, version = 0, label_kind = 0, input_kind = 0;
-  uint64_t num_samples = 0, input_dim = 0, label_dim = 0;
-  if (!read(&magic, 4) || magic != kSdsMagic) return Fail("bad magic in '" + path + "'");
-  if (!read(&version, 4) || version < 1 || version > 2) return Fail("unsupported version");
-  if (!read(&num_samples, 8) || !read(&input_dim, 8) || !read(&label_kind, 4) ||
-      !read(&input_kind, 4) || !read(&label_dim, 8))
-    return Fail("truncated header");
-
+  if (!RecordBytes(0, input_dim, lb, &rec) || !MulOk(num_samples, rec, &total))
+    return Fail("input buffer size mismatch");
   Dataset d;
   d.num_samples_ = num_samples;
   d.input_dim_ = input_dim;
   d.label_kind_ = label_kind;
   d.label_dim_ = label_dim;
-  d.input_kind_ = input_kind;
-  if (num_samples == 0 || input_dim == 0) return Fail("empty dataset");
-  if (label_kind > 2) return Fail("unknown label kind");
-  if (label_kind == 2 && (label_dim == 0 || label_dim > UINT64_MAX / sizeof(float)))
+  d.record_bytes_ = rec;
+  d.records_.resize(total);
+  const uint64_t in_bytes = input_dim * sizeof(float);
+  for (uint64_t i = 0; i < num_samples; ++i) {
+    uint8_t* r = d.records_.data() + i * rec;
+    std::memcpy(r, inputs + i * input_dim, in_bytes);
+    if (lb) std::memcpy(r + in_bytes, labels + i * lb, lb);
+  }
+  *out = std::move(d);
+  return Status::Ok();
+}
+
+Status Dataset::LoadFromFile(const std::string& path, Dataset* out) {
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  if (!f) return Fail("cannot open '" + path + "'");
+  const std::streamoff end = f.tellg();
+  if (end < 0) return Fail("cannot stat '" + path + "'");
+  const uint64_t file_size = static_cast<uint64_t>(end);
+  f.seekg(0);
+  SdsHeader h{};
+  f.read(reinterpret_cast<char*>(&h), sizeof h);
+  const uint64_t got = static_cast<uint64_t>(std::max<std::streamsize>(f.gcount(), 0));
+  // The header's fields are judged in file order: a file cut short inside
+  // one reports that field.
+  if (got < 4 || h.magic != kSdsMagic) return Fail("bad magic in '" + path + "'");
+  if (got < 8 || h.version < 1 || h.version > 2) return Fail("unsupported version");
+  if (got < kSdsHeaderBytes) return Fail("truncated header");
+  if (h.num_samples == 0 || h.input_dim == 0) return Fail("empty dataset");
+  if (h.label_kind > 2) return Fail("unknown label kind");
+  if (h.label_kind == 2 && (h.label_dim == 0 || h.label_dim > UINT64_MAX / sizeof(float)))
     return Fail("label dim out of range");
   // v1's input_kind word was header padding (always 0).
-  if (input_kind > 1 || (version < 2 && input_kind != 0)) return Fail("unknown input kind");
-
-  if (input_kind == 1) {
-    if (label_kind != 1 || label_dim != 0)
-      return Fail("token corpora derive next-token class labels (label_kind 1, label_dim 0)");
-    uint64_t record_bytes = 0, payload = 0;
-    if (input_dim == UINT64_MAX || !MulOk(input_dim + 1, sizeof(int32_t), &record_bytes) ||
-        !MulOk(num_samples, record_bytes, &payload) || payload > file_size - kSdsHeaderBytes)
-      return Fail("sample section exceeds file size");
-    d.tokens_.resize(payload / sizeof(int32_t));
-    if (!read(d.tokens_.data(), payload)) return Fail("truncated inputs");
-    for (const int32_t t : d.tokens_)
-      if (t < 0) return Fail("negative token id");
-    *out = std::move(d);
-    return Status::Ok();
-  }
-
-  const uint64_t lbytes = d.label_bytes_per_sample();
-  uint64_t input_bytes = 0, payload = 0;
-  if (!MulOk(input_dim, sizeof(float), &input_bytes) || input_bytes > UINT64_MAX - lbytes ||
-      !MulOk(num_samples, input_bytes + lbytes, &payload) ||
-      payload > file_size - kSdsHeaderBytes)
+  if (h.input_kind > 1 || (h.version < 2 && h.input_kind != 0)) return Fail("unknown input kind");
+  if (h.input_kind == 1 && (h.label_kind != 1 || h.label_dim != 0))
+    return Fail("token corpora derive next-token class labels (label_kind 1, label_dim 0)");
+  const uint64_t lb = ServedLabelBytes(h.input_kind, h.label_kind, h.input_dim, h.label_dim);
+  uint64_t rec = 0, payload = 0;
+  if (!RecordBytes(h.input_kind, h.input_dim, h.input_kind == 1 ? 0 : lb, &rec) ||
+      !MulOk(h.num_samples, rec, &payload) || payload > file_size - kSdsHeaderBytes)
     return Fail("sample section exceeds file size");
-  d.inputs_.resize(num_samples * input_dim);
-  d.labels_.resize(num_samples * lbytes);
-  if (lbytes == 0) {
-    if (!read(d.inputs_.data(), num_samples * input_bytes)) return Fail("truncated inputs");
-    *out = std::move(d);
-    return Status::Ok();
-  }
-  // Interleaved records, de-interleaved through a bounded chunk.
-  const uint64_t record = input_bytes + lbytes;
-  const uint64_t per_chunk = record >= kChunkBudget ? 1 : kChunkBudget / record;
-  std::vector<uint8_t> chunk(per_chunk * record);
-  for (uint64_t i = 0; i < num_samples;) {
-    const uint64_t n = std::min(per_chunk, num_samples - i);
-    if (!read(chunk.data(), n * record)) return Fail("truncated inputs");
-    for (uint64_t s = 0; s < n; ++s) {
-      const uint8_t* rec = chunk.data() + s * record;
-      std::memcpy(d.inputs_.data() + (i + s) * input_dim, rec, input_bytes);
-      std::memcpy(d.labels_.data() + (i + s) * lbytes, rec + input_bytes, lbytes);
-    }
-    i += n;
-  }
+  if (payload > SIZE_MAX) return Fail("dataset too large for this host");
+  Dataset d;
+  d.num_samples_ = h.num_samples;
+  d.input_dim_ = h.input_dim;
+  d.label_kind_ = h.label_kind;
+  d.input_kind_ = h.input_kind;
+  d.label_dim_ = h.label_dim;
+  d.record_bytes_ = rec;
+  d.records_.resize(payload);
+  f.read(reinterpret_cast<char*>(d.records_.data()), static_cast<std::streamsize>(payload));
+  if (!f) return Fail("truncated inputs");
+  if (h.input_kind == 1)
+    for (uint64_t at = 0; at < payload; at += sizeof(int32_t))
+      if (IdAt(d.records_.data() + at) < 0) return Fail("negative token id");
   *out = std::move(d);
   return Status::Ok();
 }
@@ -159,156 +186,87 @@ Status Dataset::LoadFromFile(const std::string& path, Dataset* out) {
 Status Dataset::SaveToFile(const std::string& path) const {
   std::ofstream f(path, std::ios::binary | std::ios::trunc);
   if (!f) return Fail("cannot write '" + path + "'");
-  auto write = [&](const void* src, uint64_t n) {
-    f.write(static_cast<const char*>(src), static_cast<std::streamsize>(n));
-  };
-  const uint32_t version = input_kind_ == 1 ? 2 : 1;
-  write(&kSdsMagic, 4);
-  write(&version, 4);
-  write(&num_samples_, 8);
-  write(&input_dim_, 8);
-  write(&label_kind_, 4);
-  write(&input_kind_, 4);
-  write(&label_dim_, 8);
-  if (input_kind_ == 1) {
-    write(tokens_.data(), tokens_.size() * sizeof(int32_t));
-  } else {
-    const uint64_t lbytes = label_bytes_per_sample();
-    if (lbytes == 0) {
-      write(inputs_.data(), num_samples_ * input_dim_ * sizeof(float));
-    } else {
-      const uint64_t input_bytes = input_dim_ * sizeof(float);
-      const uint64_t record = input_bytes + lbytes;
-      const uint64_t per_chunk = record >= kChunkBudget ? 1 : kChunkBudget / record;
-      std::vector<uint8_t> chunk(per_chunk * record);
-      for (uint64_t i = 0; i < num_samples_;) {
-        const uint64_t n = std::min(per_chunk, num_samples_ - i);
-        for (uint64_t s = 0; s < n; ++s) {
-          uint8_t* rec = chunk.data() + s * record;
-          std::memcpy(rec, inputs_.data() + (i + s) * input_dim_, input_bytes);
-          std::memcpy(rec + input_bytes, labels_.data() + (i + s) * lbytes, lbytes);
-        }
-        write(chunk.data(), n * record);
-        i += n;
-      }
-    }
-  }
-  f.close();  // the stream tail flushes here; check after
+  const SdsHeader h{kSdsMagic, input_kind_ == 1 ? 2u : 1u, num_samples_, input_dim_,
+                    label_kind_, input_kind_, label_dim_};
+  f.write(reinterpret_cast<const char*>(&h), sizeof h);
+  f.write(reinterpret_cast<const char*>(records_.data()),
+          static_cast<std::streamsize>(records_.size()));
+  f.close();  // the buffered tail is written here: judge the stream after it
   if (f.fail()) return Fail("short write to '" + path + "'");
   return Status::Ok();
 }
 
 Status Dataset::ValidateClassLabels(uint64_t num_classes) const {
   if (label_kind_ != 1 || num_classes == 0) return Status::Ok();
-  auto outside = [&](const char* what, int64_t v, uint64_t where) {
-    return Fail(std::string(what) + std::to_string(v) + " at " +
-                (input_kind_ == 1 ? "position " : "sample ") + std::to_string(where) +
-                " outside [0, " + std::to_string(num_classes) + ")");
-  };
+  auto outside = [&](int64_t v) { return v < 0 || static_cast<uint64_t>(v) >= num_classes; };
+  const std::string bound = " outside [0, " + std::to_string(num_classes) + ")";
   if (input_kind_ == 1) {
-    // Every token is an embedding index and, shifted, a class label.
-    for (uint64_t i = 0; i < tokens_.size(); ++i)
-      if (tokens_[i] < 0 || static_cast<uint64_t>(tokens_[i]) >= num_classes)
-        return outside("token id ", tokens_[i], i);
+    // Every id is an embedding index and, one position on, a class label.
+    for (uint64_t at = 0; at < records_.size(); at += sizeof(int32_t))
+      if (const int32_t v = IdAt(records_.data() + at); outside(v))
+        return Fail("token id " + std::to_string(v) + " at position " +
+                    std::to_string(at / sizeof(int32_t)) + bound);
     return Status::Ok();
   }
-  for (uint64_t i = 0; i < num_samples_; ++i) {
-    int32_t v;
-    std::memcpy(&v, labels_.data() + i * sizeof(int32_t), sizeof v);
-    if (v < 0 || static_cast<uint64_t>(v) >= num_classes) return outside("class label ", v, i);
-  }
+  for (uint64_t i = 0; i < num_samples_; ++i)
+    if (const int32_t v = IdAt(Record(i) + LabelOffset()); outside(v))
+      return Fail("class label " + std::to_string(v) + " at sample " + std::to_string(i) + bound);
   return Status::Ok();
 }
 
+void Dataset::Advance() {
+  if (++cursor_ < num_samples_) return;
+  cursor_ = 0;
+  if (perm_.empty()) return;  // sequential serving wraps around
+  ++epoch_;
+  DrawPermutation();
+}
+
 void Dataset::FillBatch(uint64_t batch, void* input_slot, void* label_slot) {
+  // Token corpora count `batch` in token rows: one record serves input_dim_.
+  const uint64_t samples = input_kind_ == 1 ? batch / input_dim_ : batch;
+  const uint64_t in_bytes = input_dim_ * 4, lab_bytes = label_bytes_per_sample();
+  const uint64_t lab_off = LabelOffset();
   uint8_t* in = static_cast<uint8_t*>(input_slot);
-  uint8_t* lab = static_cast<uint8_t*>(label_slot);
-  if (input_kind_ == 1) {
-    // `batch` counts token rows; one record serves S of them (dataset.cc:290-313).
-    const uint64_t S = input_dim_;
-    const uint64_t row_bytes = S * sizeof(int32_t);
-    for (uint64_t r = 0; r < batch / S; ++r) {
-      const uint64_t i = order_.empty() ? cursor_ : order_[cursor_];
-      const int32_t* rec = tokens_.data() + i * (S + 1);
-      std::memcpy(in + r * row_bytes, rec, row_bytes);
-      if (lab) std::memcpy(lab + r * row_bytes, rec + 1, row_bytes);
-      if (++cursor_ == num_samples_) {
-        cursor_ = 0;
-        if (!order_.empty()) {
-          Reshuffle();
-          ++epoch_;
-        }
-      }
-    }
-    return;
+  uint8_t* lab = lab_bytes ? static_cast<uint8_t*>(label_slot) : nullptr;
+  for (uint64_t b = 0; b < samples; ++b) {
+    const uint8_t* rec = Record(CurrentRecord());
+    std::memcpy(in + b * in_bytes, rec, in_bytes);
+    if (lab) std::memcpy(lab + b * lab_bytes, rec + lab_off, lab_bytes);
+    Advance();
   }
-  const uint64_t lbytes = label_bytes_per_sample();
-  const uint64_t in_bytes = input_dim_ * sizeof(float);
-  if (order_.empty()) {
-    // Sequential: copy contiguous runs up to the wrap point.
-    for (uint64_t b = 0; b < batch;) {
-      const uint64_t run = std::min(batch - b, num_samples_ - cursor_);
-      std::memcpy(in + b * in_bytes, inputs_.data() + cursor_ * input_dim_, run * in_bytes);
-      if (lab && lbytes) std::memcpy(lab + b * lbytes, labels_.data() + cursor_ * lbytes, run * lbytes);
-      b += run;
-      cursor_ += run;
-      if (cursor_ == num_samples_) cursor_ = 0;
-    }
-    return;
-  }
-  for (uint64_t b = 0; b < batch; ++b) {
-    const uint64_t i = order_[cursor_];
-    std::memcpy(in + b * in_bytes, inputs_.data() + i * input_dim_, in_bytes);
-    if (lab && lbytes) std::memcpy(lab + b * lbytes, labels_.data() + i * lbytes, lbytes);
-    if (++cursor_ == num_samples_) {
-      cursor_ = 0;
-      Reshuffle();
-      ++epoch_;
-    }
-  }
+}
+
+void Dataset::DrawPermutation() {
+  perm_.resize(num_samples_);
+  std::iota(perm_.begin(), perm_.end(), uint64_t{0});
+  uint64_t state = origin_ + epoch_ * (num_samples_ - 1) * kGolden;
+  for (uint64_t i = num_samples_ - 1; i > 0; --i)
+    std::swap(perm_[i], perm_[SplitMix64(&state) % (i + 1)]);
 }
 
 void Dataset::EnableShuffle(uint64_t seed) {
-  // One splitmix step folds the seed so 0 is usable; the low bit keeps the
-  // state nonzero ("shuffling on").
-  shuffle_state_ = seed;
-  shuffle_state_ = SplitMix64(&shuffle_state_) | 1ULL;
-  shuffle_origin_ = shuffle_state_;
+  // The seed goes through one splitmix64 step (so 0 is a usable seed), with
+  // the low bit set (dataset.cc:356-366).
+  uint64_t s = seed;
+  origin_ = SplitMix64(&s) | 1ULL;
   epoch_ = 0;
-  order_.resize(num_samples_);
-  Reshuffle();
   cursor_ = 0;
-}
-
-void Dataset::Reshuffle() {
-  for (uint64_t i = 0; i < num_samples_; ++i) order_[i] = i;
-  for (uint64_t i = num_samples_ - 1; i > 0; --i) {
-    const uint64_t j = SplitMix64(&shuffle_state_) % (i + 1);
-    std::swap(order_[i], order_[j]);
-  }
+  DrawPermutation();
 }
 
 void Dataset::RestoreServingPos(ServingPos pos) {
   cursor_ = pos.cursor;
-  if (order_.empty() || epoch_ == pos.epoch) return;
-  // Each epoch's permutation is a function of (origin, epoch): replay.
-  shuffle_state_ = shuffle_origin_;
-  epoch_ = 0;
-  Reshuffle();
-  while (epoch_ < pos.epoch) {
-    Reshuffle();
-    ++epoch_;
-  }
+  if (perm_.empty() || epoch_ == pos.epoch) return;
+  epoch_ = pos.epoch;
+  DrawPermutation();
 }
 
 Status Dataset::SkipServed(uint64_t rows) {
-  uint64_t records = rows;
-  if (input_kind_ == 1) {
-    if (rows % input_dim_ != 0)
-      return Fail("served rows are not a whole number of token records — cannot replay the "
-                  "serving position");
-    records = rows / input_dim_;
-  }
+  if (input_kind_ == 1 && rows % input_dim_ != 0)
+    return Fail("served rows are not a whole number of token records — cannot replay the "
+                "serving position");
+  const uint64_t records = input_kind_ == 1 ? rows / input_dim_ : rows;
   RestoreServingPos({records % num_samples_, records / num_samples_});
   return Status::Ok();
 }
@@ -316,33 +274,24 @@ Status Dataset::SkipServed(uint64_t rows) {
 Status Dataset::SplitValidation(double fraction, Dataset* val_out) {
   if (!(fraction > 0.0) || fraction >= 1.0) return Fail("validation fraction must be in (0, 1)");
   if (num_samples_ < 2) return Fail("too few samples to split");
-  if (!order_.empty()) return Fail("split before enabling shuffle");
-  uint64_t val_n = static_cast<uint64_t>(static_cast<double>(num_samples_) * fraction);
-  if (val_n == 0) val_n = 1;
-  if (val_n >= num_samples_) val_n = num_samples_ - 1;
-  const uint64_t train_n = num_samples_ - val_n;
-  const uint64_t lbytes = label_bytes_per_sample();
-
+  if (!perm_.empty()) return Fail("split before enabling shuffle");
+  // The tail fraction of the records (whole records: no sequence is cut),
+  // at least one on each side.
+  const uint64_t val_n =
+      std::clamp<uint64_t>(static_cast<uint64_t>(static_cast<double>(num_samples_) * fraction), 1,
+                           num_samples_ - 1);
+  const uint64_t cut = (num_samples_ - val_n) * record_bytes_;
   Dataset val;
+  val.record_bytes_ = record_bytes_;
   val.num_samples_ = val_n;
   val.input_dim_ = input_dim_;
   val.label_kind_ = label_kind_;
-  val.label_dim_ = label_dim_;
   val.input_kind_ = input_kind_;
-  if (input_kind_ == 1) {
-    // Whole records move: no sequence is cut.
-    const uint64_t rec = input_dim_ + 1;
-    val.tokens_.assign(tokens_.begin() + static_cast<std::ptrdiff_t>(train_n * rec), tokens_.end());
-    tokens_.resize(train_n * rec);
-  } else {
-    val.inputs_.assign(inputs_.begin() + static_cast<std::ptrdiff_t>(train_n * input_dim_),
-                       inputs_.end());
-    val.labels_.assign(labels_.begin() + static_cast<std::ptrdiff_t>(train_n * lbytes),
-                       labels_.end());
-    inputs_.resize(train_n * input_dim_);
-    labels_.resize(train_n * lbytes);
-  }
-  num_samples_ = train_n;
+  val.label_dim_ = label_dim_;
+  val.records_.assign(records_.begin() + static_cast<std::ptrdiff_t>(cut), records_.end());
+  records_.resize(cut);
+  records_.shrink_to_fit();
+  num_samples_ -= val_n;
   cursor_ = 0;
   *val_out = std::move(val);
   return Status::Ok();

@@ -1,12 +1,13 @@
 // feeder.h — the batch feeder's dataset, host side (no GPU code).
 //
-// Restates runtime/feeder/dataset.{h,cc}: fixed-shape samples served into the
-// plan's I/O slots, sequentially with wraparound or through a seeded
-// splitmix64 Fisher–Yates permutation re-drawn every epoch; token corpora
-// (input_kind 1) serve whole records of seq+1 ids as inputs tokens[0..S) and
-// shifted labels tokens[1..S]. The .sds file format is the same bytes.
-// Serving order and bytes are bit-identical to the reference (integer and
-// copy work only).
+// Serves fixed-shape samples into the plan's I/O slots, the contract of
+// runtime/feeder/dataset.{h,cc}: sequentially with wraparound, or through a
+// seeded splitmix64 Fisher–Yates permutation re-drawn at every epoch; token
+// corpora (input_kind 1) serve whole records of seq+1 ids as inputs
+// tokens[0..S) and shifted labels tokens[1..S]. The .sds bytes, the error
+// texts and the served bytes and order are the reference's (integer and copy
+// work only). The storage is this file's own: the corpus is held as the
+// .sds sample section itself, one fixed-size record per sample.
 #pragma once
 
 #include <cstdint>
@@ -59,21 +60,26 @@ class Dataset {
   Status SplitValidation(double fraction, Dataset* val);
 
  private:
-  void Reshuffle();
+  // Record geometry: the served input is the record's first input_dim_ * 4
+  // bytes; the label bytes follow it (feature rows) or are the same ids one
+  // position on (token records).
+  uint64_t LabelOffset() const { return input_kind_ == 1 ? sizeof(int32_t) : input_dim_ * 4; }
+  const uint8_t* Record(uint64_t i) const { return records_.data() + i * record_bytes_; }
+  uint64_t CurrentRecord() const { return perm_.empty() ? cursor_ : perm_[cursor_]; }
+  void Advance();
+  void DrawPermutation();
 
-  std::vector<float> inputs_;
-  std::vector<uint8_t> labels_;
-  std::vector<int32_t> tokens_;
+  std::vector<uint8_t> records_;  // num_samples_ * record_bytes_, the .sds sample section
+  uint64_t record_bytes_ = 0;
   uint64_t num_samples_ = 0;
   uint64_t input_dim_ = 0;
   uint32_t label_kind_ = 0;
   uint32_t input_kind_ = 0;
   uint64_t label_dim_ = 0;
   uint64_t cursor_ = 0;
-  std::vector<uint64_t> order_;  // shuffled serving order; empty = sequential
-  uint64_t shuffle_state_ = 0;
-  uint64_t shuffle_origin_ = 0;
   uint64_t epoch_ = 0;
+  std::vector<uint64_t> perm_;  // this epoch's serving order; empty = sequential
+  uint64_t origin_ = 0;         // splitmix64 state at epoch 0's first draw
 };
 
 // VerifyFeederContract (contract.cc:170-235): the dataset's geometry matches
