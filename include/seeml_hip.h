@@ -252,6 +252,41 @@ int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
                     seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
                     seeml_hip_train_report* out);
 
+/* TrainOptions (update_engine.h:40-60): with checkpoint_path and
+ * checkpoint_every > 0, a checkpoint is saved whenever step_ is a multiple
+ * of checkpoint_every; with resume, checkpoint_path is loaded first (a
+ * missing or unusable one is reported on stderr and training starts from
+ * the current state) and the feeder skips the step_ * batch rows already
+ * served, so a resumed run is the uninterrupted one bit for bit
+ * (update_engine.cc:676-696, 766-770). */
+typedef struct seeml_hip_train_options {
+  const char* checkpoint_path; /* NULL or "": no checkpointing */
+  uint64_t checkpoint_every;   /* steps between checkpoints; 0 = off */
+  int32_t resume;
+} seeml_hip_train_options;
+/* seeml_hip_train with TrainOptions (options may be NULL). */
+int seeml_hip_train_ex(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
+                       seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
+                       const seeml_hip_train_options* options, seeml_hip_train_report* out);
+
+/* SaveCheckpoint / LoadCheckpoint (update_engine.cc:894-913): the arena's
+ * persistent segment and step_ in the SEKP container
+ * (runtime/custodian/checkpoint.h:8-24): u32 "SEKP", u32 version 3,
+ * u64 plan_hash, u64 step, u64 persistent_size, u64 ContentHash64 of the
+ * payload, then the payload. Saves are durable (temporary file, fsync,
+ * rename, directory fsync); loads verify magic, version, plan binding, size
+ * and payload hash before any byte reaches the arena, then set step_.
+ * Errors read "Checkpoint: <message>". */
+int seeml_hip_save_checkpoint(seeml_hip_engine* e, const char* path);
+int seeml_hip_load_checkpoint(seeml_hip_engine* e, const char* path);
+/* The container alone, host only (SaveCheckpointFile / LoadCheckpointFile,
+ * checkpoint.cc:39-83): read copies the verified payload (exactly `size`
+ * bytes) into dst and the saved step into *step; dst is untouched on error. */
+int seeml_hip_checkpoint_write(const char* path, uint64_t plan_hash, uint64_t step,
+                               const uint8_t* payload, uint64_t size, char* err, uint64_t err_cap);
+int seeml_hip_checkpoint_read(const char* path, uint64_t plan_hash, uint64_t size, uint8_t* dst,
+                              uint64_t* step, char* err, uint64_t err_cap);
+
 /* Profiling (outside any timed step): replays `program` eagerly `reps`
  * times on the engine stream with a HIP event pair around every
  * instruction, and writes each instruction's mean duration in ms to

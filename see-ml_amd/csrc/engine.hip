@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -31,6 +32,7 @@
 #include "../../include/seeml_hip.h"
 #include "device_common.h"
 #include "kernels.h"
+#include "checkpoint.h"
 #include "stager.h"
 #include "plan_checks.h"
 
@@ -1630,8 +1632,33 @@ class Engine {
     return Status::Ok();
   }
 
+  // SaveCheckpoint / LoadCheckpoint (update_engine.cc:894-913): the
+  // persistent segment [0, persistent_size) and step_, in the SEKP container.
+  Status SaveCheckpoint(const std::string& path) {
+    const uint64_t n = plan_.header.persistent_size;
+    std::vector<uint8_t> host(n);
+    if (Status s = Access(0, host.data(), n, false); !s) return s;
+    return WriteCheckpoint(path, plan_.header.plan_hash, step_, host.data(), n);
+  }
+  Status LoadCheckpoint(const std::string& path) {
+    const uint64_t n = plan_.header.persistent_size;
+    std::vector<uint8_t> host(n);
+    uint64_t step = 0;
+    if (Status s = ReadCheckpoint(path, plan_.header.plan_hash, n, host.data(), &step); !s)
+      return s;
+    if (Status s = Access(0, host.data(), n, true); !s) return s;
+    return SetStep(step);
+  }
+
+  // TrainOptions (update_engine.h:40-60): checkpoint file, period, resume.
+  struct TrainOptions {
+    std::string checkpoint_path;
+    uint64_t checkpoint_every = 0;
+    bool resume = false;
+  };
+
   Status Train(Dataset& data, uint64_t steps, Dataset* validation, float* curve,
-               uint64_t curve_cap, ReportOut* rep) {
+               uint64_t curve_cap, ReportOut* rep, const TrainOptions& opt) {
     const PlanHeader& h = plan_.header;
     if (steps == 0) steps = h.default_steps;
     if (steps == 0)
@@ -1641,6 +1668,21 @@ class Engine {
     if (validation)
       if (Status s = VerifyFeederContract(h, *validation, plan_.num_classes, plan_.vocab_bound); !s)
         return s;
+    if (opt.resume && !opt.checkpoint_path.empty()) {
+      // A missing or unusable checkpoint is reported and training starts
+      // from the current state (update_engine.cc:676-680). A resumed step
+      // replays the feeder to where the interrupted run stood: step_
+      // batches of h.batch rows, epoch reshuffles included, so the resumed
+      // run is the uninterrupted one bit for bit (update_engine.cc:681-695).
+      if (Status s = LoadCheckpoint(opt.checkpoint_path); !s) {
+        std::fprintf(stderr, "seeml-update: no checkpoint resumed (%s)\n", s.error.c_str());
+      } else if (step_ > 0) {
+        uint64_t served = 0;
+        if (!MulOk(step_, h.batch, &served))
+          return Status::Fail(kUnitEngine, "resumed step count overflows the feeder position");
+        if (Status s = data.SkipServed(served); !s) return s;
+      }
+    }
     ReportOut report;
     if (validation) {
       EvalOut v;
@@ -1684,6 +1726,11 @@ class Engine {
         if (s - start >= steps - window) {
           last_sum += loss;
           ++last_n;
+        }
+        if (opt.checkpoint_every && !opt.checkpoint_path.empty() &&
+            step_ % opt.checkpoint_every == 0) {
+          st = SaveCheckpoint(opt.checkpoint_path);
+          if (!st) break;
         }
       }
     }
@@ -2322,9 +2369,21 @@ int seeml_hip_evaluate_metrics(seeml_hip_engine* e, seeml_hip_dataset* d,
 int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
                     seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
                     seeml_hip_train_report* out) {
+  return seeml_hip_train_ex(e, d, steps, validation, loss_curve, curve_cap, nullptr, out);
+}
+
+int seeml_hip_train_ex(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
+                       seeml_hip_dataset* validation, float* loss_curve, uint64_t curve_cap,
+                       const seeml_hip_train_options* options, seeml_hip_train_report* out) {
   Engine::ReportOut r;
+  Engine::TrainOptions opt;
+  if (options) {
+    opt.checkpoint_path = options->checkpoint_path ? options->checkpoint_path : "";
+    opt.checkpoint_every = options->checkpoint_every;
+    opt.resume = options->resume != 0;
+  }
   if (const Status s = e->impl.Train(d->impl, steps, validation ? &validation->impl : nullptr,
-                                     loss_curve, curve_cap, &r);
+                                     loss_curve, curve_cap, &r, opt);
       !s)
     return Ret(e, s);
   out->steps = r.steps;
@@ -2338,6 +2397,25 @@ int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
   out->val_final_accuracy = r.val_final_accuracy;
   out->improved = r.improved() ? 1 : 0;
   return SEEML_HIP_OK;
+}
+
+int seeml_hip_save_checkpoint(seeml_hip_engine* e, const char* path) {
+  return Ret(e, e->impl.SaveCheckpoint(path ? path : ""));
+}
+int seeml_hip_load_checkpoint(seeml_hip_engine* e, const char* path) {
+  return Ret(e, e->impl.LoadCheckpoint(path ? path : ""));
+}
+int seeml_hip_checkpoint_write(const char* path, uint64_t plan_hash, uint64_t step,
+                               const uint8_t* payload, uint64_t size, char* err, uint64_t err_cap) {
+  const Status s = seeml_hip::WriteCheckpoint(path ? path : "", plan_hash, step, payload, size);
+  if (!s) seeml_hip::CopyError(s.error, err, err_cap);
+  return s.ok ? SEEML_HIP_OK : SEEML_HIP_ERROR;
+}
+int seeml_hip_checkpoint_read(const char* path, uint64_t plan_hash, uint64_t size, uint8_t* dst,
+                              uint64_t* step, char* err, uint64_t err_cap) {
+  const Status s = seeml_hip::ReadCheckpoint(path ? path : "", plan_hash, size, dst, step);
+  if (!s) seeml_hip::CopyError(s.error, err, err_cap);
+  return s.ok ? SEEML_HIP_OK : SEEML_HIP_ERROR;
 }
 
 int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,

@@ -26,6 +26,11 @@ class _EvalMetrics(C.Structure):
     _fields_ = [("loss", C.c_float), ("has_accuracy", C.c_int32), ("accuracy", C.c_float)]
 
 
+class _TrainOptions(C.Structure):
+    _fields_ = [("checkpoint_path", C.c_char_p), ("checkpoint_every", C.c_uint64),
+                ("resume", C.c_int32)]
+
+
 class _TrainReport(C.Structure):
     _fields_ = [("steps", C.c_uint64), ("initial_avg_loss", C.c_float),
                 ("final_avg_loss", C.c_float), ("has_validation", C.c_int32),
@@ -134,20 +139,31 @@ class DeviceUpdateEngine:
                     "evaluate_metrics")
         return dict(loss=m.loss, has_accuracy=bool(m.has_accuracy), accuracy=m.accuracy)
 
-    def train_dataset(self, dataset, steps: int = 0, validation=None) -> dict:
-        """TrainImpl (update_engine.cc:664-787) with the native feeder; the
-        report's loss_curve holds every step's loss."""
+    def train_dataset(self, dataset, steps: int = 0, validation=None, checkpoint_path=None,
+                      checkpoint_every: int = 0, resume: bool = False) -> dict:
+        """TrainImpl (update_engine.cc:664-787) with the native feeder and
+        TrainOptions (checkpointing, resume); the report's loss_curve holds
+        every step's loss."""
         r = _TrainReport()
         cap = steps if steps else 0
         curve = np.zeros(max(cap, 1), np.float32)
-        self._check(self._L.seeml_hip_train(self._h, dataset._h, steps,
-                                            validation._h if validation is not None else None,
-                                            curve.ctypes.data, cap, C.byref(r)), "train")
+        opt = _TrainOptions(checkpoint_path.encode() if checkpoint_path else None,
+                            checkpoint_every, 1 if resume else 0)
+        self._check(self._L.seeml_hip_train_ex(self._h, dataset._h, steps,
+                                               validation._h if validation is not None else None,
+                                               curve.ctypes.data, cap, C.byref(opt), C.byref(r)),
+                    "train")
         out = {f: getattr(r, f) for f, _ in _TrainReport._fields_}
         for k in ("has_validation", "has_val_accuracy", "improved"):
             out[k] = bool(out[k])
         out["loss_curve"] = curve[:min(cap, r.steps)]
         return out
+
+    def save_checkpoint(self, path: str):
+        self._check(self._L.seeml_hip_save_checkpoint(self._h, path.encode()), "save_checkpoint")
+
+    def load_checkpoint(self, path: str):
+        self._check(self._L.seeml_hip_load_checkpoint(self._h, path.encode()), "load_checkpoint")
 
     def run_merge(self):
         self._check(self._L.seeml_hip_run_merge(self._h), "run_merge")

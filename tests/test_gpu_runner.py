@@ -175,3 +175,75 @@ def test_train_rejects_mismatched_dataset(torch_dev):
     with pytest.raises(RuntimeError, match="takes feature rows, but the dataset carries token ids"):
         e.evaluate_metrics(toks)
     e.close()
+
+
+def _ten_sample_set(seed=42):
+    """Ten class-labelled feature rows under a shuffled feeder: every
+    32-row batch of C1 wraps several epochs, so a resumed serving position
+    must replay reshuffles, not just a cursor."""
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal(10 * 256).astype(f32)
+    y = rng.integers(0, 256, 10).astype(np.int32).tobytes()
+    ds = feeder.Dataset.from_memory(X, y, 10, 256, 1)
+    ds.enable_shuffle(seed)
+    return ds
+
+
+def test_resumed_run_matches_uninterrupted_run_bitwise(torch_dev, tmp_path):
+    """update_engine_test.cc:402-444: six uninterrupted steps, against three
+    steps, a checkpoint, a cold engine and feeder, and a resume for three
+    more: the same run, bit for bit (the persistent segment and step_)."""
+    w = configs.make("c1")
+    plan = planner.compile_update(w.model, w.cfg)
+    n = plan.header["persistent_size"] // 4
+    straight = DeviceUpdateEngine(plan.blob)
+    straight.train_dataset(_ten_sample_set(), steps=6)
+    ck = str(tmp_path / "ck.sekp")
+    first = DeviceUpdateEngine(plan.blob)
+    first.train_dataset(_ten_sample_set(), steps=3)
+    first.save_checkpoint(ck)
+    first.close()
+    resumed = DeviceUpdateEngine(plan.blob)
+    resumed.train_dataset(_ten_sample_set(), steps=3, checkpoint_path=ck, resume=True)
+    assert straight.step == 6 and resumed.step == 6
+    assert np.array_equal(straight.read(0, n).view(np.uint32), resumed.read(0, n).view(np.uint32))
+    straight.close()
+    resumed.close()
+
+
+def test_checkpoint_restores_step_and_state(torch_dev, tmp_path):
+    """update_engine_test.cc:380-400: a load after further training puts
+    step_ and the persistent segment back; periodic checkpoints
+    (checkpoint_every) hold the step they were taken at; a checkpoint of
+    another plan is refused and leaves the arena alone."""
+    w = configs.make("c1")
+    plan = planner.compile_update(w.model, w.cfg)
+    n = plan.header["persistent_size"] // 4
+    e = DeviceUpdateEngine(plan.blob)
+    ck = str(tmp_path / "ck.sekp")
+    e.train_dataset(_ten_sample_set(), steps=3)
+    e.save_checkpoint(ck)
+    saved = e.read(0, n)
+    e.train_dataset(_ten_sample_set(), steps=4)
+    assert e.step == 7
+    e.load_checkpoint(ck)
+    assert e.step == 3
+    assert np.array_equal(e.read(0, n).view(np.uint32), saved.view(np.uint32))
+    periodic = str(tmp_path / "every2.sekp")
+    e.train_dataset(_ten_sample_set(), steps=5, checkpoint_path=periodic, checkpoint_every=2)
+    assert e.step == 8
+    from seeml_amd import _lib
+    err = C.create_string_buffer(256)
+    dst = (C.c_uint8 * (4 * n))()
+    step = C.c_uint64()
+    assert _lib.lib().seeml_hip_checkpoint_read(periodic.encode(), plan.header["plan_hash"], 4 * n,
+                                                dst, C.byref(step), err, 256) == 0
+    assert step.value == 8
+    other = planner.compile_update(w.model, planner.UpdateConfig(**{**w.cfg.__dict__, "lr": 2e-3}))
+    o = DeviceUpdateEngine(other.blob)
+    before = o.read(0, n)
+    with pytest.raises(RuntimeError, match="Checkpoint: checkpoint belongs to a different plan"):
+        o.load_checkpoint(ck)
+    assert np.array_equal(o.read(0, n).view(np.uint32), before.view(np.uint32)) and o.step == 0
+    o.close()
+    e.close()
