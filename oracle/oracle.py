@@ -77,6 +77,7 @@ _ORACLE_ONLY = {
     "chunk_grain": ([_Z, _Z], _Z),
     "chunk_count": ([_Z, _Z], _Z),
     "effective_lr": ([_F, C.c_uint32, _U64, _U64, _F, _U64], _F),
+    "counter_randn": ([_U64, _U64, _P], None),
 }
 _REF_ONLY = {
     "set_threads": ([_Z], None),

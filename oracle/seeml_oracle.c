@@ -664,6 +664,30 @@ void orc_adamw_step(float* p, const float* g, float* m, float* v, size_t n,
   }
 }
 
+/* ---- Compiler pieces (compiler/driver/update_compiler.cc) --------------------- */
+
+/* update_compiler.cc:415-436: element j of a "randn" adapter tensor mixes two
+ * splitmix64 draws from the counter seed + golden * (2j + 1) and feeds
+ * Box-Muller in double, with the C library's log, sqrt and cos, rounded to
+ * f32 (the tensor's std is applied by the caller). */
+void orc_counter_randn(uint64_t seed, uint64_t count, float* out) {
+  const uint64_t golden = 0x9E3779B97F4A7C15ULL;
+  for (uint64_t j = 0; j < count; ++j) {
+    uint64_t s = seed + golden * (2 * j + 1);
+    uint64_t d[2];
+    for (int k = 0; k < 2; ++k) {
+      uint64_t z = (s += golden);
+      z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+      z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+      d[k] = z ^ (z >> 31);
+    }
+    const double u1 = ((double)(d[0] >> 11) + 1.0) * 0x1.0p-53;
+    const double u2 = (double)(d[1] >> 11) * 0x1.0p-53;
+    const double two_pi = 6.283185307179586476925286766559;
+    out[j] = (float)(sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+  }
+}
+
 /* ---- Engine pieces (update_engine.cc) ----------------------------------------- */
 
 /* update_engine.cc:515-534 */

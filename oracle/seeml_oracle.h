@@ -114,6 +114,7 @@ void orc_adamw_step(float* p, const float* g, float* m, float* v, size_t n,
                     uint64_t step);
 
 /* Engine pieces (update_engine.cc). */
+void orc_counter_randn(uint64_t seed, uint64_t count, float* out);
 float orc_effective_lr(float lr, uint32_t schedule, uint64_t warmup_steps,
                        uint64_t default_steps, float min_lr_factor,
                        uint64_t step);
