@@ -17,8 +17,11 @@ Emits ONE JSON line (rank 0) with, besides the driver's fields:
                 the HBM bytes per launch from the committed rocprofv3 PMC
                 summary for that kernel (profiles/), when one matches
   cpu_baseline  the reference's own executor kernels (oracle/_ref, built
-                from the reference sources) timed on this host on a bounded
-                sample of the same workload
+                from the reference sources) timed on this host's cores and on
+                one thread: steps-lo/hi slopes (C1-C3) or the per-kernel-group
+                model (C4/C5), oracle/cpu_baseline.py
+  ms_per_step_slope  the reference bench's own step timing: the slope
+                between steps-4 and steps-12 runs, median of 3
   kernels       per-opcode time split, dense-GEMM MFMA utilisation and the
                 HBM throughput of the bandwidth-bound kernels
 """
@@ -41,56 +44,24 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, plan, cores, budget_s=20.0):
-    """The reference executor (oracle/_ref: runtime/executor/*.cc compiled
-    from the reference sources) running the same workload on host cores.
-
-    Small configs run the GPU's own plan. When one full CPU step would exceed
-    the budget (C3 and up), the sample is the same model and weights compiled
-    at a reduced batch — one sequence for token models (per-token work,
-    attention included, is unchanged) — timed for one step."""
+def cpu_baseline(w, plan, cores):
+    """The reference's own executor kernels (oracle/_ref, compiled from the
+    reference sources) timed on this host's cores and on one thread, as
+    oracle/cpu_baseline.py describes: whole-step steps-lo/hi slopes for C1-C3,
+    the per-kernel-group model (each distinct instruction group timed on a
+    bounded sample of its work, times its multiplicity) for C4/C5 and for
+    every one-thread figure."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import dataclasses
+    import cpu_baseline as cb
     import oracle
-    from helpers import HostPlanRunner
-    from seeml_amd import configs, planner, workmodel
+    from seeml_amd import planner
 
-    if oracle.ref_available():
-        lib, kind = oracle.ref(), "reference"
-        lib.set_threads(cores)
-    else:
-        lib, kind, cores = oracle.oracle(), "port", 1
-    flops = sum(workmodel.work(i)["flops"] for i in plan.train)
-    est_s = flops / 150e9 / max(1, cores / 16)
-    sample_plan, sample_w, note = plan, w, "the GPU run's plan"
-    if est_s > budget_s:
-        rows = w.seq if w.cfg.token_input else max(64, int(w.cfg.batch * budget_s / est_s) // 64 * 64)
-        cfg = dataclasses.replace(w.cfg, batch=rows)
-        sample_w = dataclasses.replace(w, cfg=cfg)
-        sample_plan = planner.compile_update(w.model, cfg)
-        note = (f"the same model and weights compiled at batch {rows} "
-                f"({'one sequence' if w.cfg.token_input else 'rows'}) instead of {w.cfg.batch}")
-    if sample_plan.blob is None:  # the bench released the host copy after upload
-        sample_plan = planner.compile_update(w.model, w.cfg)
-    r = HostPlanRunner(sample_plan, lib)
-    x, y = configs.batch(sample_w, 0)
-    n_warm = 1 if est_s * sample_w.cfg.batch / w.cfg.batch < budget_s / 4 else 0
-    for _ in range(n_warm):
-        r.train_step(x, y)
-    t0 = time.perf_counter()
-    r.train_step(x, y)
-    one = time.perf_counter() - t0
-    n = max(1, min(5, int(budget_s / max(one, 1e-3)))) - 1
-    t0 = time.perf_counter()
-    for _ in range(n):
-        r.train_step(x, y)
-    dt = one + (time.perf_counter() - t0)
-    steps = n + 1
-    tokens = sample_w.cfg.batch * steps
-    return dict(value=tokens / dt, unit="tokens/s", cores=cores, kind=kind,
-                sample=f"{steps} train step(s) of {note}, {n_warm} warm-up; "
-                       f"{dt / steps * 1e3:.1f} ms/step for {sample_w.cfg.batch} tokens")
+    if not oracle.ref_available():
+        raise RuntimeError("oracle/_ref is not built (the reference sources were absent)")
+    if w.name in cb.STEP_SLOPE and plan.blob is None:  # released after upload
+        plan = planner.compile_update(w.model, w.cfg)
+    return cb.measure(w, plan, cores)
 
 
 def measured_traffic(kernel: str):
@@ -116,6 +87,8 @@ def main():
     ap.add_argument("--no-autotune", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-reps", type=int, default=3)
+    ap.add_argument("--slope-lo", type=int, default=4)
+    ap.add_argument("--slope-hi", type=int, default=12)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -203,6 +176,28 @@ def main():
     tokens_per_s = w.cfg.batch * args.steps / dt
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.1f} tok/s")
 
+    # The reference bench's method (tool/seeml_bench.cc:288-310): per-step
+    # time = the slope between a steps-lo and a steps-hi run, median of 3
+    # (reported beside the contract's K-step figure; outside its timing).
+    e.mark_timed(PROGRAM_TRAIN, [])
+    losses.append(e.train_step(*batches[0]))  # the unsplit graph's first replay, untimed
+    slopes = []
+    lo, hi = args.slope_lo, args.slope_hi
+    for _ in range(3 if hi > lo else 0):
+        walls = []
+        for n in (lo, hi):
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for s in range(n):
+                xb, yb = batches[s % 2]
+                losses.append(e.train_step(xb, yb))
+            torch.cuda.synchronize()
+            walls.append(time.perf_counter() - t1)
+        slopes.append((walls[1] - walls[0]) / (hi - lo) * 1e3)
+    slope_ms = float(np.median(slopes)) if slopes else None
+    if slope_ms:
+        log(f"steps-{lo}/{hi} slope: {slope_ms:.3f} ms/step (median of 3)")
+
     dom_ms = float(np.mean(np.concatenate(launch_ms)))
     if dom_row["cls"] == "mfma" or (dom_row["cls"] == "attn" and dom_row["flops"]):
         achieved = dom_row["flops"] / (dom_ms * 1e-3) / 1e12
@@ -229,7 +224,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cores = min(16, os.cpu_count() or 1)
+        # this process's cores, capped at a GPU box's CPU share per GPU (16)
+        cores = min(16, len(os.sched_getaffinity(0)))
         log(f"cpu baseline on {cores} cores ...")
         try:
             cpu = cpu_baseline(w, plan, cores)
@@ -244,6 +240,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_slope": round(slope_ms, 4) if slope_ms else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
