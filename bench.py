@@ -257,6 +257,8 @@ def main():
         "gemm_dense_mfma_util": summ["gemm_dense_mfma_util"],
         "gemm_all_mfma_util": summ["gemm_all_mfma_util"],
         "hbm_kernels_gbps": summ["hbm_kernels_gbps"],
+        "hbm_elementwise_gbps": summ["hbm_elementwise_gbps"],
+        "hbm_skinny_gemm_gbps": summ["hbm_skinny_gemm_gbps"],
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": by_op,

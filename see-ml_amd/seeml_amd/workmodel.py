@@ -144,7 +144,11 @@ def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: fl
     rows = [dict(work(ins, v), ms=t) for ins, t, v in zip(program, ms, variants)]
     dense = [r for r in rows if r["cls"] == "mfma"]
     gem_all = [r for r in rows if r["op"] in GEMMS]
-    hbm = [r for r in rows if r["cls"] == "hbm" and r["op"] not in GEMMS]
+    # every HBM-bound kernel, the skinny LoRA GEMMs (a dim = the rank)
+    # included; and the north star's narrower set, the elementwise, norm,
+    # RoPE, loss, embed and optimizer kernels
+    hbm = [r for r in rows if r["cls"] == "hbm"]
+    elementwise = [r for r in hbm if r["op"] not in GEMMS]
 
     def util(rs):
         t = sum(r["ms"] for r in rs) * 1e-3
@@ -170,4 +174,6 @@ def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: fl
         gemm_dense_mfma_util=util(dense), gemm_all_mfma_util=util(gem_all),
         hbm_kernels_gbps=gbps(hbm),
         hbm_kernels_frac=(gbps(hbm) / peak_gbps) if gbps(hbm) else None,
+        hbm_elementwise_gbps=gbps(elementwise),
+        hbm_skinny_gemm_gbps=gbps([r for r in hbm if r["op"] in GEMMS]),
     )
