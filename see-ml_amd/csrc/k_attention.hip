@@ -75,13 +75,24 @@ namespace {
 //
 // Pass 1 walks the causal key tiles for the row maximum m and the exp-sum l
 // (online: l = l * exp(m_old - m_new) + sum exp(s - m_new)), in the base-2
-// domain on the hardware exp2. Pass 2 recomputes the scores, forms
-// p = exp(s - m) * (1/l) (exact 0 for j > i), writes P
-// once and accumulates O^T = V^T P^T with the probabilities straight from
-// the score registers as the B operand (MFMA t's k index is the lane's own
+// domain on the hardware exp2, and parks each tile's raw dot products in
+// the lane's own slots of its P row. Pass 2 reads them back, forms
+// p = exp(s - m) * (1/l) (exact 0 for j > i), writes P over them and
+// accumulates O^T = V^T P^T with the probabilities straight from those
+// registers as the B operand (MFMA t's k index is the lane's own
 // accumulator element t). The row tail beyond the diagonal tile is written
-// as exact zeros. QK^T is computed twice; P is written once and never read
-// back, against the three P-sized passes of scores -> softmax -> PV.
+// as exact zeros. QK^T is computed once: the second pass costs a write and
+// a read of the causal half of P instead of a second score GEMM, and every
+// value and its order of evaluation are those of recomputing it. P's range
+// is the instruction's own output, so parking scores there disturbs no
+// other value (with P unused, the scores are all it ever holds).
+//
+// Each pass loads the next key tile into registers at the top of an
+// iteration, runs the tile's MFMAs and vector work, then stages the loaded
+// tile into the other LDS buffer ahead of the iteration's one barrier (the
+// order AttnDP uses). Measured on MI355X at C4's shape (B 8, S 1024, H 16,
+// d 128): about 0.40 ms per launch, 86 TFLOP/s of causal QK^T + PV; the
+// MFMAs alone, without the parked-score and P traffic, take 0.34 ms.
 //
 // Heavy (late) query blocks are scheduled first, for causal load balance.
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -220,56 +231,51 @@ __device__ __forceinline__ void StoreRow(float* __restrict__ out, const floatx16
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d,
-    int pstore) {
-  constexpr int TS = KvTile<D>::kStride;
+// One wavefront's share of the forward: queries qw .. qw+31 of one (b, h),
+// key tiles 0 .. tiles_w-1 (the last one its diagonal tile), inside a
+// workgroup that stages tiles 0 .. tiles_wg-1. CHECKED: some of the
+// wavefront's rows lie past S (the last query block of a ragged S); every
+// other wavefront's P slots and parked scores need no per-lane test, since
+// its keys j <= qw + 31 < S. Every iteration ends in one barrier whatever
+// the wavefront computes, so the four wavefronts stay in step.
+template <int D, bool CHECKED>
+__device__ __forceinline__ void AttnFwdWave(const float* __restrict__ qh, const float* __restrict__ kh,
+                                            const float* __restrict__ vh, float* __restrict__ oh,
+                                            float* __restrict__ ph, float* __restrict__ lds, int S,
+                                            int64_t ld, int qw, int tiles_wg, int tiles_w, int h,
+                                            int r, float c2, int pstore) {
   constexpr int NB = D / 32;
-  __shared__ __align__(16) float kt[2][kAttnK * TS];
-  __shared__ __align__(16) float vt[2][kAttnK * TS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int h = lane >> 5, r = lane & 31;
-  const int BH = B * H;
-  const int nqb = (S + kAttnQ - 1) / kAttnQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / BH;
-  const int bh = static_cast<int>(blockIdx.x) % BH;
-  const int b = bh / H, hh = bh % H;
-  const int64_t ld = static_cast<int64_t>(H) * D;
-  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
-  const float* qh = q + head;
-  const float* kh = k + head;
-  const float* vh = v + head;
-  float* oh = o + head;
-  float* ph = probs + static_cast<int64_t>(bh) * S * S;
-
-  const int q0 = qb * kAttnQ;
-  const int qw = q0 + 32 * w;  // first query of this wavefront
-  const int i = qw + r;        // this lane's query
+  constexpr int kBuf = kAttnK * KvTile<D>::kStride;
+  const int i = qw + r;  // this lane's query
   const int ic = min(i, S - 1);
-  const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
-  const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
-  // Scores are kept in the base-2 domain: s2 = dot * (1/sqrt(d)) * log2(e),
-  // so exp(s - max) is the hardware exp2 of s2 - max2.
-  const float c2 = inv_sqrt_d * 1.44269504088896340736f;
-
-  float4 qf[D / 8];
+  const bool row_ok = !CHECKED || i < S;
+  float* prow = ph + static_cast<int64_t>(ic) * S;
+  // The lane's 16 slots of tile t in its P row (keys 8 q4 + 4h .. + 3).
+  auto store_row = [&](const floatx16& p, int t) {
 #pragma unroll
-  for (int g = 0; g < D / 8; ++g)
-    qf[g] = *reinterpret_cast<const float4*>(qh + static_cast<int64_t>(ic) * ld + 8 * g + 4 * h);
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int j = t * kAttnK + 8 * q4 + 4 * h;
+      if (!CHECKED || (row_ok && j < S))
+        *reinterpret_cast<float4*>(prow + j) =
+            make_float4(p[4 * q4], p[4 * q4 + 1], p[4 * q4 + 2], p[4 * q4 + 3]);
+    }
+  };
+  auto load_row = [&](int t) {
+    floatx16 p;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int j = t * kAttnK + 8 * q4 + 4 * h;
+      float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (!CHECKED || (row_ok && j < S)) x = *reinterpret_cast<const float4*>(prow + j);
+      p[4 * q4] = x.x;
+      p[4 * q4 + 1] = x.y;
+      p[4 * q4 + 2] = x.z;
+      p[4 * q4 + 3] = x.w;
+    }
+    return p;
+  };
 
-  // Both passes are software-pipelined by one key tile: iteration t stages
-  // K(t+1) (and in pass 2 V(t)) into LDS, then issues the score MFMAs of
-  // tile t+1 in the same basic block as the VALU work on tile t (the
-  // softmax statistics; the probabilities, their stores and P V), so the
-  // matrix cores run while the vector ALU works. The values and their order
-  // of evaluation are the unpipelined loop's: the results are the same bits.
-  // LDS: kt[(t+1) & 1] was last read by the scores of tile t-1 (iteration
-  // t-2), vt[t & 1] by P V of tile t-2; the barrier of iteration t-1 orders
-  // both before the stores of iteration t.
-
-  // ---- pass 1: row maximum and exp-sum ----
+  // ---- pass 1: scores parked in P, row maximum and exp-sum ----
   float m = -__builtin_inff(), l = 0.0f;
   auto stats = [&](floatx16 sc, int t, bool diag) {
 #pragma unroll
@@ -288,92 +294,64 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     l = l * alpha + ssum;
     m = mn;
   };
-  KvTile<D> ks, vs;
-  floatx16 sc;
+  {
+    float4 qf[D / 8];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
-  ks.load(kh, ld, 0, S);
-  ks.store(kt[0]);
-  __syncthreads();
-  if (tiles_w > 0) sc = ScoreTile<D>(kt[0], qf, h, r);
-  if (tiles_wg > 1) ks.load(kh, ld, kAttnK, S);
-  for (int t = 0; t < tiles_wg; ++t) {
-    if (t + 1 < tiles_wg) ks.store(kt[(t + 1) & 1]);
+    for (int g = 0; g < D / 8; ++g)
+      qf[g] = *reinterpret_cast<const float4*>(qh + static_cast<int64_t>(ic) * ld + 8 * g + 4 * h);
+    KvTile<D> ks;
+    ks.load(kh, ld, 0, S);
+    ks.store(lds);
     __syncthreads();
-    if (t + 2 < tiles_wg) ks.load(kh, ld, (t + 2) * kAttnK, S);
-    if (t + 1 < tiles_w) {
-      const floatx16 sn = ScoreTile<D>(kt[(t + 1) & 1], qf, h, r);
-      stats(sc, t, false);
-      sc = sn;
-      // One VALU op of tile t's statistics after each score MFMA of tile t+1.
-#pragma unroll
-      for (int x = 0; x < 2 * D / 4; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+    for (int t = 0; t < tiles_wg; ++t) {
+      if (t + 1 < tiles_wg) ks.load(kh, ld, (t + 1) * kAttnK, S);
+      if (t < tiles_w) {
+        const floatx16 sc = ScoreTile<D>(lds + (t & 1) * kBuf, qf, h, r);
+        store_row(sc, t);
+        stats(sc, t, t + 1 == tiles_w);
       }
-    } else if (t < tiles_w) {
-      stats(sc, t, true);
+      if (t + 1 < tiles_wg) ks.store(lds + ((t + 1) & 1) * kBuf);
+      __syncthreads();
     }
   }
 
-  // ---- pass 2: probabilities, P, O ----
+  // ---- pass 2: probabilities over the parked scores, P, O ----
   const float inv_l = 1.0f / l;
   floatx16 oacc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[nb][e] = 0.0f;
-  const bool row_ok = i < S;
   const bool store_p = (pstore & kAttnStoreP) != 0;
-  // Every row of the wavefront exists: its stores before the diagonal tile
-  // need no per-lane test.
-  const bool rows_ok = qw + 31 < S;
-  float* prow = ph + static_cast<int64_t>(ic) * S;
-  // Tile t's probabilities from its scores (in place), and their stores to P.
-  auto to_probs = [&](floatx16& p, int t, bool diag) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) p[e] = __builtin_amdgcn_exp2f(p[e] * c2 - m) * inv_l;
-    if (diag) MaskDiagonal(p, t, i, h, 0.0f);
-  };
-  auto store_row = [&](const floatx16& p, int t, bool checked) {
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int j = t * kAttnK + 8 * q4 + 4 * h;
-      if (!checked || (row_ok && j < S))
-        *reinterpret_cast<float4*>(prow + j) = make_float4(p[4 * q4], p[4 * q4 + 1], p[4 * q4 + 2], p[4 * q4 + 3]);
-    }
-  };
+  KvTile<D> vs;
+  vs.load(vh, ld, 0, S);
+  floatx16 sc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
-  ks.load(kh, ld, 0, S);
-  vs.load(vh, ld, 0, S);
-  ks.store(kt[0]);
+  if (tiles_w > 0) sc = load_row(0);
+  vs.store(lds);
   __syncthreads();
-  if (tiles_w > 0) sc = ScoreTile<D>(kt[0], qf, h, r);
-  if (tiles_wg > 1) ks.load(kh, ld, kAttnK, S);
   for (int t = 0; t < tiles_wg; ++t) {
-    if (t + 1 < tiles_wg) ks.store(kt[(t + 1) & 1]);
-    vs.store(vt[t & 1]);
-    __syncthreads();
-    if (t + 2 < tiles_wg) ks.load(kh, ld, (t + 2) * kAttnK, S);
     if (t + 1 < tiles_wg) vs.load(vh, ld, (t + 1) * kAttnK, S);
-    if (t + 1 < tiles_w) {
-      // Tile t lies wholly below the diagonal (j < i for every lane).
-      const floatx16 sn = ScoreTile<D>(kt[(t + 1) & 1], qf, h, r);
-      to_probs(sc, t, false);
-      if (store_p) store_row(sc, t, !rows_ok);
-      AccumulateTile<D>(vt[t & 1], sc, h, r, oacc);
+    if (t < tiles_w) {
+      // The lane reads back exactly the slots it parked (program order).
+      floatx16 sn;
+      if (t + 1 < tiles_w) sn = load_row(t + 1);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(sc[e] * c2 - m) * inv_l;
+      if (t + 1 == tiles_w) MaskDiagonal(sc, t, i, h, 0.0f);
+      if (store_p) store_row(sc, t);
+      AccumulateTile<D>(lds + (t & 1) * kBuf, sc, h, r, oacc);
       sc = sn;
-    } else if (t < tiles_w) {
-      to_probs(sc, t, true);
-      if (store_p) store_row(sc, t, true);
-      AccumulateTile<D>(vt[t & 1], sc, h, r, oacc);
     }
+    if (t + 1 < tiles_wg) vs.store(lds + ((t + 1) & 1) * kBuf);
+    __syncthreads();
   }
 
   if (row_ok) StoreRow<D>(oh + static_cast<int64_t>(i) * ld, oacc, h);
   // Causal tail: columns past this wavefront's diagonal tile are exact 0.
   if (!(pstore & kAttnStoreTail)) return;
+  const int lane = 32 * h + r;
   const int zc = tiles_w * kAttnK;
   for (int rr = 0; rr < 32; ++rr) {
     const int row = qw + rr;
@@ -382,6 +360,43 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     for (int c4 = zc / 4 + lane; c4 < S / 4; c4 += 64)
       *reinterpret_cast<float4*>(pz + 4 * c4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d,
+    int pstore) {
+  // One double buffer of key tiles serves both passes: pass 1 stages K
+  // there, pass 2 V (pass 1's last barrier orders its reads before pass 2's
+  // first stores).
+  __shared__ __align__(16) float lds[2 * kAttnK * KvTile<D>::kStride];
+  const int lane = threadIdx.x & 63;
+  // The wavefront index is uniform; saying so keeps every branch on the
+  // tile counts scalar.
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int h = lane >> 5, r = lane & 31;
+  const int BH = B * H;
+  const int nqb = (S + kAttnQ - 1) / kAttnQ;
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / BH;
+  const int bh = static_cast<int>(blockIdx.x) % BH;
+  const int b = bh / H, hh = bh % H;
+  const int64_t ld = static_cast<int64_t>(H) * D;
+  const int64_t head = static_cast<int64_t>(b) * S * ld + static_cast<int64_t>(hh) * D;
+  float* ph = probs + static_cast<int64_t>(bh) * S * S;
+  const int q0 = qb * kAttnQ;
+  const int qw = q0 + 32 * w;  // first query of this wavefront
+  const int tiles_wg = min((min(q0 + kAttnQ, S) - 1) / kAttnK + 1, (S + kAttnK - 1) / kAttnK);
+  const int tiles_w = qw < S ? qw / kAttnK + 1 : 0;
+  // Scores are kept in the base-2 domain: s2 = dot * (1/sqrt(d)) * log2(e),
+  // so exp(s - max) is the hardware exp2 of s2 - max2.
+  const float c2 = inv_sqrt_d * 1.44269504088896340736f;
+  if (qw + 31 < S)
+    AttnFwdWave<D, false>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw, tiles_wg,
+                          tiles_w, h, r, c2, pstore);
+  else
+    AttnFwdWave<D, true>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw, tiles_wg,
+                         tiles_w, h, r, c2, pstore);
 }
 
 // ---- fused causal backward primitives (d = 64 or 128) ----------------------
