@@ -340,6 +340,15 @@ int seeml_hip_gemm_nt_q8(const float* A, const int8_t* B, float* C, uint64_t M, 
 /* GEMM with an explicit tile config / split count (autotuner arms, tests). */
 int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, uint64_t M,
                           uint64_t N, uint64_t K, int cfg, int splits, void* stream);
+/* The LoRA backward's two GEMMs over one stream x [T, D] in one pass (the
+ * engine fuses the plan's adjacent pair; tests call it directly): dt = x b^T
+ * (b [r_rd, D]) and db = t^T x (t [T, r_cs]), ranks <= 16, x scaled by
+ * `scale` as loaded when `scaled`. which: 1 = dt only, 2 = db only, 3 =
+ * both; each output has the same bits in every form. No reference
+ * counterpart: the reference runs the two GEMMs (gemm.cc:173-200). */
+int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const float* b,
+                               uint64_t r_rd, float* dt, const float* t, uint64_t r_cs, float* db,
+                               int which, int scaled, float scale, void* stream);
 /* GEMM as two launches over column ranges (tests): columns [0, n_split) on
  * tile config `cfg`, the rest on `tail_cfg` (both one split); with `out`,
  * the fused AddEW out = addend + C. n_split = 0: one launch of `cfg`. */

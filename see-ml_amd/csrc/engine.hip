@@ -170,6 +170,7 @@ class Engine {
     for (int p = 0; p < 3; ++p)
       for (size_t i = 0; i < plan_.program[p].size(); ++i)
         if (IsGemmOp(plan_.program[p][i].opcode)) plans_[p][i] = PlanGemm(DescOf(plan_.program[p][i]));
+    for (int p = 0; p < 3; ++p) PlanDuals(p);
     if (Status s = SetStep(0); !s) return s;
     return HipOk(hipStreamSynchronize(stream_), "open");
   }
@@ -505,7 +506,11 @@ class Engine {
   size_t WorkspaceFor(int program, size_t idx) const {
     const UpdateInstruction& ins = plan_.program[program][idx];
     const auto op = static_cast<Op>(ins.opcode);
-    if (IsGemmOp(ins.opcode)) return plans_[program][idx].ws_bytes;
+    if (IsGemmOp(ins.opcode)) {
+      if (duals_[program][idx] >= 0)
+        return std::max(plans_[program][idx].ws_bytes, SkinnyDualWorkspace(DualRowdot(program, idx)));
+      return plans_[program][idx].ws_bytes;
+    }
     switch (op) {
       case Op::kMseFwd: return MseFwdWorkspace(ins.out[0]);
       case Op::kClipNorm: return ClipNormWorkspace(ins.out[0]);
@@ -524,6 +529,7 @@ class Engine {
       case Op::kNop: return Status::Ok();
       case Op::kGemmNN: case Op::kGemmNT: case Op::kGemmTN: case Op::kGemmAccNN:
       case Op::kGemmNNQ8: case Op::kGemmNTQ8:
+        if (duals_[program][idx] >= 0) return LaunchDual(program, idx, 0, nullptr, 1.0f, c);
         return LaunchGemm(DescOf(ins), plans_[program][idx], c);
       case Op::kAddEW: return AddEW(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
       case Op::kMulEW: return MulEW(RP(ins.in[0]), RP(ins.in[1]), WP(ins.in[2]), d0, c);
@@ -732,11 +738,73 @@ class Engine {
     PlanChains(program);
     PlanPointwiseRuns(program);
     PlanScaleFolds(program);
+    PlanDualRuns(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
     return HipOk(hipMemcpy(fused_segs_[program], segs.data(), bytes, hipMemcpyHostToDevice),
                  "fused AdamW table upload");
+  }
+
+  // Dual skinny pairs (kernels.h LaunchSkinnyDual): adjacent rowdot and
+  // colsum GEMMs on the skinny kernels streaming one operand (the LoRA
+  // backward's dt = du B^T and dB = t^T du). Every run of either, eager or
+  // fused, takes the dual kernel, so a pair launched as one pass and its two
+  // single launches give the same bits. As one launch the pair reads all its
+  // operands before it writes: the first's writes must not overlap what the
+  // second depends on, and the two outputs must be disjoint.
+  void PlanDuals(int program) {
+    const auto& prog = plan_.program[program];
+    duals_[program].assign(prog.size(), -1);
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      const UpdateInstruction& g0 = prog[i];
+      const UpdateInstruction& g1 = prog[i + 1];
+      if (!IsGemmOp(g0.opcode) || !IsGemmOp(g1.opcode) || g0.flags != 0 || g1.flags != 0) continue;
+      if (plans_[program][i].cfg != GemmSkinnyConfig() ||
+          plans_[program][i + 1].cfg != GemmSkinnyConfig())
+        continue;
+      const GemmDesc d0 = DescOf(g0), d1 = DescOf(g1);
+      const bool rd_first = SkinnyKindOf(d0) == SkinnyKind::kRowDot;
+      if (!SkinnyDualFits(rd_first ? d0 : d1, rd_first ? d1 : d0)) continue;
+      Ranges w0, w1;
+      if (!WriteRangesOf(g0, &w0) || !WriteRangesOf(g1, &w1)) continue;
+      bool clash = false;
+      for (const auto& w : w0)
+        if (Overlaps(depends_[program][i + 1], w.first, w.second) || Overlaps(w1, w.first, w.second))
+          clash = true;
+      if (clash) continue;
+      duals_[program][i] = static_cast<int64_t>(i + 1);
+      duals_[program][i + 1] = static_cast<int64_t>(i);
+      ++i;
+    }
+  }
+  // The rowdot and colsum descriptors of the pair instruction idx belongs to.
+  GemmDesc DualRowdot(int program, size_t idx) const {
+    const size_t j = static_cast<size_t>(duals_[program][idx]);
+    const GemmDesc d = DescOf(plan_.program[program][idx]);
+    return SkinnyKindOf(d) == SkinnyKind::kRowDot ? d : DescOf(plan_.program[program][j]);
+  }
+  // Launches instruction idx's output (which 0) or both of its pair's (which
+  // 3) on the dual kernel; fold_x: the pair's stream is a folded Scale's
+  // input, scaled by fold_alpha as loaded.
+  Status LaunchDual(int program, size_t idx, int which, const float* fold_x, float fold_alpha,
+                    const Ctx& c) const {
+    const size_t j = static_cast<size_t>(duals_[program][idx]);
+    GemmDesc a = DescOf(plan_.program[program][idx]), b = DescOf(plan_.program[program][j]);
+    const bool a_rd = SkinnyKindOf(a) == SkinnyKind::kRowDot;
+    GemmDesc& rd = a_rd ? a : b;
+    GemmDesc& cs = a_rd ? b : a;
+    if (fold_x) {
+      int64_t elems = 0;
+      const void* stream = SkinnyStream(cs, &elems);
+      if (cs.A == stream) cs.A = fold_x;
+      else cs.B = fold_x;
+      rd.A = fold_x;
+      rd.scale_stream = cs.scale_stream = true;
+      rd.stream_scale = cs.stream_scale = fold_alpha;
+    }
+    if (which == 0) which = a_rd ? 1 : 2;
+    return LaunchSkinnyDual(rd, cs, which, c);
   }
 
   // Fused chains, each launched as one kernel when its results are provably
@@ -764,7 +832,7 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -1044,6 +1112,40 @@ class Engine {
               [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
   }
 
+  // Dual pairs outside every other fusion run as one launch (kDual); a pair
+  // among a scale fold's consumers launches once inside the fold.
+  void PlanDualRuns(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      if (duals_[program][i] != static_cast<int64_t>(i + 1) || taken[i] || taken[i + 1]) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = 2;
+      run.kind = ChainKind::kDual;
+      chains_[program].push_back(run);
+      ++i;
+    }
+    std::sort(chains_[program].begin(), chains_[program].end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  // The consumers of a scale fold from idx on: a dual pair inside the fold
+  // launches once (returns 2), any other consumer alone (returns 1).
+  size_t FoldStep(int program, const ChainRun& run, size_t idx, const Ctx& c, Status* st) {
+    if (duals_[program][idx] == static_cast<int64_t>(idx + 1) && idx + 1 < run.first + run.count) {
+      *st = LaunchDual(program, idx, 3, run.fold_x, run.fold_alpha, c);
+      return 2;
+    }
+    *st = LaunchFolded(program, run, idx, c);
+    return 1;
+  }
+
   // Consumer idx of a scale fold, reading x with the factor applied.
   Status LaunchFolded(int program, const ChainRun& run, size_t idx, const Ctx& c) {
     GemmDesc d = DescOf(plan_.program[program][idx]);
@@ -1260,9 +1362,13 @@ class Engine {
       }
       case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
       case ChainKind::kScaleFold:
-        for (size_t k = run.first + 1; k < run.first + run.count; ++k)
-          if (Status s = LaunchFolded(program, run, k, c); !s) return s;
+        for (size_t k = run.first + 1; k < run.first + run.count;) {
+          Status s = Status::Ok();
+          k += FoldStep(program, run, k, c, &s);
+          if (!s) return s;
+        }
         return Status::Ok();
+      case ChainKind::kDual: return LaunchDual(program, run.first, 3, nullptr, 1.0f, c);
       default: return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
     }
   }
@@ -1911,9 +2017,11 @@ class Engine {
           const ChainRun& run = chains[fq++];
           if (run.kind == ChainKind::kScaleFold) {  // timed launch by launch
             (void)hipEventRecord(ev[i + 1], stream_);  // the Scale launches nothing
-            for (size_t k = i + 1; k < i + run.count && result; ++k) {
-              result = LaunchFolded(program, run, k, c);
-              (void)hipEventRecord(ev[k + 1], stream_);
+            for (size_t k = i + 1; k < i + run.count && result;) {
+              const size_t step = FoldStep(program, run, k, c, &result);
+              // A dual pair's one launch is timed on its first instruction.
+              for (size_t e = 0; e < step; ++e) (void)hipEventRecord(ev[k + 1 + e], stream_);
+              k += step;
             }
             if (!result) break;
             i += run.count;
@@ -2026,9 +2134,15 @@ class Engine {
     const ChainRun* run = ChainAt(program, idx);
     if (run && run->kind == ChainKind::kScaleFold) {
       if (idx == run->first) return "in the next GEMMs' loads";
+      const int64_t pair = duals_[program][idx];
+      if (pair >= 0 && pair >= static_cast<int64_t>(run->first) &&
+          pair < static_cast<int64_t>(run->first + run->count))
+        return pair > static_cast<int64_t>(idx) ? "skinny/dual dt+dB scaled loads" : "in the dual pass";
       return std::string(SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])))) +
              " scaled loads";
     }
+    if (run && run->kind == ChainKind::kDual)
+      return idx == run->first ? "skinny/dual dt+dB" : "in the dual pass";
     if (run && idx != run->first) {
       switch (run->kind) {
         case ChainKind::kDense: return "in GEMM epilogue";
@@ -2097,6 +2211,7 @@ class Engine {
 
   DecodedPlan plan_;
   std::vector<GemmPlan> plans_[3];
+  std::vector<int64_t> duals_[3];         // per instruction: its dual partner, or -1 (PlanDuals)
   int device_ = 0;
   hipStream_t stream_ = nullptr;
   uint8_t* arena_ = nullptr;
@@ -2501,6 +2616,19 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
                           : layout == 2 ? seeml_hip::GemmTNDesc(A, B, C, M, N, K)
                                         : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
   return RunGemm(d, stream, cfg, splits);
+}
+int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const float* b,
+                               uint64_t r_rd, float* dt, const float* t, uint64_t r_cs, float* db,
+                               int which, int scaled, float scale, void* stream) {
+  seeml_hip::GemmDesc rd = seeml_hip::GemmNTDesc(x, b, dt, T, r_rd, D);
+  seeml_hip::GemmDesc cs = seeml_hip::GemmTNDesc(t, x, db, r_cs, D, T);
+  rd.scale_stream = cs.scale_stream = scaled != 0;
+  rd.stream_scale = cs.stream_scale = scale;
+  if (!seeml_hip::SkinnyDualFits(rd, cs))
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
+                                                     "Gemm: the pair does not fit the dual skinny pass"));
+  SEEML_CTX(seeml_hip::SkinnyDualWorkspace(rd));
+  return seeml_hip::Report(seeml_hip::LaunchSkinnyDual(rd, cs, which, ctx));
 }
 int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
                                 uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,

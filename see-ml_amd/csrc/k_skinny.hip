@@ -462,6 +462,220 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
   }
 }
 
+// ---- dual: rowdot and colsum over one stream ---------------------------------
+//
+// The LoRA backward streams du twice: dt = du B^T (rowdot) and dB = t^T du
+// (colsum). This pass reads the [T, D] stream X once for both. A workgroup
+// owns a tile of 128 rows x 256 columns and walks it in four chunks of 32
+// rows, the next chunk's loads in flight: each wavefront loads its 64
+// columns of the chunk in the colsum layout (lane (q, c): X[row 4u + q][4c
+// .. 4c + 3], 4 rows x 256 B per instruction) and runs the colsum MFMAs
+// straight from those registers, then stages the chunk in LDS, from which
+// two wavefronts run the rowdot MFMAs of its two 16-row blocks across the
+// tile's 256 columns (lane (q, c): row c, columns 16g + 4q .. + 3, B
+// fragments held in registers for the tile).
+// Partials go to the workspace: one per 256-column block for each dt row,
+// one per 128-row block for each dB column; skinny_dual_finish sums them in
+// block order and applies each output's epilogue. Either output may be
+// left out (the engine's one-instruction form); each output's summation
+// order is the same either way, so the pair and its two single launches
+// give the same bits.
+
+constexpr int kDualRows = 128;  // rows per workgroup (four chunks)
+constexpr int kDualChunk = 32;  // rows staged in LDS at a time
+constexpr int kDualCols = 256;  // columns per workgroup (4 wavefronts x 64)
+constexpr int kDualR = 16;      // partial stride: outputs per row / column
+
+struct DualArgs {
+  const float* X;
+  int64_t ldx, T, D;
+  int scale_stream;
+  float stream_scale;
+  // rowdot: Crd(row, n) = epi(sum_d X[row][d] Bf(n, d)), n < r_rd
+  int r_rd;
+  const float* Bf;
+  int64_t ldb;
+  int b_kc;
+  float* Crd;
+  int64_t ldc_rd;
+  float alpha_rd;
+  int acc_rd;
+  const float* bias_rd;
+  int act_rd;
+  // colsum: C at (w = d, n') = epi(sum_row X[row][d] Y[row][n']), n' < r_cs;
+  // stored at C[w * ldc + n'] when big_is_m, else C[n' * ldc + w]
+  int r_cs;
+  const float* Y;
+  int64_t ldy;
+  float* Ccs;
+  int64_t ldc_cs;
+  int big_is_m;
+  float alpha_cs;
+  int acc_cs;
+  const float* bias_cs;
+  int act_cs;
+  float* ws_rd;  // [ncb][T][16]
+  float* ws_cs;  // [nrb][D][16]
+  int64_t ncb, nrb;
+};
+
+__device__ __forceinline__ float DualEpi(float acc, float alpha, int accumulate, const float* C,
+                                         int64_t at, const float* bias, int64_t col, int act) {
+  float val = alpha * acc;
+  if (accumulate) val = C[at] + val;
+  if (bias) val = val + bias[col];
+  return dev_act(act, val);
+}
+
+template <bool RD, bool CS>
+__global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
+  __shared__ __align__(16) float tile[kDualChunk][kDualCols + 4];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kDualRows;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kDualCols;
+  const int64_t wl = c0 + 64 * w + 4 * c;  // this lane's four colsum columns
+  const bool w_ok = wl < p.D;               // D % 4 == 0: wholly in or out
+  // Chunk ch's stream rows in the colsum layout (and Y's values for them).
+  auto load = [&](int ch, float4 (&x)[kDualChunk / 4], float (&y)[kDualChunk / 4]) {
+#pragma unroll
+    for (int u = 0; u < kDualChunk / 4; ++u) {
+      const int64_t row = r0 + ch * kDualChunk + 4 * u + q;
+      const bool in = row < p.T;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (in && w_ok) {
+        v = *reinterpret_cast<const float4*>(p.X + row * p.ldx + wl);
+        if (p.scale_stream)
+          v = make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
+                          p.stream_scale * v.w);
+      }
+      x[u] = v;
+      y[u] = CS && in && c < p.r_cs ? p.Y[row * p.ldy + c] : 0.0f;
+    }
+  };
+  float4 xs[2][kDualChunk / 4];
+  float ys[2][kDualChunk / 4];
+  load(0, xs[0], ys[0]);
+  // Rowdot B fragments for the tile: Bf(n = c, c0 + 16g + 4q + j).
+  float4 bf[16];
+  if constexpr (RD) {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const int64_t k0 = c0 + 16 * g + 4 * q;
+      const bool in = c < p.r_rd && k0 < p.D;
+      if (p.b_kc) {
+        bf[g] = in ? *reinterpret_cast<const float4*>(p.Bf + c * p.ldb + k0)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      } else {
+        bf[g].x = in ? p.Bf[(k0 + 0) * p.ldb + c] : 0.0f;
+        bf[g].y = in ? p.Bf[(k0 + 1) * p.ldb + c] : 0.0f;
+        bf[g].z = in ? p.Bf[(k0 + 2) * p.ldb + c] : 0.0f;
+        bf[g].w = in ? p.Bf[(k0 + 3) * p.ldb + c] : 0.0f;
+      }
+    }
+  }
+  floatx4 cs[4];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) cs[c4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int kChunks = kDualRows / kDualChunk;
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ++ch) {
+    float4 (&x)[kDualChunk / 4] = xs[ch & 1];
+    const float (&y)[kDualChunk / 4] = ys[ch & 1];
+    if (ch + 1 < kChunks) load(ch + 1, xs[(ch + 1) & 1], ys[(ch + 1) & 1]);  // in flight
+    if constexpr (CS) {
+      // Row quads in order; MFMA c4 takes column component c4 (as skinny_colsum).
+#pragma unroll
+      for (int u = 0; u < kDualChunk / 4; ++u) {
+        cs[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, y[u], cs[0], 0, 0, 0);
+        cs[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, y[u], cs[1], 0, 0, 0);
+        cs[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, y[u], cs[2], 0, 0, 0);
+        cs[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, y[u], cs[3], 0, 0, 0);
+      }
+    }
+    if constexpr (RD) {
+#pragma unroll
+      for (int u = 0; u < kDualChunk / 4; ++u)
+        *reinterpret_cast<float4*>(&tile[4 * u + q][64 * w + 4 * c]) = x[u];
+      __syncthreads();
+      // The chunk's two 16-row blocks go to wavefronts 2(ch % 2) and
+      // 2(ch % 2) + 1: rows of block j = w % 2, the tile's 16 column groups
+      // in order (as skinny_rowdot's slice of a wavefront).
+      if ((w >> 1) == (ch & 1)) {
+        const int j = w & 1;
+        floatx4 rd = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+          const float4 a = *reinterpret_cast<const float4*>(&tile[16 * j + c][16 * g + 4 * q]);
+          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bf[g].x, rd, 0, 0, 0);
+          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bf[g].y, rd, 0, 0, 0);
+          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bf[g].z, rd, 0, 0, 0);
+          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bf[g].w, rd, 0, 0, 0);
+        }
+        // Lane (q, c) element v: row (block start) + 4q + v, n = c.
+        float* part = p.ws_rd + (static_cast<int64_t>(blockIdx.y) * p.T) * kDualR;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = r0 + ch * kDualChunk + 16 * j + 4 * q + v;
+          if (row < p.T) part[row * kDualR + c] = rd[v];
+        }
+      }
+      __syncthreads();  // the next chunk overwrites the tile
+    }
+  }
+  if constexpr (CS) {
+    // Element v of cs[c4] at lane (q, c): column c0 + 64w + 4(4q + v) + c4, n' = c.
+    float* part = p.ws_cs + (static_cast<int64_t>(blockIdx.x) * p.D) * kDualR;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t col = c0 + 64 * w + 4 * (4 * q + v) + c4;
+        if (col < p.D) part[col * kDualR + c] = cs[c4][v];
+      }
+  }
+}
+
+// Sum of n partials src[0], src[stride], .. in index order, loaded 16 at a
+// time so each batch's loads are in flight together.
+__device__ __forceinline__ float SumPartials(const float* __restrict__ src, int64_t n, int64_t stride) {
+  float s = src[0];
+  for (int64_t b0 = 1; b0 < n; b0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = b0 + u < n ? src[(b0 + u) * stride] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (b0 + u < n) s += v[u];
+  }
+  return s;
+}
+
+// Sums the partials in block order and applies each output's epilogue:
+// indices [0, T * r_rd) are dt outputs, then [.., + D * r_cs) dB outputs.
+template <bool RD, bool CS>
+__global__ __launch_bounds__(kThreads) void skinny_dual_finish(DualArgs p) {
+  const int64_t n_rd = RD ? p.T * p.r_rd : 0, n_cs = CS ? p.D * p.r_cs : 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < n_rd + n_cs;
+       idx += stride) {
+    if (idx < n_rd) {
+      const int64_t row = idx / p.r_rd, n = idx % p.r_rd;
+      const float s = SumPartials(p.ws_rd + row * kDualR + n, p.ncb, p.T * kDualR);
+      const int64_t at = row * p.ldc_rd + n;
+      p.Crd[at] = DualEpi(s, p.alpha_rd, p.acc_rd, p.Crd, at, p.bias_rd, n, p.act_rd);
+    } else {
+      const int64_t j = idx - n_rd;
+      const int64_t col = j / p.r_cs, n = j % p.r_cs;
+      const float s = SumPartials(p.ws_cs + col * kDualR + n, p.nrb, p.D * kDualR);
+      const int64_t m = p.big_is_m ? col : n, nn = p.big_is_m ? n : col;
+      const int64_t at = m * p.ldc_cs + nn;
+      p.Ccs[at] = DualEpi(s, p.alpha_cs, p.acc_cs, p.Ccs, at, p.bias_cs, nn, p.act_cs);
+    }
+  }
+}
+
 bool Vec4(const void* base, int64_t ld) { return aligned16(base) && ld % 4 == 0; }
 
 int64_t ColsumGroups(int64_t W, int64_t K) {
@@ -526,6 +740,87 @@ size_t SkinnyWorkspace(const GemmDesc& d) {
   const bool big_m = d.N <= 64 && d.M >= 128;
   const int64_t W = big_m ? d.M : d.N, R = big_m ? d.N : d.M;
   return static_cast<size_t>(ColsumGroups(W, d.K)) * W * R * sizeof(float);
+}
+
+bool SkinnyDualFits(const GemmDesc& rd, const GemmDesc& cs) {
+  if (SkinnyKindOf(rd) != SkinnyKind::kRowDot || SkinnyKindOf(cs) != SkinnyKind::kColSum)
+    return false;
+  int64_t elems = 0;
+  if (SkinnyStream(cs, &elems) != rd.A || elems != rd.M * rd.K) return false;
+  const bool big_is_m = cs.N <= 64 && cs.M >= 128;
+  const int64_t W = big_is_m ? cs.M : cs.N, R = big_is_m ? cs.N : cs.M;
+  const int64_t ldx = big_is_m ? cs.lda : cs.ldb;
+  if (cs.K != rd.M || W != rd.K || ldx != rd.lda) return false;
+  if (rd.N > kDualR || R > kDualR) return false;
+  if (rd.scale_stream != cs.scale_stream || (rd.scale_stream && rd.stream_scale != cs.stream_scale))
+    return false;
+  const int64_t nrb = (rd.M + kDualRows - 1) / kDualRows, ncb = (rd.K + kDualCols - 1) / kDualCols;
+  return nrb <= 0x7FFFFFFF && ncb <= 65535;
+}
+
+size_t SkinnyDualWorkspace(const GemmDesc& rd) {
+  const int64_t nrb = (rd.M + kDualRows - 1) / kDualRows, ncb = (rd.K + kDualCols - 1) / kDualCols;
+  return static_cast<size_t>(ncb * rd.M + nrb * rd.K) * kDualR * sizeof(float);
+}
+
+Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const Ctx& ctx) {
+  if (!SkinnyDualFits(rd, cs) || which < 1 || which > 3)
+    return Status::Fail(kUnitEngine, "Gemm: the pair does not fit the dual skinny pass");
+  const size_t need = SkinnyDualWorkspace(rd);
+  if (ctx.ws_bytes < need || !aligned16(ctx.ws))
+    return Status::Fail(kUnitEngine, "Gemm: workspace too small for the dual skinny pass");
+  DualArgs a{};
+  a.X = static_cast<const float*>(rd.A);
+  a.ldx = rd.lda;
+  a.T = rd.M;
+  a.D = rd.K;
+  a.scale_stream = rd.scale_stream ? 1 : 0;
+  a.stream_scale = rd.stream_scale;
+  a.r_rd = static_cast<int>(rd.N);
+  a.Bf = static_cast<const float*>(rd.B);
+  a.ldb = rd.ldb;
+  a.b_kc = rd.b_kc ? 1 : 0;
+  a.Crd = rd.C;
+  a.ldc_rd = rd.ldc;
+  a.alpha_rd = rd.alpha;
+  a.acc_rd = rd.accumulate ? 1 : 0;
+  a.bias_rd = rd.bias;
+  a.act_rd = rd.act;
+  a.big_is_m = (cs.N <= 64 && cs.M >= 128) ? 1 : 0;
+  a.r_cs = static_cast<int>(a.big_is_m ? cs.N : cs.M);
+  a.Y = static_cast<const float*>(a.big_is_m ? cs.B : cs.A);
+  a.ldy = a.big_is_m ? cs.ldb : cs.lda;
+  a.Ccs = cs.C;
+  a.ldc_cs = cs.ldc;
+  a.alpha_cs = cs.alpha;
+  a.acc_cs = cs.accumulate ? 1 : 0;
+  a.bias_cs = cs.bias;
+  a.act_cs = cs.act;
+  a.nrb = (a.T + kDualRows - 1) / kDualRows;
+  a.ncb = (a.D + kDualCols - 1) / kDualCols;
+  a.ws_rd = static_cast<float*>(ctx.ws);
+  a.ws_cs = a.ws_rd + a.ncb * a.T * kDualR;
+  const dim3 grid(static_cast<unsigned>(a.nrb), static_cast<unsigned>(a.ncb));
+  const size_t outs = static_cast<size_t>((which & 1 ? a.T * a.r_rd : 0) + (which & 2 ? a.D * a.r_cs : 0));
+  const dim3 fgrid(grid_for(outs, kThreads, 4096));
+  switch (which) {
+    case 1:
+      hipLaunchKernelGGL((skinny_dual<true, false>), grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
+      hipLaunchKernelGGL((skinny_dual_finish<true, false>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((skinny_dual<false, true>), grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
+      hipLaunchKernelGGL((skinny_dual_finish<false, true>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((skinny_dual<true, true>), grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
+      hipLaunchKernelGGL((skinny_dual_finish<true, true>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+  }
+  return LaunchStatus("Gemm(skinny dual finish)");
 }
 
 namespace {

@@ -156,6 +156,16 @@ size_t SkinnyWorkspace(const GemmDesc& d);
 // null for other shapes: the one GemmDesc::scale_stream applies to.
 const void* SkinnyStream(const GemmDesc& d, int64_t* elems);
 Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx);
+// A rowdot and a colsum GEMM over the same stream X [T, D] (the LoRA
+// backward's dt = du B^T and dB = t^T du) in one pass over X: rd is the
+// rowdot (A = X), cs the colsum (its large operand X). Fits: both ranks
+// <= 16, one stream with one row stride, equal stream scaling. which: 1 =
+// rd's output only, 2 = cs's only, 3 = both; each output has the same bits
+// in every form. The caller proves the pair may run as one launch (neither
+// output overlaps the other or an operand the pair reads).
+bool SkinnyDualFits(const GemmDesc& rd, const GemmDesc& cs);
+size_t SkinnyDualWorkspace(const GemmDesc& rd);
+Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const Ctx& ctx);
 // The plan index that selects the skinny kernels (one past the tile configs).
 int GemmSkinnyConfig();
 

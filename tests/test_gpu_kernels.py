@@ -170,6 +170,33 @@ def test_gemm_skinny(env, orc, layout, M, N, K):
         assert rel_err(env.H(generic), got) <= TOL_STEP
 
 
+@pytest.mark.parametrize("T,D,r_rd,r_cs,scaled", [
+    (8192, 2048, 16, 16, 1), (4096, 512, 8, 8, 0), (300, 260, 5, 16, 1), (257, 1028, 16, 3, 0),
+    (256, 256, 1, 1, 1)])
+def test_skinny_dual_pass(env, orc, T, D, r_rd, r_cs, scaled):
+    """dt = x b^T and db = t^T x in one pass over x (the LoRA backward pair):
+    each output against the oracle's GEMM on the stream as the Scale would
+    have stored it, and bit-equal whether computed alone or with the other
+    (the engine's eager and fused forms). Ragged T and D, ranks below 16."""
+    alpha = f32(0.37)
+    x, b, t = rnd(T * D, 71), rnd(r_rd * D, 72), rnd(T * r_cs, 73)
+    xs = (alpha * x).astype(f32) if scaled else x
+    want_dt, want_db = np.zeros(T * r_rd, f32), np.zeros(r_cs * D, f32)
+    orc.gemm_nt(xs, b, want_dt, T, r_rd, D)
+    orc.gemm_tn(t, xs, want_db, r_cs, D, T)
+    outs = {}
+    for which in (3, 1, 2):
+        dt = env.T(np.full(T * r_rd, np.nan, f32))
+        db = env.T(np.full(r_cs * D, np.nan, f32))
+        env.call("seeml_hip_gemm_skinny_dual", env.T(x), T, D, env.T(b), r_rd, dt, env.T(t), r_cs, db,
+                 which, scaled, alpha)
+        outs[which] = (env.H(dt), env.H(db))
+    dt3, db3 = outs[3]
+    assert rel_err(dt3, want_dt) <= TOL_STEP and rel_err(db3, want_db) <= TOL_STEP
+    assert same_bits(outs[1][0], dt3) and same_bits(outs[2][1], db3)
+    assert np.all(np.isnan(outs[1][1])) and np.all(np.isnan(outs[2][0]))  # the other is untouched
+
+
 @pytest.mark.parametrize("layout,M,N,K,tail,n_split", [
     (1, 512, 1000, 256, 0, 768), (0, 300, 520, 128, 4, 384), (2, 256, 640, 96, 0, 512),
     (1, 256, 5504, 64, 4, 5120)])
