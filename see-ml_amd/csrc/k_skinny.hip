@@ -533,8 +533,9 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int q = lane >> 4, c = lane & 15;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kDualRows;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kDualCols;
+  // Column blocks vary fastest: neighbouring workgroups read whole rows.
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kDualRows;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kDualCols;
   const int64_t wl = c0 + 64 * w + 4 * c;  // this lane's four colsum columns
   const bool w_ok = wl < p.D;               // D % 4 == 0: wholly in or out
   // Chunk ch's stream rows in the colsum layout (and Y's values for them).
@@ -614,7 +615,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
           rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bf[g].w, rd, 0, 0, 0);
         }
         // Lane (q, c) element v: row (block start) + 4q + v, n = c.
-        float* part = p.ws_rd + (static_cast<int64_t>(blockIdx.y) * p.T) * kDualR;
+        float* part = p.ws_rd + (static_cast<int64_t>(blockIdx.x) * p.T) * kDualR;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int64_t row = r0 + ch * kDualChunk + 16 * j + 4 * q + v;
@@ -626,7 +627,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
   }
   if constexpr (CS) {
     // Element v of cs[c4] at lane (q, c): column c0 + 64w + 4(4q + v) + c4, n' = c.
-    float* part = p.ws_cs + (static_cast<int64_t>(blockIdx.x) * p.D) * kDualR;
+    float* part = p.ws_cs + (static_cast<int64_t>(blockIdx.y) * p.D) * kDualR;
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4)
 #pragma unroll
@@ -755,7 +756,7 @@ bool SkinnyDualFits(const GemmDesc& rd, const GemmDesc& cs) {
   if (rd.scale_stream != cs.scale_stream || (rd.scale_stream && rd.stream_scale != cs.stream_scale))
     return false;
   const int64_t nrb = (rd.M + kDualRows - 1) / kDualRows, ncb = (rd.K + kDualCols - 1) / kDualCols;
-  return nrb <= 0x7FFFFFFF && ncb <= 65535;
+  return ncb <= 0x7FFFFFFF && nrb <= 65535;
 }
 
 size_t SkinnyDualWorkspace(const GemmDesc& rd) {
@@ -800,7 +801,7 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
   a.ncb = (a.D + kDualCols - 1) / kDualCols;
   a.ws_rd = static_cast<float*>(ctx.ws);
   a.ws_cs = a.ws_rd + a.ncb * a.T * kDualR;
-  const dim3 grid(static_cast<unsigned>(a.nrb), static_cast<unsigned>(a.ncb));
+  const dim3 grid(static_cast<unsigned>(a.ncb), static_cast<unsigned>(a.nrb));
   const size_t outs = static_cast<size_t>((which & 1 ? a.T * a.r_rd : 0) + (which & 2 ? a.D * a.r_cs : 0));
   const dim3 fgrid(grid_for(outs, kThreads, 4096));
   switch (which) {

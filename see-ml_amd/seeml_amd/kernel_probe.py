@@ -4,6 +4,10 @@ plain copy of known size, for hardware-counter runs under rocprofv3:
   python3 -m seeml_amd.kernel_probe --layout NN --m 8192 --n 5504 --k 2048 \\
       --cfg 128x64x32/w4x1 --reps 3 --copy-mib 1024
 
+With --dual it launches the LoRA backward's dual skinny pass instead: the
+stream x [m, k] read once for dt = x b^T and db = t^T x, both of rank n
+(the stream scaled as loaded, as the engine's folded Scale does).
+
 Each dispatch's FETCH_SIZE / WRITE_SIZE (KiB) is read from the profiler's
 counter file; the copy's counters against its known 2 x copy-mib MiB of
 traffic calibrate the GEMM's. Inputs are seeded normals in device memory.
@@ -23,7 +27,9 @@ def main(argv=None):
     ap.add_argument("--m", type=int, required=True)
     ap.add_argument("--n", type=int, required=True)
     ap.add_argument("--k", type=int, required=True)
-    ap.add_argument("--cfg", required=True, help="tile config name, e.g. 128x64x32/w4x1")
+    ap.add_argument("--cfg", default="skinny", help="tile config name, e.g. 128x64x32/w4x1")
+    ap.add_argument("--dual", action="store_true",
+                    help="the dual skinny pass over x [m, k] at rank n (no --cfg)")
     ap.add_argument("--splits", type=int, default=1)
     ap.add_argument("--tail-cfg", default=None,
                     help="column split: tile config of columns [n-split, n) (two launches)")
@@ -51,7 +57,7 @@ def main(argv=None):
     s = torch.cuda.current_stream().cuda_stream
     if a.tail_cfg is not None and a.tail_cfg not in names:
         sys.exit(f"kernel_probe: unknown tile config {a.tail_cfg!r}; have {sorted(names)}")
-    for _ in range(a.reps):
+    for _ in range(a.reps if not a.dual else 0):
         if a.tail_cfg is not None:
             rc = L.seeml_hip_gemm_forced_split(LAYOUTS[a.layout], A.data_ptr(), B.data_ptr(),
                                                Cm.data_ptr(), M, N, K, cfg, names[a.tail_cfg],
@@ -61,6 +67,16 @@ def main(argv=None):
                                          M, N, K, cfg, a.splits, s)
         if rc != 0:
             sys.exit(f"kernel_probe: {_lib.kernel_error()}")
+    if a.dual:
+        b = torch.randn(N * K, device=dev, generator=g)
+        t = torch.randn(M * N, device=dev, generator=g)
+        dt = torch.empty(M * N, device=dev)
+        db = torch.empty(N * K, device=dev)
+        for _ in range(a.reps):
+            rc = L.seeml_hip_gemm_skinny_dual(A.data_ptr(), M, K, b.data_ptr(), N, dt.data_ptr(),
+                                              t.data_ptr(), N, db.data_ptr(), 3, 1, 0.5, s)
+            if rc != 0:
+                sys.exit(f"kernel_probe: {_lib.kernel_error()}")
     n = a.copy_mib * (1 << 20) // 4
     x = torch.randn(n, device=dev, generator=g)
     y = torch.empty(n, device=dev)
@@ -70,8 +86,8 @@ def main(argv=None):
             sys.exit(f"kernel_probe: {_lib.kernel_error()}")
     torch.cuda.synchronize()
     tail = f" | {a.tail_cfg} @ {a.n_split}" if a.tail_cfg is not None else ""
-    print(f"kernel_probe: {a.layout} {M}x{N}x{K} {a.cfg}{tail} x{a.reps}, copy {a.copy_mib} MiB x{a.reps}",
-          flush=True)
+    what = f"dual x {M}x{K} rank {N}" if a.dual else f"{a.layout} {M}x{N}x{K} {a.cfg}{tail}"
+    print(f"kernel_probe: {what} x{a.reps}, copy {a.copy_mib} MiB x{a.reps}", flush=True)
 
 
 if __name__ == "__main__":
