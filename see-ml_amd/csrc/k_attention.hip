@@ -91,8 +91,9 @@ namespace {
 // iteration, runs the tile's MFMAs and vector work, then stages the loaded
 // tile into the other LDS buffer ahead of the iteration's one barrier (the
 // order AttnDP uses). Measured on MI355X at C4's shape (B 8, S 1024, H 16,
-// d 128): about 0.40 ms per launch, 86 TFLOP/s of causal QK^T + PV; the
-// MFMAs alone, without the parked-score and P traffic, take 0.34 ms.
+// d 128): 0.40 ms per launch standalone and 0.37 ms inside the train graph
+// (92.7 TFLOP/s of causal QK^T + PV); the MFMAs alone, without the
+// parked-score and P traffic, take 0.34 ms standalone.
 //
 // Heavy (late) query blocks are scheduled first, for causal load balance.
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -426,7 +427,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dp_fused(
     const float* __restrict__ dout, const float* __restrict__ v, float* __restrict__ dp, int B,
     int S, int H, int tail) {
   __shared__ __align__(16) float vt[2][kAttnK * KvTile<D>::kStride];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // uniform
   const int h = lane >> 5, r = lane & 31;
   const int BH = B * H;
   const int nqb = (S + kAttnQ - 1) / kAttnQ;
@@ -499,7 +501,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
   constexpr int TS = KvTile<D>::kStride;
   constexpr int NB = D / 32;
   __shared__ __align__(16) float kt[2][kAttnK * TS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // uniform
   const int h = lane >> 5, r = lane & 31;
   const int BH = B * H;
   const int nqb = (S + kAttnQ - 1) / kAttnQ;
@@ -569,7 +572,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dkv_fused(
   constexpr int TS = KvTile<D>::kStride;
   constexpr int NB = D / 32;
   __shared__ __align__(16) float xt[2][kAttnK * TS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // uniform
   const int h = lane >> 5, r = lane & 31;
   const int BH = B * H;
   const int kb = static_cast<int>(blockIdx.x) / BH;  // early key blocks first

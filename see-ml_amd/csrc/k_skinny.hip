@@ -539,42 +539,56 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
   const int64_t wl = c0 + 64 * w + 4 * c;  // this lane's four colsum columns
   const bool w_ok = wl < p.D;               // D % 4 == 0: wholly in or out
   // Chunk ch's stream rows in the colsum layout (and Y's values for them).
+  // The loads are unconditional, from addresses clamped into the operands,
+  // so they issue back to back; rows past T, columns past D and ranks past
+  // r_cs are zeroed, and the stream scaled, where the values are used.
+  const int64_t wlc = w_ok ? wl : 0;
+  const int cy = min(c, p.r_cs - 1);
   auto load = [&](int ch, float4 (&x)[kDualChunk / 4], float (&y)[kDualChunk / 4]) {
 #pragma unroll
     for (int u = 0; u < kDualChunk / 4; ++u) {
-      const int64_t row = r0 + ch * kDualChunk + 4 * u + q;
-      const bool in = row < p.T;
-      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (in && w_ok) {
-        v = *reinterpret_cast<const float4*>(p.X + row * p.ldx + wl);
-        if (p.scale_stream)
-          v = make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
-                          p.stream_scale * v.w);
-      }
-      x[u] = v;
-      y[u] = CS && in && c < p.r_cs ? p.Y[row * p.ldy + c] : 0.0f;
+      const int64_t row = min<int64_t>(r0 + ch * kDualChunk + 4 * u + q, p.T - 1);
+      x[u] = *reinterpret_cast<const float4*>(p.X + row * p.ldx + wlc);
+      if constexpr (CS) y[u] = p.Y[row * p.ldy + cy];
+    }
+  };
+  // Chunk ch's loaded values as the pass uses them (in place).
+  auto prepare = [&](int ch, float4 (&x)[kDualChunk / 4], float (&y)[kDualChunk / 4]) {
+#pragma unroll
+    for (int u = 0; u < kDualChunk / 4; ++u) {
+      const bool in = r0 + ch * kDualChunk + 4 * u + q < p.T;
+      float4 v = x[u];
+      if (p.scale_stream)
+        v = make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
+                        p.stream_scale * v.w);
+      x[u] = in && w_ok ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (CS) y[u] = in && c < p.r_cs ? y[u] : 0.0f;
     }
   };
   float4 xs[2][kDualChunk / 4];
   float ys[2][kDualChunk / 4];
   load(0, xs[0], ys[0]);
   // Rowdot B fragments for the tile: Bf(n = c, c0 + 16g + 4q + j).
+  // Loaded from clamped addresses, then zeroed past r_rd and D (as the
+  // stream, so the loads issue back to back).
   float4 bf[16];
   if constexpr (RD) {
+    const int cb = min(c, p.r_rd - 1);
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
-      const int64_t k0 = c0 + 16 * g + 4 * q;
-      const bool in = c < p.r_rd && k0 < p.D;
+      const int64_t kc = min<int64_t>(c0 + 16 * g + 4 * q, p.D - 4);
       if (p.b_kc) {
-        bf[g] = in ? *reinterpret_cast<const float4*>(p.Bf + c * p.ldb + k0)
-                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        bf[g] = *reinterpret_cast<const float4*>(p.Bf + cb * p.ldb + kc);
       } else {
-        bf[g].x = in ? p.Bf[(k0 + 0) * p.ldb + c] : 0.0f;
-        bf[g].y = in ? p.Bf[(k0 + 1) * p.ldb + c] : 0.0f;
-        bf[g].z = in ? p.Bf[(k0 + 2) * p.ldb + c] : 0.0f;
-        bf[g].w = in ? p.Bf[(k0 + 3) * p.ldb + c] : 0.0f;
+        bf[g].x = p.Bf[(kc + 0) * p.ldb + cb];
+        bf[g].y = p.Bf[(kc + 1) * p.ldb + cb];
+        bf[g].z = p.Bf[(kc + 2) * p.ldb + cb];
+        bf[g].w = p.Bf[(kc + 3) * p.ldb + cb];
       }
     }
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+      if (!(c < p.r_rd && c0 + 16 * g + 4 * q < p.D)) bf[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   floatx4 cs[4];
 #pragma unroll
@@ -583,8 +597,9 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
 #pragma unroll
   for (int ch = 0; ch < kChunks; ++ch) {
     float4 (&x)[kDualChunk / 4] = xs[ch & 1];
-    const float (&y)[kDualChunk / 4] = ys[ch & 1];
+    float (&y)[kDualChunk / 4] = ys[ch & 1];
     if (ch + 1 < kChunks) load(ch + 1, xs[(ch + 1) & 1], ys[(ch + 1) & 1]);  // in flight
+    prepare(ch, x, y);
     if constexpr (CS) {
       // Row quads in order; MFMA c4 takes column component c4 (as skinny_colsum).
 #pragma unroll

@@ -457,9 +457,9 @@ def test_dense_scale_chains_are_planned(torch_gpu):
 
 
 def test_fusions_are_planned(torch_gpu):
-    """On a decoder the GEMM + AddEW fusion, the pointwise runs and the Scale
-    folds fire (so the graph == eager bitwise test above compares fused
-    against unfused launches): every AddEW reported inside a GEMM epilogue
+    """On a decoder the GEMM + AddEW fusion, the pointwise runs, the Scale
+    folds and the dual skinny pairs fire (so the graph == eager bitwise test
+    above compares fused against unfused launches): every AddEW reported inside a GEMM epilogue
     directly follows a GEMM reported "+AddEW"; an eager engine plans no
     fusion."""
     from seeml_amd import PROGRAM_TRAIN
@@ -480,6 +480,10 @@ def test_fusions_are_planned(torch_gpu):
     folds = [i for i, c in enumerate(ch) if c == "in the next GEMMs' loads"]
     assert folds, ch
     assert all(ch[i + 1].endswith("scaled loads") for i in folds)
+    # the LoRA backward's dt / dB pairs run as one dual pass over du
+    duals = [i for i, c in enumerate(ch) if c.startswith("skinny/dual")]
+    assert duals, ch
+    assert all(ch[i + 1] == "in the dual pass" for i in duals)
     e.close()
     e = engine(p, use_graph=False)
     e.train_step(x, y)
