@@ -8,6 +8,12 @@ With --dual it launches the LoRA backward's dual skinny pass instead: the
 stream x [m, k] read once for dt = x b^T and db = t^T x, both of rank n
 (the stream scaled as loaded, as the engine's folded Scale does).
 
+With --step CFG it runs one eager train step of a BASELINE config (every
+instruction dispatched on its own, batch 0), for per-dispatch counters of
+all of a step's kernels:
+
+  python3 -m seeml_amd.kernel_probe --step c4
+
 Each dispatch's FETCH_SIZE / WRITE_SIZE (KiB) is read from the profiler's
 counter file; the copy's counters against its known 2 x copy-mib MiB of
 traffic calibrate the GEMM's. Inputs are seeded normals in device memory.
@@ -23,10 +29,11 @@ LAYOUTS = {"NN": 0, "NT": 1, "TN": 2}
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
+    ap.add_argument("--step", default=None, help="one eager train step of this config")
     ap.add_argument("--layout", default="NN", choices=sorted(LAYOUTS))
-    ap.add_argument("--m", type=int, required=True)
-    ap.add_argument("--n", type=int, required=True)
-    ap.add_argument("--k", type=int, required=True)
+    ap.add_argument("--m", type=int, default=0)
+    ap.add_argument("--n", type=int, default=0)
+    ap.add_argument("--k", type=int, default=0)
     ap.add_argument("--cfg", default="skinny", help="tile config name, e.g. 128x64x32/w4x1")
     ap.add_argument("--dual", action="store_true",
                     help="the dual skinny pass over x [m, k] at rank n (no --cfg)")
@@ -37,6 +44,18 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=1024)
     a = ap.parse_args(argv)
+    if a.step:
+        from . import configs, planner
+        from .engine import DeviceUpdateEngine
+        w = configs.make(a.step)
+        plan = planner.compile_update(w.model, w.cfg, teacher=w.teacher)
+        e = DeviceUpdateEngine(plan.blob, use_graph=False)
+        x, y = configs.batch(w, 0)
+        print(f"kernel_probe: {a.step} eager step, loss {e.train_step(x, y)}", flush=True)
+        e.close()
+        return
+    if min(a.m, a.n, a.k) <= 0:
+        sys.exit("kernel_probe: --m, --n and --k are required (or --step)")
 
     import torch
     from . import _lib
