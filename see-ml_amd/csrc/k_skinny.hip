@@ -70,6 +70,16 @@ struct SkArgs {
   float stream_scale;
 };
 
+// v * scale where `keep`, else +0.0, with no branch: the mask is an AND of
+// the bits (a select of a float4 can be lowered to per-lane branches).
+__device__ __forceinline__ float4 Keep4(float4 v, bool keep, float scale) {
+  const unsigned m = 0u - static_cast<unsigned>(keep);
+  return make_float4(__uint_as_float(__float_as_uint(scale * v.x) & m),
+                     __uint_as_float(__float_as_uint(scale * v.y) & m),
+                     __uint_as_float(__float_as_uint(scale * v.z) & m),
+                     __uint_as_float(__float_as_uint(scale * v.w) & m));
+}
+
 __device__ __forceinline__ float4 ScaleLoaded(const SkArgs& p, float4 v) {
   if (!p.scale_stream) return v;
   return make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
@@ -466,14 +476,17 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
 //
 // The LoRA backward streams du twice: dt = du B^T (rowdot) and dB = t^T du
 // (colsum). This pass reads the [T, D] stream X once for both. A workgroup
-// owns a tile of 128 rows x 256 columns and walks it in four chunks of 32
-// rows, the next chunk's loads in flight: each wavefront loads its 64
-// columns of the chunk in the colsum layout (lane (q, c): X[row 4u + q][4c
-// .. 4c + 3], 4 rows x 256 B per instruction) and runs the colsum MFMAs
-// straight from those registers, then stages the chunk in LDS, from which
-// two wavefronts run the rowdot MFMAs of its two 16-row blocks across the
-// tile's 256 columns (lane (q, c): row c, columns 16g + 4q .. + 3, B
-// fragments held in registers for the tile).
+// owns a tile of 128 rows x 256 columns; wavefront w owns its 64 columns
+// over all 128 rows, eight strips of 16 rows (32 KB), and keeps six strips'
+// loads in flight (each strip's registers are reloaded as soon as it is
+// used), so nearly the whole stream is requested at entry:
+//  * colsum: lane (q, c) holds X[row 4u + q][4c .. 4c + 3] of the strip's
+//    quad u; MFMA c4 takes component c4 against the Y values of those rows
+//    (staged in LDS once per workgroup), rows in order;
+//  * rowdot: the wavefront writes the strip to its own LDS buffer and reads
+//    it back transposed (lane (q, c): row c, columns 16g + 4q .. + 3), so
+//    the MFMAs contract over its 64 columns with no workgroup barrier; the
+//    four wavefronts' partials are summed in wavefront order at the end.
 // Partials go to the workspace: one per 256-column block for each dt row,
 // one per 128-row block for each dB column; skinny_dual_finish sums them in
 // block order and applies each output's epilogue. Either output may be
@@ -481,10 +494,14 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
 // order is the same either way, so the pair and its two single launches
 // give the same bits.
 
-constexpr int kDualRows = 128;  // rows per workgroup (four chunks)
-constexpr int kDualChunk = 32;  // rows staged in LDS at a time
+constexpr int kDualRows = 128;  // rows per workgroup
 constexpr int kDualCols = 256;  // columns per workgroup (4 wavefronts x 64)
 constexpr int kDualR = 16;      // partial stride: outputs per row / column
+constexpr int kDualStrip = 16;  // rows per strip (one rowdot MFMA block)
+constexpr int kDualStrips = kDualRows / kDualStrip;
+constexpr int kDualTs = 68;     // floats per row of a wavefront's transpose buffer
+constexpr int kDualAhead = 6;   // strips of loads in flight per wavefront
+
 
 struct DualArgs {
   const float* X;
@@ -529,7 +546,10 @@ __device__ __forceinline__ float DualEpi(float acc, float alpha, int accumulate,
 
 template <bool RD, bool CS>
 __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
-  __shared__ __align__(16) float tile[kDualChunk][kDualCols + 4];
+  __shared__ __align__(16) float ty[CS ? kDualRows * kDualR : 4];       // Y rows of the tile
+  __shared__ __align__(16) float tb[RD ? 4 * kDualStrip * kDualTs : 4];  // per-wavefront transpose
+  __shared__ __align__(16) float rdl[RD ? 4 * kDualRows * kDualR : 4];   // per-wavefront dt partials
+  constexpr int kPerThread = kDualRows * kDualR / kThreads;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int q = lane >> 4, c = lane & 15;
@@ -538,45 +558,26 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kDualCols;
   const int64_t wl = c0 + 64 * w + 4 * c;  // this lane's four colsum columns
   const bool w_ok = wl < p.D;               // D % 4 == 0: wholly in or out
-  // Chunk ch's stream rows in the colsum layout (and Y's values for them).
-  // The loads are unconditional, from addresses clamped into the operands,
+  // Every load is unconditional, from an address clamped into its operand,
   // so they issue back to back; rows past T, columns past D and ranks past
-  // r_cs are zeroed, and the stream scaled, where the values are used.
+  // the rank are zeroed (and the stream scaled) where the values are used.
   const int64_t wlc = w_ok ? wl : 0;
-  const int cy = min(c, p.r_cs - 1);
-  auto load = [&](int ch, float4 (&x)[kDualChunk / 4], float (&y)[kDualChunk / 4]) {
+  float yv[CS ? kPerThread : 1];
+  if constexpr (CS) {
 #pragma unroll
-    for (int u = 0; u < kDualChunk / 4; ++u) {
-      const int64_t row = min<int64_t>(r0 + ch * kDualChunk + 4 * u + q, p.T - 1);
-      x[u] = *reinterpret_cast<const float4*>(p.X + row * p.ldx + wlc);
-      if constexpr (CS) y[u] = p.Y[row * p.ldy + cy];
+    for (int k = 0; k < kPerThread; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kThreads;
+      const int64_t row = min<int64_t>(r0 + (i >> 4), p.T - 1);
+      yv[k] = p.Y[row * p.ldy + min(i & 15, p.r_cs - 1)];
     }
-  };
-  // Chunk ch's loaded values as the pass uses them (in place).
-  auto prepare = [&](int ch, float4 (&x)[kDualChunk / 4], float (&y)[kDualChunk / 4]) {
-#pragma unroll
-    for (int u = 0; u < kDualChunk / 4; ++u) {
-      const bool in = r0 + ch * kDualChunk + 4 * u + q < p.T;
-      float4 v = x[u];
-      if (p.scale_stream)
-        v = make_float4(p.stream_scale * v.x, p.stream_scale * v.y, p.stream_scale * v.z,
-                        p.stream_scale * v.w);
-      x[u] = in && w_ok ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if constexpr (CS) y[u] = in && c < p.r_cs ? y[u] : 0.0f;
-    }
-  };
-  float4 xs[2][kDualChunk / 4];
-  float ys[2][kDualChunk / 4];
-  load(0, xs[0], ys[0]);
-  // Rowdot B fragments for the tile: Bf(n = c, c0 + 16g + 4q + j).
-  // Loaded from clamped addresses, then zeroed past r_rd and D (as the
-  // stream, so the loads issue back to back).
-  float4 bf[16];
+  }
+  // Rowdot B fragments of the wavefront's columns: Bf(n = c, 64w + 16g + 4q + j).
+  float4 bf[4];
   if constexpr (RD) {
     const int cb = min(c, p.r_rd - 1);
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const int64_t kc = min<int64_t>(c0 + 16 * g + 4 * q, p.D - 4);
+    for (int g = 0; g < 4; ++g) {
+      const int64_t kc = min<int64_t>(c0 + 64 * w + 16 * g + 4 * q, p.D - 4);
       if (p.b_kc) {
         bf[g] = *reinterpret_cast<const float4*>(p.Bf + cb * p.ldb + kc);
       } else {
@@ -586,69 +587,105 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
         bf[g].w = p.Bf[(kc + 3) * p.ldb + cb];
       }
     }
+  }
+  // The wavefront's stream, kDualAhead strips in flight: strip s, quad u
+  // holds row 16s + 4u + q.
+  float4 x[kDualStrips][4];
+  auto load_strip = [&](int s) {
 #pragma unroll
-    for (int g = 0; g < 16; ++g)
-      if (!(c < p.r_rd && c0 + 16 * g + 4 * q < p.D)) bf[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int u = 0; u < 4; ++u) {
+      const int64_t row = min<int64_t>(r0 + kDualStrip * s + 4 * u + q, p.T - 1);
+      x[s][u] = *reinterpret_cast<const float4*>(p.X + row * p.ldx + wlc);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < kDualAhead; ++s) load_strip(s);
+  if constexpr (RD) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const bool keep = static_cast<int>(c < p.r_rd) & static_cast<int>(c0 + 64 * w + 16 * g + 4 * q < p.D);
+      bf[g] = Keep4(bf[g], keep, 1.0f);
+    }
+  }
+  if constexpr (CS) {
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kThreads;
+      const bool keep = static_cast<int>(r0 + (i >> 4) < p.T) & static_cast<int>((i & 15) < p.r_cs);
+      ty[i] = __uint_as_float(__float_as_uint(yv[k]) & (0u - static_cast<unsigned>(keep)));
+    }
+    __syncthreads();
   }
   floatx4 cs[4];
 #pragma unroll
   for (int c4 = 0; c4 < 4; ++c4) cs[c4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  constexpr int kChunks = kDualRows / kDualChunk;
+  float* buf = tb + w * kDualStrip * kDualTs;
+  const float sc = p.scale_stream ? p.stream_scale : 1.0f;  // x * 1 is x, bit for bit
 #pragma unroll
-  for (int ch = 0; ch < kChunks; ++ch) {
-    float4 (&x)[kDualChunk / 4] = xs[ch & 1];
-    float (&y)[kDualChunk / 4] = ys[ch & 1];
-    if (ch + 1 < kChunks) load(ch + 1, xs[(ch + 1) & 1], ys[(ch + 1) & 1]);  // in flight
-    prepare(ch, x, y);
+  for (int s = 0; s < kDualStrips; ++s) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool keep = static_cast<int>(r0 + kDualStrip * s + 4 * u + q < p.T) & static_cast<int>(w_ok);
+      v[u] = Keep4(x[s][u], keep, sc);
+    }
+    if (s + kDualAhead < kDualStrips) load_strip(s + kDualAhead);  // into the registers just freed
     if constexpr (CS) {
       // Row quads in order; MFMA c4 takes column component c4 (as skinny_colsum).
 #pragma unroll
-      for (int u = 0; u < kDualChunk / 4; ++u) {
-        cs[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, y[u], cs[0], 0, 0, 0);
-        cs[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, y[u], cs[1], 0, 0, 0);
-        cs[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, y[u], cs[2], 0, 0, 0);
-        cs[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, y[u], cs[3], 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        const float y = ty[(kDualStrip * s + 4 * u + q) * kDualR + c];
+        cs[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[u].x, y, cs[0], 0, 0, 0);
+        cs[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[u].y, y, cs[1], 0, 0, 0);
+        cs[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[u].z, y, cs[2], 0, 0, 0);
+        cs[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[u].w, y, cs[3], 0, 0, 0);
       }
     }
     if constexpr (RD) {
+      // The strip through the wavefront's own buffer (its LDS operations run
+      // in order, so no barrier), read back as rows of the MFMA's A operand.
 #pragma unroll
-      for (int u = 0; u < kDualChunk / 4; ++u)
-        *reinterpret_cast<float4*>(&tile[4 * u + q][64 * w + 4 * c]) = x[u];
-      __syncthreads();
-      // The chunk's two 16-row blocks go to wavefronts 2(ch % 2) and
-      // 2(ch % 2) + 1: rows of block j = w % 2, the tile's 16 column groups
-      // in order (as skinny_rowdot's slice of a wavefront).
-      if ((w >> 1) == (ch & 1)) {
-        const int j = w & 1;
-        floatx4 rd = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int u = 0; u < 4; ++u)
+        *reinterpret_cast<float4*>(&buf[(4 * u + q) * kDualTs + 4 * c]) = v[u];
+      floatx4 rd = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-          const float4 a = *reinterpret_cast<const float4*>(&tile[16 * j + c][16 * g + 4 * q]);
-          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bf[g].x, rd, 0, 0, 0);
-          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bf[g].y, rd, 0, 0, 0);
-          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bf[g].z, rd, 0, 0, 0);
-          rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bf[g].w, rd, 0, 0, 0);
-        }
-        // Lane (q, c) element v: row (block start) + 4q + v, n = c.
-        float* part = p.ws_rd + (static_cast<int64_t>(blockIdx.x) * p.T) * kDualR;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t row = r0 + ch * kDualChunk + 16 * j + 4 * q + v;
-          if (row < p.T) part[row * kDualR + c] = rd[v];
-        }
+      for (int g = 0; g < 4; ++g) {
+        const float4 a = *reinterpret_cast<const float4*>(&buf[c * kDualTs + 16 * g + 4 * q]);
+        rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bf[g].x, rd, 0, 0, 0);
+        rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bf[g].y, rd, 0, 0, 0);
+        rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bf[g].z, rd, 0, 0, 0);
+        rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bf[g].w, rd, 0, 0, 0);
       }
-      __syncthreads();  // the next chunk overwrites the tile
+      // Lane (q, c) element e: strip row 4q + e, n = c.
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        rdl[(w * kDualRows + kDualStrip * s + 4 * q + e) * kDualR + c] = rd[e];
+    }
+  }
+  if constexpr (RD) {
+    __syncthreads();
+    // The tile's dt partial: the four wavefronts' column partials in order.
+    float* part = p.ws_rd + (static_cast<int64_t>(blockIdx.x) * p.T) * kDualR;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kThreads;
+      const int rr = i >> 4, n = i & 15;
+      float sum = rdl[rr * kDualR + n] + rdl[(kDualRows + rr) * kDualR + n];
+      sum = sum + rdl[(2 * kDualRows + rr) * kDualR + n];
+      sum = sum + rdl[(3 * kDualRows + rr) * kDualR + n];
+      const int64_t row = r0 + rr;
+      if (row < p.T) part[row * kDualR + n] = sum;
     }
   }
   if constexpr (CS) {
-    // Element v of cs[c4] at lane (q, c): column c0 + 64w + 4(4q + v) + c4, n' = c.
+    // Element e of cs[c4] at lane (q, c): column c0 + 64w + 4(4q + e) + c4, n' = c.
     float* part = p.ws_cs + (static_cast<int64_t>(blockIdx.y) * p.D) * kDualR;
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t col = c0 + 64 * w + 4 * (4 * q + v) + c4;
-        if (col < p.D) part[col * kDualR + c] = cs[c4][v];
+      for (int e = 0; e < 4; ++e) {
+        const int64_t col = c0 + 64 * w + 4 * (4 * q + e) + c4;
+        if (col < p.D) part[col * kDualR + c] = cs[c4][e];
       }
   }
 }
@@ -668,23 +705,42 @@ __device__ __forceinline__ float SumPartials(const float* __restrict__ src, int6
   return s;
 }
 
-// Sums the partials in block order and applies each output's epilogue:
-// indices [0, T * r_rd) are dt outputs, then [.., + D * r_cs) dB outputs.
+constexpr int kDualSubs = 8;                     // threads per dB output in the finish
+constexpr int kDualOuts = kThreads / kDualSubs;  // dB outputs per finish workgroup
+
+// Sums the partials and applies each output's epilogue. The first
+// `rd_blocks` workgroups take the dt outputs, one thread each, its ncb
+// partials in block order. The rest take kDualOuts dB outputs each, with
+// kDualSubs threads per output: thread `sub` sums its run of consecutive
+// row blocks in order (all its loads in flight at once), and the runs' sums
+// are added in run order.
 template <bool RD, bool CS>
-__global__ __launch_bounds__(kThreads) void skinny_dual_finish(DualArgs p) {
-  const int64_t n_rd = RD ? p.T * p.r_rd : 0, n_cs = CS ? p.D * p.r_cs : 0;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < n_rd + n_cs;
-       idx += stride) {
-    if (idx < n_rd) {
-      const int64_t row = idx / p.r_rd, n = idx % p.r_rd;
-      const float s = SumPartials(p.ws_rd + row * kDualR + n, p.ncb, p.T * kDualR);
-      const int64_t at = row * p.ldc_rd + n;
-      p.Crd[at] = DualEpi(s, p.alpha_rd, p.acc_rd, p.Crd, at, p.bias_rd, n, p.act_rd);
-    } else {
-      const int64_t j = idx - n_rd;
-      const int64_t col = j / p.r_cs, n = j % p.r_cs;
-      const float s = SumPartials(p.ws_cs + col * kDualR + n, p.nrb, p.D * kDualR);
+__global__ __launch_bounds__(kThreads) void skinny_dual_finish(DualArgs p, int64_t rd_blocks) {
+  if (RD && static_cast<int64_t>(blockIdx.x) < rd_blocks) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (idx >= p.T * p.r_rd) return;
+    const int64_t row = idx / p.r_rd, n = idx % p.r_rd;
+    const float s = SumPartials(p.ws_rd + row * kDualR + n, p.ncb, p.T * kDualR);
+    const int64_t at = row * p.ldc_rd + n;
+    p.Crd[at] = DualEpi(s, p.alpha_rd, p.acc_rd, p.Crd, at, p.bias_rd, n, p.act_rd);
+    return;
+  }
+  if constexpr (CS) {
+    __shared__ float runs[kDualSubs][kDualOuts];
+    const int o = static_cast<int>(threadIdx.x) % kDualOuts;
+    const int sub = static_cast<int>(threadIdx.x) / kDualOuts;
+    const int64_t j = (static_cast<int64_t>(blockIdx.x) - (RD ? rd_blocks : 0)) * kDualOuts + o;
+    const bool out_ok = j < p.D * p.r_cs;
+    const int64_t jc = out_ok ? j : 0;
+    const int64_t col = jc / p.r_cs, n = jc % p.r_cs;
+    const int64_t per = (p.nrb + kDualSubs - 1) / kDualSubs;
+    const int64_t b0 = sub * per, nb = min<int64_t>(p.nrb - b0, per);
+    if (nb > 0)
+      runs[sub][o] = SumPartials(p.ws_cs + (b0 * p.D + col) * kDualR + n, nb, p.D * kDualR);
+    __syncthreads();
+    if (sub == 0 && out_ok) {
+      float s = runs[0][o];
+      for (int k = 1; k < kDualSubs && k * per < p.nrb; ++k) s += runs[k][o];
       const int64_t m = p.big_is_m ? col : n, nn = p.big_is_m ? n : col;
       const int64_t at = m * p.ldc_cs + nn;
       p.Ccs[at] = DualEpi(s, p.alpha_cs, p.acc_cs, p.Ccs, at, p.bias_cs, nn, p.act_cs);
@@ -817,23 +873,26 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
   a.ws_rd = static_cast<float*>(ctx.ws);
   a.ws_cs = a.ws_rd + a.ncb * a.T * kDualR;
   const dim3 grid(static_cast<unsigned>(a.ncb), static_cast<unsigned>(a.nrb));
-  const size_t outs = static_cast<size_t>((which & 1 ? a.T * a.r_rd : 0) + (which & 2 ? a.D * a.r_cs : 0));
-  const dim3 fgrid(grid_for(outs, kThreads, 4096));
+  const int64_t rd_blocks = which & 1 ? (a.T * a.r_rd + kThreads - 1) / kThreads : 0;
+  const int64_t cs_blocks = which & 2 ? (a.D * a.r_cs + kDualOuts - 1) / kDualOuts : 0;
+  if (rd_blocks + cs_blocks > 0x7FFFFFFF)
+    return Status::Fail(kUnitEngine, "Gemm: the dual skinny pass's outputs exceed one grid");
+  const dim3 fgrid(static_cast<unsigned>(rd_blocks + cs_blocks));
   switch (which) {
     case 1:
       hipLaunchKernelGGL((skinny_dual<true, false>), grid, dim3(kThreads), 0, ctx.stream, a);
       if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
-      hipLaunchKernelGGL((skinny_dual_finish<true, false>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      hipLaunchKernelGGL((skinny_dual_finish<true, false>), fgrid, dim3(kThreads), 0, ctx.stream, a, rd_blocks);
       break;
     case 2:
       hipLaunchKernelGGL((skinny_dual<false, true>), grid, dim3(kThreads), 0, ctx.stream, a);
       if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
-      hipLaunchKernelGGL((skinny_dual_finish<false, true>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      hipLaunchKernelGGL((skinny_dual_finish<false, true>), fgrid, dim3(kThreads), 0, ctx.stream, a, rd_blocks);
       break;
     default:
       hipLaunchKernelGGL((skinny_dual<true, true>), grid, dim3(kThreads), 0, ctx.stream, a);
       if (Status s = LaunchStatus("Gemm(skinny dual)"); !s) return s;
-      hipLaunchKernelGGL((skinny_dual_finish<true, true>), fgrid, dim3(kThreads), 0, ctx.stream, a);
+      hipLaunchKernelGGL((skinny_dual_finish<true, true>), fgrid, dim3(kThreads), 0, ctx.stream, a, rd_blocks);
       break;
   }
   return LaunchStatus("Gemm(skinny dual finish)");
