@@ -63,16 +63,24 @@ const char* GemmConfigName(int cfg) {
 
 // The heuristic takes the skinny kernels only for the shapes that stream a
 // rank-wide operand through a reduction over the token rows (rowdot: N is
-// the rank; colsum: a weight gradient). A rank-K outer product (K <= 64)
+// the rank; colsum: a weight gradient), up to rank kSkinnyMaxRank. Wider
+// ranks run on the tile kernels with split-K, which re-read the rank-wide
+// operand far less (measured with the stream cold, rank 64: 8192x64x4096
+// rowdot 110 -> 63 us, 64x4096x8192 colsum 85 -> 56 us; at rank 16 the two
+// are within a few percent either way). A rank-K outer product (K <= 64)
 // runs on the tile kernels: they time within 1% of the skinny outer kernel
 // alone and their epilogue takes a following Scale + AddEW or a whole LoRA
 // run. A forced skinny config still selects the outer kernel (tests).
+constexpr int64_t kSkinnyMaxRank = 16;
+
 GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
   GemmPlan plan;
   const SkinnyKind kind = SkinnyKindOf(d);
+  const int64_t rank = kind == SkinnyKind::kRowDot ? d.N : std::min(d.M, d.N);
   const bool skinny = forced_cfg == kNumCfgs
                           ? kind != SkinnyKind::kNone
-                          : forced_cfg < 0 && (kind == SkinnyKind::kRowDot || kind == SkinnyKind::kColSum);
+                          : forced_cfg < 0 && (kind == SkinnyKind::kRowDot || kind == SkinnyKind::kColSum) &&
+                                rank <= kSkinnyMaxRank;
   if (skinny) {
     plan.cfg = kNumCfgs;
     plan.splits = 1;

@@ -124,16 +124,37 @@ def test_gemm_nn_equals_nt_on_the_transposed_operand_bitwise(env, M, N, K):
 
 
 # LoRA-shaped GEMMs: the heuristic takes the skinny kernels for rowdot (N <=
-# 64 with A k-contiguous) and colsum (TN with min(M, N) <= 64) and the tile
-# kernels for rank-K outer products (K <= 64); the skinny outer kernel stays
-# reachable as a forced config. The same shapes forced onto a generic tile
-# config give the reference for run-to-run and path-to-path agreement.
+# 64 with A k-contiguous) and colsum (TN with min(M, N) <= 64) up to rank 16,
+# the tile kernels with split-K for wider ranks, and the tile kernels for
+# rank-K outer products (K <= 64); the skinny kernels stay reachable as a
+# forced config. The same shapes forced onto a generic tile config give the
+# reference for run-to-run and path-to-path agreement.
 SKINNY = [
     (0, 1000, 520, 16), (0, 256, 2048, 64), (0, 300, 132, 8), (0, 129, 68, 4), (1, 1000, 520, 16),
     (1, 200, 256, 64), (0, 1000, 16, 2048), (0, 130, 64, 1024), (0, 77, 8, 260), (1, 300, 40, 512),
     (1, 1000, 16, 2048), (2, 520, 16, 1000), (2, 16, 520, 1000), (2, 64, 1024, 300),
     (2, 1024, 64, 2048), (2, 8, 132, 256), (2, 2048, 16, 4096),
 ]
+
+
+def heuristic_splits(M, N, K):
+    """The untuned plan's split-K count for a batch-1 GEMM (PlanGemmWith,
+    csrc/k_gemm.hip): its tile (128x32 for N <= 32, 32x128 for M <= 32,
+    else 128x128 or, when that leaves few tiles or an extent <= 64, 64x64);
+    fewer than 512 tiles and K >= 256 split K so the slices cover the chip
+    twice, each at least 128 deep."""
+    cdiv = lambda a, b: -(-a // b)
+    if N <= 32 < M:
+        mt = (128, 32)
+    elif M <= 32 < N:
+        mt = (32, 128)
+    else:
+        big, mid = cdiv(M, 128) * cdiv(N, 128), cdiv(M, 64) * cdiv(N, 64)
+        mt = (128, 128) if big >= 512 else ((64, 64) if (mid >= 256 or M <= 64 or N <= 64) else (128, 128))
+    tiles = cdiv(M, mt[0]) * cdiv(N, mt[1])
+    if tiles >= 512 or K < 256:
+        return 1
+    return max(1, min(cdiv(512, tiles), K // 128, 64))
 
 
 @pytest.mark.parametrize("layout,M,N,K", SKINNY)
@@ -163,8 +184,15 @@ def test_gemm_skinny(env, orc, layout, M, N, K):
     generic = env.T(np.full(M * N, np.nan, f32))
     env.call("seeml_hip_gemm_forced", layout, env.T(A), env.T(B), generic, M, N, K, 0, 1)
     outer = layout != 2 and K <= 64
+    wide = not outer and (min(M, N) if layout == 2 else N) > 16
     if outer:   # heuristic = a tile kernel at one slice: any tile config's bits
         assert same_bits(env.H(generic), got)
+    elif wide:  # heuristic = the tile kernels at the rule's split count
+        tiled = env.T(np.full(M * N, np.nan, f32))
+        env.call("seeml_hip_gemm_forced", layout, env.T(A), env.T(B), tiled, M, N, K, 0,
+                 heuristic_splits(M, N, K))
+        assert same_bits(env.H(tiled), got)
+        assert rel_err(env.H(forced), got) <= TOL_STEP
     else:       # heuristic = the skinny kernel
         assert same_bits(env.H(forced), got)
         assert rel_err(env.H(generic), got) <= TOL_STEP
