@@ -508,11 +508,10 @@ struct DualArgs {
   int64_t ldx, T, D;
   int scale_stream;
   float stream_scale;
-  // rowdot: Crd(row, n) = epi(sum_d X[row][d] Bf(n, d)), n < r_rd
+  // rowdot: Crd(row, n) = epi(sum_d X[row][d] Bf[n * ldb + d]), n < r_rd
   int r_rd;
   const float* Bf;
   int64_t ldb;
-  int b_kc;
   float* Crd;
   int64_t ldc_rd;
   float alpha_rd;
@@ -578,14 +577,7 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int64_t kc = min<int64_t>(c0 + 64 * w + 16 * g + 4 * q, p.D - 4);
-      if (p.b_kc) {
-        bf[g] = *reinterpret_cast<const float4*>(p.Bf + cb * p.ldb + kc);
-      } else {
-        bf[g].x = p.Bf[(kc + 0) * p.ldb + cb];
-        bf[g].y = p.Bf[(kc + 1) * p.ldb + cb];
-        bf[g].z = p.Bf[(kc + 2) * p.ldb + cb];
-        bf[g].w = p.Bf[(kc + 3) * p.ldb + cb];
-      }
+      bf[g] = *reinterpret_cast<const float4*>(p.Bf + cb * p.ldb + kc);
     }
   }
   // The wavefront's stream, kDualAhead strips in flight: strip s, quad u
@@ -824,6 +816,8 @@ bool SkinnyDualFits(const GemmDesc& rd, const GemmDesc& cs) {
   const int64_t ldx = big_is_m ? cs.lda : cs.ldb;
   if (cs.K != rd.M || W != rd.K || ldx != rd.lda) return false;
   if (rd.N > kDualR || R > kDualR) return false;
+  // dt = du B^T: B's rows are the rank's (GemmNT, 16-byte aligned rows).
+  if (!rd.b_kc || !Vec4(rd.B, rd.ldb)) return false;
   if (rd.scale_stream != cs.scale_stream || (rd.scale_stream && rd.stream_scale != cs.stream_scale))
     return false;
   const int64_t nrb = (rd.M + kDualRows - 1) / kDualRows, ncb = (rd.K + kDualCols - 1) / kDualCols;
@@ -851,7 +845,6 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
   a.r_rd = static_cast<int>(rd.N);
   a.Bf = static_cast<const float*>(rd.B);
   a.ldb = rd.ldb;
-  a.b_kc = rd.b_kc ? 1 : 0;
   a.Crd = rd.C;
   a.ldc_rd = rd.ldc;
   a.alpha_rd = rd.alpha;
