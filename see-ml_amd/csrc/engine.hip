@@ -1907,7 +1907,7 @@ class Engine {
       const GemmOrder order = GemmOrderOf(d);
       // Arm 0 is the heuristic plan; the others are every tile config at
       // the order's split count and, at one split, the column splits (whole
-      // rounds of 256x128 tiles, the rest on 128x128 or 128x64 tiles). The
+      // rounds of 256x128 tiles, the rest on 128x128, 128x64 or 64x64 tiles). The
       // skinny kernels' order has one kernel: nothing to tune.
       const GemmPlan hint = PlanGemm(d);
       const uint64_t gid = group++;
@@ -1925,7 +1925,7 @@ class Engine {
       };
       for (int cfg = 0; cfg < GemmSkinnyConfig(); ++cfg) add(PlanGemmWith(d, cfg, order.splits));
       if (order.splits == 1)
-        for (int tail : {0, 4}) {
+        for (int tail : {0, 4, 5}) {
           const GemmPlan sp = PlanGemmSplit(d, 2, tail);
           if (sp.n_split > 0) add(sp);
         }

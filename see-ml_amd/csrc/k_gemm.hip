@@ -146,12 +146,14 @@ bool GemmPlanKeepsOrder(const GemmDesc& d, const GemmPlan& p) {
 
 // The heuristic plan, and for large GEMMs whose 256x128 tiles leave a
 // partial last round, the column split of at least two whole rounds with
-// the remainder on 128x128 tiles (2-3% faster inside the C4 step on
-// 8192x5504x2048 and 8192x32000x2048; the autotuner's first arm).
+// the remainder on 64x64 tiles (the autotuner's first arm). The split was
+// 2-3% faster inside the C4 step on 8192x5504x2048 and 8192x32000x2048 with
+// a 128x128 remainder; 64x64 tiles spread the remainder over every CU
+// (8192x5504x2048: 1282 against 1319 us per pair, 128x64 1310).
 GemmPlan PlanGemm(const GemmDesc& d) {
   const GemmPlan plan = PlanGemmWith(d, -1, -1);
   if (plan.cfg == kNumCfgs || plan.splits != 1) return plan;
-  const GemmPlan sp = PlanGemmSplit(d, 2, 0);
+  const GemmPlan sp = PlanGemmSplit(d, 2, gemm::kCfgSmall);
   const int64_t cus = DeviceCUs();
   if (sp.n_split > 0 && cus > 0 && CeilDiv(d.M, 256) * (sp.n_split / 128) >= 2 * cus) return sp;
   return plan;
