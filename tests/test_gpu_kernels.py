@@ -227,7 +227,7 @@ def test_skinny_dual_pass(env, orc, T, D, r_rd, r_cs, scaled):
 
 @pytest.mark.parametrize("layout,M,N,K,tail,n_split", [
     (1, 512, 1000, 256, 0, 768), (0, 300, 520, 128, 4, 384), (2, 256, 640, 96, 0, 512),
-    (1, 256, 5504, 64, 4, 5120)])
+    (1, 256, 5504, 64, 4, 5120), (1, 512, 5504, 96, 5, 5120), (0, 300, 1000, 128, 5, 768)])
 def test_gemm_column_split_is_bitwise_one_launch(env, layout, M, N, K, tail, n_split):
     """A column-split plan (256x128 tiles on [0, n_split), smaller tiles on
     the rest) gives every output the same k order as one launch: bit-equal
