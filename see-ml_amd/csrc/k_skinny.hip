@@ -543,11 +543,13 @@ __device__ __forceinline__ float DualEpi(float acc, float alpha, int accumulate,
   return dev_act(act, val);
 }
 
-template <bool RD, bool CS>
-__global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
-  __shared__ __align__(16) float ty[CS ? kDualRows * kDualR : 4];       // Y rows of the tile
-  __shared__ __align__(16) float tb[RD ? 4 * kDualStrip * kDualTs : 4];  // per-wavefront transpose
-  __shared__ __align__(16) float rdl[RD ? 4 * kDualRows * kDualR : 4];   // per-wavefront dt partials
+// One workgroup's tile. EDGE: the tile reaches past T or D, and each value
+// is masked (and scaled) where used; inside, every loaded value is kept, so
+// the masks are left out, and SCALED multiplies by the folded Scale's
+// factor (the same float product).
+template <bool RD, bool CS, bool EDGE, bool SCALED>
+__device__ __forceinline__ void DualTile(const DualArgs& p, float* __restrict__ ty,
+                                         float* __restrict__ tb, float* __restrict__ rdl) {
   constexpr int kPerThread = kDualRows * kDualR / kThreads;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -618,8 +620,14 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
     float4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const bool keep = static_cast<int>(r0 + kDualStrip * s + 4 * u + q < p.T) & static_cast<int>(w_ok);
-      v[u] = Keep4(x[s][u], keep, sc);
+      if constexpr (EDGE) {
+        const bool keep = static_cast<int>(r0 + kDualStrip * s + 4 * u + q < p.T) & static_cast<int>(w_ok);
+        v[u] = Keep4(x[s][u], keep, sc);
+      } else if constexpr (SCALED) {
+        v[u] = make_float4(sc * x[s][u].x, sc * x[s][u].y, sc * x[s][u].z, sc * x[s][u].w);
+      } else {
+        v[u] = x[s][u];
+      }
     }
     if (s + kDualAhead < kDualStrips) load_strip(s + kDualAhead);  // into the registers just freed
     if constexpr (CS) {
@@ -680,6 +688,21 @@ __global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
         if (col < p.D) part[col * kDualR + c] = cs[c4][e];
       }
   }
+}
+
+template <bool RD, bool CS>
+__global__ __launch_bounds__(kThreads, 2) void skinny_dual(DualArgs p) {
+  __shared__ __align__(16) float ty[CS ? kDualRows * kDualR : 4];       // Y rows of the tile
+  __shared__ __align__(16) float tb[RD ? 4 * kDualStrip * kDualTs : 4];  // per-wavefront transpose
+  __shared__ __align__(16) float rdl[RD ? 4 * kDualRows * kDualR : 4];   // per-wavefront dt partials
+  const bool edge = (static_cast<int64_t>(blockIdx.y) + 1) * kDualRows > p.T ||
+                    (static_cast<int64_t>(blockIdx.x) + 1) * kDualCols > p.D;
+  if (edge)
+    DualTile<RD, CS, true, true>(p, ty, tb, rdl);
+  else if (p.scale_stream)
+    DualTile<RD, CS, false, true>(p, ty, tb, rdl);
+  else
+    DualTile<RD, CS, false, false>(p, ty, tb, rdl);
 }
 
 // Sum of n partials src[0], src[stride], .. in index order, loaded 16 at a
