@@ -413,6 +413,19 @@ __device__ __forceinline__ void store_row(float* __restrict__ row, int nv, int t
   }
 }
 
+// A per-column parameter (gamma, beta) at this thread's row positions,
+// loaded with the row: unconditionally, from indices clamped into the
+// vector, so the loads issue back to back and their latency overlaps the
+// row's (under a per-position test each load was followed by a full wait).
+// Positions past the row are never used.
+template <int TPR, int V>
+__device__ __forceinline__ void load_param(const float* __restrict__ p, int nv, int t,
+                                           float4 (&v)[V]) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int i = 0; i < V; ++i) v[i] = p4[min(t + i * TPR, nv - 1)];
+}
+
 // Row index and lane of this thread; false past the last row (uniform per
 // row group, and per block when TPR == kBlock).
 template <int TPR>
@@ -441,7 +454,8 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
-  float4 xv[V];
+  float4 gm[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
   load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double s = 0.0;
 #pragma unroll
@@ -449,12 +463,11 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
   const double ss = row_sum_d<TPR>(s, dscratch);
   const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f);
   if (t == 0) rstd[r] = rs;
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
     if (j < nv) {
-      const float4 g = g4[j];
+      const float4 g = gm[i];
       xv[i] = make_float4(xv[i].x * rs * g.x, xv[i].y * rs * g.y, xv[i].z * rs * g.z,
                           xv[i].w * rs * g.w);
     }
@@ -472,15 +485,16 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
   const float inv_d = 1.0f / static_cast<float>(cols);
-  float4 gv[V], xv[V];
+  const float rs = rstd[r];  // issued with the row's loads
+  float4 gm[V], gv[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
   load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
   load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
-    const float4 g = j < nv ? g4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 g = j < nv ? gm[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     gv[i] = make_float4(gv[i].x * g.x, gv[i].y * g.y, gv[i].z * g.z, gv[i].w * g.w);
     s += static_cast<double>(gv[i].x) * static_cast<double>(xv[i].x);
     s += static_cast<double>(gv[i].y) * static_cast<double>(xv[i].y);
@@ -488,7 +502,6 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
     s += static_cast<double>(gv[i].w) * static_cast<double>(xv[i].w);
   }
   const float mgx = static_cast<float>(row_sum_d<TPR>(s, dscratch)) * inv_d;
-  const float rs = rstd[r];
 #pragma unroll
   for (int i = 0; i < V; ++i)
     gv[i] = make_float4(rs * (gv[i].x - xv[i].x * rs * rs * mgx),
@@ -508,7 +521,9 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
   int t;
   if (!row_of<TPR>(rows, &r, &t)) return;
   const int nv = cols / 4;
-  float4 xv[V];
+  float4 gm[V], bm[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_param<TPR, V>(beta, nv, t, bm);
   load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double s = 0.0;
 #pragma unroll
@@ -539,13 +554,11 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
     mean[r] = mu;
     rstd[r] = rs;
   }
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
-  const float4* b4 = reinterpret_cast<const float4*>(beta);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
     if (j < nv) {
-      const float4 g = g4[j], b = b4[j];
+      const float4 g = gm[i], b = bm[i];
       xv[i] = make_float4((xv[i].x - mu) * rs * g.x + b.x, (xv[i].y - mu) * rs * g.y + b.y,
                           (xv[i].z - mu) * rs * g.z + b.z, (xv[i].w - mu) * rs * g.w + b.w);
     }
@@ -565,16 +578,16 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
   const int nv = cols / 4;
   const float inv_d = 1.0f / static_cast<float>(cols);
   const float mu = mean[r], rs = rstd[r];
-  float4 gv[V], xv[V];
+  float4 gm[V], gv[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
   load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
   load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
   double sg = 0.0, sgx = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
     if (j < nv) {
-      const float4 g = g4[j];
+      const float4 g = gm[i];
       // xv becomes x-hat, gv becomes g = dy * gamma.
       xv[i] = make_float4((xv[i].x - mu) * rs, (xv[i].y - mu) * rs, (xv[i].z - mu) * rs,
                           (xv[i].w - mu) * rs);
