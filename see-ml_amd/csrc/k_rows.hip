@@ -157,16 +157,24 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
   const size_t n = blockIdx.x;
   const int nv = static_cast<int>(C / 4);
   const int t = threadIdx.x;
+  // Every load first, unconditionally from float4s clamped into the row, so
+  // they are in flight together (loaded under a per-position test and used
+  // at once, each was followed by a full wait); then the max in the same
+  // order as before. Thread 0 also fetches the label's logit up front.
   float4 v[kXentVec];
+#pragma unroll
+  for (int i = 0; i < kXentVec; ++i)
+    v[i] = ld4(logits + n * C + 4 * static_cast<size_t>(min(t + i * NT, nv - 1)), nt);
+  int32_t lab = 0;
+  float xl = 0.0f;
+  if (t == 0) {
+    lab = labels[n];
+    if (lab >= 0 && static_cast<size_t>(lab) < C) xl = logits[n * C + lab];
+  }
   float mx = logits[n * C];
 #pragma unroll
-  for (int i = 0; i < kXentVec; ++i) {
-    const int j = t + i * NT;
-    if (j < nv) {
-      v[i] = ld4(logits + n * C + 4 * static_cast<size_t>(j), nt);
-      mx = fmaxf(fmaxf(fmaxf(fmaxf(mx, v[i].x), v[i].y), v[i].z), v[i].w);
-    }
-  }
+  for (int i = 0; i < kXentVec; ++i)
+    if (t + i * NT < nv) mx = fmaxf(fmaxf(fmaxf(fmaxf(mx, v[i].x), v[i].y), v[i].z), v[i].w);
   mx = block_max<NT>(mx, fscratch);
   float sacc = 0.0f;
 #pragma unroll
@@ -193,12 +201,11 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
           make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), nt);
   }
   if (t == 0) {
-    const int32_t lab = labels[n];
     double term;
     if (lab < 0 || static_cast<size_t>(lab) >= C) {
       term = __builtin_nan("");  // outside the feeder contract: poison the loss
     } else {
-      const float pl = expf(logits[n * C + lab] - mx) * inv;  // same expression as p[lab]
+      const float pl = expf(xl - mx) * inv;  // same expression as p[lab]
       const double safe = isnan(pl) ? static_cast<double>(pl)
                                     : static_cast<double>(fmaxf(pl, 1e-12f));
       term = -log(safe);
