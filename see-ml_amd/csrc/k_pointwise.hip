@@ -575,13 +575,17 @@ __global__ __launch_bounds__(kBlock) void rope_angle_table_kernel(float* __restr
 }
 
 // RoPE through the angle table: each float4 of x is two pairs of one
-// position; its cos/sin are one float4 of the (cache-resident) table.
-template <int DIR, bool NT>
+// position; its cos/sin are one float4 of the (cache-resident) table. POW2:
+// the row width (in float4s), S and d are powers of two, and the element's
+// row, column and position come from shifts and masks (nv_shift = log2 of
+// the row width) rather than three integer divisions per float4.
+template <int DIR, bool NT, bool POW2>
 __global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restrict__ x,
                                                             float* __restrict__ y,
                                                             const float* __restrict__ table,
                                                             uint32_t nv_row, uint32_t total4,
-                                                            uint32_t S, uint32_t d) {
+                                                            uint32_t S, uint32_t d,
+                                                            uint32_t nv_shift) {
   constexpr int kU = Unroll(NT);
   const uint32_t stride = gridDim.x * kBlock * kU;
   for (uint32_t base = blockIdx.x * kBlock * kU + threadIdx.x; base < total4; base += stride) {
@@ -590,10 +594,18 @@ __global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restr
     for (int u = 0; u < kU; ++u) {
       const uint32_t i = base + u * kBlock;
       if (i >= total4) continue;
-      const uint32_t row = i / nv_row, col4 = i - row * nv_row;
-      const uint32_t c2 = ((4 * col4) % d) / 2;  // even: the float4 below is aligned
+      uint32_t pos, c2;  // c2 even: the float4 below is aligned
+      if constexpr (POW2) {
+        const uint32_t row = i >> nv_shift, col4 = i & (nv_row - 1);
+        c2 = ((4 * col4) & (d - 1)) >> 1;
+        pos = row & (S - 1);
+      } else {
+        const uint32_t row = i / nv_row, col4 = i - row * nv_row;
+        c2 = ((4 * col4) % d) / 2;
+        pos = row % S;
+      }
       v[u] = ld4(x + 4 * static_cast<size_t>(i), NT);
-      t[u] = *reinterpret_cast<const float4*>(table + 2 * ((row % S) * (d / 2) + c2));
+      t[u] = *reinterpret_cast<const float4*>(table + 2 * (pos * (d / 2) + c2));
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
@@ -901,13 +913,21 @@ Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, siz
   const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
   const uint32_t nv_row = static_cast<uint32_t>(width / 4), S32 = static_cast<uint32_t>(S),
                  d32 = static_cast<uint32_t>(d);
+  auto pow2 = [](uint32_t v) { return v != 0 && (v & (v - 1)) == 0; };
+  const bool p2 = pow2(nv_row) && pow2(S32) && pow2(d32);
+  uint32_t shift = 0;
+  while (p2 && (1u << shift) < nv_row) ++shift;
+#define SEEML_ROPE(D, N, P)                                                                  \
+  hipLaunchKernelGGL((rope_table_kernel<D, N, P>), grid, dim3(kBlock), 0, c.stream, x, y, table, \
+                     nv_row, total4, S32, d32, shift)
   if (dir > 0) {
-    if (nt) hipLaunchKernelGGL((rope_table_kernel<1, true>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
-    else hipLaunchKernelGGL((rope_table_kernel<1, false>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+    if (p2) { if (nt) SEEML_ROPE(1, true, true); else SEEML_ROPE(1, false, true); }
+    else { if (nt) SEEML_ROPE(1, true, false); else SEEML_ROPE(1, false, false); }
   } else {
-    if (nt) hipLaunchKernelGGL((rope_table_kernel<-1, true>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
-    else hipLaunchKernelGGL((rope_table_kernel<-1, false>), grid, dim3(kBlock), 0, c.stream, x, y, table, nv_row, total4, S32, d32);
+    if (p2) { if (nt) SEEML_ROPE(-1, true, true); else SEEML_ROPE(-1, false, true); }
+    else { if (nt) SEEML_ROPE(-1, true, false); else SEEML_ROPE(-1, false, false); }
   }
+#undef SEEML_ROPE
   return LaunchStatus(dir > 0 ? "RopeFwd" : "RopeBwd");
 }
 

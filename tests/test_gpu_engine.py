@@ -493,13 +493,15 @@ def test_fusions_are_planned(torch_gpu):
     e.close()
 
 
-def test_rope_through_the_angle_table_is_the_standalone_kernel(torch_gpu):
+@pytest.mark.parametrize("name", ["c4m", "c4m48"])
+def test_rope_through_the_angle_table_is_the_standalone_kernel(torch_gpu, name):
     """The engine runs RoPE from an angle table built at open; replaying the
     plan up to the first RopeFwd and the first RopeBwd, each output equals
-    the standalone kernel's (which evaluates the angles itself) bit for bit."""
+    the standalone kernel's (which evaluates the angles itself) bit for bit
+    (c4m: power-of-two row width, S and d; c4m48: S = 48)."""
     from seeml_amd import PROGRAM_TRAIN, _lib, planner
     torch = torch_gpu
-    w, p = compile_workload("c4m")
+    w, p = compile_workload(name)
     e = engine(p, use_graph=False)
     x, y = configs.batch(w, 0)
     e.stage(x, y)
