@@ -489,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
 //    four wavefronts' partials are summed in wavefront order at the end.
 // Partials go to the workspace: one per 256-column block for each dt row,
 // one per 128-row block for each dB column; skinny_dual_finish sums them in
-// block order and applies each output's epilogue. Either output may be
+// a fixed order (below) and applies each output's epilogue. Either output may be
 // left out (the engine's one-instruction form); each output's summation
 // order is the same either way, so the pair and its two single launches
 // give the same bits.
@@ -501,7 +501,6 @@ constexpr int kDualStrip = 16;  // rows per strip (one rowdot MFMA block)
 constexpr int kDualStrips = kDualRows / kDualStrip;
 constexpr int kDualTs = 68;     // floats per row of a wavefront's transpose buffer
 constexpr int kDualAhead = 6;   // strips of loads in flight per wavefront
-
 
 struct DualArgs {
   const float* X;
