@@ -91,9 +91,9 @@ namespace {
 // iteration, runs the tile's MFMAs and vector work, then stages the loaded
 // tile into the other LDS buffer ahead of the iteration's one barrier (the
 // order AttnDP uses). Measured on MI355X at C4's shape (B 8, S 1024, H 16,
-// d 128): 0.40 ms per launch standalone and 0.37 ms inside the train graph
-// (92.7 TFLOP/s of causal QK^T + PV); the MFMAs alone, without the
-// parked-score and P traffic, take 0.34 ms standalone.
+// d 128): 0.356 ms per launch inside the train graph (96.5 TFLOP/s of
+// causal QK^T + PV); the MFMAs alone, without the parked-score and P
+// traffic, take 0.34 ms standalone.
 //
 // Heavy (late) query blocks are scheduled first, for causal load balance.
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -238,8 +238,13 @@ __device__ __forceinline__ void StoreRow(float* __restrict__ out, const floatx16
 // wavefront's rows lie past S (the last query block of a ragged S); every
 // other wavefront's P slots and parked scores need no per-lane test, since
 // its keys j <= qw + 31 < S. Every iteration ends in one barrier whatever
-// the wavefront computes, so the four wavefronts stay in step.
-template <int D, bool CHECKED>
+// the wavefront computes, so the four wavefronts stay in step. STOREP
+// (whether P is stored) is a compile-time choice: with a run-time one, the
+// wait for the next tile's parked scores at the end of a pass-2 iteration
+// also covered the P stores just issued (loads and stores share one
+// counter), so every tile waited for its stores to complete (C4 step:
+// 5.94 -> 5.70 ms per 16 forwards without that wait).
+template <int D, bool CHECKED, bool STOREP>
 __device__ __forceinline__ void AttnFwdWave(const float* __restrict__ qh, const float* __restrict__ kh,
                                             const float* __restrict__ vh, float* __restrict__ oh,
                                             float* __restrict__ ph, float* __restrict__ lds, int S,
@@ -323,7 +328,7 @@ __device__ __forceinline__ void AttnFwdWave(const float* __restrict__ qh, const 
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[nb][e] = 0.0f;
-  const bool store_p = (pstore & kAttnStoreP) != 0;
+  constexpr bool store_p = STOREP;
   KvTile<D> vs;
   vs.load(vh, ld, 0, S);
   floatx16 sc;
@@ -363,7 +368,7 @@ __device__ __forceinline__ void AttnFwdWave(const float* __restrict__ qh, const 
   }
 }
 
-template <int D>
+template <int D, bool STOREP>
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ o, float* __restrict__ probs, int B, int S, int H, float inv_sqrt_d,
@@ -393,11 +398,11 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_fwd_fused(
   // so exp(s - max) is the hardware exp2 of s2 - max2.
   const float c2 = inv_sqrt_d * 1.44269504088896340736f;
   if (qw + 31 < S)
-    AttnFwdWave<D, false>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw, tiles_wg,
-                          tiles_w, h, r, c2, pstore);
+    AttnFwdWave<D, false, STOREP>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw,
+                                  tiles_wg, tiles_w, h, r, c2, pstore);
   else
-    AttnFwdWave<D, true>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw, tiles_wg,
-                         tiles_w, h, r, c2, pstore);
+    AttnFwdWave<D, true, STOREP>(q + head, k + head, v + head, o + head, ph, lds, S, ld, qw,
+                                 tiles_wg, tiles_w, h, r, c2, pstore);
 }
 
 // ---- fused causal backward primitives (d = 64 or 128) ----------------------
@@ -664,14 +669,17 @@ Status AttnFwd(const float* q, const float* k, const float* v, float* o, float* 
   if (FusedEligible({q, k, v, o, probs}, B, S, H, d)) {
     const unsigned blocks = FusedBlocks(B, S, H);
     const float inv = InvSqrtD(static_cast<int64_t>(d));
-    if (d == 128)
-      hipLaunchKernelGGL(attn_fwd_fused<128>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
-                         v, o, probs, static_cast<int>(B), static_cast<int>(S),
-                         static_cast<int>(H), inv, pstore);
-    else
-      hipLaunchKernelGGL(attn_fwd_fused<64>, dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, k,
-                         v, o, probs, static_cast<int>(B), static_cast<int>(S),
-                         static_cast<int>(H), inv, pstore);
+#define SEEML_FWD(DD, SP)                                                                  \
+  hipLaunchKernelGGL((attn_fwd_fused<DD, SP>), dim3(blocks), dim3(kAttnThreads), 0, c.stream, q, \
+                     k, v, o, probs, static_cast<int>(B), static_cast<int>(S),                    \
+                     static_cast<int>(H), inv, pstore)
+    const bool sp = (pstore & kAttnStoreP) != 0;
+    if (d == 128) {
+      if (sp) SEEML_FWD(128, true); else SEEML_FWD(128, false);
+    } else {
+      if (sp) SEEML_FWD(64, true); else SEEML_FWD(64, false);
+    }
+#undef SEEML_FWD
     return LaunchStatus("AttnFwd");
   }
   const Geo g = MakeGeo(B, S, H, d);
