@@ -314,6 +314,27 @@ def test_eval_program_matches_oracle(torch_gpu, orc):
     assert abs(e.loss() - r.loss()) <= TOL_STEP * abs(r.loss())
 
 
+def test_eval_program_with_the_fused_forward_storing_no_p(torch_gpu, orc):
+    """c4m's eval program runs the fused attention forward (d = 128) with
+    nothing reading P, so the engine launches the form that stores no P
+    (the compile-time no-P instantiation): the loss still matches the
+    oracle's eval of the same plan."""
+    from seeml_amd import PROGRAM_EVAL
+    w, p = compile_workload("c4m")
+    e = engine(p)
+    r = HostPlanRunner(p, orc)
+    for s in (3, 4):
+        x, y = configs.batch(w, s)
+        e.stage(x, y)
+        e.run(PROGRAM_EVAL)
+        r.stage(x, y)
+        r.run(2)
+        assert abs(e.loss() - r.loss()) <= TOL_STEP * abs(r.loss()), (s, e.loss(), r.loss())
+    ch = [e.gemm_choice(PROGRAM_EVAL, i) for i in range(e.program_length(PROGRAM_EVAL))]
+    assert "P unused" in ch, ch
+    e.close()
+
+
 def test_c2_full_size_invariants(torch_gpu):
     """Full-size C2 (8192x4096x4096, r16): step-0 identity — B = 0 makes the
     grafted model equal the frozen one, so loss_0 = mean((XW - T)^2) computed
