@@ -739,6 +739,7 @@ class Engine {
     PlanPointwiseRuns(program);
     PlanScaleFolds(program);
     PlanDualRuns(program);
+    PlanRowdotGroups(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -842,6 +843,13 @@ class Engine {
     uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
     const float* fold_x = nullptr;  // scale fold: the Scale's input and factor
     float fold_alpha = 1.0f;
+    // LoRA run in a rowdot group (PlanRowdotGroups): 1 = launches the group's
+    // rowdots (listed in grp_rowdots), -1 = its rowdot ran with the group;
+    // both only when the executed range holds the group's whole span
+    // [grp_first, grp_end), else the run launches its own rowdot.
+    int rd_mode = 0;
+    size_t grp_first = 0, grp_end = 0;
+    std::vector<size_t> grp_rowdots;
   };
 
   void PlanChains(int program) {
@@ -1166,6 +1174,89 @@ class Engine {
   // memory. The up-projection must run on a tile plan with one slice, so the
   // epilogue's u (the tile kernels' k order) has its bits; y, u and s must be
   // dead after the AddEW. Returns the run's length (0: none).
+  // Rowdot groups (kernels.h LaunchSkinnyRowdotGroup): the down-projection
+  // rowdots t_j = x A_j of consecutive LoRA runs over one layer input x (the
+  // q, k and v projections) run as one pass over x when the first run
+  // launches. Member j's rowdot moves from its own run's launch to the
+  // first's, which is legal when no launch in between writes x, A_j or t_j
+  // or reads t_j. A LoRA run's launch writes only its sum o and t and reads
+  // only its GEMMs' operands (y, u and s stay in registers); any other
+  // instruction counts with its plan-level ranges. Each member's t has the
+  // bits of its own launch, so fused and eager replays agree.
+  void PlanRowdotGroups(int program) {
+    auto& chains = chains_[program];
+    std::sort(chains.begin(), chains.end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+    const auto& prog = plan_.program[program];
+    std::vector<int> chain_of(prog.size(), -1);
+    for (size_t c = 0; c < chains.size(); ++c)
+      for (size_t k = chains[c].first; k < chains[c].first + chains[c].count; ++k)
+        chain_of[k] = static_cast<int>(c);
+    auto member_ok = [&](const ChainRun& r) {
+      return r.kind == ChainKind::kLoraBase && r.rd_mode == 0 &&
+             plans_[program][r.first + 1].cfg == GemmSkinnyConfig();
+    };
+    // What the launches of instructions [from, to) write and read.
+    auto launched = [&](size_t from, size_t to, Ranges* w, Ranges* rd) {
+      for (size_t k = from; k < to; ++k) {
+        const int c = chain_of[k];
+        if (c >= 0 && chains[c].kind == ChainKind::kLoraBase) {
+          const ChainRun& r = chains[c];
+          if (k != r.first) continue;  // the run, counted at its first instruction
+          const UpdateInstruction& add = prog[r.first + r.count - 1];
+          const uint64_t bytes = static_cast<uint64_t>(r.d.M) * r.d.N * sizeof(float);
+          (void)WriteRangesOf(prog[r.first + 1], w);
+          w->emplace_back(RefOffset(add.in[2]), bytes);
+          for (size_t g = r.first; g < r.first + 3; ++g) (void)DependRangesOf(prog[g], rd);
+          continue;
+        }
+        (void)WriteRangesOf(prog[k], w);
+        (void)DependRangesOf(prog[k], rd);
+      }
+    };
+    auto overlap = [](const Ranges& a, const Ranges& b) {
+      for (const auto& x : a)
+        if (Overlaps(b, x.first, x.second)) return true;
+      return false;
+    };
+    for (size_t a = 0; a < chains.size(); ++a) {
+      if (!member_ok(chains[a])) continue;
+      const ChainRun& r1 = chains[a];
+      GemmDesc ds[4];
+      ds[0] = DescOf(prog[r1.first + 1]);
+      std::vector<size_t> members{a};
+      for (size_t b = a + 1; b < chains.size() && members.size() < 4; ++b) {
+        const ChainRun& rb = chains[b];
+        if (!member_ok(rb)) break;
+        const size_t ib = rb.first + 1;
+        ds[members.size()] = DescOf(prog[ib]);
+        if (!SkinnyRowdotGroupFits(ds, static_cast<int>(members.size()) + 1)) break;
+        bool marked = false;
+        for (size_t k = r1.first; k < rb.first + rb.count; ++k)
+          marked = marked || std::binary_search(marked_[program].begin(), marked_[program].end(), k);
+        if (marked) break;
+        Ranges w, rd, in_b, out_b;
+        launched(r1.first, rb.first, &w, &rd);
+        (void)DependRangesOf(prog[ib], &in_b);  // x and A_b
+        (void)WriteRangesOf(prog[ib], &out_b);  // t_b
+        if (overlap(in_b, w) || overlap(out_b, w) || overlap(out_b, rd) || overlap(out_b, in_b)) break;
+        members.push_back(b);
+      }
+      if (members.size() < 2) continue;
+      const size_t grp_first = chains[members.front()].first;
+      const size_t grp_end = chains[members.back()].first + chains[members.back()].count;
+      for (size_t j = 0; j < members.size(); ++j) {
+        ChainRun& r = chains[members[j]];
+        r.rd_mode = j == 0 ? 1 : -1;
+        r.grp_first = grp_first;
+        r.grp_end = grp_end;
+        if (j == 0)
+          for (size_t m : members) r.grp_rowdots.push_back(chains[m].first + 1);
+      }
+      a = members.back();
+    }
+  }
+
   size_t PlanLoraBase(int program, size_t i) {
     const auto& prog = plan_.program[program];
     auto marked = [&](size_t k) {
@@ -1351,13 +1442,21 @@ class Engine {
     return nullptr;
   }
 
-  Status LaunchChain(int program, const ChainRun& run, const Ctx& c) {
+  Status LaunchChain(int program, const ChainRun& run, const Ctx& c, size_t begin, size_t end) {
     switch (run.kind) {
       case ChainKind::kDense: return LaunchGemm(run.d, plans_[program][run.first], c);
       case ChainKind::kLoraBase: {
         const size_t i1 = run.first + 1;
-        if (Status s = LaunchGemm(DescOf(plan_.program[program][i1]), plans_[program][i1], c); !s)
-          return s;
+        const bool grouped = run.rd_mode != 0 && run.grp_first >= begin && run.grp_end <= end;
+        if (grouped && run.rd_mode == 1) {
+          GemmDesc ds[4];
+          const int n = static_cast<int>(run.grp_rowdots.size());
+          for (int j = 0; j < n; ++j) ds[j] = DescOf(plan_.program[program][run.grp_rowdots[j]]);
+          if (Status s = LaunchSkinnyRowdotGroup(ds, n, c); !s) return s;
+        } else if (!grouped) {
+          if (Status s = LaunchGemm(DescOf(plan_.program[program][i1]), plans_[program][i1], c); !s)
+            return s;
+        }
         return LaunchGemm(run.d, plans_[program][run.first], c);
       }
       case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
@@ -1385,7 +1484,7 @@ class Engine {
     while (q < chains.size() && chains[q].first < begin) ++q;
     for (size_t i = begin; i < end;) {
       if (q < chains.size() && chains[q].first == i && i + chains[q].count <= end) {
-        if (Status s = LaunchChain(program, chains[q], c); !s) return s;
+        if (Status s = LaunchChain(program, chains[q], c, begin, end); !s) return s;
         i += chains[q].count;
         ++q;
         continue;
@@ -2027,7 +2126,7 @@ class Engine {
             i += run.count;
             continue;
           }
-          if (Status s = LaunchChain(program, run, c); !s) {
+          if (Status s = LaunchChain(program, run, c, 0, n); !s) {
             result = s;
             break;
           }
@@ -2147,7 +2246,12 @@ class Engine {
       switch (run->kind) {
         case ChainKind::kDense: return "in GEMM epilogue";
         case ChainKind::kLoraBase:
-          return idx == run->first + 1 ? "in LoRA run (launched first)" : "in LoRA epilogue";
+          if (idx != run->first + 1) return "in LoRA epilogue";
+          if (run->rd_mode == 1)
+            return "in LoRA run: rowdot group of " + std::to_string(run->grp_rowdots.size()) +
+                   " (launched first)";
+          if (run->rd_mode == -1) return "in LoRA run: in an earlier rowdot group";
+          return "in LoRA run (launched first)";
         case ChainKind::kPointwise: return "in pointwise run";
         default: return "in chain";
       }

@@ -68,6 +68,10 @@ struct SkArgs {
   // would have stored it.
   int scale_stream;
   float stream_scale;
+  // rowdot group: block nb of the output reads its own B operand Bm[nb] and
+  // writes its own C, Cm[nb]; each is N <= 16 columns wide (same ldb, ldc).
+  const float* Bm[4];
+  float* Cm[4];
 };
 
 // v * scale where `keep`, else +0.0, with no branch: the mask is an AND of
@@ -313,6 +317,102 @@ __global__ __launch_bounds__(64 * kRowdotWaves) void skinny_rowdot(SkArgs p) {
       if (mo < p.M) p.C[mo * p.ldc + n] = Epilogue(p, mo, n, s[i]);
     }
   }
+}
+
+// ---- rowdot group -------------------------------------------------------------
+//
+// NB rowdots over the same A (the LoRA down-projections of one layer input:
+// t_nb = x A_nb), A read once. The layout and the per-output k order are the
+// lone rowdot's (lane (q, c), wavefront K slices summed in order), so each
+// member's output has the bits of its own launch; a workgroup takes RB
+// blocks of 16 rows, so each of its B fragments serves RB row blocks.
+template <int NB, int RB, int U>
+__global__ __launch_bounds__(64 * kRowdotWaves) void skinny_rowdot_group(SkArgs p) {
+  __shared__ floatx4 red[kRowdotWaves][RB][NB][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * (16 * RB);
+  const int64_t ngroups = (p.K + 15) / 16;
+  const int64_t per = (ngroups + kRowdotWaves - 1) / kRowdotWaves;
+  const int64_t gb = w * per, ge = std::min<int64_t>(gb + per, ngroups);
+  const float* arow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+    arow[rb] = p.A + std::min<int64_t>(m0 + 16 * rb + c, p.M - 1) * p.lda;
+  const int64_t ncol = std::min<int64_t>(c, p.N - 1);
+  floatx4 acc[RB][NB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[rb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto load = [&](int64_t g, float4 (&a)[RB], float4 (&b)[NB]) {
+    const int64_t k0 = 16 * g + 4 * q;
+    const bool in = g < ge && k0 < p.K;  // K % 4 == 0: a float4 is wholly in or out
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      a[rb] = in ? *reinterpret_cast<const float4*>(arow[rb] + k0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float* B = p.Bm[nb];
+      if (p.b_kc) {
+        b[nb] = in ? *reinterpret_cast<const float4*>(B + ncol * p.ldb + k0)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      } else {
+        b[nb].x = in ? B[(k0 + 0) * p.ldb + ncol] : 0.0f;
+        b[nb].y = in ? B[(k0 + 1) * p.ldb + ncol] : 0.0f;
+        b[nb].z = in ? B[(k0 + 2) * p.ldb + ncol] : 0.0f;
+        b[nb].w = in ? B[(k0 + 3) * p.ldb + ncol] : 0.0f;
+      }
+    }
+  };
+  float4 a[U][RB], b[U][NB], an[U][RB], bn[U][NB];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load(gb + u, a[u], b[u]);
+  for (int64_t g = gb; g < ge; g += U) {
+    if (g + U < ge)
+#pragma unroll
+      for (int u = 0; u < U; ++u) load(g + U + u, an[u], bn[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][rb].x, b[u][nb].x, acc[rb][nb], 0, 0, 0);
+          acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][rb].y, b[u][nb].y, acc[rb][nb], 0, 0, 0);
+          acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][rb].z, b[u][nb].z, acc[rb][nb], 0, 0, 0);
+          acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][rb].w, b[u][nb].w, acc[rb][nb], 0, 0, 0);
+        }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) a[u][rb] = an[u][rb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) b[u][nb] = bn[u][nb];
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[w][rb][nb][lane] = acc[rb][nb];
+  __syncthreads();
+  if (w != 0) return;
+  // Lane (q, c) element i: row m0 + 16 rb + 4q + i, column c of member nb;
+  // wavefront partials in order.
+  if (c >= p.N) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      floatx4 s = red[0][rb][nb][lane];
+#pragma unroll
+      for (int ww = 1; ww < kRowdotWaves; ++ww) s += red[ww][rb][nb][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t mo = m0 + 16 * rb + 4 * q + i;
+        if (mo < p.M) p.Cm[nb][mo * p.ldc + c] = s[i];
+      }
+    }
 }
 
 // ---- colsum (TN, small M or N) --------------------------------------------------
@@ -911,6 +1011,51 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
       break;
   }
   return LaunchStatus("Gemm(skinny dual finish)");
+}
+
+bool SkinnyRowdotGroupFits(const GemmDesc* ds, int n) {
+  if (n < 2 || n > 4) return false;
+  const GemmDesc& d = ds[0];
+  for (int j = 0; j < n; ++j) {
+    const GemmDesc& e = ds[j];
+    if (SkinnyKindOf(e) != SkinnyKind::kRowDot || e.A != d.A || e.M != d.M || e.K != d.K ||
+        e.lda != d.lda || e.N != d.N || e.N > 16 || e.ldb != d.ldb || e.ldc != d.ldc ||
+        e.b_kc != d.b_kc || e.alpha != 1.0f || e.accumulate || e.bias || e.act != 0 ||
+        e.scale_stream || !e.B || !e.C)
+      return false;
+  }
+  return true;
+}
+
+Status LaunchSkinnyRowdotGroup(const GemmDesc* ds, int n, const Ctx& ctx) {
+  if (!SkinnyRowdotGroupFits(ds, n))
+    return Status::Fail(kUnitEngine, "Gemm: the rowdots do not form a group");
+  const GemmDesc& d = ds[0];
+  SkArgs a{};
+  a.A = static_cast<const float*>(d.A);
+  a.M = d.M; a.N = d.N; a.K = d.K;
+  a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
+  a.alpha = 1.0f;
+  a.b_kc = d.b_kc ? 1 : 0;
+  a.write_u = 1;
+  for (int j = 0; j < n; ++j) {
+    a.Bm[j] = static_cast<const float*>(ds[j].B);
+    a.Cm[j] = ds[j].C;
+  }
+  // Two 16-row blocks per workgroup, two k groups per batch: in the C4 step
+  // the q/k/v group took 12 us less per layer than the three rowdots; with
+  // one row block it took as long as they did (each workgroup re-reads all
+  // of the group's B operands from L2), and four k groups per batch spill.
+  constexpr int kRB = 2, kU = 2;
+  const int64_t gx = (d.M + 16 * kRB - 1) / (16 * kRB);
+  if (gx > 0x7FFFFFFF) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+  const dim3 grid(static_cast<unsigned>(gx)), block(64 * kRowdotWaves);
+  switch (n) {
+    case 2: hipLaunchKernelGGL((skinny_rowdot_group<2, kRB, kU>), grid, block, 0, ctx.stream, a); break;
+    case 3: hipLaunchKernelGGL((skinny_rowdot_group<3, kRB, kU>), grid, block, 0, ctx.stream, a); break;
+    default: hipLaunchKernelGGL((skinny_rowdot_group<4, kRB, kU>), grid, block, 0, ctx.stream, a); break;
+  }
+  return LaunchStatus("Gemm(skinny rowdot group)");
 }
 
 namespace {

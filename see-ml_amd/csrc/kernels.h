@@ -166,6 +166,13 @@ Status LaunchSkinny(const GemmDesc& d, const Ctx& ctx);
 bool SkinnyDualFits(const GemmDesc& rd, const GemmDesc& cs);
 size_t SkinnyDualWorkspace(const GemmDesc& rd);
 Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const Ctx& ctx);
+// 2..4 rowdots over the same A (the LoRA down-projections of one layer
+// input: t_i = x A_i) in one pass over A. Fits: each on the skinny rowdot
+// kernel with the same shape, N <= 16 and a plain epilogue. Each output has
+// the bits of its rowdot's own launch. The caller proves the group may run
+// as one launch at the first member's place.
+bool SkinnyRowdotGroupFits(const GemmDesc* ds, int n);
+Status LaunchSkinnyRowdotGroup(const GemmDesc* ds, int n, const Ctx& ctx);
 // The plan index that selects the skinny kernels (one past the tile configs).
 int GemmSkinnyConfig();
 

@@ -451,7 +451,12 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
             ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
             heads = [c for c in ch if "+LoRA" in c]
             assert len(heads) >= 4, ch
-            assert sum(c == "in LoRA run (launched first)" for c in ch) == len(heads)
+            assert sum(c.startswith("in LoRA run") for c in ch) == len(heads)
+            # the q/k/v down-projections over one layer input run as one pass
+            groups = [c for c in ch if c.startswith("in LoRA run: rowdot group of ")]
+            assert groups, ch
+            assert sum(int(c.split()[6]) for c in groups) == sum(
+                c.startswith("in LoRA run: in an earlier") for c in ch) + len(groups)
         runs.append((np.array(losses, np.float32), persistent(e, p)))
         e.close()
     assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
