@@ -507,6 +507,15 @@ class Engine {
     const UpdateInstruction& ins = plan_.program[program][idx];
     const auto op = static_cast<Op>(ins.opcode);
     if (IsGemmOp(ins.opcode)) {
+      if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
+        const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
+        if (idx == g.members.back()) {
+          GemmDesc ds[4];
+          for (size_t j = 0; j < g.members.size(); ++j) ds[j] = DescOf(plan_.program[program][g.members[j]]);
+          return std::max(plans_[program][idx].ws_bytes,
+                          SkinnyColsumGroupWorkspace(ds, static_cast<int>(g.members.size())));
+        }
+      }
       if (duals_[program][idx] >= 0)
         return std::max(plans_[program][idx].ws_bytes, SkinnyDualWorkspace(DualRowdot(program, idx)));
       return plans_[program][idx].ws_bytes;
@@ -740,6 +749,7 @@ class Engine {
     PlanScaleFolds(program);
     PlanDualRuns(program);
     PlanRowdotGroups(program);
+    if (Status s = PlanColsumGroups(program); !s) return s;
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -1442,6 +1452,138 @@ class Engine {
     return nullptr;
   }
 
+  // Colsum groups (kernels.h LaunchSkinnyColsumGroup): 2..4 standalone
+  // colsums on the skinny kernel over one large operand X (the LoRA
+  // dA_j = x^T dt_j of the q/k/v projections, which share the layer input)
+  // launch as one pass over X at the last member's position. The plan
+  // reuses one slot for the dt_j, so each earlier member copies its small
+  // operand to a private buffer at its own position: the group then reads
+  // every operand's value of that position. An earlier member's output is
+  // written later than in plan order, so nothing between the first and the
+  // last member may write X, or read or write an earlier member's output;
+  // the outputs are disjoint from each other and from every member's
+  // operands. Each output has the bits of its own launch. Applied only when
+  // the executed range holds the whole group.
+  struct ColsumGroup {
+    std::vector<size_t> members;      // plan order
+    std::vector<size_t> priv_off;     // per earlier member: its copy, in floats
+    std::vector<size_t> priv_floats;  // into cs_priv_[program]
+  };
+
+  static bool ColsumBigIsA(const GemmDesc& d) { return d.N <= 64 && d.M >= 128; }
+
+  Status PlanColsumGroups(int program) {
+    cs_groups_[program].clear();
+    const auto& prog = plan_.program[program];
+    cs_group_of_[program].assign(prog.size(), -1);
+    if (cs_priv_[program]) {
+      // A replay of the previous graph may still read the old copies.
+      if (Status s = HipOk(hipStreamSynchronize(stream_), "colsum group sync"); !s) return s;
+      (void)hipFree(cs_priv_[program]);
+      cs_priv_[program] = nullptr;
+    }
+    const auto& chains = chains_[program];
+    std::vector<int> chain_of(prog.size(), -1);
+    std::vector<uint8_t> rd_span(prog.size(), 0);  // inside a rowdot group's span
+    for (size_t c = 0; c < chains.size(); ++c) {
+      for (size_t k = chains[c].first; k < chains[c].first + chains[c].count; ++k)
+        chain_of[k] = static_cast<int>(c);
+      if (chains[c].rd_mode != 0)
+        for (size_t k = chains[c].grp_first; k < chains[c].grp_end && k < prog.size(); ++k) rd_span[k] = 1;
+    }
+    auto marked = [&](size_t k) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), k);
+    };
+    auto candidate = [&](size_t k) {
+      const UpdateInstruction& g = prog[k];
+      return IsGemmOp(g.opcode) && g.flags == 0 && chain_of[k] < 0 && cs_group_of_[program][k] < 0 &&
+             duals_[program][k] < 0 && plans_[program][k].cfg == GemmSkinnyConfig() &&
+             SkinnyKindOf(DescOf(g)) == SkinnyKind::kColSum;
+    };
+    auto overlap = [](const Ranges& a, const Ranges& b) {
+      for (const auto& x : a)
+        if (Overlaps(b, x.first, x.second)) return true;
+      return false;
+    };
+    size_t total = 0;
+    for (size_t i = 0; i < prog.size(); ++i) {
+      if (rd_span[i] || marked(i) || !candidate(i)) continue;
+      GemmDesc ds[4];
+      ds[0] = DescOf(prog[i]);
+      const bool big_a = ColsumBigIsA(ds[0]);
+      const uint64_t xref = big_a ? prog[i].in[0] : prog[i].in[1];
+      const int64_t ldx = big_a ? ds[0].lda : ds[0].ldb, W = big_a ? ds[0].M : ds[0].N;
+      Ranges xr;
+      if (!IsRodataRef(xref))
+        xr.emplace_back(RefOffset(xref), static_cast<uint64_t>((ds[0].K - 1) * ldx + W) * sizeof(float));
+      std::vector<size_t> members{i};
+      Ranges outs, ins;  // the members' outputs and operands
+      if (!WriteRangesOf(prog[i], &outs) || !DependRangesOf(prog[i], &ins)) continue;
+      for (size_t k = i + 1; k < prog.size() && k < i + 64 && members.size() < 4; ++k) {
+        if (marked(k) || rd_span[k]) break;
+        if (candidate(k)) {
+          ds[members.size()] = DescOf(prog[k]);
+          Ranges wk, rk;
+          if (SkinnyColsumGroupFits(ds, static_cast<int>(members.size()) + 1) && WriteRangesOf(prog[k], &wk) &&
+              DependRangesOf(prog[k], &rk) && !overlap(wk, ins) && !overlap(wk, outs) && !overlap(wk, rk) &&
+              !overlap(rk, outs)) {
+            members.push_back(k);
+            outs.insert(outs.end(), wk.begin(), wk.end());
+            ins.insert(ins.end(), rk.begin(), rk.end());
+            continue;
+          }
+        }
+        // an instruction between members, run in plan order
+        const Ranges& w = writes_[program][k];
+        if (overlap(w, xr) || overlap(w, outs) || overlap(depends_[program][k], outs)) break;
+      }
+      if (members.size() < 2) continue;
+      ColsumGroup g;
+      g.members = members;
+      for (size_t j = 0; j + 1 < members.size(); ++j) {
+        const GemmDesc d = DescOf(prog[members[j]]);
+        const int64_t ld = big_a ? d.ldb : d.lda, R = big_a ? d.N : d.M;
+        const size_t floats = static_cast<size_t>((d.K - 1) * ld + R);
+        g.priv_off.push_back(total);
+        g.priv_floats.push_back(floats);
+        total += (floats + 63) / 64 * 64;  // 256-byte aligned copies
+      }
+      for (size_t m : members) cs_group_of_[program][m] = static_cast<int>(cs_groups_[program].size());
+      cs_groups_[program].push_back(std::move(g));
+    }
+    if (total == 0) return Status::Ok();
+    return HipOk(hipMalloc(&cs_priv_[program], total * sizeof(float)), "colsum group copies");
+  }
+
+  // The colsum group instruction idx belongs to when the executed range
+  // [begin, end) holds the whole group, else -1.
+  int ColsumGroupAt(int program, size_t idx, size_t begin, size_t end) const {
+    if (idx >= cs_group_of_[program].size() || cs_group_of_[program][idx] < 0) return -1;
+    const int g = cs_group_of_[program][idx];
+    const ColsumGroup& grp = cs_groups_[program][g];
+    return grp.members.front() >= begin && grp.members.back() < end ? g : -1;
+  }
+
+  // Member idx's step of colsum group g: an earlier member copies its small
+  // operand; the last launches the group.
+  Status ColsumGroupStep(int program, int g, size_t idx, const Ctx& c) const {
+    const ColsumGroup& grp = cs_groups_[program][g];
+    const auto& prog = plan_.program[program];
+    float* priv = static_cast<float*>(cs_priv_[program]);
+    const size_t n = grp.members.size();
+    GemmDesc ds[4];
+    for (size_t j = 0; j < n; ++j) ds[j] = DescOf(prog[grp.members[j]]);
+    const bool big_a = ColsumBigIsA(ds[0]);
+    for (size_t j = 0; j + 1 < n; ++j) {
+      const void*& small = big_a ? ds[j].B : ds[j].A;
+      if (grp.members[j] == idx)
+        return Copy(static_cast<const float*>(small), priv + grp.priv_off[j], grp.priv_floats[j], c);
+      small = priv + grp.priv_off[j];
+    }
+    if (idx != grp.members.back()) return Status::Fail(kUnitEngine, "not a colsum group member");
+    return LaunchSkinnyColsumGroup(ds, static_cast<int>(n), c);
+  }
+
   Status LaunchChain(int program, const ChainRun& run, const Ctx& c, size_t begin, size_t end) {
     switch (run.kind) {
       case ChainKind::kDense: return LaunchGemm(run.d, plans_[program][run.first], c);
@@ -1496,6 +1638,11 @@ class Engine {
           return s;
         i += runs[r].count;
         ++r;
+        continue;
+      }
+      if (const int g = ColsumGroupAt(program, i, begin, end); g >= 0) {
+        if (Status s = ColsumGroupStep(program, g, i, c); !s) return s;
+        ++i;
         continue;
       }
       if (Status s = Dispatch(program, i, c); !s) return s;
@@ -1580,6 +1727,8 @@ class Engine {
       return Status::Ok();
     }
     if (Status s = PlanFusion(program); !s) return s;
+    // the colsum groups' partials can need more workspace than any launch alone
+    if (Status s = EnsureWorkspace(program); !s) return s;
     // One graph for the whole program; with marked instructions, one graph
     // per unmarked stretch and each marked launch between them.
     const size_t n = plan_.program[program].size();
@@ -2145,7 +2294,11 @@ class Engine {
           (void)hipEventRecord(ev[i], stream_);
           continue;
         }
-        if (Status s = Dispatch(program, i, c); !s) { result = s; break; }
+        const int cg = use_graph_ ? ColsumGroupAt(program, i, 0, n) : -1;
+        if (Status s = cg >= 0 ? ColsumGroupStep(program, cg, i, c) : Dispatch(program, i, c); !s) {
+          result = s;
+          break;
+        }
         (void)hipEventRecord(ev[++i], stream_);
       }
       if (!result) break;
@@ -2258,6 +2411,12 @@ class Engine {
     }
     if (run && run->kind == ChainKind::kPointwise)
       return "pointwise run of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
+    if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
+      const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
+      return idx == g.members.back()
+                 ? "skinny/colsum group of " + std::to_string(g.members.size()) + " (launched last)"
+                 : std::string("copies its operand for a later colsum group");
+    }
     if (!IsGemmOp(plan_.program[program][idx].opcode)) return std::string();
     const GemmPlan& p = plans_[program][idx];
     if (p.cfg == GemmSkinnyConfig()) {
@@ -2293,6 +2452,10 @@ class Engine {
       if (fused_segs_[p]) (void)hipFree(fused_segs_[p]);
       fused_segs_[p] = nullptr;
       fused_runs_[p].clear();
+      if (cs_priv_[p]) (void)hipFree(cs_priv_[p]);
+      cs_priv_[p] = nullptr;
+      cs_groups_[p].clear();
+      cs_group_of_[p].clear();
     }
     if (d_argmax_) (void)hipFree(d_argmax_);
     d_argmax_ = nullptr;
@@ -2337,6 +2500,9 @@ class Engine {
   uint64_t* h_count_ = nullptr;
   std::vector<FusedRun> fused_runs_[3];
   std::vector<ChainRun> chains_[3];
+  std::vector<ColsumGroup> cs_groups_[3];  // PlanColsumGroups
+  std::vector<int> cs_group_of_[3];        // per instruction: its colsum group, or -1
+  void* cs_priv_[3] = {nullptr, nullptr, nullptr};  // the groups' operand copies
   std::vector<Ranges> depends_[3];  // per instruction: DependRangesOf
   std::vector<Ranges> writes_[3];   // per instruction: WriteRangesOf
   Ranges observed_;

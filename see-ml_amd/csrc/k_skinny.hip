@@ -572,6 +572,120 @@ __global__ __launch_bounds__(kThreads) void skinny_colsum_finish1(SkArgs p) {
   }
 }
 
+// ---- colsum group ---------------------------------------------------------------
+//
+// NB colsums over the same large operand X (the LoRA dA_j = x^T dt_j of one
+// layer input), X read once: member nb's small operand is Bm[nb] (its rank
+// <= 16 wide, ldy shared) and its output Cm[nb]. The k-groups, the
+// wavefronts' k ranges, the quad order and the group-order sum of the
+// partials are those of skinny_colsum and its finish, so every member's
+// output has the bits of its own launch. Partial layout: ws[g][w][16 nb + n].
+
+template <int NB>
+__global__ __launch_bounds__(kThreads) void skinny_colsum_group(SkArgs p) {
+  __shared__ floatx4 red[4][NB][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int q = lane >> 4, c = lane & 15;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kColW;
+  const int g = static_cast<int>(blockIdx.y);
+  const float* X = p.big_is_m ? p.A : p.B;  // X[k][w]
+  const int64_t ldx = p.big_is_m ? p.lda : p.ldb;
+  const int64_t ldy = p.big_is_m ? p.ldb : p.lda;
+  const int64_t kb0 = static_cast<int64_t>(g) * p.k_per_group;
+  const int64_t ke0 = std::min<int64_t>(p.K, kb0 + p.k_per_group);
+  const int64_t span = ke0 > kb0 ? ke0 - kb0 : 0;
+  const int64_t sub = ((span + 15) / 16) * 4;  // k per wavefront, whole quads
+  const int64_t kb = kb0 + w * sub, ke = std::min<int64_t>(ke0, kb + sub);
+  const int64_t wl = w0 + 4 * c;
+  const bool w_ok = wl < p.W;
+  const bool n_ok = c < p.R;
+  floatx4 acc[4][NB];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[c4][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int U = 4;  // k quads per batch; the next batch is in flight
+  auto load = [&](int64_t k4, float4 (&x)[U], float (&y)[U][NB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = k4 + 4 * u + q;
+      const bool kin = k < ke;
+      x[u] = kin && w_ok ? *reinterpret_cast<const float4*>(X + k * ldx + wl)
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) y[u][nb] = kin && n_ok ? p.Bm[nb][k * ldy + c] : 0.0f;
+    }
+  };
+  float4 x[U], xn[U];
+  float y[U][NB], yn[U][NB];
+  load(kb, x, y);
+  for (int64_t k4 = kb; k4 < ke; k4 += 4 * U) {
+    if (k4 + 4 * U < ke) load(k4 + 4 * U, xn, yn);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].x, y[u][nb], acc[0][nb], 0, 0, 0);
+        acc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].y, y[u][nb], acc[1][nb], 0, 0, 0);
+        acc[2][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].z, y[u][nb], acc[2][nb], 0, 0, 0);
+        acc[3][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u].w, y[u][nb], acc[3][nb], 0, 0, 0);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      x[u] = xn[u];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) y[u][nb] = yn[u][nb];
+    }
+  }
+  // Wavefront partials summed in order 0 + 1 + 2 + 3 through LDS.
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) {
+    __syncthreads();
+    if (w != 0)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[w][nb][lane] = acc[c4][nb];
+    __syncthreads();
+    if (w == 0)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[c4][nb] += red[1][nb][lane];
+        acc[c4][nb] += red[2][nb][lane];
+        acc[c4][nb] += red[3][nb][lane];
+      }
+  }
+  if (w != 0 || !n_ok) return;
+  constexpr int RT = 16 * NB;  // partial row width
+  float* part = p.ws + static_cast<int64_t>(g) * p.W * RT;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t wi = w0 + 4 * (4 * q + i) + c4;
+        if (wi < p.W) part[wi * RT + 16 * nb + c] = acc[c4][nb][i];
+      }
+}
+
+// The group's partials summed in group order, one output per thread
+// (skinny_colsum_finish's order).
+template <int NB>
+__global__ __launch_bounds__(kThreads) void skinny_colsum_group_finish(SkArgs p) {
+  constexpr int RT = 16 * NB;
+  const int64_t total = p.W * RT;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; idx < total;
+       idx += stride) {
+    const int64_t wi = idx / RT;
+    const int nb = static_cast<int>((idx % RT) / 16), n = static_cast<int>(idx % 16);
+    if (n >= p.R) continue;
+    float s = p.ws[idx];
+    for (int g = 1; g < p.groups; ++g) s += p.ws[static_cast<int64_t>(g) * total + idx];
+    const int64_t m = p.big_is_m ? wi : n, nn = p.big_is_m ? n : wi;
+    p.Cm[nb][m * p.ldc + nn] = s;
+  }
+}
+
 // ---- dual: rowdot and colsum over one stream ---------------------------------
 //
 // The LoRA backward streams du twice: dt = du B^T (rowdot) and dB = t^T du
@@ -1011,6 +1125,79 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
       break;
   }
   return LaunchStatus("Gemm(skinny dual finish)");
+}
+
+bool SkinnyColsumGroupFits(const GemmDesc* ds, int n) {
+  if (n < 2 || n > 4) return false;
+  const GemmDesc& d = ds[0];
+  if (SkinnyKindOf(d) != SkinnyKind::kColSum) return false;
+  const bool big_m = d.N <= 64 && d.M >= 128;
+  for (int j = 0; j < n; ++j) {
+    const GemmDesc& e = ds[j];
+    const bool em = e.N <= 64 && e.M >= 128;
+    if (SkinnyKindOf(e) != SkinnyKind::kColSum || em != big_m || e.M != d.M || e.N != d.N ||
+        e.K != d.K || e.lda != d.lda || e.ldb != d.ldb || e.ldc != d.ldc ||
+        e.alpha != 1.0f || e.accumulate || e.bias || e.act != 0 || e.scale_stream || !e.C)
+      return false;
+    // the large operand is shared; the rank-wide one is the member's own
+    if (big_m ? (e.A != d.A || !e.B) : (e.B != d.B || !e.A)) return false;
+    if ((big_m ? d.N : d.M) > 16) return false;
+  }
+  return true;
+}
+
+size_t SkinnyColsumGroupWorkspace(const GemmDesc* ds, int n) {
+  const GemmDesc& d = ds[0];
+  const bool big_m = d.N <= 64 && d.M >= 128;
+  const int64_t W = big_m ? d.M : d.N;
+  return static_cast<size_t>(ColsumGroups(W, d.K)) * W * 16 * n * sizeof(float);
+}
+
+Status LaunchSkinnyColsumGroup(const GemmDesc* ds, int n, const Ctx& ctx) {
+  if (!SkinnyColsumGroupFits(ds, n))
+    return Status::Fail(kUnitEngine, "Gemm: the colsums do not form a group");
+  if (ctx.ws_bytes < SkinnyColsumGroupWorkspace(ds, n))
+    return Status::Fail(kUnitEngine, "Gemm: workspace too small for the colsum group");
+  const GemmDesc& d = ds[0];
+  SkArgs a{};
+  a.big_is_m = (d.N <= 64 && d.M >= 128) ? 1 : 0;
+  a.A = static_cast<const float*>(d.A);
+  a.B = static_cast<const float*>(d.B);
+  a.M = d.M; a.N = d.N; a.K = d.K;
+  a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
+  a.alpha = 1.0f;
+  a.ws = static_cast<float*>(ctx.ws);
+  a.W = a.big_is_m ? d.M : d.N;
+  a.R = a.big_is_m ? d.N : d.M;
+  // The rank-wide operand of member j: B when the large one is A, else A.
+  for (int j = 0; j < n; ++j) {
+    a.Bm[j] = static_cast<const float*>(a.big_is_m ? ds[j].B : ds[j].A);
+    a.Cm[j] = ds[j].C;
+  }
+  a.groups = static_cast<int>(ColsumGroups(a.W, d.K));
+  a.k_per_group = (d.K + a.groups - 1) / a.groups;
+  const int64_t gx = (a.W + kColW - 1) / kColW;
+  if (gx > 0x7FFFFFFF) return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(a.groups));
+  const dim3 fgrid(grid_for(static_cast<size_t>(a.W * 16 * n), kThreads, 4096));
+  switch (n) {
+    case 2:
+      hipLaunchKernelGGL(skinny_colsum_group<2>, grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny colsum group)"); !s) return s;
+      hipLaunchKernelGGL(skinny_colsum_group_finish<2>, fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+    case 3:
+      hipLaunchKernelGGL(skinny_colsum_group<3>, grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny colsum group)"); !s) return s;
+      hipLaunchKernelGGL(skinny_colsum_group_finish<3>, fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL(skinny_colsum_group<4>, grid, dim3(kThreads), 0, ctx.stream, a);
+      if (Status s = LaunchStatus("Gemm(skinny colsum group)"); !s) return s;
+      hipLaunchKernelGGL(skinny_colsum_group_finish<4>, fgrid, dim3(kThreads), 0, ctx.stream, a);
+      break;
+  }
+  return LaunchStatus("Gemm(skinny colsum group finish)");
 }
 
 bool SkinnyRowdotGroupFits(const GemmDesc* ds, int n) {

@@ -173,6 +173,13 @@ Status LaunchSkinnyDual(const GemmDesc& rd, const GemmDesc& cs, int which, const
 // as one launch at the first member's place.
 bool SkinnyRowdotGroupFits(const GemmDesc* ds, int n);
 Status LaunchSkinnyRowdotGroup(const GemmDesc* ds, int n, const Ctx& ctx);
+// 2..4 colsums over the same large operand (the LoRA dA_j = x^T dt_j of one
+// layer input) in one pass over it. Fits: each on the skinny colsum kernel
+// with the same shape, rank <= 16 and a plain epilogue. Each output has the
+// bits of its colsum's own launch.
+bool SkinnyColsumGroupFits(const GemmDesc* ds, int n);
+size_t SkinnyColsumGroupWorkspace(const GemmDesc* ds, int n);
+Status LaunchSkinnyColsumGroup(const GemmDesc* ds, int n, const Ctx& ctx);
 // The plan index that selects the skinny kernels (one past the tile configs).
 int GemmSkinnyConfig();
 

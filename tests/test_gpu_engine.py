@@ -420,6 +420,43 @@ def _check_dense_chains(ch, scaled=False):
         assert sum(c.endswith("+Scale+AddEW") for c in ch) >= 4, ch
 
 
+def test_colsum_groups_read_the_layer_input_once_and_are_bitwise(torch_gpu):
+    """The q/k/v LoRA dA = x^T dt colsums over one layer input run as one
+    pass over x at the last of them; each earlier one copies its dt (the plan
+    reuses that slot) at its own position. The fused graph equals the eager
+    engine bit for bit, also with a group member marked for timing (which
+    splits the graph there, so that group is not formed) and through the
+    per-instruction profile loop."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c4m")
+    runs, members = [], []
+    for mode in ("graph", "marked", "eager"):
+        e = engine(p, use_graph=mode != "eager")
+        if mode == "marked":
+            e.mark_timed(PROGRAM_TRAIN, [members[0]])
+        losses = []
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+        if mode != "eager":
+            ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+            groups = [i for i, c in enumerate(ch) if c.startswith("skinny/colsum group of ")]
+            copies = [i for i, c in enumerate(ch) if c.startswith("copies its operand")]
+            assert sum(int(ch[i].split()[3]) - 1 for i in groups) == len(copies), ch
+            if mode == "graph":
+                assert any(ch[i].split()[3] == "3" for i in groups), ch
+                members = copies
+            else:
+                assert members[0] not in copies and members[0] not in groups
+        runs.append((np.array(losses, np.float32), persistent(e, p)))
+        if mode == "graph":
+            assert np.all(np.isfinite(e.profile(PROGRAM_TRAIN, reps=1)))
+        e.close()
+    for k in (1, 2):
+        assert np.array_equal(runs[0][0].view(np.uint32), runs[k][0].view(np.uint32)), k
+        assert np.array_equal(runs[0][1].view(np.uint32), runs[k][1].view(np.uint32)), k
+
+
 def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
     """With the projection GEMMs on the 256x128 tile and the rank-16
     up-projections on a tile plan (both forced here; the C4 autotuner picks
