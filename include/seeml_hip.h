@@ -349,6 +349,16 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
 int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const float* b,
                                uint64_t r_rd, float* dt, const float* t, uint64_t r_cs, float* db,
                                int which, int scaled, float scale, void* stream);
+/* The q/k/v LoRA GEMMs over one layer input x [T, D] as one pass over x
+ * (the engine groups the plan's members; tests call it directly), n = 2..4
+ * members of rank r <= 16. kind 0, the rowdot group: out[j] = x a[j]
+ * (a[j] [D, r] row-major, out[j] [T, r]). kind 1, the colsum group:
+ * out[j] = x^T a[j] (a[j] [T, r], out[j] [D, r]). Each output has the bits
+ * of its own skinny GEMM. No reference counterpart: the reference runs each
+ * GEMM on its own (gemm.cc:173-200). */
+int seeml_hip_gemm_skinny_group(int kind, const float* x, uint64_t T, uint64_t D,
+                                const float* const* a, uint64_t r, float* const* out, int n,
+                                void* stream);
 /* GEMM as two launches over column ranges (tests): columns [0, n_split) on
  * tile config `cfg`, the rest on `tail_cfg` (both one split); with `out`,
  * the fused AddEW out = addend + C. n_split = 0: one launch of `cfg`. */

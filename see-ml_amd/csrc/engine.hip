@@ -2900,6 +2900,22 @@ int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const flo
   SEEML_CTX(seeml_hip::SkinnyDualWorkspace(rd));
   return seeml_hip::Report(seeml_hip::LaunchSkinnyDual(rd, cs, which, ctx));
 }
+int seeml_hip_gemm_skinny_group(int kind, const float* x, uint64_t T, uint64_t D,
+                                const float* const* a, uint64_t r, float* const* out, int n,
+                                void* stream) {
+  if (kind < 0 || kind > 1 || n < 2 || n > 4 || !a || !out)
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine, "skinny group: bad arguments"));
+  seeml_hip::GemmDesc ds[4];
+  for (int j = 0; j < n; ++j)
+    ds[j] = kind == 0 ? seeml_hip::GemmNNDesc(x, a[j], out[j], T, r, D)
+                      : seeml_hip::GemmTNDesc(x, a[j], out[j], D, r, T);
+  if (kind == 0 ? !seeml_hip::SkinnyRowdotGroupFits(ds, n) : !seeml_hip::SkinnyColsumGroupFits(ds, n))
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
+                                                     "skinny group: the GEMMs do not form a group"));
+  SEEML_CTX(kind == 0 ? 0 : seeml_hip::SkinnyColsumGroupWorkspace(ds, n));
+  return seeml_hip::Report(kind == 0 ? seeml_hip::LaunchSkinnyRowdotGroup(ds, n, ctx)
+                                     : seeml_hip::LaunchSkinnyColsumGroup(ds, n, ctx));
+}
 int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
                                 uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
                                 const float* addend, float* out, void* stream) {

@@ -225,6 +225,40 @@ def test_skinny_dual_pass(env, orc, T, D, r_rd, r_cs, scaled):
     assert np.all(np.isnan(outs[1][1])) and np.all(np.isnan(outs[2][0]))  # the other is untouched
 
 
+@pytest.mark.parametrize("kind,T,D,r,n", [
+    (0, 8192, 2048, 16, 3), (0, 1000, 520, 8, 2), (0, 300, 256, 16, 4), (0, 4096, 1028, 5, 3),
+    (1, 8192, 2048, 16, 3), (1, 1000, 520, 8, 2), (1, 257, 256, 16, 4), (1, 4100, 1028, 5, 3)])
+def test_skinny_groups_are_bitwise_their_members(env, orc, kind, T, D, r, n):
+    """The q/k/v LoRA GEMMs over one layer input as one pass over x: the
+    rowdot group (t_j = x a_j, the down-projections) and the colsum group
+    (dA_j = x^T dt_j). Each member's output has the bits of its own skinny
+    GEMM and matches the oracle's GEMM; ragged T and D, ranks below 16, and
+    2 to 4 members."""
+    import ctypes
+    skinny = env.L.seeml_hip_gemm_config_count() - 1
+    x = rnd(T * D, 81)
+    k_small = D if kind == 0 else T
+    rows = T if kind == 0 else D
+    a = [rnd(k_small * r, 82 + j) for j in range(n)]
+    xd, ad = env.T(x), [env.T(v) for v in a]
+    outs = [env.T(np.full(rows * r, np.nan, f32)) for _ in range(n)]
+    ap = (ctypes.c_void_p * n)(*[t.data_ptr() for t in ad])
+    op = (ctypes.c_void_p * n)(*[t.data_ptr() for t in outs])
+    env.call("seeml_hip_gemm_skinny_group", kind, xd, T, D, ctypes.addressof(ap), r, ctypes.addressof(op), n)
+    for j in range(n):
+        lone = env.T(np.full(rows * r, np.nan, f32))
+        want = np.zeros(rows * r, f32)
+        if kind == 0:
+            env.call("seeml_hip_gemm_forced", 0, xd, ad[j], lone, T, r, D, skinny, 1)
+            orc.gemm_nn(x, a[j], want, T, r, D, None, 0)
+        else:
+            env.call("seeml_hip_gemm_forced", 2, xd, ad[j], lone, D, r, T, skinny, 1)
+            orc.gemm_tn(x, a[j], want, D, r, T)
+        got = env.H(outs[j])
+        assert same_bits(got, env.H(lone)), j
+        assert rel_err(got, want) <= TOL_STEP, j
+
+
 @pytest.mark.parametrize("layout,M,N,K,tail,n_split", [
     (1, 512, 1000, 256, 0, 768), (0, 300, 520, 128, 4, 384), (2, 256, 640, 96, 0, 512),
     (1, 256, 5504, 64, 4, 5120), (1, 512, 5504, 96, 5, 5120), (0, 300, 1000, 128, 5, 768)])
