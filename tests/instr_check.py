@@ -6,7 +6,7 @@ The engine replays a program instruction by instruction
 read from the arena (and rodata); after it runs, its outputs. The oracle
 then recomputes the outputs from those same inputs — for GEMMs on 64
 sampled output rows (each output row's k order does not depend on the other
-rows, so the oracle's rows are its full product's rows), for attention on
+rows, so the oracle's rows are its full product's rows; 16 for a further fused variant of an already checked group), for attention on
 one (batch, head), for row kernels on sampled rows, for everything else on
 whole tensors. Operand layouts follow the lowering
 (compiler/backend/trainer/instruction_lowering.cc:55-340, restated in
@@ -48,7 +48,9 @@ CHECKED = {"GemmNN", "GemmNT", "GemmTN", "GemmAccNN", "GemmNNQ8", "GemmNTQ8", "A
            "AddBias", "Scale", "ReluFwd", "ReluBwd", "GeluFwd", "GeluBwd", "SiluFwd", "SiluBwd",
            "RmsNormFwd", "RmsNormBwd", "LayerNormFwd", "LayerNormBwd", "RopeFwd", "RopeBwd",
            "AttnFwd", "AttnDP", "AttnDV", "SoftmaxRowsBwd", "AttnDQ", "AttnDK", "EmbedFwd",
-           "SoftmaxXEntFwd", "SoftmaxXEntBwd", "Fill", "AdamWStep"}
+           "SoftmaxXEntFwd", "SoftmaxXEntBwd", "MseFwd", "MseBwd", "Fill", "AdamWStep"}
+
+GEMMS = {"GemmNN", "GemmNT", "GemmTN", "GemmAccNN", "GemmNNQ8", "GemmNTQ8"}
 
 
 class Checker:
@@ -57,6 +59,7 @@ class Checker:
         self.rng = np.random.default_rng(seed)
         self.rows = sample_rows
         self.step = 1
+        self.peak = None  # max|want| of the latest GEMM check
 
     def rd(self, ref, count, dtype=np.float32):
         if dtype == np.float32:
@@ -138,6 +141,12 @@ class Checker:
         if op == "SoftmaxXEntBwd":
             N, Cc = int(o[0]), int(o[1])
             return {"p": r(i[0], N * Cc), "labels": r(i[1], N, np.int32), "seed": r(i[2], 1)}
+        if op in ("MseFwd", "MseBwd"):
+            n = int(o[0])
+            d = {"pred": r(i[0], n), "target": r(i[1], n)}
+            if op == "MseBwd":
+                d["seed"] = r(i[2], 1)
+            return d
         if op == "Fill":
             return {}
         if op == "AdamWStep":
@@ -181,6 +190,7 @@ class Checker:
                 orc.gemm_nt_q8(Asub, d["B"], want, m, N, K, fbits(i[3]))
             got = r(i[2], M * N).reshape(M, N)[rows].ravel()
             close(got, want, f"{M}x{N}x{K}")
+            self.peak = float(np.max(np.abs(want))) if want.size else 0.0
             return
         if op in ("AddEW", "MulEW"):
             n = int(o[0])
@@ -319,6 +329,17 @@ class Checker:
             orc.softmax_xent_bwd(d["p"], d["labels"], d["seed"], want, N, Cc)
             exact(r(i[3], N * Cc), want)
             return
+        if op == "MseFwd":
+            loss = np.zeros(1, f32)
+            orc.mse_fwd(d["pred"], d["target"], loss, int(o[0]))
+            close(r(i[2], 1), loss)
+            return
+        if op == "MseBwd":
+            n = int(o[0])
+            want = np.zeros(n, f32)
+            orc.mse_bwd(d["pred"], d["target"], d["seed"], want, n)
+            exact(r(i[3], n), want)
+            return
         if op == "Fill":
             n = int(o[0])
             exact(r(i[0], n), np.full(n, fbits(i[1]), f32))
@@ -338,26 +359,41 @@ class Checker:
         raise KeyError(op)
 
 
-def replay_and_check(engine, plan, orc, program_words, x, y, step=1, skip=()):
+def replay_and_check(engine, plan, orc, program_words, x, y, step=1, skip=(), variants=None,
+                     progress=None):
     """Stages (x, y), sets step_, replays the train program instruction by
     instruction and checks the first instance of every (opcode, shape)
-    group. Returns the checked group keys."""
+    group against the oracle on 64 sampled rows. `variants(j)`, when given,
+    names how the fused graph runs instruction j (the engine's gemm_choice:
+    tile, split, epilogue chain, dual pass, rowdot/colsum group member);
+    then the first instance of every (group, variant) pair is checked too,
+    on 16 rows when its group was already checked. Returns {checked key:
+    max|oracle output| for GEMMs, None otherwise}."""
     from seeml_amd import PROGRAM_TRAIN
     ck = Checker(engine, plan.header, orc)
     ck.step = step
     engine.stage(x, y)
     engine.set_step(step)
-    seen, done = set(), 0
+    seen, groups, done = {}, set(), 0
     for j, ins in enumerate(program_words):
         key = group_key(ins)
         name = key[0]
-        if name not in CHECKED or key in seen or name in skip:
+        if name not in CHECKED or name in skip:
             continue
-        seen.add(key)
+        if variants is not None:
+            key = key + (variants(j),)
+        if key in seen:
+            continue
+        ck.rows = 16 if key[:4] in groups else 64
+        groups.add(key[:4])
         engine.run_range(PROGRAM_TRAIN, done, j)
         d = ck.before(ins)
         engine.run_range(PROGRAM_TRAIN, j, j + 1)
+        ck.peak = None
         ck.check(ins, d)
+        seen[key] = ck.peak if name in GEMMS else None
+        if progress is not None:
+            progress(j, key)
         done = j + 1
     engine.run_range(PROGRAM_TRAIN, done, len(program_words))
     return seen

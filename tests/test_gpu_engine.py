@@ -193,6 +193,47 @@ def test_fused_attention_decoder_100_steps_tolerance(torch_gpu, orc):
     e.close()
 
 
+def test_c5_structure_100_steps_per_tensor(torch_gpu, orc):
+    """C5's structure (LayerNorm, GELU MLP with AddBias, LoRA rank 64 on
+    every MatMul including the head) over 100 steps: the loss and the whole
+    persistent state within the long-run bar (TOL_100), and every LoRA A/B
+    tensor on its own, printed beside the oracle's drift floor — how far
+    the oracle moves from itself when every frozen weight is nudged by one
+    ulp (an equally valid fp32 evaluation of the same update). AdamW's
+    m/sqrt(v) turns near-zero gradient entries into full-size steps of
+    either sign, so a tensor's spread under rounding is set by that floor,
+    not by the kernels. After 100 steps each tensor on its own must lie
+    within TOL_100 (measured: at most 2.6e-4, against floors up to 2.8e-4);
+    at step 3 the B tensors spread up to ~4e-3, as the floor does (3.3e-3),
+    which is why the short per-step checks compare gradients from one shared
+    state instead."""
+    w, p = compile_workload("c5s64")
+    e = engine(p)
+    r = HostPlanRunner(p, orc)
+    nudged = HostPlanRunner(p, orc)
+    nudged.rodata[:] = np.nextafter(nudged.rodata, np.float32(np.inf))
+    n = p.header["persistent_size"] // 4
+    rows = {}
+    for s in range(100):
+        x, y = configs.batch(w, s)
+        lg, lr = e.train_step(x, y), r.train_step(x, y)
+        nudged.train_step(x, y)
+        if s + 1 in (3, 100):
+            for pid, ref, _, cnt in p.params:
+                rows.setdefault(pid, []).append((rel_err(e.read(ref, cnt), r.read(ref, cnt)),
+                                                 rel_err(nudged.read(ref, cnt), r.read(ref, cnt))))
+    print("\nc5s64 per-tensor rel err (gpu vs oracle | oracle drift floor), steps 3 and 100")
+    for pid, v in rows.items():
+        print(f"  {pid:16s} step3 {v[0][0]:.2e} | {v[0][1]:.2e}   step100 {v[1][0]:.2e} | {v[1][1]:.2e}")
+    state_err = rel_err(persistent(e, p), persistent(r, p))
+    print(f"  loss gpu {lg:.7f} oracle {lr:.7f}; whole state {state_err:.2e}")
+    assert abs(lg - lr) <= TOL_100 * abs(lr), (lg, lr)
+    assert state_err <= TOL_100
+    for pid, v in rows.items():
+        assert v[1][0] <= TOL_100, (pid, v[1])
+    e.close()
+
+
 @pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr", "c5s64"])
 def test_bitwise_determinism_and_graph_equals_eager(torch_gpu, name):
     w, p = compile_workload(name)

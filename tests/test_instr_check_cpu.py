@@ -57,7 +57,7 @@ class OracleEngine:
         return self.r.loss()
 
 
-@pytest.mark.parametrize("name", ["c1", "c3m", "c4m", "c5s", "f1", "q1", "k2"])
+@pytest.mark.parametrize("name", ["c1", "c2sdx", "c3m", "c4m", "c5s", "f1", "q1", "k2"])
 def test_checker_accepts_the_oracle(orc, name):
     w, p = compile_workload(name)
     e = OracleEngine(p, orc)
@@ -66,7 +66,7 @@ def test_checker_accepts_the_oracle(orc, name):
     assert {k[0] for k in seen} == {OPN[i["opcode"]] for i in p.train} & CHECKED
 
 
-@pytest.mark.parametrize("op", ["GemmNN", "AddEW", "RmsNormFwd"])
+@pytest.mark.parametrize("op", ["GemmNN", "GemmTN", "AddEW", "RmsNormFwd"])
 def test_checker_rejects_a_wrong_output(orc, op):
     w, p = compile_workload("c4m")
     e = OracleEngine(p, orc, corrupt=op)
