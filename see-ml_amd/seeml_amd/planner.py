@@ -921,6 +921,10 @@ class UpdateConfig:
     distill_weight: float = 0.5
     quantize_base: bool = False
     fuse_epilogues: bool = True
+    # source/plan/config.h:74-76: when false the train program is forward
+    # + backward only (no parameter mutation), the build the reference's
+    # finite-difference gradient checks use (update_compiler.cc:253).
+    emit_optimizer: bool = True
 
 
 @dataclass
@@ -1038,7 +1042,8 @@ def compile_update(model: Model, cfg: UpdateConfig, hash_fn=None, materialize: b
     if cfg.input_grad and cfg.token_input:
         raise ValueError("input_grad needs a float input")
     grads = autodiff(block, loss, trainables, (inp,) if cfg.input_grad else ())
-    synthesize_optimizer(block, trainables, grads, cfg.optimizer, cfg.clip_norm)
+    if cfg.emit_optimizer:
+        synthesize_optimizer(block, trainables, grads, cfg.optimizer, cfg.clip_norm)
     merge_block, aliases, merge_outputs = build_merge(adapters)
 
     # --- frozen-weight quantization (update_compiler.cc:272-285): the

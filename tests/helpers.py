@@ -140,6 +140,10 @@ class HostPlanRunner:
         self.run(0)
         return self.loss()
 
+    def write(self, ref, data):
+        b = np.ascontiguousarray(data).view(np.uint8)
+        self.arena.view(np.uint8)[ref:ref + b.size] = b
+
     def read(self, ref, count, dtype=np.float32):
         a8 = self.arena.view(np.uint8)
         nb = count * np.dtype(dtype).itemsize
