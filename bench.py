@@ -135,8 +135,9 @@ def main():
     # the largest share of the step.
     ms = e.profile(PROGRAM_TRAIN, reps=args.profile_reps)
     variants = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(plan.train))]
+    launches = [e.launch_work(PROGRAM_TRAIN, i) for i in range(len(plan.train))]
     summ = workmodel.summarize(plan.train, list(ms), PEAK_FP32_MFMA_TFLOPS, PEAK_HBM_GBPS,
-                               variants=variants)
+                               variants=variants, launches=launches)
     rows = summ["rows"]
     groups = {}
     for i, r in enumerate(rows):
@@ -224,14 +225,21 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        # this process's cores, capped at a GPU box's CPU share per GPU (16)
-        cores = min(16, len(os.sched_getaffinity(0)))
-        log(f"cpu baseline on {cores} cores ...")
+        # This process's cores, capped at a GPU box's CPU share per GPU (16
+        # threads per GPU, whatever the host reports); the host's own count
+        # and this process's affinity are recorded beside it.
+        affinity = len(os.sched_getaffinity(0))
+        cores = min(16, affinity)
+        log(f"cpu baseline on {cores} cores (host reports {os.cpu_count()}, affinity {affinity}) ...")
         try:
             cpu = cpu_baseline(w, plan, cores)
         except Exception as ex:  # reported, never fatal for the GPU figure
             cpu = dict(value=None, unit="tokens/s", cores=cores, kind="reference",
                        sample=f"unavailable: {ex}")
+        cpu["host_cpus"] = os.cpu_count()
+        cpu["affinity_cpus"] = affinity
+        cpu["cores_note"] = ("threads capped at the GPU box's CPU share of 16 per GPU; "
+                             "host_cpus is os.cpu_count() on the box")
     out = {
         "metric": "train tokens/sec per update step on 1 MI355X; GEMM MFMA util %; HBM GB/s",
         "value": round(tokens_per_s, 2),

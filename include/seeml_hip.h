@@ -153,6 +153,17 @@ typedef double (*seeml_hip_arm_reward_fn)(void* ctx, uint64_t arm);
 int seeml_hip_ucb1_run(uint64_t arms, double exploration, uint64_t trials,
                        seeml_hip_arm_reward_fn reward, void* ctx, uint64_t* picks,
                        uint64_t* pulls, double* means, uint64_t* best_arm);
+/* Profiling support, no reference counterpart: the algorithmic work of
+ * what instruction `index`'s row carries in seeml_hip_profile_program's
+ * breakdown where the fused graph launches it differently from the lone
+ * instruction — a colsum group's one pass over its shared operand (the
+ * large operand counted once; an earlier member's operand copy as bytes
+ * only), a dual pass, a LoRA run's base GEMM with its epilogue and the
+ * rowdots it launches, a dense GEMM with its fused AddEW. *flops and
+ * *bytes are -1 where the instruction's own work applies. Fusions are
+ * planned when the program's graph is built. */
+int seeml_hip_launch_work(seeml_hip_engine* e, int program, uint64_t index, double* flops,
+                          double* bytes);
 /* Describe the kernel variant chosen for instruction `index` of `program`:
  * GEMMs "cfg-name splits=S" (or "skinny/<kind>"; a column split reads
  * "cfg|tail-cfg@n_split splits=1"), with " +AddEW" when the
@@ -238,6 +249,7 @@ typedef struct seeml_hip_train_report { /* TrainReport, update_engine.h:91-117 *
   float val_initial_accuracy;
   float val_final_accuracy;
   int32_t improved; /* TrainReport::improved(): the regression gate */
+  int32_t stopped_early; /* should_stop interrupted the run (update_engine.h:93) */
 } seeml_hip_train_report;
 /* EvaluateMetrics (update_engine.cc:557-650): snapshot + rewind the set, the
  * eval program per compiled batch (the last batch wraps), loss mean in
@@ -258,11 +270,18 @@ int seeml_hip_train(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,
  * missing or unusable one is reported on stderr and training starts from
  * the current state) and the feeder skips the step_ * batch rows already
  * served, so a resumed run is the uninterrupted one bit for bit
- * (update_engine.cc:676-696, 766-770). */
+ * (update_engine.cc:676-696, 766-770). should_stop (may be NULL) is
+ * TrainOptions::should_stop, polled once before each step on the calling
+ * thread; a nonzero return ends the run there with report.stopped_early
+ * set and report.steps the steps executed (update_engine.cc:737-740). With
+ * checkpointing, a stopped run resumes where it stopped. */
+typedef int (*seeml_hip_should_stop_fn)(void* ctx);
 typedef struct seeml_hip_train_options {
   const char* checkpoint_path; /* NULL or "": no checkpointing */
   uint64_t checkpoint_every;   /* steps between checkpoints; 0 = off */
   int32_t resume;
+  seeml_hip_should_stop_fn should_stop; /* NULL: never stop early */
+  void* should_stop_ctx;
 } seeml_hip_train_options;
 /* seeml_hip_train with TrainOptions (options may be NULL). */
 int seeml_hip_train_ex(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps,

@@ -31,6 +31,7 @@
 
 #include "../../include/seeml_hip.h"
 #include "device_common.h"
+#include "device_mem.h"
 #include "kernels.h"
 #include "checkpoint.h"
 #include "stager.h"
@@ -135,7 +136,7 @@ class Engine {
     const PlanHeader& h = plan_.header;
     arena_bytes_ = Round64(h.arena_size);
     if (arena_bytes_ == 0) arena_bytes_ = kAlign;
-    if (Status s = HipOk(hipMalloc(&arena_, arena_bytes_), "arena allocation failed"); !s)
+    if (Status s = HipOk(LockedMalloc(&arena_, arena_bytes_), "arena allocation failed"); !s)
       return s;
     if (Status s = HipOk(hipMemsetAsync(arena_, 0, arena_bytes_, stream_), "arena clear"); !s)
       return s;
@@ -146,7 +147,7 @@ class Engine {
           !s)
         return s;
     rodata_bytes_ = Round64(std::max<uint64_t>(h.rodata_size, 1));
-    if (Status s = HipOk(hipMalloc(&rodata_, rodata_bytes_), "rodata allocation failed"); !s)
+    if (Status s = HipOk(LockedMalloc(&rodata_, rodata_bytes_), "rodata allocation failed"); !s)
       return s;
     if (h.rodata_size)
       if (Status s = HipOk(hipMemcpyAsync(rodata_, plan + h.rodata_offset, h.rodata_size,
@@ -154,13 +155,13 @@ class Engine {
                            "rodata upload");
           !s)
         return s;
-    if (Status s = HipOk(hipMalloc(&d_scalars_, sizeof(StepScalars)), "scalars"); !s) return s;
-    if (Status s = HipOk(hipHostMalloc(&h_scalars_, 2 * sizeof(StepScalars)), "pinned scalars"); !s)
+    if (Status s = HipOk(LockedMalloc(&d_scalars_, sizeof(StepScalars)), "scalars"); !s) return s;
+    if (Status s = HipOk(LockedHostMalloc(&h_scalars_, 2 * sizeof(StepScalars)), "pinned scalars"); !s)
       return s;
     for (hipEvent_t& ev : scalar_ev_)
       if (Status s = HipOk(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "scalar event"); !s)
         return s;
-    if (Status s = HipOk(hipHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
+    if (Status s = HipOk(LockedHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
     if (Status s = MakeWeightCopies(); !s) return s;
     if (Status s = MakeRopeTables(); !s) return s;
     for (int p = 0; p < 3; ++p) PlanCausalRows(p);
@@ -251,7 +252,7 @@ class Engine {
         wcopies_.push_back(w);
       }
     if (wcopies_.empty()) return Status::Ok();
-    if (Status s = HipOk(hipMalloc(&wcopy_buf_, total), "weight copies allocation failed"); !s)
+    if (Status s = HipOk(LockedMalloc(&wcopy_buf_, total), "weight copies allocation failed"); !s)
       return s;
     const Ctx c = MakeCtx();
     for (WeightCopy& w : wcopies_) {
@@ -291,7 +292,7 @@ class Engine {
         ropetabs_.push_back(r);
       }
     if (ropetabs_.empty()) return Status::Ok();
-    if (Status s = HipOk(hipMalloc(&ropetab_buf_, total), "RoPE tables allocation failed"); !s)
+    if (Status s = HipOk(LockedMalloc(&ropetab_buf_, total), "RoPE tables allocation failed"); !s)
       return s;
     const Ctx c = MakeCtx();
     for (RopeTab& r : ropetabs_) {
@@ -635,16 +636,17 @@ class Engine {
     // Growing the workspace moves it: every captured graph holds the old
     // address, so all of them are rebuilt on next use.
     if (Status s = HipOk(hipStreamSynchronize(stream_), "workspace sync"); !s) return s;
-    if (ws_) (void)hipFree(ws_);
+    if (ws_) (void)LockedFree(ws_);
     ws_ = nullptr;
     ws_bytes_ = 0;
-    if (Status s = HipOk(hipMalloc(&ws_, Round64(need)), "workspace allocation"); !s) return s;
+    if (Status s = HipOk(LockedMalloc(&ws_, Round64(need)), "workspace allocation"); !s) return s;
     ws_bytes_ = Round64(need);
     for (int p = 0; p < 3; ++p) DropGraph(p);
     return Status::Ok();
   }
 
   void DropGraph(int p) {
+    std::lock_guard<std::recursive_mutex> lock(DeviceMemMutex());
     for (Segment& g : segs_[p]) {
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
       if (g.graph) (void)hipGraphDestroy(g.graph);
@@ -695,7 +697,7 @@ class Engine {
     if (fused_segs_[program]) {
       // A replay of the previous graph may still read the old table.
       if (Status s = HipOk(hipStreamSynchronize(stream_), "fusion table sync"); !s) return s;
-      (void)hipFree(fused_segs_[program]);
+      (void)LockedFree(fused_segs_[program]);
     }
     fused_segs_[program] = nullptr;
     const auto& prog = plan_.program[program];
@@ -752,9 +754,13 @@ class Engine {
     if (Status s = PlanColsumGroups(program); !s) return s;
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
-    if (Status s = HipOk(hipMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
-    return HipOk(hipMemcpy(fused_segs_[program], segs.data(), bytes, hipMemcpyHostToDevice),
-                 "fused AdamW table upload");
+    if (Status s = HipOk(LockedMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
+    if (Status s = HipOk(hipMemcpyAsync(fused_segs_[program], segs.data(), bytes,
+                                        hipMemcpyHostToDevice, stream_),
+                         "fused AdamW table upload");
+        !s)
+      return s;
+    return HipOk(hipStreamSynchronize(stream_), "fused AdamW table upload");  // segs is local
   }
 
   // Dual skinny pairs (kernels.h LaunchSkinnyDual): adjacent rowdot and
@@ -1479,7 +1485,7 @@ class Engine {
     if (cs_priv_[program]) {
       // A replay of the previous graph may still read the old copies.
       if (Status s = HipOk(hipStreamSynchronize(stream_), "colsum group sync"); !s) return s;
-      (void)hipFree(cs_priv_[program]);
+      (void)LockedFree(cs_priv_[program]);
       cs_priv_[program] = nullptr;
     }
     const auto& chains = chains_[program];
@@ -1552,7 +1558,7 @@ class Engine {
       cs_groups_[program].push_back(std::move(g));
     }
     if (total == 0) return Status::Ok();
-    return HipOk(hipMalloc(&cs_priv_[program], total * sizeof(float)), "colsum group copies");
+    return HipOk(LockedMalloc(&cs_priv_[program], total * sizeof(float)), "colsum group copies");
   }
 
   // The colsum group instruction idx belongs to when the executed range
@@ -1697,6 +1703,7 @@ class Engine {
 
   // Captures instructions [begin, end) as one graph segment.
   Status Capture(int program, size_t begin, size_t end) {
+    std::lock_guard<std::recursive_mutex> lock(DeviceMemMutex());
     if (Status s = HipOk(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal),
                          "graph capture begin");
         !s)
@@ -1867,11 +1874,12 @@ class Engine {
     std::vector<float> buf;
     for (const EmitEntry& e : plan_.emit) {
       buf.resize(e.byte_size / 4);
-      if (Status s = HipOk(hipMemcpy(buf.data(), arena_ + e.arena_offset, e.byte_size,
-                                     hipMemcpyDeviceToHost),
+      if (Status s = HipOk(hipMemcpyAsync(buf.data(), arena_ + e.arena_offset, e.byte_size,
+                                          hipMemcpyDeviceToHost, stream_),
                            "delta read");
           !s)
         return s;
+      if (Status s = HipOk(hipStreamSynchronize(stream_), "delta read"); !s) return s;
       for (float v : buf)
         if (!std::isfinite(v))
           return Status::Fail(kUnitEngine,
@@ -1894,6 +1902,7 @@ class Engine {
     float val_initial_loss = 0.0f, val_final_loss = 0.0f;
     bool has_val_accuracy = false;
     float val_initial_accuracy = 0.0f, val_final_accuracy = 0.0f;
+    bool stopped_early = false;
     bool improved() const {
       return has_validation ? val_final_loss < val_initial_loss
                             : final_avg_loss < initial_avg_loss;
@@ -1910,16 +1919,16 @@ class Engine {
       mark_ev_[p].clear();
       marked_[p].clear();
     }
-    if (d_argmax_) (void)hipFree(d_argmax_);
+    if (d_argmax_) (void)LockedFree(d_argmax_);
     d_argmax_ = nullptr;
     argmax_cap_ = 0;
     // [total u64][partials u32 ...]
-    if (Status s = HipOk(hipMalloc(&d_argmax_, 8 + 4 * std::max<size_t>(need, 1)), "argmax buffers");
+    if (Status s = HipOk(LockedMalloc(&d_argmax_, 8 + 4 * std::max<size_t>(need, 1)), "argmax buffers");
         !s)
       return s;
     argmax_cap_ = need;
     if (!h_count_)
-      if (Status s = HipOk(hipHostMalloc(&h_count_, sizeof(uint64_t)), "pinned count"); !s) return s;
+      if (Status s = HipOk(LockedHostMalloc(&h_count_, sizeof(uint64_t)), "pinned count"); !s) return s;
     return Status::Ok();
   }
 
@@ -2009,6 +2018,8 @@ class Engine {
     std::string checkpoint_path;
     uint64_t checkpoint_every = 0;
     bool resume = false;
+    int (*should_stop)(void*) = nullptr;  // polled once per step
+    void* should_stop_ctx = nullptr;
   };
 
   Status Train(Dataset& data, uint64_t steps, Dataset* validation, float* curve,
@@ -2058,6 +2069,10 @@ class Engine {
       BatchStager feeder(data, h.batch, h.input_floats * 4, has_labels ? h.label_bytes : 0);
       st = feeder.Start();
       for (uint64_t s = start; st && s < start + steps; ++s) {
+        if (opt.should_stop && opt.should_stop(opt.should_stop_ctx)) {
+          report.stopped_early = true;  // update_engine.cc:737-740
+          break;
+        }
         st = SetStep(s + 1);  // 1-indexed step for AdamW bias correction
         if (st)
           st = feeder.Next(SlotPtr(h.input_ref), has_labels ? SlotPtr(h.label_ref) : nullptr,
@@ -2110,9 +2125,12 @@ class Engine {
     if (!RangeOk(off, bytes, space)) return Status::Fail(kUnitEngine, "probe out of bounds");
     uint8_t* dev = (ro ? rodata_ : arena_) + off;
     if (Status s = HipOk(hipStreamSynchronize(stream_), "probe sync"); !s) return s;
-    return HipOk(write ? hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice)
-                       : hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost),
-                 "probe copy");
+    if (Status s = HipOk(write ? hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_)
+                              : hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, stream_),
+                         "probe copy");
+        !s)
+      return s;
+    return HipOk(hipStreamSynchronize(stream_), "probe copy");
   }
 
   // Test hook: one GEMM instruction's plan, forced; the graph is rebuilt (and
@@ -2200,10 +2218,10 @@ class Engine {
       for (const auto& a : arms) need = std::max(need, a.ws_bytes);
       if (need > ws_bytes_) {
         if (Status s = HipOk(hipStreamSynchronize(stream_), "tune sync"); !s) { result = s; break; }
-        if (ws_) (void)hipFree(ws_);
+        if (ws_) (void)LockedFree(ws_);
         ws_ = nullptr;
         ws_bytes_ = 0;
-        if (Status s = HipOk(hipMalloc(&ws_, Round64(need)), "workspace"); !s) { result = s; break; }
+        if (Status s = HipOk(LockedMalloc(&ws_, Round64(need)), "workspace"); !s) { result = s; break; }
         ws_bytes_ = Round64(need);
         for (int p = 0; p < 3; ++p) DropGraph(p);
       }
@@ -2372,6 +2390,100 @@ class Engine {
     return Status::Ok();
   }
 
+  static double GemmFlops(const GemmDesc& d) {
+    return 2.0 * static_cast<double>(d.batch) * d.M * d.N * d.K;
+  }
+  // A, B and C once each, at 4 B per f32 and 1 B per int8 weight.
+  static double GemmOperandBytes(const GemmDesc& d) {
+    return static_cast<double>(d.batch) *
+           (4.0 * d.M * d.K + (d.b_int8 ? 1.0 : 4.0) * d.K * d.N + 4.0 * d.M * d.N);
+  }
+
+  // Algorithmic work (FLOPs, compulsory HBM bytes) of what instruction idx's
+  // row carries in Profile()'s breakdown, where the fused graph's launch
+  // differs from the instruction alone; false where the instruction's own
+  // work applies. Bytes count each operand of the launch once:
+  //  - colsum group, last member (the group's one launch): the shared large
+  //    operand once, every member's small operand and output; the members'
+  //    FLOPs. An earlier member copies its small operand: read + write of
+  //    that copy, no FLOPs.
+  //  - dual pass (its first instruction): both GEMMs' FLOPs, their operands
+  //    with the shared stream read once.
+  //  - LoRA run (its base GEMM): the base GEMM, the up-projection in its
+  //    epilogue (t and B read, y/u/s in registers, one store of the sum) and
+  //    the down-projection rowdots this run launches (its own, or its rowdot
+  //    group's; the layer input they share is read once).
+  //  - dense chain (the GEMM): A, B, the AddEW's addend and the stores made.
+  bool LaunchWork(int program, size_t idx, double* flops, double* bytes) const {
+    const auto& prog = plan_.program[program];
+    if (idx >= prog.size()) return false;
+    if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
+      const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
+      if (idx != g.members.back()) {
+        for (size_t j = 0; j + 1 < g.members.size(); ++j)
+          if (g.members[j] == idx) {
+            *flops = 0.0;
+            *bytes = 8.0 * static_cast<double>(g.priv_floats[j]);
+            return true;
+          }
+        return false;
+      }
+      const GemmDesc d0 = DescOf(prog[g.members[0]]);
+      const bool big_a = ColsumBigIsA(d0);
+      double f = 0.0, b = big_a ? 4.0 * d0.K * d0.M : 4.0 * d0.K * d0.N;
+      for (size_t m : g.members) {
+        const GemmDesc d = DescOf(prog[m]);
+        f += GemmFlops(d);
+        b += (big_a ? 4.0 * d.K * d.N : 4.0 * d.K * d.M) + 4.0 * d.M * d.N;
+      }
+      *flops = f;
+      *bytes = b;
+      return true;
+    }
+    const ChainRun* run = ChainAt(program, idx);
+    if (!run) return false;
+    const bool dual_here =
+        duals_[program][idx] == static_cast<int64_t>(idx + 1) &&
+        ((run->kind == ChainKind::kDual && idx == run->first) ||
+         (run->kind == ChainKind::kScaleFold && idx > run->first && idx + 1 < run->first + run->count));
+    if (dual_here) {
+      const GemmDesc a = DescOf(prog[idx]), b = DescOf(prog[idx + 1]);
+      const GemmDesc& cs = SkinnyKindOf(a) == SkinnyKind::kRowDot ? b : a;
+      int64_t elems = 0;
+      (void)SkinnyStream(cs, &elems);
+      *flops = GemmFlops(a) + GemmFlops(b);
+      *bytes = GemmOperandBytes(a) + GemmOperandBytes(b) - 4.0 * static_cast<double>(elems);
+      return true;
+    }
+    if (idx != run->first) return false;
+    if (run->kind == ChainKind::kLoraBase) {
+      const GemmDesc g0 = DescOf(prog[idx]), up = DescOf(prog[idx + 2]);
+      double f = GemmFlops(g0) + GemmFlops(up);
+      double b = 4.0 * g0.M * g0.K + (g0.b_int8 ? 1.0 : 4.0) * g0.K * g0.N + 4.0 * g0.M * g0.N +
+                 4.0 * up.M * up.K + 4.0 * up.K * up.N;
+      std::vector<size_t> rowdots;
+      if (run->rd_mode == 1) rowdots = run->grp_rowdots;
+      else if (run->rd_mode == 0) rowdots.push_back(idx + 1);
+      for (size_t k : rowdots) {
+        const GemmDesc r = DescOf(prog[k]);
+        f += GemmFlops(r);
+        b += 4.0 * r.K * r.N + 4.0 * r.M * r.N + (r.A == g0.A ? 0.0 : 4.0 * r.M * r.K);
+      }
+      *flops = f;
+      *bytes = b;
+      return true;
+    }
+    if (run->kind == ChainKind::kDense) {
+      const GemmDesc& d = run->d;
+      const double mn = 4.0 * static_cast<double>(d.batch) * d.M * d.N;
+      *flops = GemmFlops(d);
+      *bytes = GemmOperandBytes(d) - (d.write_c ? 0.0 : mn) + (d.addend ? mn : 0.0) +
+               (d.out ? mn : 0.0);
+      return true;
+    }
+    return false;
+  }
+
   std::string GemmChoice(int program, size_t idx) const {
     const auto op = static_cast<Op>(plan_.program[program][idx].opcode);
     const uint8_t tf = tails_[program][idx];
@@ -2438,36 +2550,36 @@ class Engine {
   void Release() {
     for (int p = 0; p < 3; ++p) DropGraph(p);
     if (stream_) (void)hipStreamSynchronize(stream_);
-    if (arena_) (void)hipFree(arena_);
-    if (rodata_) (void)hipFree(rodata_);
-    if (wcopy_buf_) (void)hipFree(wcopy_buf_);
+    if (arena_) (void)LockedFree(arena_);
+    if (rodata_) (void)LockedFree(rodata_);
+    if (wcopy_buf_) (void)LockedFree(wcopy_buf_);
     wcopy_buf_ = nullptr;
     wcopies_.clear();
-    if (ropetab_buf_) (void)hipFree(ropetab_buf_);
+    if (ropetab_buf_) (void)LockedFree(ropetab_buf_);
     ropetab_buf_ = nullptr;
     ropetabs_.clear();
-    if (ws_) (void)hipFree(ws_);
-    if (d_scalars_) (void)hipFree(d_scalars_);
+    if (ws_) (void)LockedFree(ws_);
+    if (d_scalars_) (void)LockedFree(d_scalars_);
     for (int p = 0; p < 3; ++p) {
-      if (fused_segs_[p]) (void)hipFree(fused_segs_[p]);
+      if (fused_segs_[p]) (void)LockedFree(fused_segs_[p]);
       fused_segs_[p] = nullptr;
       fused_runs_[p].clear();
-      if (cs_priv_[p]) (void)hipFree(cs_priv_[p]);
+      if (cs_priv_[p]) (void)LockedFree(cs_priv_[p]);
       cs_priv_[p] = nullptr;
       cs_groups_[p].clear();
       cs_group_of_[p].clear();
     }
-    if (d_argmax_) (void)hipFree(d_argmax_);
+    if (d_argmax_) (void)LockedFree(d_argmax_);
     d_argmax_ = nullptr;
     argmax_cap_ = 0;
-    if (h_count_) (void)hipHostFree(h_count_);
+    if (h_count_) (void)LockedHostFree(h_count_);
     h_count_ = nullptr;
-    if (h_scalars_) (void)hipHostFree(h_scalars_);
+    if (h_scalars_) (void)LockedHostFree(h_scalars_);
     for (hipEvent_t& ev : scalar_ev_) {
       if (ev) (void)hipEventDestroy(ev);
       ev = nullptr;
     }
-    if (h_loss_) (void)hipHostFree(h_loss_);
+    if (h_loss_) (void)LockedHostFree(h_loss_);
     if (stream_) (void)hipStreamDestroy(stream_);
     arena_ = rodata_ = nullptr;
     ws_ = nullptr;
@@ -2550,6 +2662,11 @@ int Report(const Status& s) {
 // seeml_hip_kernel_error() on this thread.
 int ReportStandalone(const Status& s) { return Report(s); }
 
+std::recursive_mutex& DeviceMemMutex() {
+  static std::recursive_mutex m;
+  return m;
+}
+
 namespace {
 
 Status StandaloneCtx(void* stream, size_t ws_need, Ctx* out) {
@@ -2560,17 +2677,18 @@ Status StandaloneCtx(void* stream, size_t ws_need, Ctx* out) {
   auto& w = st.ws[dev];
   if (ws_need > w.second) {
     if (w.first) {
+      std::lock_guard<std::recursive_mutex> dev_lock(DeviceMemMutex());
       (void)hipDeviceSynchronize();
-      (void)hipFree(w.first);
+      (void)LockedFree(w.first);
     }
     w = {nullptr, 0};
-    if (Status s = HipOk(hipMalloc(&w.first, Round64(ws_need)), "standalone workspace"); !s)
+    if (Status s = HipOk(LockedMalloc(&w.first, Round64(ws_need)), "standalone workspace"); !s)
       return s;
     w.second = Round64(ws_need);
   }
   auto& sc = st.scalars[dev];
   if (!sc)
-    if (Status s = HipOk(hipMalloc(&sc, sizeof(StepScalars)), "standalone scalars"); !s) return s;
+    if (Status s = HipOk(LockedMalloc(&sc, sizeof(StepScalars)), "standalone scalars"); !s) return s;
   out->stream = static_cast<hipStream_t>(stream);
   out->ws = w.first;
   out->ws_bytes = w.second;
@@ -2733,6 +2851,14 @@ int seeml_hip_set_gemm_plan(seeml_hip_engine* e, int program, uint64_t index, in
   return Ret(e, e->impl.SetGemmPlan(program, index, cfg, splits));
 }
 
+int seeml_hip_launch_work(seeml_hip_engine* e, int program, uint64_t index, double* flops,
+                          double* bytes) {
+  if (program < 0 || program > 2 || index >= e->impl.plans_[program].size() || !flops || !bytes)
+    return Ret(e, Status::Fail(seeml_hip::kUnitEngine, "instruction index out of range"));
+  if (!e->impl.LaunchWork(program, index, flops, bytes)) *flops = *bytes = -1.0;
+  return SEEML_HIP_OK;
+}
+
 int seeml_hip_gemm_choice(seeml_hip_engine* e, int program, uint64_t index, char* buf,
                           uint64_t cap) {
   if (program < 0 || program > 2 || index >= e->impl.plans_[program].size())
@@ -2766,6 +2892,8 @@ int seeml_hip_train_ex(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps
     opt.checkpoint_path = options->checkpoint_path ? options->checkpoint_path : "";
     opt.checkpoint_every = options->checkpoint_every;
     opt.resume = options->resume != 0;
+    opt.should_stop = options->should_stop;
+    opt.should_stop_ctx = options->should_stop_ctx;
   }
   if (const Status s = e->impl.Train(d->impl, steps, validation ? &validation->impl : nullptr,
                                      loss_curve, curve_cap, &r, opt);
@@ -2781,6 +2909,7 @@ int seeml_hip_train_ex(seeml_hip_engine* e, seeml_hip_dataset* d, uint64_t steps
   out->val_initial_accuracy = r.val_initial_accuracy;
   out->val_final_accuracy = r.val_final_accuracy;
   out->improved = r.improved() ? 1 : 0;
+  out->stopped_early = r.stopped_early ? 1 : 0;
   return SEEML_HIP_OK;
 }
 

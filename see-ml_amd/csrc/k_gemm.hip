@@ -6,6 +6,7 @@
 // Serves runtime/executor/gemm.cc:173-228 (GemmNN + fused bias/act
 // epilogue, GemmNT, GemmTN, GemmAccNN, GemmNNQ8/NTQ8) and the attention
 // contractions of attention.cc.
+#include <atomic>
 #include "k_gemm_kernel.h"
 
 namespace seeml_hip {
@@ -117,16 +118,21 @@ GemmPlan PlanGemmWith(const GemmDesc& d, int forced_cfg, int forced_splits) {
 }
 
 namespace {
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; engines on
+// several host threads may ask at once, and all store the same value).
 int DeviceCUs() {
-  static int cus[16] = {};
+  static std::atomic<int> cus[16] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
-  if (cus[dev] == 0) {
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cus[dev] = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) {
+      cus[dev].store(v, std::memory_order_relaxed);
+      n = v;
+    }
   }
-  return cus[dev];
+  return n;
 }
 }  // namespace
 

@@ -855,11 +855,16 @@ __device__ __forceinline__ void DualTile(const DualArgs& p, float* __restrict__ 
       }
     }
     if constexpr (RD) {
-      // The strip through the wavefront's own buffer (its LDS operations run
-      // in order, so no barrier), read back as rows of the MFMA's A operand.
+      // The strip through the wavefront's own buffer, read back by other
+      // lanes as rows of the MFMA's A operand. A wavefront's LDS operations
+      // execute in issue order, so no workgroup barrier is needed; the wave
+      // barriers keep the compiler from moving the reads above the writes,
+      // or the next strip's writes above these reads (different addresses
+      // per lane, so alias analysis alone would allow either).
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         *reinterpret_cast<float4*>(&buf[(4 * u + q) * kDualTs + 4 * c]) = v[u];
+      __builtin_amdgcn_wave_barrier();
       floatx4 rd = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -869,6 +874,7 @@ __device__ __forceinline__ void DualTile(const DualArgs& p, float* __restrict__ 
         rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bf[g].z, rd, 0, 0, 0);
         rd = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bf[g].w, rd, 0, 0, 0);
       }
+      __builtin_amdgcn_wave_barrier();
       // Lane (q, c) element e: strip row 4q + e, n = c.
 #pragma unroll
       for (int e = 0; e < 4; ++e)

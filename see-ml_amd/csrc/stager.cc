@@ -1,6 +1,8 @@
 // stager.cc — pinned double-buffered batch staging (runtime/feeder/batch_pipeline.cc).
 #include "stager.h"
 
+#include "device_mem.h"
+
 #include <string>
 
 namespace seeml_hip {
@@ -20,7 +22,7 @@ BatchStager::BatchStager(Dataset& data, uint64_t batch, uint64_t in_bytes, uint6
 Status BatchStager::Start() {
   const uint64_t bytes = (in_bytes_ + label_bytes_) ? (in_bytes_ + label_bytes_) : 1;
   for (int k = 0; k < 2; ++k) {
-    if (Status s = Hip(hipHostMalloc(reinterpret_cast<void**>(&buf_[k]), bytes), "pinned staging");
+    if (Status s = Hip(LockedHostMalloc(&buf_[k], bytes), "pinned staging");
         !s)
       return s;
     if (Status s = Hip(hipEventCreateWithFlags(&copied_[k], hipEventDisableTiming), "event"); !s)
@@ -96,7 +98,7 @@ BatchStager::~BatchStager() {
       if (copy_pending_[k]) (void)hipEventSynchronize(copied_[k]);
       (void)hipEventDestroy(copied_[k]);
     }
-    if (buf_[k]) (void)hipHostFree(buf_[k]);
+    if (buf_[k]) (void)LockedHostFree(buf_[k]);
   }
 }
 

@@ -26,9 +26,13 @@ class _EvalMetrics(C.Structure):
     _fields_ = [("loss", C.c_float), ("has_accuracy", C.c_int32), ("accuracy", C.c_float)]
 
 
+_SHOULD_STOP = C.CFUNCTYPE(C.c_int, C.c_void_p)
+
+
 class _TrainOptions(C.Structure):
     _fields_ = [("checkpoint_path", C.c_char_p), ("checkpoint_every", C.c_uint64),
-                ("resume", C.c_int32)]
+                ("resume", C.c_int32), ("should_stop", C.c_void_p),
+                ("should_stop_ctx", C.c_void_p)]
 
 
 class _TrainReport(C.Structure):
@@ -36,7 +40,8 @@ class _TrainReport(C.Structure):
                 ("final_avg_loss", C.c_float), ("has_validation", C.c_int32),
                 ("val_initial_loss", C.c_float), ("val_final_loss", C.c_float),
                 ("has_val_accuracy", C.c_int32), ("val_initial_accuracy", C.c_float),
-                ("val_final_accuracy", C.c_float), ("improved", C.c_int32)]
+                ("val_final_accuracy", C.c_float), ("improved", C.c_int32),
+                ("stopped_early", C.c_int32)]
 
 
 def _buf(a):
@@ -140,21 +145,24 @@ class DeviceUpdateEngine:
         return dict(loss=m.loss, has_accuracy=bool(m.has_accuracy), accuracy=m.accuracy)
 
     def train_dataset(self, dataset, steps: int = 0, validation=None, checkpoint_path=None,
-                      checkpoint_every: int = 0, resume: bool = False) -> dict:
+                      checkpoint_every: int = 0, resume: bool = False,
+                      should_stop=None) -> dict:
         """TrainImpl (update_engine.cc:664-787) with the native feeder and
-        TrainOptions (checkpointing, resume); the report's loss_curve holds
-        every step's loss."""
+        TrainOptions (checkpointing, resume, should_stop polled once per
+        step); the report's loss_curve holds every step's loss."""
         r = _TrainReport()
         cap = steps if steps else 0
         curve = np.zeros(max(cap, 1), np.float32)
+        stop_cb = _SHOULD_STOP(lambda _ctx: 1 if should_stop() else 0) if should_stop else None
         opt = _TrainOptions(checkpoint_path.encode() if checkpoint_path else None,
-                            checkpoint_every, 1 if resume else 0)
+                            checkpoint_every, 1 if resume else 0,
+                            C.cast(stop_cb, C.c_void_p) if stop_cb else None, None)
         self._check(self._L.seeml_hip_train_ex(self._h, dataset._h, steps,
                                                validation._h if validation is not None else None,
                                                curve.ctypes.data, cap, C.byref(opt), C.byref(r)),
                     "train")
         out = {f: getattr(r, f) for f, _ in _TrainReport._fields_}
-        for k in ("has_validation", "has_val_accuracy", "improved"):
+        for k in ("has_validation", "has_val_accuracy", "improved", "stopped_early"):
             out[k] = bool(out[k])
         out["loss_curve"] = curve[:min(cap, r.steps)]
         return out
@@ -176,6 +184,14 @@ class DeviceUpdateEngine:
         self._check(self._L.seeml_hip_gemm_choice(self._h, program, index, buf, len(buf)),
                     "gemm_choice")
         return buf.value.decode()
+
+    def launch_work(self, program: int, index: int):
+        """(flops, bytes) of the fused launch instruction `index`'s profile
+        row carries, or None where the instruction's own work applies."""
+        f, b = C.c_double(), C.c_double()
+        self._check(self._L.seeml_hip_launch_work(self._h, program, index, C.byref(f), C.byref(b)),
+                    "launch_work")
+        return None if f.value < 0 else (f.value, b.value)
 
     def program_length(self, program: int = PROGRAM_TRAIN) -> int:
         return self._L.seeml_hip_program_length(self._h, program)

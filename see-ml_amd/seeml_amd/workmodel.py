@@ -138,10 +138,25 @@ def work(ins: dict, variant: str = "") -> dict:
 
 
 def summarize(program: list, ms: list, peak_tflops: float = 157.3, peak_gbps: float = 8000.0,
-              variants: list = None):
-    """Aggregate per-instruction timings into the BASELINE metric's parts."""
+              variants: list = None, launches: list = None):
+    """Aggregate per-instruction timings into the BASELINE metric's parts.
+
+    `launches[i]`, when given and not None, is the engine's (flops, bytes)
+    for the fused launch row i carries (seeml_hip_launch_work): a colsum
+    group's one pass over its shared operand, an operand copy (bytes, no
+    FLOPs), a dual pass, a LoRA run or a GEMM with its fused AddEW. It
+    replaces the lone instruction's work, so no operand is counted once per
+    member of a launch that reads it once."""
     variants = variants or [""] * len(program)
-    rows = [dict(work(ins, v), ms=t) for ins, t, v in zip(program, ms, variants)]
+    launches = launches or [None] * len(program)
+    rows = []
+    for ins, t, v, lw in zip(program, ms, variants, launches):
+        r = dict(work(ins, v), ms=t)
+        if lw is not None and r["cls"] != "fused":
+            r["flops"], r["bytes"] = int(lw[0]), int(lw[1])
+            if r["flops"] == 0:
+                r["cls"] = "hbm"
+        rows.append(r)
     dense = [r for r in rows if r["cls"] == "mfma"]
     gem_all = [r for r in rows if r["op"] in GEMMS]
     # every HBM-bound kernel, the skinny LoRA GEMMs (a dim = the rank)

@@ -498,6 +498,101 @@ def test_colsum_groups_read_the_layer_input_once_and_are_bitwise(torch_gpu):
         assert np.array_equal(runs[0][1].view(np.uint32), runs[k][1].view(np.uint32)), k
 
 
+def test_launch_work_counts_a_colsum_groups_shared_operand_once(torch_gpu):
+    """seeml_hip_launch_work on c4m's colsum groups: the group's row carries
+    every member's FLOPs and the members' bytes with the shared layer input
+    counted once; each earlier member's row is its operand copy (read +
+    write of dt, no FLOPs). summarize() then counts x once per group."""
+    from seeml_amd import PROGRAM_TRAIN, workmodel
+    w, p = compile_workload("c4m")
+    e = engine(p)
+    x, y = configs.batch(w, 0)
+    e.train_step(x, y)
+    ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+    lw = [e.launch_work(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+    groups = [i for i, c in enumerate(ch) if c.startswith("skinny/colsum group of ")]
+    assert groups
+    for last in groups:
+        n = int(ch[last].split()[3])
+        xref = p.train[last]["inp"][0]
+        copies = [i for i in range(last) if ch[i].startswith("copies its operand")
+                  and p.train[i]["inp"][0] == xref][-(n - 1):]
+        assert len(copies) == n - 1
+        lone = [workmodel.work(p.train[i]) for i in copies + [last]]
+        M, N, K = (int(v) for v in p.train[last]["out"])
+        x_bytes = 4 * K * M
+        f, b = lw[last]
+        assert f == sum(r["flops"] for r in lone)
+        assert b == sum(r["bytes"] for r in lone) - (n - 1) * x_bytes
+        for i in copies:
+            assert lw[i] == (0.0, 8.0 * K * N), (i, lw[i])
+    ms = [1.0] * len(p.train)
+    summ = workmodel.summarize(p.train, ms, variants=ch, launches=lw)
+    for last in groups:
+        assert summ["rows"][last]["bytes"] == int(lw[last][1])
+    e.close()
+
+
+def _colsum_pair_plan(between):
+    """c4m with, appended to its train program: a copy of a frozen weight
+    into a fresh arena tensor x [K, M] (live: nothing else touches it; an
+    activation slot is dead by the program's end, and the fused graph need
+    not store dead values), then two colsum candidates over x with two LoRA
+    A tensors as dt — the shape of c4m's LoRA dA GemmTNs — and the
+    instructions `between(x, out1, scratch, n)` between them."""
+    from helpers import PlanView, append_train_instructions, instr
+    w, p = compile_workload("c4m")
+    da = next(i for i in p.train if planner.OP_NAME[i["opcode"]] == "GemmTN"
+              and int(i["out"][1]) == w.cfg.lora.rank and int(i["out"][0]) >= 128)
+    M, N, K = (int(v) for v in da["out"])
+    a0, a1 = p.adapters[0][1], p.adapters[1][1]
+    assert K * N == p.adapters[0][3][0] * w.cfg.lora.rank  # an A tensor is a dt's size
+    wq = planner.RODATA_BIT | p.weights["l0.wq"]
+    assert K * M == int(np.prod(w.model.tensor("l0.wq").dims))
+    base = planner.align_up(p.header["arena_size"])
+    xb = planner.align_up(4 * K * M)
+    ob = planner.align_up(4 * M * N)
+    x, o1, o2, o3 = base, base + xb, base + xb + ob, base + xb + 2 * ob
+    words = [instr(planner.OP["Copy"], (wq, x), (K * M,)),
+             instr(planner.OP["GemmTN"], (x, a0, o1), (M, N, K))] + between(x, o1, o3, M * N) + \
+            [instr(planner.OP["GemmTN"], (x, a1, o2), (M, N, K))]
+    blob, h = append_train_instructions(p, words, extra_arena=xb + 3 * ob)
+    return w, PlanView(blob, h), len(p.train) + 1, (o1, o2, M * N)
+
+
+@pytest.mark.parametrize("case", ["adjacent", "writes x", "reads the first output"])
+def test_colsum_groups_refuse_a_hazard_between_members(torch_gpu, case):
+    """PlanColsumGroups' refusal rules: two colsums over one x group when
+    nothing between them interferes; an instruction between them that writes
+    x, or that reads the first member's output, stops the group (the group
+    would launch at the last member's position and reorder that access).
+    Either way the fused graph equals the eager engine bit for bit."""
+    from seeml_amd import PROGRAM_TRAIN, DeviceUpdateEngine
+    from helpers import instr
+    between = {
+        "adjacent": lambda x, o1, o3, n: [],
+        "writes x": lambda x, o1, o3, n: [instr(planner.OP["Fill"], (x, planner.f32_bits(0.5)), (1,))],
+        "reads the first output": lambda x, o1, o3, n: [instr(planner.OP["AddEW"], (o1, o1, o3), (n,))],
+    }[case]
+    w, view, first, (o1, o2, n) = _colsum_pair_plan(between)
+    outs = []
+    for use_graph in (True, False):
+        e = DeviceUpdateEngine(view.blob, use_graph=use_graph)
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            e.train_step(x, y)
+        if use_graph:
+            ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(first, view.header["train_instr_count"])]
+            grouped = ch[0].startswith("copies its operand") and \
+                ch[-1].startswith("skinny/colsum group of 2")
+            assert grouped == (case == "adjacent"), ch
+        outs.append([e.read(o1, n), e.read(o2, n), e.read(0, view.header["persistent_size"] // 4)])
+        assert np.any(outs[-1][0] != 0) and np.any(outs[-1][1] != 0)
+        e.close()
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), case
+
+
 def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
     """With the projection GEMMs on the 256x128 tile and the rank-16
     up-projections on a tile plan (both forced here; the C4 autotuner picks

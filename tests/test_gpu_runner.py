@@ -247,3 +247,72 @@ def test_checkpoint_restores_step_and_state(torch_dev, tmp_path):
     assert np.array_equal(o.read(0, n).view(np.uint32), before.view(np.uint32)) and o.step == 0
     o.close()
     e.close()
+
+
+def test_should_stop_interrupts_and_the_loss_curve_records(torch_dev):
+    """update_engine_test.cc:730-745: should_stop polled once per step; the
+    26th poll stops a 400-step run after 25 steps, with stopped_early set,
+    25 recorded losses, and the state of a plain 25-step run."""
+    w = configs.make("c1")
+    plan = planner.compile_update(w.model, w.cfg)
+    n = plan.header["persistent_size"] // 4
+    polled = [0]
+
+    def stop():
+        polled[0] += 1
+        return polled[0] > 25
+
+    e = DeviceUpdateEngine(plan.blob)
+    rep = e.train_dataset(_ten_sample_set(), steps=400, should_stop=stop)
+    assert rep["stopped_early"] and rep["steps"] == 25 and polled[0] == 26
+    assert len(rep["loss_curve"]) == 25 and e.step == 25
+    plain = DeviceUpdateEngine(plan.blob)
+    rep2 = plain.train_dataset(_ten_sample_set(), steps=25)
+    assert not rep2["stopped_early"]
+    assert np.array_equal(rep["loss_curve"].view(np.uint32), rep2["loss_curve"].view(np.uint32))
+    assert np.array_equal(e.read(0, n).view(np.uint32), plain.read(0, n).view(np.uint32))
+    e.close()
+    plain.close()
+
+
+def test_concurrent_engines_on_one_gpu_equal_their_serial_runs(torch_dev):
+    """update_system_test.cc:784-822: two engines training at once from two
+    host threads — each with its own arena, stream, graph and feeder, on
+    the one GPU — each end bit for bit where its serial run ends."""
+    import threading
+
+    def make(name):
+        w = configs.make(name)
+        return w, planner.compile_update(w.model, w.cfg)
+
+    jobs = [make("c3s"), make("c4m")]
+
+    def dataset(w, seed):
+        seq = w.seq
+        records = 3 * (w.cfg.batch // seq) + 1
+        toks = configs.zipf_tokens(np.random.default_rng(seed), w.vocab,
+                                   records * (seq + 1)).astype(np.int32)
+        ds = feeder.Dataset.from_tokens(toks, records, seq)
+        ds.enable_shuffle(seed)
+        return ds
+
+    def run(k, out):
+        w, plan = jobs[k]
+        e = DeviceUpdateEngine(plan.blob)
+        rep = e.train_dataset(dataset(w, 40 + k), steps=12)
+        out[k] = (rep["loss_curve"].copy(), e.read(0, plan.header["persistent_size"] // 4))
+        e.close()
+
+    serial = [None, None]
+    run(0, serial)
+    run(1, serial)
+    threaded = [None, None]
+    ts = [threading.Thread(target=run, args=(k, threaded)) for k in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    for k in range(2):
+        assert threaded[k] is not None, k
+        for a, b in zip(threaded[k], serial[k]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), k

@@ -305,3 +305,27 @@ def test_backend_effective_lr_equals_the_oracle(orc, lr, warmup, horizon, floor)
     raw0 = planner.HEADER.pack(*[h[n] for n, _ in planner.HEADER_FIELDS])
     buf0 = (C.c_uint8 * len(raw0)).from_buffer_copy(raw0)
     assert L.seeml_hip_effective_lr(buf0, 7) == np.float32(lr)
+
+
+def test_summarize_takes_a_fused_launchs_work_over_its_instructions():
+    """workmodel.summarize with the engine's launch work: a colsum group of
+    three over one x [K, M] — two operand copies and the group's launch —
+    counts x once (not once per member) and credits the members' FLOPs to
+    the launch, none to the copies."""
+    from seeml_amd import workmodel
+    M, N, K = 2048, 16, 8192
+    ins = dict(opcode=planner.OP["GemmTN"], flags=0, inp=(0, 0, 0, 0), out=(M, N, K))
+    prog = [ins, ins, ins]
+    lone = workmodel.work(ins)
+    x_bytes, small, out = 4 * K * M, 4 * K * N, 4 * M * N
+    assert lone["bytes"] == x_bytes + small + out and lone["flops"] == 2 * M * N * K
+    group = (3 * lone["flops"], x_bytes + 3 * (small + out))
+    launches = [(0.0, 2.0 * small), (0.0, 2.0 * small), group]
+    s = workmodel.summarize(prog, [0.01, 0.01, 0.05], variants=["", "", ""], launches=launches)
+    total_bytes = sum(r["bytes"] for r in s["rows"])
+    assert total_bytes == 4 * small + x_bytes + 3 * (small + out)
+    assert sum(r["flops"] for r in s["rows"]) == 3 * lone["flops"]
+    assert [r["flops"] for r in s["rows"][:2]] == [0, 0]
+    assert s["hbm_skinny_gemm_gbps"] == pytest.approx(total_bytes / 0.07e-3 / 1e9)
+    naive = workmodel.summarize(prog, [0.01, 0.01, 0.05], variants=["", "", ""])
+    assert naive["hbm_skinny_gemm_gbps"] > 2 * s["hbm_skinny_gemm_gbps"]
