@@ -1,7 +1,7 @@
 """Launches one backend GEMM (a bench workload's dominant kernel) and a
 plain copy of known size, for hardware-counter runs under rocprofv3:
 
-  python3 -m seeml_amd.kernel_probe --layout NN --m 8192 --n 5504 --k 2048 \\
+  python3 tests/perf/kernel_probe.py --layout NN --m 8192 --n 5504 --k 2048 \\
       --cfg 128x64x32/w4x1 --reps 3 --copy-mib 1024
 
 With --dual it launches the LoRA backward's dual skinny pass instead: the
@@ -12,17 +12,21 @@ With --step CFG it runs one eager train step of a BASELINE config (every
 instruction dispatched on its own, batch 0), for per-dispatch counters of
 all of a step's kernels:
 
-  python3 -m seeml_amd.kernel_probe --step c4
+  python3 tests/perf/kernel_probe.py --step c4
 
 Each dispatch's FETCH_SIZE / WRITE_SIZE (KiB) is read from the profiler's
 counter file; the copy's counters against its known 2 x copy-mib MiB of
 traffic calibrate the GEMM's. Inputs are seeded normals in device memory.
+A profiling harness beside the tests: the product never imports it.
 """
 from __future__ import annotations
 
 import argparse
 import ctypes as C
+import os
 import sys
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "..", "see-ml_amd"))
 
 LAYOUTS = {"NN": 0, "NT": 1, "TN": 2}
 
@@ -45,8 +49,7 @@ def main(argv=None):
     ap.add_argument("--copy-mib", type=int, default=1024)
     a = ap.parse_args(argv)
     if a.step:
-        from . import configs, planner
-        from .engine import DeviceUpdateEngine
+        from seeml_amd import DeviceUpdateEngine, configs, planner
         w = configs.make(a.step)
         plan = planner.compile_update(w.model, w.cfg, teacher=w.teacher)
         e = DeviceUpdateEngine(plan.blob, use_graph=False)
@@ -58,7 +61,7 @@ def main(argv=None):
         sys.exit("kernel_probe: --m, --n and --k are required (or --step)")
 
     import torch
-    from . import _lib
+    from seeml_amd import _lib
 
     L = _lib.lib()
     names = {}

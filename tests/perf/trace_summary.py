@@ -2,7 +2,7 @@
 
 Grouping by the grid as well as the name separates the different GEMM
 shapes that share one kernel template. Usage:
-    python see-ml_amd/seeml_amd/trace_summary.py <..._kernel_trace.csv> [top_n]
+    python tests/perf/trace_summary.py <..._kernel_trace.csv> [top_n]
 """
 import collections
 import csv
