@@ -75,3 +75,65 @@ def test_noalloc_gemm_tn_equals_the_allocating_entry_point(orc):
                                        stream) == 1
     torch.cuda.synchronize()
     assert bool((c == 7.0).all())
+
+
+_CHILD = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+from seeml_amd import _lib
+L = _lib.lib()
+dev = torch.device("cuda:0")
+s = torch.cuda.current_stream().cuda_stream
+
+def call(M, N, K):
+    a = torch.randn(K * M, device=dev)
+    b = torch.randn(K * N, device=dev)
+    c = torch.empty(M * N, device=dev)
+    torch.cuda.synchronize()
+    return a, b, c
+
+# warm-up through the no-alloc entry point only: code objects loaded, the
+# scratch symbol looked up, on a skinny colsum and a split-K tile shape
+for M, N, K in ((64, 16, 512), (192, 136, 1024)):
+    a, b, c = call(M, N, K)
+    assert L.seeml_hip_gemm_tn_noalloc(a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, s) == 0
+torch.cuda.synchronize()
+# a split-K shape whose partials (8 slices of 512 x 512) fill half the scratch
+M, N, K = 512, 512, 1024
+a, b, c = call(M, N, K)
+free0 = torch.cuda.mem_get_info()[0]
+for _ in range(3):
+    assert L.seeml_hip_gemm_tn_noalloc(a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, s) == 0, \
+        L.seeml_hip_kernel_error()
+torch.cuda.synchronize()
+free1 = torch.cuda.mem_get_info()[0]
+print(f"noalloc child: free device memory {free0} -> {free1}", flush=True)
+assert free1 == free0, (free0, free1)
+# the allocating entry point, by contrast, grows its workspace here
+assert L.seeml_hip_gemm_tn(a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, s) == 0
+torch.cuda.synchronize()
+free2 = torch.cuda.mem_get_info()[0]
+print(f"noalloc child: after the allocating entry point {free2}", flush=True)
+assert free2 < free1, (free1, free2)
+print("noalloc child ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_allocates_no_device_memory():
+    """The entry point's promise itself, in a fresh process (no library
+    workspace yet, so any allocation on its path would show): free device
+    memory is unchanged across three calls whose plan needs megabytes of
+    split-K partials, while the allocating entry point's first call with
+    the same shape takes memory. A child process, not an exec."""
+    import os
+    import subprocess
+    import sys
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "see-ml_amd")
+    r = subprocess.run([sys.executable, "-c", _CHILD, pkg], capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "noalloc child ok" in r.stdout
