@@ -747,6 +747,10 @@ class Engine {
       }
     }
     PlanChains(program);
+    // Before the pointwise runs: folding the AddEW into the norm's rows saves
+    // the dx store and re-read (8 B/elem), a pointwise run over that AddEW and
+    // the next pointwise instruction only the sum's re-read.
+    PlanRowAddChains(program);
     PlanPointwiseRuns(program);
     PlanScaleFolds(program);
     PlanDualRuns(program);
@@ -849,13 +853,14 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
     SkinnyChain ch;      // skinny
     GemmDesc d;          // dense: the GEMM with its fused AddEW
     PointwiseRun pw;     // pointwise
+    RowAddend ra;        // row + AddEW: the AddEW in the norm backward's write-back
     uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
     const float* fold_x = nullptr;  // scale fold: the Scale's input and factor
     float fold_alpha = 1.0f;
@@ -1138,6 +1143,89 @@ class Engine {
 
   // Dual pairs outside every other fusion run as one launch (kDual); a pair
   // among a scale fold's consumers launches once inside the fold.
+  // Norm backward + AddEW (kernels.h RowAddend): RmsNormBwd or LayerNormBwd
+  // followed by an AddEW that consumes its dx (the residual stream's
+  // gradient sum) runs as one row kernel writing out = addend (+) dx, and dx
+  // too while a later instruction reads it. The row operands (dy, x, dx,
+  // addend, out) must be pairwise the same range or disjoint, and the writes
+  // disjoint from the per-column and per-row parameters: each row is read
+  // whole before any of it is written, by the threads that write it.
+  void PlanRowAddChains(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    bool added = false;
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      const UpdateInstruction& g = prog[i];
+      const auto op = static_cast<Op>(g.opcode);
+      if ((op != Op::kRmsNormBwd && op != Op::kLayerNormBwd) || taken[i] || taken[i + 1]) continue;
+      const UpdateInstruction& a = prog[i + 1];
+      if (static_cast<Op>(a.opcode) != Op::kAddEW) continue;
+      const bool ln = op == Op::kLayerNormBwd;
+      const uint64_t dims = ln ? g.out[2] : g.out[1];
+      const uint64_t rows = Hi(dims), cols = Lo(dims), n = rows * cols;
+      if (a.out[0] != n || n == 0) continue;
+      const uint64_t dx = g.in[3];
+      if ((a.in[0] == dx) == (a.in[1] == dx)) continue;  // exactly one operand is dx
+      const bool add_first = a.in[1] == dx;
+      const uint64_t y = add_first ? a.in[0] : a.in[1];
+      const uint64_t o = a.in[2];
+      if (IsRodataRef(o) || IsRodataRef(dx)) continue;
+      const uint64_t bytes = n * sizeof(float);
+      const uint64_t row_refs[5] = {g.in[0], g.in[1], dx, y, o};
+      bool ok = true;
+      for (int x1 = 0; x1 < 5 && ok; ++x1)
+        for (int x2 = x1 + 1; x2 < 5 && ok; ++x2) {
+          const uint64_t r1 = row_refs[x1], r2 = row_refs[x2];
+          if (IsRodataRef(r1) || IsRodataRef(r2)) continue;  // reads only (o, dx are arena)
+          if (RefOffset(r1) == RefOffset(r2)) continue;
+          if (Overlaps(Ranges{{RefOffset(r1), bytes}}, RefOffset(r2), bytes)) ok = false;
+        }
+      if (!ok) continue;
+      const bool store_dx = o != dx && !DeadAfter(program, i + 1, RefOffset(dx), bytes);
+      Ranges writes{{RefOffset(o), bytes}};
+      if (store_dx) writes.emplace_back(RefOffset(dx), bytes);
+      Ranges params;
+      auto param = [&](uint64_t ref, uint64_t count) {
+        if (!IsRodataRef(ref)) params.emplace_back(RefOffset(ref), count * sizeof(float));
+      };
+      param(g.in[2], cols);  // gamma
+      if (ln) {
+        param(g.out[0], rows);  // mean
+        param(g.out[1], rows);  // rstd
+      } else {
+        param(g.out[0], rows);  // rstd
+      }
+      bool clash = false;
+      for (const auto& w : writes)
+        if (Overlaps(params, w.first, w.second)) clash = true;
+      if (clash) continue;
+      RowAddend ra;
+      ra.addend = RP(y);
+      ra.out = WP(o);
+      ra.add_first = add_first;
+      ra.store_dx = store_dx;
+      if (!RowAddendForm(cols, {RP(g.in[0]), RP(g.in[1]), RP(g.in[2]), WP(dx), ra.addend, ra.out}))
+        continue;
+      ChainRun run;
+      run.first = i;
+      run.count = 2;
+      run.kind = ChainKind::kRowAdd;
+      run.ra = ra;
+      chains_[program].push_back(run);
+      taken[i] = taken[i + 1] = 1;
+      added = true;
+      ++i;
+    }
+    if (added)
+      std::sort(chains_[program].begin(), chains_[program].end(),
+                [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
   void PlanDualRuns(int program) {
     const auto& prog = plan_.program[program];
     std::vector<char> taken(prog.size(), 0);
@@ -1616,6 +1704,14 @@ class Engine {
         }
         return Status::Ok();
       case ChainKind::kDual: return LaunchDual(program, run.first, 3, nullptr, 1.0f, c);
+      case ChainKind::kRowAdd: {
+        const UpdateInstruction& g = plan_.program[program][run.first];
+        if (static_cast<Op>(g.opcode) == Op::kLayerNormBwd)
+          return LayerNormBwd(RP(g.in[0]), RP(g.in[1]), RP(g.in[2]), RP(g.out[0]), RP(g.out[1]),
+                              WP(g.in[3]), Hi(g.out[2]), Lo(g.out[2]), c, &run.ra);
+        return RmsNormBwd(RP(g.in[0]), RP(g.in[1]), RP(g.in[2]), RP(g.out[0]), WP(g.in[3]),
+                          Hi(g.out[1]), Lo(g.out[1]), c, &run.ra);
+      }
       default: return LaunchSkinnyChain(DescOf(plan_.program[program][run.first]), run.ch, c);
     }
   }
@@ -2473,6 +2569,17 @@ class Engine {
       *bytes = b;
       return true;
     }
+    if (run->kind == ChainKind::kRowAdd) {
+      const UpdateInstruction& g = prog[idx];
+      const bool ln = static_cast<Op>(g.opcode) == Op::kLayerNormBwd;
+      const uint64_t dims = ln ? g.out[2] : g.out[1];
+      const double rows = static_cast<double>(Hi(dims)), cols = static_cast<double>(Lo(dims));
+      // dy, x and the addend read, out (and dx) written; gamma; the row stats.
+      *flops = 0.0;
+      *bytes = 4.0 * rows * cols * (run->ra.store_dx ? 5.0 : 4.0) + 4.0 * cols +
+               (ln ? 8.0 : 4.0) * rows;
+      return true;
+    }
     if (run->kind == ChainKind::kDense) {
       const GemmDesc& d = run->d;
       const double mn = 4.0 * static_cast<double>(d.batch) * d.M * d.N;
@@ -2518,11 +2625,14 @@ class Engine {
           if (run->rd_mode == -1) return "in LoRA run: in an earlier rowdot group";
           return "in LoRA run (launched first)";
         case ChainKind::kPointwise: return "in pointwise run";
+        case ChainKind::kRowAdd: return "in row epilogue";
         default: return "in chain";
       }
     }
     if (run && run->kind == ChainKind::kPointwise)
       return "pointwise run of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
+    if (run && run->kind == ChainKind::kRowAdd)
+      return run->ra.store_dx ? "with the next AddEW (dx stored)" : "with the next AddEW";
     if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
       const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
       return idx == g.members.back()

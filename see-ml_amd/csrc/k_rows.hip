@@ -482,21 +482,13 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
   store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
 
+// dx of one register-resident RmsNormBwd row (normalization.cc:97-113): gv
+// holds dy on entry and dx on return.
 template <int TPR, int V>
-__global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
-    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, int cols, int nt) {
-  __shared__ double dscratch[kBlock / kWave];
-  size_t r;
-  int t;
-  if (!row_of<TPR>(rows, &r, &t)) return;
-  const int nv = cols / 4;
+__device__ __forceinline__ void rms_bwd_math(float4 (&gv)[V], const float4 (&xv)[V],
+                                             const float4 (&gm)[V], float rs, int nv, int t,
+                                             int cols, double* dscratch) {
   const float inv_d = 1.0f / static_cast<float>(cols);
-  const float rs = rstd[r];  // issued with the row's loads
-  float4 gm[V], gv[V], xv[V];
-  load_param<TPR, V>(gamma, nv, t, gm);
-  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
-  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -515,7 +507,64 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
                         rs * (gv[i].y - xv[i].y * rs * rs * mgx),
                         rs * (gv[i].z - xv[i].z * rs * rs * mgx),
                         rs * (gv[i].w - xv[i].w * rs * rs * mgx));
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_reg(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ rstd, float* __restrict__ dx, size_t rows, int cols, int nt) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float rs = rstd[r];  // issued with the row's loads
+  float4 gm[V], gv[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+  rms_bwd_math<TPR, V>(gv, xv, gm, rs, nv, t, cols, dscratch);
   store_row<TPR, V>(dx + r * cols, nv, t, gv, nt);
+}
+
+// out = addend (+) dx for a following AddEW, in its operand order (IEEE
+// addition: the AddEW's bits either way); dx is stored as well when live.
+template <int TPR, int V>
+__device__ __forceinline__ void store_with_addend(const float4 (&dxv)[V], float4 (&av)[V],
+                                                  float* dx, float* out, int nv, int t, int nt,
+                                                  int add_first, int store_dx) {
+  if (store_dx) store_row<TPR, V>(dx, nv, t, dxv, nt);
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    av[i] = add_first ? make_float4(av[i].x + dxv[i].x, av[i].y + dxv[i].y, av[i].z + dxv[i].z,
+                                    av[i].w + dxv[i].w)
+                      : make_float4(dxv[i].x + av[i].x, dxv[i].y + av[i].y, dxv[i].z + av[i].z,
+                                    dxv[i].w + av[i].w);
+  store_row<TPR, V>(out, nv, t, av, nt);
+}
+
+// RmsNormBwd with the AddEW that consumes its dx in the write-back. The row
+// operands (dy, x, dx, addend, out) may be the same range as one another:
+// every thread reads its float4 positions of a row before it writes any,
+// and writes only those positions, so they carry no __restrict__.
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void rms_norm_bwd_add_reg(
+    const float* dy, const float* x, const float* __restrict__ gamma,
+    const float* __restrict__ rstd, float* dx, const float* addend, float* out, size_t rows,
+    int cols, int nt, int add_first, int store_dx) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float rs = rstd[r];
+  float4 gm[V], gv[V], xv[V], av[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+  load_row<TPR, V>(addend + r * cols, nv, t, av, nt);
+  rms_bwd_math<TPR, V>(gv, xv, gm, rs, nv, t, cols, dscratch);
+  store_with_addend<TPR, V>(gv, av, dx + r * cols, out + r * cols, nv, t, nt, add_first, store_dx);
 }
 
 template <int TPR, int V>
@@ -573,22 +622,13 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
   store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
 
+// dx of one register-resident LayerNormBwd row (normalization.cc:45-73): gv
+// holds dy on entry and dx on return; xv is overwritten with x-hat.
 template <int TPR, int V>
-__global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
-    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
-    const float* __restrict__ mean, const float* __restrict__ rstd, float* __restrict__ dx,
-    size_t rows, int cols, int nt) {
-  __shared__ double dscratch[kBlock / kWave];
-  size_t r;
-  int t;
-  if (!row_of<TPR>(rows, &r, &t)) return;
-  const int nv = cols / 4;
+__device__ __forceinline__ void ln_bwd_math(float4 (&gv)[V], float4 (&xv)[V],
+                                            const float4 (&gm)[V], float mu, float rs, int nv,
+                                            int t, int cols, double* dscratch) {
   const float inv_d = 1.0f / static_cast<float>(cols);
-  const float mu = mean[r], rs = rstd[r];
-  float4 gm[V], gv[V], xv[V];
-  load_param<TPR, V>(gamma, nv, t, gm);
-  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
-  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
   double sg = 0.0, sgx = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -617,7 +657,46 @@ __global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
   for (int i = 0; i < V; ++i)
     gv[i] = make_float4(rs * (gv[i].x - mg - xv[i].x * mgx), rs * (gv[i].y - mg - xv[i].y * mgx),
                         rs * (gv[i].z - mg - xv[i].z * mgx), rs * (gv[i].w - mg - xv[i].w * mgx));
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_bwd_reg(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, float* __restrict__ dx,
+    size_t rows, int cols, int nt) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float mu = mean[r], rs = rstd[r];
+  float4 gm[V], gv[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+  ln_bwd_math<TPR, V>(gv, xv, gm, mu, rs, nv, t, cols, dscratch);
   store_row<TPR, V>(dx + r * cols, nv, t, gv, nt);
+}
+
+// LayerNormBwd with the AddEW that consumes its dx (as rms_norm_bwd_add_reg).
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_bwd_add_reg(
+    const float* dy, const float* x, const float* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, float* dx,
+    const float* addend, float* out, size_t rows, int cols, int nt, int add_first, int store_dx) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  const float mu = mean[r], rs = rstd[r];
+  float4 gm[V], gv[V], xv[V], av[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_row<TPR, V>(dy + r * cols, nv, t, gv, nt);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+  load_row<TPR, V>(addend + r * cols, nv, t, av, nt);
+  ln_bwd_math<TPR, V>(gv, xv, gm, mu, rs, nv, t, cols, dscratch);
+  store_with_addend<TPR, V>(gv, av, dx + r * cols, out + r * cols, nv, t, nt, add_first, store_dx);
 }
 
 // causal_s > 0: row r is query i = r % causal_s and the entries j > i of P
@@ -890,9 +969,23 @@ Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float
   return LaunchStatus("LayerNormFwd");
 }
 
+bool RowAddendForm(size_t cols, std::initializer_list<const void*> rows_base) {
+  return RegCase(cols, rows_base) >= 0;
+}
+
 Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const float* mean,
-                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c) {
+                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c,
+                    const RowAddend* add) {
   if (rows == 0 || cols == 0) return Status::Ok();
+  if (add) {
+    const int rc = RegCase(cols, {dy, x, gamma, dx, add->addend, add->out});
+    if (rc < 0) return Status::Fail(kUnitEngine, "LayerNormBwd+AddEW: rows not register-resident");
+    REG_DISPATCH(layer_norm_bwd_add_reg, rc, rows, dy, x, gamma, mean, rstd, dx, add->addend,
+                 add->out, rows, static_cast<int>(cols),
+                 StreamPolicy((add->store_dx ? 20 : 16) * rows * cols) ? 1 : 0,
+                 add->add_first ? 1 : 0, add->store_dx ? 1 : 0);
+    return LaunchStatus("LayerNormBwd+AddEW");
+  }
   const int rc = RegCase(cols, {dy, x, gamma, dx});
   if (rc >= 0)
     REG_DISPATCH(layer_norm_bwd_reg, rc, rows, dy, x, gamma, mean, rstd, dx, rows,
@@ -915,8 +1008,17 @@ Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, siz
 }
 
 Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
-                  float* dx, size_t rows, size_t cols, const Ctx& c) {
+                  float* dx, size_t rows, size_t cols, const Ctx& c, const RowAddend* add) {
   if (rows == 0 || cols == 0) return Status::Ok();
+  if (add) {
+    const int rc = RegCase(cols, {dy, x, gamma, dx, add->addend, add->out});
+    if (rc < 0) return Status::Fail(kUnitEngine, "RmsNormBwd+AddEW: rows not register-resident");
+    REG_DISPATCH(rms_norm_bwd_add_reg, rc, rows, dy, x, gamma, rstd, dx, add->addend, add->out,
+                 rows, static_cast<int>(cols),
+                 StreamPolicy((add->store_dx ? 20 : 16) * rows * cols) ? 1 : 0,
+                 add->add_first ? 1 : 0, add->store_dx ? 1 : 0);
+    return LaunchStatus("RmsNormBwd+AddEW");
+  }
   const int rc = RegCase(cols, {dy, x, gamma, dx});
   if (rc >= 0)
     REG_DISPATCH(rms_norm_bwd_reg, rc, rows, dy, x, gamma, rstd, dx, rows,

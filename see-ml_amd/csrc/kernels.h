@@ -313,12 +313,26 @@ Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, flo
                     size_t C, float T, const Ctx& c);
 Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
                     float* rstd, size_t rows, size_t cols, const Ctx& c);
+// A following AddEW folded into a norm backward's write-back: out =
+// addend (+) dx in the AddEW's operand order, dx itself stored only when
+// store_dx. The row operands (dy, x, dx, addend, out) may be the same range
+// as one another but must not partially overlap; register-resident rows only
+// (RowAddendForm).
+struct RowAddend {
+  const float* addend = nullptr;
+  float* out = nullptr;
+  bool add_first = true;
+  bool store_dx = true;
+};
+bool RowAddendForm(size_t cols, std::initializer_list<const void*> rows_base);
 Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const float* mean,
-                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c);
+                    const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c,
+                    const RowAddend* add = nullptr);
 Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
                   size_t cols, const Ctx& c);
 Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
-                  float* dx, size_t rows, size_t cols, const Ctx& c);
+                  float* dx, size_t rows, size_t cols, const Ctx& c,
+                  const RowAddend* add = nullptr);
 // causal_s > 0: the caller has proven that rows are (b, h, i) with i = row %
 // causal_s, cols == causal_s, and that probs and dp hold exact +0 at every
 // j > i (AttnFwd / AttnDP outputs). Those entries are then not read: their

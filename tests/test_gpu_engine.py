@@ -683,13 +683,46 @@ def test_fusions_are_planned(torch_gpu):
     duals = [i for i, c in enumerate(ch) if c.startswith("skinny/dual")]
     assert duals, ch
     assert all(ch[i + 1] == "in the dual pass" for i in duals)
+    # the residual stream's gradient sums in the RMSNorm backward's rows
+    rows = [i for i, c in enumerate(ch) if c.startswith("with the next AddEW")]
+    assert rows, ch
+    assert all(planner.OP_NAME[p.train[i]["opcode"]] == "RmsNormBwd" for i in rows)
+    assert all(ch[i + 1] == "in row epilogue" for i in rows)
+    assert {i + 1 for i in rows} == {i for i, c in enumerate(ch) if c == "in row epilogue"}
     e.close()
     e = engine(p, use_graph=False)
     e.train_step(x, y)
     for i in range(len(p.train)):
         c = e.gemm_choice(PROGRAM_TRAIN, i)
-        assert not (c.startswith("in ") or "+AddEW" in c or "run of" in c or "chain of" in c), c
+        assert not (c.startswith("in ") or "AddEW" in c or "run of" in c or "chain of" in c), c
     e.close()
+
+
+@pytest.mark.parametrize("name,norm", [("c3s", "RmsNormBwd"), ("c5s64", "LayerNormBwd")])
+def test_norm_backward_runs_the_next_addew_in_its_rows(torch_gpu, name, norm):
+    """The residual stream's gradient sum after a norm backward (AddEW of an
+    accumulated gradient and the norm's dx) runs in the norm kernel's
+    write-back: planned on RMSNorm and LayerNorm decoders, and the fused
+    graph equals the eager engine bit for bit over two steps."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload(name)
+    runs = []
+    for use_graph in (True, False):
+        e = engine(p, use_graph=use_graph)
+        losses = []
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+        if use_graph:
+            ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+            rows = [i for i, c in enumerate(ch) if c.startswith("with the next AddEW")]
+            assert rows, ch
+            assert all(planner.OP_NAME[p.train[i]["opcode"]] == norm for i in rows)
+            assert all(ch[i + 1] == "in row epilogue" for i in rows)
+        runs.append((np.array(losses, np.float32), persistent(e, p)))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
 
 
 @pytest.mark.parametrize("name", ["c4m", "c4m48"])
