@@ -751,6 +751,7 @@ class Engine {
     // the dx store and re-read (8 B/elem), a pointwise run over that AddEW and
     // the next pointwise instruction only the sum's re-read.
     PlanRowAddChains(program);
+    PlanAddRowChains(program);
     PlanPointwiseRuns(program);
     PlanScaleFolds(program);
     PlanDualRuns(program);
@@ -853,7 +854,7 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd, kAddRow };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -861,6 +862,7 @@ class Engine {
     GemmDesc d;          // dense: the GEMM with its fused AddEW
     PointwiseRun pw;     // pointwise
     RowAddend ra;        // row + AddEW: the AddEW in the norm backward's write-back
+    RowPreAdd pa;        // AddEW + row: the AddEW in the norm forward's load
     uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
     const float* fold_x = nullptr;  // scale fold: the Scale's input and factor
     float fold_alpha = 1.0f;
@@ -1216,6 +1218,86 @@ class Engine {
       run.count = 2;
       run.kind = ChainKind::kRowAdd;
       run.ra = ra;
+      chains_[program].push_back(run);
+      taken[i] = taken[i + 1] = 1;
+      added = true;
+      ++i;
+    }
+    if (added)
+      std::sort(chains_[program].begin(), chains_[program].end(),
+                [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  // AddEW + norm forward (kernels.h RowPreAdd): an AddEW whose sum is the
+  // next instruction's RmsNormFwd / LayerNormFwd input (the residual stream
+  // x + f(x) entering the next block's norm) runs in that norm kernel's load:
+  // the sum is formed per row in registers, stored while a later instruction
+  // reads it, and normalised without being read back. The row operands (the
+  // AddEW's a, b and sum, the norm's y) must be pairwise the same range or
+  // disjoint, and the norm's per-row statistics apart from all of them.
+  void PlanAddRowChains(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    bool added = false;
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      const UpdateInstruction& a = prog[i];
+      const UpdateInstruction& g = prog[i + 1];
+      const auto op = static_cast<Op>(g.opcode);
+      if (static_cast<Op>(a.opcode) != Op::kAddEW || taken[i] || taken[i + 1]) continue;
+      if (op != Op::kRmsNormFwd && op != Op::kLayerNormFwd) continue;
+      const bool ln = op == Op::kLayerNormFwd;
+      const uint64_t rows = Hi(g.out[0]), cols = Lo(g.out[0]), n = rows * cols;
+      const uint64_t sum = a.in[2];
+      if (a.out[0] != n || n == 0 || g.in[0] != sum || IsRodataRef(sum)) continue;
+      const uint64_t y = ln ? g.in[3] : g.in[2];
+      if (IsRodataRef(y)) continue;
+      const uint64_t bytes = n * sizeof(float);
+      const uint64_t row_refs[4] = {a.in[0], a.in[1], sum, y};
+      bool ok = true;
+      for (int x1 = 0; x1 < 4 && ok; ++x1)
+        for (int x2 = x1 + 1; x2 < 4 && ok; ++x2) {
+          const uint64_t r1 = row_refs[x1], r2 = row_refs[x2];
+          if (IsRodataRef(r1) || IsRodataRef(r2)) continue;
+          if (RefOffset(r1) == RefOffset(r2)) continue;
+          if (Overlaps(Ranges{{RefOffset(r1), bytes}}, RefOffset(r2), bytes)) ok = false;
+        }
+      if (!ok) continue;
+      const bool store_sum = sum != y && !DeadAfter(program, i + 1, RefOffset(sum), bytes);
+      Ranges rowr;  // every arena row operand
+      for (uint64_t ref : row_refs)
+        if (!IsRodataRef(ref)) rowr.emplace_back(RefOffset(ref), bytes);
+      Ranges stats;  // written per row by the norm
+      if (ln) {
+        stats.emplace_back(RefOffset(g.out[1]), rows * sizeof(float));
+        stats.emplace_back(RefOffset(g.out[2]), rows * sizeof(float));
+      } else {
+        stats.emplace_back(RefOffset(g.in[3]), rows * sizeof(float));
+      }
+      Ranges params;
+      if (!IsRodataRef(g.in[1])) params.emplace_back(RefOffset(g.in[1]), cols * sizeof(float));
+      if (ln && !IsRodataRef(g.in[2])) params.emplace_back(RefOffset(g.in[2]), cols * sizeof(float));
+      bool clash = false;
+      for (const auto& st : stats)
+        if (Overlaps(rowr, st.first, st.second) || Overlaps(params, st.first, st.second)) clash = true;
+      for (const auto& w : rowr)
+        if (Overlaps(params, w.first, w.second)) clash = true;
+      if (clash) continue;
+      RowPreAdd pa;
+      pa.a = RP(a.in[0]);
+      pa.b = RP(a.in[1]);
+      pa.sum = WP(sum);
+      pa.store_sum = store_sum;
+      if (!RowAddendForm(cols, {pa.a, pa.b, pa.sum, RP(g.in[1]), WP(y)})) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = 2;
+      run.kind = ChainKind::kAddRow;
+      run.pa = pa;
       chains_[program].push_back(run);
       taken[i] = taken[i + 1] = 1;
       added = true;
@@ -1704,6 +1786,14 @@ class Engine {
         }
         return Status::Ok();
       case ChainKind::kDual: return LaunchDual(program, run.first, 3, nullptr, 1.0f, c);
+      case ChainKind::kAddRow: {
+        const UpdateInstruction& g = plan_.program[program][run.first + 1];
+        if (static_cast<Op>(g.opcode) == Op::kLayerNormFwd)
+          return LayerNormFwd(RP(g.in[0]), RP(g.in[1]), RP(g.in[2]), WP(g.in[3]), WP(g.out[1]),
+                              WP(g.out[2]), Hi(g.out[0]), Lo(g.out[0]), c, &run.pa);
+        return RmsNormFwd(RP(g.in[0]), RP(g.in[1]), WP(g.in[2]), WP(g.in[3]), Hi(g.out[0]),
+                          Lo(g.out[0]), c, &run.pa);
+      }
       case ChainKind::kRowAdd: {
         const UpdateInstruction& g = plan_.program[program][run.first];
         if (static_cast<Op>(g.opcode) == Op::kLayerNormBwd)
@@ -2569,6 +2659,16 @@ class Engine {
       *bytes = b;
       return true;
     }
+    if (run->kind == ChainKind::kAddRow) {
+      const UpdateInstruction& g = prog[idx + 1];
+      const bool ln = static_cast<Op>(g.opcode) == Op::kLayerNormFwd;
+      const double rows = static_cast<double>(Hi(g.out[0])), cols = static_cast<double>(Lo(g.out[0]));
+      // a and b read, y (and the sum) written; gamma (beta); the row stats.
+      *flops = 0.0;
+      *bytes = 4.0 * rows * cols * (run->pa.store_sum ? 4.0 : 3.0) + (ln ? 8.0 : 4.0) * cols +
+               (ln ? 8.0 : 4.0) * rows;
+      return true;
+    }
     if (run->kind == ChainKind::kRowAdd) {
       const UpdateInstruction& g = prog[idx];
       const bool ln = static_cast<Op>(g.opcode) == Op::kLayerNormBwd;
@@ -2626,6 +2726,7 @@ class Engine {
           return "in LoRA run (launched first)";
         case ChainKind::kPointwise: return "in pointwise run";
         case ChainKind::kRowAdd: return "in row epilogue";
+        case ChainKind::kAddRow: return "in row prologue";
         default: return "in chain";
       }
     }
@@ -2633,6 +2734,8 @@ class Engine {
       return "pointwise run of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
     if (run && run->kind == ChainKind::kRowAdd)
       return run->ra.store_dx ? "with the next AddEW (dx stored)" : "with the next AddEW";
+    if (run && run->kind == ChainKind::kAddRow)
+      return run->pa.store_sum ? "with the next norm (sum stored)" : "with the next norm";
     if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
       const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
       return idx == g.members.back()

@@ -450,6 +450,28 @@ __device__ __forceinline__ double sq4(float4 a) {
   return s;
 }
 
+// y of one register-resident RmsNormFwd row (normalization.cc:75-95): xv
+// holds x on entry and y on return; returns rstd.
+template <int TPR, int V>
+__device__ __forceinline__ float rms_fwd_math(float4 (&xv)[V], const float4 (&gm)[V], int nv,
+                                              int t, int cols, double* dscratch) {
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) s += sq4(xv[i]);
+  const double ss = row_sum_d<TPR>(s, dscratch);
+  const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = t + i * TPR;
+    if (j < nv) {
+      const float4 g = gm[i];
+      xv[i] = make_float4(xv[i].x * rs * g.x, xv[i].y * rs * g.y, xv[i].z * rs * g.z,
+                          xv[i].w * rs * g.w);
+    }
+  }
+  return rs;
+}
+
 template <int TPR, int V>
 __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restrict__ x,
                                                            const float* __restrict__ gamma,
@@ -464,21 +486,43 @@ __global__ __launch_bounds__(kBlock) void rms_norm_fwd_reg(const float* __restri
   float4 gm[V], xv[V];
   load_param<TPR, V>(gamma, nv, t, gm);
   load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
-  double s = 0.0;
-#pragma unroll
-  for (int i = 0; i < V; ++i) s += sq4(xv[i]);
-  const double ss = row_sum_d<TPR>(s, dscratch);
-  const float rs = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(cols)) + 1e-5f);
+  const float rs = rms_fwd_math<TPR, V>(xv, gm, nv, t, cols, dscratch);
   if (t == 0) rstd[r] = rs;
+  store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
+}
+
+// The preceding AddEW's sum x = a + b, formed from the two rows as the AddEW
+// forms it (its operand order), and stored when a later reader needs it.
+template <int TPR, int V>
+__device__ __forceinline__ void load_sum(const float* a, const float* b, float* sum, int nv, int t,
+                                         int nt, int store_sum, float4 (&xv)[V]) {
+  float4 bv[V];
+  load_row<TPR, V>(a, nv, t, xv, nt);
+  load_row<TPR, V>(b, nv, t, bv, nt);
 #pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int j = t + i * TPR;
-    if (j < nv) {
-      const float4 g = gm[i];
-      xv[i] = make_float4(xv[i].x * rs * g.x, xv[i].y * rs * g.y, xv[i].z * rs * g.z,
-                          xv[i].w * rs * g.w);
-    }
-  }
+  for (int i = 0; i < V; ++i)
+    xv[i] = make_float4(xv[i].x + bv[i].x, xv[i].y + bv[i].y, xv[i].z + bv[i].z, xv[i].w + bv[i].w);
+  if (store_sum) store_row<TPR, V>(sum, nv, t, xv, nt);
+}
+
+// RmsNormFwd of the preceding AddEW's output, that AddEW in its prologue. The
+// row operands (a, b, sum, y) may be the same range as one another: every
+// thread reads its float4 positions of a row before it writes any, and
+// writes only those positions, so they carry no __restrict__.
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void rms_norm_fwd_add_reg(
+    const float* a, const float* b, float* sum, const float* __restrict__ gamma, float* y,
+    float* __restrict__ rstd, size_t rows, int cols, int nt, int store_sum) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 gm[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_sum<TPR, V>(a + r * cols, b + r * cols, sum + r * cols, nv, t, nt, store_sum, xv);
+  const float rs = rms_fwd_math<TPR, V>(xv, gm, nv, t, cols, dscratch);
+  if (t == 0) rstd[r] = rs;
   store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
 
@@ -567,20 +611,12 @@ __global__ __launch_bounds__(kBlock) void rms_norm_bwd_add_reg(
   store_with_addend<TPR, V>(gv, av, dx + r * cols, out + r * cols, nv, t, nt, add_first, store_dx);
 }
 
+// y of one register-resident LayerNormFwd row (normalization.cc:17-43): xv
+// holds x on entry and y on return; returns (mean, rstd).
 template <int TPR, int V>
-__global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
-    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
-    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, size_t rows,
-    int cols, int nt) {
-  __shared__ double dscratch[kBlock / kWave];
-  size_t r;
-  int t;
-  if (!row_of<TPR>(rows, &r, &t)) return;
-  const int nv = cols / 4;
-  float4 gm[V], bm[V], xv[V];
-  load_param<TPR, V>(gamma, nv, t, gm);
-  load_param<TPR, V>(beta, nv, t, bm);
-  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+__device__ __forceinline__ float2 ln_fwd_math(float4 (&xv)[V], const float4 (&gm)[V],
+                                              const float4 (&bm)[V], int nv, int t, int cols,
+                                              double* dscratch) {
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -606,10 +642,6 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
   }
   const double var = row_sum_d<TPR>(v, dscratch);
   const float rs = 1.0f / sqrtf(static_cast<float>(var / static_cast<double>(cols)) + 1e-5f);
-  if (t == 0) {
-    mean[r] = mu;
-    rstd[r] = rs;
-  }
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = t + i * TPR;
@@ -618,6 +650,52 @@ __global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
       xv[i] = make_float4((xv[i].x - mu) * rs * g.x + b.x, (xv[i].y - mu) * rs * g.y + b.y,
                           (xv[i].z - mu) * rs * g.z + b.z, (xv[i].w - mu) * rs * g.w + b.w);
     }
+  }
+  return make_float2(mu, rs);
+}
+
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_fwd_reg(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ y, float* __restrict__ mean, float* __restrict__ rstd, size_t rows,
+    int cols, int nt) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 gm[V], bm[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_param<TPR, V>(beta, nv, t, bm);
+  load_row<TPR, V>(x + r * cols, nv, t, xv, nt);
+  const float2 st = ln_fwd_math<TPR, V>(xv, gm, bm, nv, t, cols, dscratch);
+  if (t == 0) {
+    mean[r] = st.x;
+    rstd[r] = st.y;
+  }
+  store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
+}
+
+// LayerNormFwd of the preceding AddEW's output, that AddEW in its prologue
+// (as rms_norm_fwd_add_reg).
+template <int TPR, int V>
+__global__ __launch_bounds__(kBlock) void layer_norm_fwd_add_reg(
+    const float* a, const float* b, float* sum, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float* y, float* __restrict__ mean, float* __restrict__ rstd,
+    size_t rows, int cols, int nt, int store_sum) {
+  __shared__ double dscratch[kBlock / kWave];
+  size_t r;
+  int t;
+  if (!row_of<TPR>(rows, &r, &t)) return;
+  const int nv = cols / 4;
+  float4 gm[V], bm[V], xv[V];
+  load_param<TPR, V>(gamma, nv, t, gm);
+  load_param<TPR, V>(beta, nv, t, bm);
+  load_sum<TPR, V>(a + r * cols, b + r * cols, sum + r * cols, nv, t, nt, store_sum, xv);
+  const float2 st = ln_fwd_math<TPR, V>(xv, gm, bm, nv, t, cols, dscratch);
+  if (t == 0) {
+    mean[r] = st.x;
+    rstd[r] = st.y;
   }
   store_row<TPR, V>(y + r * cols, nv, t, xv, nt);
 }
@@ -958,8 +1036,17 @@ static int RegCase(size_t cols, std::initializer_list<const void*> rows_base) {
   } while (0)
 
 Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
-                    float* rstd, size_t rows, size_t cols, const Ctx& c) {
+                    float* rstd, size_t rows, size_t cols, const Ctx& c, const RowPreAdd* pre) {
   if (rows == 0 || cols == 0) return Status::Ok();
+  if (pre) {
+    const int rc = RegCase(cols, {pre->a, pre->b, pre->sum, gamma, beta, y});
+    if (rc < 0) return Status::Fail(kUnitEngine, "AddEW+LayerNormFwd: rows not register-resident");
+    REG_DISPATCH(layer_norm_fwd_add_reg, rc, rows, pre->a, pre->b, pre->sum, gamma, beta, y, mean,
+                 rstd, rows, static_cast<int>(cols),
+                 StreamPolicy((pre->store_sum ? 16 : 12) * rows * cols) ? 1 : 0,
+                 pre->store_sum ? 1 : 0);
+    return LaunchStatus("AddEW+LayerNormFwd");
+  }
   const int rc = RegCase(cols, {x, gamma, beta, y});
   if (rc >= 0)
     REG_DISPATCH(layer_norm_fwd_reg, rc, rows, x, gamma, beta, y, mean, rstd, rows,
@@ -996,8 +1083,16 @@ Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const f
 }
 
 Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
-                  size_t cols, const Ctx& c) {
+                  size_t cols, const Ctx& c, const RowPreAdd* pre) {
   if (rows == 0 || cols == 0) return Status::Ok();
+  if (pre) {
+    const int rc = RegCase(cols, {pre->a, pre->b, pre->sum, gamma, y});
+    if (rc < 0) return Status::Fail(kUnitEngine, "AddEW+RmsNormFwd: rows not register-resident");
+    REG_DISPATCH(rms_norm_fwd_add_reg, rc, rows, pre->a, pre->b, pre->sum, gamma, y, rstd, rows,
+                 static_cast<int>(cols), StreamPolicy((pre->store_sum ? 16 : 12) * rows * cols) ? 1 : 0,
+                 pre->store_sum ? 1 : 0);
+    return LaunchStatus("AddEW+RmsNormFwd");
+  }
   const int rc = RegCase(cols, {x, gamma, y});
   if (rc >= 0)
     REG_DISPATCH(rms_norm_fwd_reg, rc, rows, x, gamma, y, rstd, rows, static_cast<int>(cols),

@@ -311,8 +311,20 @@ Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, f
 size_t KLDistillFwdWorkspace(size_t N);
 Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, float* p_t, size_t N,
                     size_t C, float T, const Ctx& c);
+// The preceding AddEW folded into a norm forward's load: the norm's input
+// x = a + b (the AddEW's operand order) is formed per row in registers and
+// stored to `sum` only when store_sum; x itself is not read. The row
+// operands (a, b, sum, y) may be the same range as one another but must not
+// partially overlap; register-resident rows only (RowAddendForm).
+struct RowPreAdd {
+  const float* a = nullptr;
+  const float* b = nullptr;
+  float* sum = nullptr;
+  bool store_sum = true;
+};
 Status LayerNormFwd(const float* x, const float* gamma, const float* beta, float* y, float* mean,
-                    float* rstd, size_t rows, size_t cols, const Ctx& c);
+                    float* rstd, size_t rows, size_t cols, const Ctx& c,
+                    const RowPreAdd* pre = nullptr);
 // A following AddEW folded into a norm backward's write-back: out =
 // addend (+) dx in the AddEW's operand order, dx itself stored only when
 // store_dx. The row operands (dy, x, dx, addend, out) may be the same range
@@ -329,7 +341,7 @@ Status LayerNormBwd(const float* dy, const float* x, const float* gamma, const f
                     const float* rstd, float* dx, size_t rows, size_t cols, const Ctx& c,
                     const RowAddend* add = nullptr);
 Status RmsNormFwd(const float* x, const float* gamma, float* y, float* rstd, size_t rows,
-                  size_t cols, const Ctx& c);
+                  size_t cols, const Ctx& c, const RowPreAdd* pre = nullptr);
 Status RmsNormBwd(const float* dy, const float* x, const float* gamma, const float* rstd,
                   float* dx, size_t rows, size_t cols, const Ctx& c,
                   const RowAddend* add = nullptr);

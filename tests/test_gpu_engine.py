@@ -689,6 +689,12 @@ def test_fusions_are_planned(torch_gpu):
     assert all(planner.OP_NAME[p.train[i]["opcode"]] == "RmsNormBwd" for i in rows)
     assert all(ch[i + 1] == "in row epilogue" for i in rows)
     assert {i + 1 for i in rows} == {i for i, c in enumerate(ch) if c == "in row epilogue"}
+    # the residual sums entering the next block's RMSNorm, in its load
+    pre = [i for i, c in enumerate(ch) if c.startswith("with the next norm")]
+    assert pre, ch
+    assert all(planner.OP_NAME[p.train[i]["opcode"]] == "AddEW" for i in pre)
+    assert all(planner.OP_NAME[p.train[i + 1]["opcode"]] == "RmsNormFwd" for i in pre)
+    assert {i + 1 for i in pre} == {i for i, c in enumerate(ch) if c == "in row prologue"}
     e.close()
     e = engine(p, use_graph=False)
     e.train_step(x, y)
@@ -699,11 +705,13 @@ def test_fusions_are_planned(torch_gpu):
 
 
 @pytest.mark.parametrize("name,norm", [("c3s", "RmsNormBwd"), ("c5s64", "LayerNormBwd")])
-def test_norm_backward_runs_the_next_addew_in_its_rows(torch_gpu, name, norm):
-    """The residual stream's gradient sum after a norm backward (AddEW of an
-    accumulated gradient and the norm's dx) runs in the norm kernel's
-    write-back: planned on RMSNorm and LayerNorm decoders, and the fused
-    graph equals the eager engine bit for bit over two steps."""
+def test_norm_kernels_run_the_adjacent_addews(torch_gpu, name, norm):
+    """The residual stream's AddEWs next to a norm run inside the norm
+    kernel: the gradient sum after a norm backward (an accumulated gradient
+    plus the norm's dx) in its write-back, and the sum x + f(x) entering
+    the next block's norm forward in its load. Planned on RMSNorm and
+    LayerNorm decoders; the fused graph equals the eager engine bit for bit
+    over two steps."""
     from seeml_amd import PROGRAM_TRAIN
     w, p = compile_workload(name)
     runs = []
@@ -719,6 +727,11 @@ def test_norm_backward_runs_the_next_addew_in_its_rows(torch_gpu, name, norm):
             assert rows, ch
             assert all(planner.OP_NAME[p.train[i]["opcode"]] == norm for i in rows)
             assert all(ch[i + 1] == "in row epilogue" for i in rows)
+            pre = [i for i, c in enumerate(ch) if c.startswith("with the next norm")]
+            assert pre, ch
+            fwd = norm.replace("Bwd", "Fwd")
+            assert all(planner.OP_NAME[p.train[i + 1]["opcode"]] == fwd for i in pre)
+            assert all(ch[i + 1] == "in row prologue" for i in pre)
         runs.append((np.array(losses, np.float32), persistent(e, p)))
         e.close()
     assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
