@@ -156,11 +156,8 @@ class Engine {
           !s)
         return s;
     if (Status s = HipOk(LockedMalloc(&d_scalars_, sizeof(StepScalars)), "scalars"); !s) return s;
-    if (Status s = HipOk(LockedHostMalloc(&h_scalars_, 2 * sizeof(StepScalars)), "pinned scalars"); !s)
-      return s;
-    for (hipEvent_t& ev : scalar_ev_)
-      if (Status s = HipOk(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "scalar event"); !s)
-        return s;
+    // Pinned and mapped: the programs that end in a loss write it here from
+    // the device (PostLoss), so reading it costs no copy launch.
     if (Status s = HipOk(LockedHostMalloc(&h_loss_, sizeof(float)), "pinned loss"); !s) return s;
     if (Status s = MakeWeightCopies(); !s) return s;
     if (Status s = MakeRopeTables(); !s) return s;
@@ -675,6 +672,7 @@ class Engine {
     if (program < 0 || program > 2 || begin > end || end > plan_.program[program].size())
       return Status::Fail(kUnitEngine, "instruction range out of bounds");
     if (Status s = EnsureWorkspace(program); !s) return s;
+    loss_posted_ = false;
     const Ctx c = MakeCtx();
     for (size_t i = begin; i < end; ++i)
       if (Status s = Dispatch(program, i, c); !s) return s;
@@ -1895,6 +1893,8 @@ class Engine {
         !s)
       return s;
     Status launched = RunFused(program, begin, end);
+    if (launched && end == plan_.program[program].size() && PostsLoss(program))
+      launched = PostLoss(RP(plan_.header.loss_ref), h_loss_, stream_);
     hipGraph_t g = nullptr;
     const hipError_t stop = hipStreamEndCapture(stream_, &g);
     if (!launched) {
@@ -1943,12 +1943,26 @@ class Engine {
     return Status::Ok();
   }
 
+  // The train and eval programs end in a loss.
+  bool PostsLoss(int program) const {
+    return (program == static_cast<int>(Program::kTrain) || program == static_cast<int>(Program::kEval)) &&
+           plan_.header.loss_ref != kNullRef;
+  }
+
   Status Run(int program) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
+    loss_posted_ = false;
     if (!built_[program])
       if (Status s = Build(program); !s) return s;
     if (plan_.program[program].empty()) return Status::Ok();
-    if (!use_graph_) return RunEager(program);
+    if (!use_graph_) {
+      if (Status s = RunEager(program); !s) return s;
+      if (PostsLoss(program)) {
+        if (Status s = PostLoss(RP(plan_.header.loss_ref), h_loss_, stream_); !s) return s;
+        loss_posted_ = true;
+      }
+      return Status::Ok();
+    }
     const Ctx c = MakeCtx();
     for (const Segment& g : segs_[program]) {
       if (g.mark < 0) {
@@ -1959,23 +1973,25 @@ class Engine {
       if (Status s = Dispatch(program, g.first, c); !s) return s;
       (void)hipEventRecord(mark_ev_[program][2 * g.mark + 1], stream_);
     }
+    if (PostsLoss(program)) {
+      // A graph ending the program posted the loss; a marked last launch did not.
+      if (segs_[program].empty() || segs_[program].back().mark >= 0)
+        if (Status s = PostLoss(RP(plan_.header.loss_ref), h_loss_, stream_); !s) return s;
+      loss_posted_ = true;
+    }
     return Status::Ok();
   }
 
-  // Two pinned scalar slots used in turn: a slot is rewritten only after
-  // the upload that last read it has completed (its event), so back-to-back
-  // steps never overwrite bytes a pending copy still reads.
+  // The step's scalars travel as the staging kernel's arguments, copied at
+  // launch: no host buffer outlives the call, and back-to-back steps need
+  // no wait on an earlier upload.
   Status SetStep(uint64_t step) {
-    const int slot = scalar_slot_ ^= 1;
-    if (Status s = HipOk(hipEventSynchronize(scalar_ev_[slot]), "scalar slot wait"); !s) return s;
-    h_scalars_[slot] = MakeStepScalars(plan_.header, step == 0 ? 1 : step);
-    if (Status s = HipOk(hipMemcpyAsync(d_scalars_, &h_scalars_[slot], sizeof(StepScalars),
-                                        hipMemcpyHostToDevice, stream_),
-                         "step scalars upload");
-        !s)
+    const StepScalars sc = MakeStepScalars(plan_.header, step == 0 ? 1 : step);
+    if (Status s = StageStep(&sc, d_scalars_, nullptr, nullptr, 0, nullptr, nullptr, 0, stream_); !s)
       return s;
     step_ = step;
-    return HipOk(hipEventRecord(scalar_ev_[slot], stream_), "scalar slot event");
+    loss_posted_ = false;
+    return Status::Ok();
   }
 
   // The feeder contract's bounds (contract.cc:173-207) on host-staged ids.
@@ -1990,6 +2006,29 @@ class Engine {
 
   Status Stage(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
                bool on_device) {
+    if (Status s = CheckStaged(input, input_bytes, labels, label_bytes, on_device); !s) return s;
+    const PlanHeader& h = plan_.header;
+    loss_posted_ = false;
+    const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    if (input_bytes)
+      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.input_ref), input, input_bytes,
+                                          kind, stream_),
+                           "input staging");
+          !s)
+        return s;
+    if (h.label_kind != 0 && labels && label_bytes)
+      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.label_ref), labels, label_bytes,
+                                          kind, stream_),
+                           "label staging");
+          !s)
+        return s;
+    return Status::Ok();
+  }
+
+  // The staged batch's sizes against the plan's slots, and (host batches)
+  // the feeder contract's id bounds.
+  Status CheckStaged(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
+                     bool on_device) const {
     const PlanHeader& h = plan_.header;
     if (input_bytes != h.input_floats * 4)
       return Status::Fail(kUnitEngine, "staged input size does not match the plan input slot");
@@ -2010,23 +2049,17 @@ class Engine {
             !s)
           return s;
     }
-    const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-    if (input_bytes)
-      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.input_ref), input, input_bytes,
-                                          kind, stream_),
-                           "input staging");
-          !s)
-        return s;
-    if (h.label_kind != 0 && labels && label_bytes)
-      if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.label_ref), labels, label_bytes,
-                                          kind, stream_),
-                           "label staging");
-          !s)
-        return s;
     return Status::Ok();
   }
 
+  // After a whole train or eval program the loss is already on its way to
+  // h_loss_ (PostLoss ends those programs); otherwise it is copied back.
   Status Loss(float* out) {
+    if (loss_posted_) {
+      if (Status s = HipOk(hipStreamSynchronize(stream_), "step"); !s) return s;
+      *out = *h_loss_;
+      return Status::Ok();
+    }
     if (Status s = HipOk(hipMemcpyAsync(h_loss_, arena_ + RefOffset(plan_.header.loss_ref),
                                         sizeof(float), hipMemcpyDeviceToHost, stream_),
                          "loss read");
@@ -2042,8 +2075,23 @@ class Engine {
   // it was.
   Status TrainStep(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
                    bool on_device, float* loss) {
-    if (Status s = Stage(input, input_bytes, labels, label_bytes, on_device); !s) return s;
-    if (Status s = SetStep(step_ + 1); !s) return s;
+    if (on_device) {
+      // One launch stages the device batch and the next step's scalars.
+      if (Status s = CheckStaged(input, input_bytes, labels, label_bytes, on_device); !s) return s;
+      const PlanHeader& h = plan_.header;
+      const bool lab = h.label_kind != 0 && labels && label_bytes;
+      const StepScalars sc = MakeStepScalars(plan_.header, step_ + 1);
+      if (Status s = StageStep(&sc, d_scalars_, input_bytes ? input : nullptr,
+                               arena_ + RefOffset(h.input_ref), input_bytes, lab ? labels : nullptr,
+                               lab ? arena_ + RefOffset(h.label_ref) : nullptr, lab ? label_bytes : 0,
+                               stream_);
+          !s)
+        return s;
+      step_ = step_ + 1;
+    } else {
+      if (Status s = Stage(input, input_bytes, labels, label_bytes, on_device); !s) return s;
+      if (Status s = SetStep(step_ + 1); !s) return s;
+    }
     if (Status s = Run(static_cast<int>(Program::kTrain)); !s) return s;
     float l = 0.0f;
     if (Status s = Loss(&l); !s) return s;
@@ -2190,6 +2238,7 @@ class Engine {
     return WriteCheckpoint(path, plan_.header.plan_hash, step_, host.data(), n);
   }
   Status LoadCheckpoint(const std::string& path) {
+    loss_posted_ = false;  // runs instructions outside Run()
     const uint64_t n = plan_.header.persistent_size;
     std::vector<uint8_t> host(n);
     uint64_t step = 0;
@@ -2310,6 +2359,7 @@ class Engine {
     const uint64_t space = ro ? plan_.header.rodata_size : plan_.header.arena_size;
     if (!RangeOk(off, bytes, space)) return Status::Fail(kUnitEngine, "probe out of bounds");
     uint8_t* dev = (ro ? rodata_ : arena_) + off;
+    if (write) loss_posted_ = false;
     if (Status s = HipOk(hipStreamSynchronize(stream_), "probe sync"); !s) return s;
     if (Status s = HipOk(write ? hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_)
                               : hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, stream_),
@@ -2336,6 +2386,7 @@ class Engine {
   // reference's injected reward closure, test/compiler/backend/tuner_test.cc:130-145).
   using RewardFn = double (*)(void*, uint64_t, uint64_t, int, int, uint64_t);
   Status Autotune(int budget, RewardFn inject = nullptr, void* inject_ctx = nullptr) {
+    loss_posted_ = false;  // runs instructions outside Run()
     const int program = static_cast<int>(Program::kTrain);
     const auto& prog = plan_.program[program];
     const uint64_t persist = plan_.header.persistent_size;
@@ -2446,6 +2497,7 @@ class Engine {
   // launch the graph makes, its time split over the run's instructions by
   // element count.
   Status Profile(int program, int reps, float* ms_out, size_t count) {
+    loss_posted_ = false;  // runs instructions outside Run()
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     const size_t n = plan_.program[program].size();
     if (count < n) return Status::Fail(kUnitEngine, "profile output too small");
@@ -2553,6 +2605,7 @@ class Engine {
   }
 
   Status TimeInstruction(int program, size_t idx, int reps, float* avg_ms) {
+    loss_posted_ = false;  // runs instructions outside Run()
     if (program < 0 || program > 2 || idx >= plan_.program[program].size())
       return Status::Fail(kUnitEngine, "instruction index out of range");
     if (Status s = EnsureWorkspace(program); !s) return s;
@@ -2787,16 +2840,11 @@ class Engine {
     argmax_cap_ = 0;
     if (h_count_) (void)LockedHostFree(h_count_);
     h_count_ = nullptr;
-    if (h_scalars_) (void)LockedHostFree(h_scalars_);
-    for (hipEvent_t& ev : scalar_ev_) {
-      if (ev) (void)hipEventDestroy(ev);
-      ev = nullptr;
-    }
     if (h_loss_) (void)LockedHostFree(h_loss_);
     if (stream_) (void)hipStreamDestroy(stream_);
     arena_ = rodata_ = nullptr;
     ws_ = nullptr;
-    d_scalars_ = h_scalars_ = nullptr;
+    d_scalars_ = nullptr;
     h_loss_ = nullptr;
     stream_ = nullptr;
   }
@@ -2833,9 +2881,7 @@ class Engine {
   Ranges observed_;
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   std::vector<uint8_t> tails_[3];         // per instruction: kAttnStore* (PlanCausalTails)
-  StepScalars* h_scalars_ = nullptr;  // two pinned slots (SetStep)
-  hipEvent_t scalar_ev_[2] = {nullptr, nullptr};
-  int scalar_slot_ = 0;
+  bool loss_posted_ = false;  // the last program run wrote its loss to h_loss_
   float* h_loss_ = nullptr;
   struct Segment {
     hipGraph_t graph = nullptr;

@@ -940,6 +940,66 @@ Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t 
   return Rope(dy, dx, B, S, H, d, base, -1, c, "RopeBwd");
 }
 
+// One launch before a step: the step's scalars (kernel arguments, so no
+// host buffer has to outlive the launch) and up to two device-resident
+// batch copies into the arena slots. Copies run in 4-byte words (every slot
+// holds f32 or i32 elements), 16-byte vectors where both ends allow.
+struct StageCopy {
+  const uint32_t* src;
+  uint32_t* dst;
+  size_t words;
+};
+
+__global__ __launch_bounds__(kBlock) void stage_step_kernel(StepScalars s, StepScalars* __restrict__ dst,
+                                                            StageCopy a, StageCopy b) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+  const size_t gid = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (dst && gid == 0) *dst = s;
+  const StageCopy cs[2] = {a, b};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const StageCopy& c = cs[k];
+    if (!c.words) continue;
+    const bool vec = aligned16(c.src) && aligned16(c.dst);
+    const size_t nv = vec ? c.words / 4 : 0;
+    const uint4* s4 = reinterpret_cast<const uint4*>(c.src);
+    uint4* d4 = reinterpret_cast<uint4*>(c.dst);
+    for (size_t i = gid; i < nv; i += stride) d4[i] = s4[i];
+    for (size_t i = nv * 4 + gid; i < c.words; i += stride) c.dst[i] = c.src[i];
+  }
+}
+
+Status StageStep(const StepScalars* s, StepScalars* dst, const void* in_src, void* in_dst,
+                 size_t in_bytes, const void* lab_src, void* lab_dst, size_t lab_bytes,
+                 hipStream_t stream) {
+  if (in_bytes % 4 != 0 || lab_bytes % 4 != 0)
+    return Status::Fail(kUnitEngine, "StageStep: slot sizes must be whole 4-byte elements");
+  const StageCopy a{static_cast<const uint32_t*>(in_src), static_cast<uint32_t*>(in_dst),
+                    in_src ? in_bytes / 4 : 0};
+  const StageCopy b{static_cast<const uint32_t*>(lab_src), static_cast<uint32_t*>(lab_dst),
+                    lab_src ? lab_bytes / 4 : 0};
+  if (!s && !a.words && !b.words) return Status::Ok();
+  const size_t work = std::max<size_t>(std::max(a.words, b.words) / 4, 1);
+  hipLaunchKernelGGL(stage_step_kernel, dim3(grid_for(work, kBlock, kGridCap)), dim3(kBlock), 0, stream,
+                     s ? *s : StepScalars{}, s ? dst : nullptr, a, b);
+  return LaunchStatus("StageStep");
+}
+
+// The loss scalar into host memory the device writes directly (a mapped
+// pinned allocation): the host reads it after the stream's synchronisation,
+// with no device-to-host copy launch.
+__global__ void post_loss_kernel(const float* __restrict__ src, float* dst) {
+  if (threadIdx.x == 0) {
+    *dst = *src;
+    __threadfence_system();
+  }
+}
+
+Status PostLoss(const float* src, float* host_dst, hipStream_t stream) {
+  hipLaunchKernelGGL(post_loss_kernel, dim3(1), dim3(64), 0, stream, src, host_dst);
+  return LaunchStatus("PostLoss");
+}
+
 StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step) {
   StepScalars s{};
   s.lr = EffectiveLr(h, step);

@@ -35,6 +35,14 @@ struct alignas(64) StepScalars {
   float pad[7];
 };
 StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step);
+// One launch that writes the step's scalars to `dst` (when s is set) and
+// copies up to two device buffers (the batch's input and labels) into the
+// arena; sizes are whole 4-byte elements.
+Status StageStep(const StepScalars* s, StepScalars* dst, const void* in_src, void* in_dst,
+                 size_t in_bytes, const void* lab_src, void* lab_dst, size_t lab_bytes,
+                 hipStream_t stream);
+// Copies the loss scalar into mapped pinned host memory from the device.
+Status PostLoss(const float* src, float* host_dst, hipStream_t stream);
 
 struct Ctx {
   hipStream_t stream = nullptr;
