@@ -755,6 +755,7 @@ class Engine {
     PlanDualRuns(program);
     PlanRowdotGroups(program);
     if (Status s = PlanColsumGroups(program); !s) return s;
+    PlanTileGroups(program);
     if (segs.empty()) return Status::Ok();
     const size_t bytes = segs.size() * sizeof(AdamWSegment);
     if (Status s = HipOk(LockedMalloc(&fused_segs_[program], bytes), "fused AdamW table"); !s) return s;
@@ -1462,7 +1463,7 @@ class Engine {
     if (d.batch != 1 || d.causal != Causal::kNone || d.accumulate || d.bias || d.b_int8 ||
         !d.a_kc || d.ldc != d.N || p0.splits != 1)
       return 0;
-    auto lora_cfg_ok = [&](int cfg) { return cfg == 2 || (cfg == 0 && d.b_kc); };
+    auto lora_cfg_ok = [&](int cfg) { return GemmLoraCfgOk(cfg, d.b_kc); };
     if (!lora_cfg_ok(p0.cfg) || (p0.n_split > 0 && !lora_cfg_ok(p0.tail_cfg))) return 0;
     // up-projection u = t B: M x N over K = r, t the down-projection's output
     const GemmDesc du = DescOf(g2);
@@ -1617,6 +1618,210 @@ class Engine {
     run.d = d;
     chains_[program].push_back(run);
     return run.count;
+  }
+
+  // Tile groups (kernels.h LaunchGemmGroup): 2..4 consecutive GEMM
+  // launches on one tile config (a plain GEMM, a GEMM with its fused AddEW,
+  // or a LoRA run's base GEMM with the up-projection in its epilogue) as
+  // one launch, e.g. a decoder layer's q/k/v projections or its gate and up
+  // projections. Each output keeps its own launch's bits. The launches run
+  // at once, so no member may write what another reads or writes; the
+  // rowdots a LoRA member launches first (its own, or its rowdot group's)
+  // move ahead of the earlier members' GEMMs, so they may not write what
+  // those read or write, nor read what those write. Ranges are the
+  // launches' own operand extents. A group is used only when the executed
+  // range holds its whole span; rowdot groups lie wholly inside a span.
+  struct TileUnit {
+    size_t first = 0, count = 1;  // instruction span
+    GemmDesc d;                   // the launch (a chain's fused form)
+    GemmPlan plan;
+    int pre = 0;                  // 1: its own rowdot first; 2: its rowdot group first
+    int chain = -1;               // chains_ index of a LoRA unit
+  };
+  struct TileGroup {
+    size_t first = 0, end = 0;
+    std::vector<TileUnit> units;
+  };
+
+  // What a tile-kernel launch of d (batch 1) reads and writes, as absolute
+  // device address ranges.
+  static void DescRanges(const GemmDesc& d, Ranges* rd, Ranges* wr) {
+    auto at = [](const void* p) { return reinterpret_cast<uint64_t>(p); };
+    auto span2 = [](int64_t rows, int64_t ld, int64_t cols) {
+      return static_cast<uint64_t>((rows - 1) * ld + cols) * sizeof(float);
+    };
+    rd->emplace_back(at(d.A), d.a_kc ? span2(d.M, d.lda, d.K) : span2(d.K, d.lda, d.M));
+    rd->emplace_back(at(d.B), d.b_kc ? span2(d.N, d.ldb, d.K) : span2(d.K, d.ldb, d.N));
+    if (d.bias) rd->emplace_back(at(d.bias), static_cast<uint64_t>(d.N) * sizeof(float));
+    const int64_t ldo = d.ldo ? d.ldo : d.N;
+    if (d.lora_t) {
+      rd->emplace_back(at(d.lora_t), span2(d.M, d.lora_ldt, d.lora_r));
+      rd->emplace_back(at(d.lora_b), span2(d.lora_r, d.lora_ldb, d.N));
+      wr->emplace_back(at(d.out), span2(d.M, ldo, d.N));
+      return;
+    }
+    if (d.out) {
+      rd->emplace_back(at(d.addend), span2(d.M, ldo, d.N));
+      wr->emplace_back(at(d.out), span2(d.M, ldo, d.N));
+    }
+    if (!d.out || d.write_c) {
+      if (d.accumulate) rd->emplace_back(at(d.C), span2(d.M, d.ldc, d.N));
+      wr->emplace_back(at(d.C), span2(d.M, d.ldc, d.N));
+    }
+  }
+
+  void PlanTileGroups(int program) {
+    tgroups_[program].clear();
+    const auto& prog = plan_.program[program];
+    tgroup_of_[program].assign(prog.size(), -1);
+    const auto& chains = chains_[program];
+    std::vector<int> chain_at(prog.size(), -1), chain_of(prog.size(), -1);
+    for (size_t c = 0; c < chains.size(); ++c) {
+      chain_at[chains[c].first] = static_cast<int>(c);
+      for (size_t k = chains[c].first; k < chains[c].first + chains[c].count; ++k)
+        chain_of[k] = static_cast<int>(c);
+    }
+    std::vector<uint8_t> cs_span(prog.size(), 0);
+    for (const ColsumGroup& g : cs_groups_[program])
+      for (size_t k = g.members.front(); k <= g.members.back(); ++k) cs_span[k] = 1;
+    auto marked = [&](size_t k) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), k);
+    };
+    auto overlap = [](const Ranges& a, const Ranges& b) {
+      for (const auto& x : a)
+        if (Overlaps(b, x.first, x.second)) return true;
+      return false;
+    };
+    // The launch unit starting at instruction i, if it is one a group takes.
+    auto unit_at = [&](size_t i, TileUnit* u) {
+      if (cs_span[i]) return false;
+      const int c = chain_at[i];
+      if (c >= 0) {
+        const ChainRun& r = chains[c];
+        if (r.kind != ChainKind::kDense && r.kind != ChainKind::kLoraBase) return false;
+        u->first = i;
+        u->count = r.count;
+        u->d = r.d;
+        u->plan = plans_[program][i];
+        u->chain = c;
+        u->pre = r.kind != ChainKind::kLoraBase ? 0 : r.rd_mode == 0 ? 1 : r.rd_mode == 1 ? 2 : 0;
+        for (size_t k = i; k < i + r.count; ++k)
+          if (cs_span[k]) return false;
+        return true;
+      }
+      if (chain_of[i] >= 0) return false;
+      const UpdateInstruction& g = prog[i];
+      if (!IsGemmOp(g.opcode) || duals_[program][i] >= 0) return false;
+      if (plans_[program][i].cfg == GemmSkinnyConfig()) return false;
+      u->first = i;
+      u->count = 1;
+      u->d = DescOf(g);
+      u->plan = plans_[program][i];
+      u->chain = -1;
+      u->pre = 0;
+      return true;
+    };
+    // The pre-launch (rowdot) ranges of unit u.
+    auto pre_ranges = [&](const TileUnit& u, Ranges* rd, Ranges* wr) {
+      if (u.pre == 1) DescRanges(DescOf(prog[u.first + 1]), rd, wr);
+      if (u.pre == 2)
+        for (size_t k : chains[u.chain].grp_rowdots) DescRanges(DescOf(prog[k]), rd, wr);
+    };
+    for (size_t i = 0; i < prog.size();) {
+      TileUnit u0;
+      if (!unit_at(i, &u0)) {
+        ++i;
+        continue;
+      }
+      std::vector<TileUnit> units{u0};
+      std::vector<Ranges> R(1), W(1), PR(1), PW(1);
+      DescRanges(u0.d, &R[0], &W[0]);
+      pre_ranges(u0, &PR[0], &PW[0]);
+      // A member marked for timing may only be the group's first instruction
+      // (the timed launch is then the whole group).
+      bool ok0 = true;
+      for (size_t k = i + 1; k < i + u0.count; ++k) ok0 = ok0 && !marked(k);
+      size_t next = i + u0.count;
+      while (ok0 && units.size() < static_cast<size_t>(kGemmGroupMax) && next < prog.size()) {
+        TileUnit u;
+        if (!unit_at(next, &u)) break;
+        bool bad = false;
+        for (size_t k = next; k < next + u.count; ++k) bad = bad || marked(k);
+        if (bad) break;
+        std::vector<GemmDesc> ds;
+        std::vector<GemmPlan> ps;
+        for (const TileUnit& x : units) {
+          ds.push_back(x.d);
+          ps.push_back(x.plan);
+        }
+        ds.push_back(u.d);
+        ps.push_back(u.plan);
+        if (!GemmGroupFits(ds.data(), ps.data(), static_cast<int>(ds.size()))) break;
+        Ranges r, w, pr, pw;
+        DescRanges(u.d, &r, &w);
+        pre_ranges(u, &pr, &pw);
+        for (size_t j = 0; j < units.size() && !bad; ++j)
+          bad = overlap(W[j], r) || overlap(W[j], w) || overlap(w, R[j]) ||
+                overlap(pw, R[j]) || overlap(pw, W[j]) || overlap(pr, W[j]);
+        if (bad) break;
+        units.push_back(u);
+        R.push_back(r);
+        W.push_back(w);
+        PR.push_back(pr);
+        PW.push_back(pw);
+        next += u.count;
+      }
+      // Rowdot groups wholly inside the span; trim members past it.
+      while (units.size() >= 2) {
+        const size_t end = units.back().first + units.back().count;
+        bool inside = true;
+        for (const TileUnit& x : units)
+          if (x.chain >= 0 && chains[x.chain].rd_mode != 0)
+            inside = inside && chains[x.chain].grp_first >= i && chains[x.chain].grp_end <= end;
+        if (inside) break;
+        units.pop_back();
+      }
+      if (units.size() < 2) {
+        i += u0.count;
+        continue;
+      }
+      TileGroup g;
+      g.first = i;
+      g.end = units.back().first + units.back().count;
+      g.units = units;
+      for (size_t k = g.first; k < g.end; ++k) tgroup_of_[program][k] = static_cast<int>(tgroups_[program].size());
+      tgroups_[program].push_back(g);
+      i = g.end;
+    }
+  }
+
+  int TileGroupAt(int program, size_t idx, size_t begin, size_t end) const {
+    if (idx >= tgroup_of_[program].size() || tgroup_of_[program][idx] < 0) return -1;
+    const int g = tgroup_of_[program][idx];
+    const TileGroup& grp = tgroups_[program][g];
+    return grp.first == idx && grp.first >= begin && grp.end <= end ? g : -1;
+  }
+
+  Status LaunchTileGroup(int program, int g, const Ctx& c) const {
+    const TileGroup& grp = tgroups_[program][g];
+    const auto& prog = plan_.program[program];
+    GemmDesc ds[kGemmGroupMax];
+    GemmPlan ps[kGemmGroupMax];
+    int n = 0;
+    for (const TileUnit& u : grp.units) {
+      if (u.pre == 1)
+        if (Status s = LaunchGemm(DescOf(prog[u.first + 1]), plans_[program][u.first + 1], c); !s) return s;
+      if (u.pre == 2) {
+        const auto& rows = chains_[program][u.chain].grp_rowdots;
+        GemmDesc rd[4];
+        for (size_t j = 0; j < rows.size(); ++j) rd[j] = DescOf(prog[rows[j]]);
+        if (Status s = LaunchSkinnyRowdotGroup(rd, static_cast<int>(rows.size()), c); !s) return s;
+      }
+      ds[n] = u.d;
+      ps[n] = u.plan;
+      ++n;
+    }
+    return LaunchGemmGroup(ds, ps, n, c);
   }
 
   // The chain instruction idx belongs to in the built program, or null.
@@ -1815,6 +2020,13 @@ class Engine {
     while (r < runs.size() && runs[r].first < begin) ++r;
     while (q < chains.size() && chains[q].first < begin) ++q;
     for (size_t i = begin; i < end;) {
+      if (const int tg = TileGroupAt(program, i, begin, end); tg >= 0) {
+        if (Status s = LaunchTileGroup(program, tg, c); !s) return s;
+        i = tgroups_[program][tg].end;
+        while (q < chains.size() && chains[q].first < i) ++q;
+        while (r < runs.size() && runs[r].first < i) ++r;
+        continue;
+      }
       if (q < chains.size() && chains[q].first == i && i + chains[q].count <= end) {
         if (Status s = LaunchChain(program, chains[q], c, begin, end); !s) return s;
         i += chains[q].count;
@@ -1931,12 +2143,14 @@ class Engine {
       if (end > begin)
         if (Status s = Capture(program, begin, end); !s) return s;
       if (k < marked_[program].size()) {
+        // A marked tile group's first instruction times the whole group.
+        const int tg = TileGroupAt(program, end, 0, n);
         Segment seg;
         seg.first = end;
-        seg.count = 1;
+        seg.count = tg >= 0 ? tgroups_[program][tg].end - end : 1;
         seg.mark = static_cast<long>(k);
         segs_[program].push_back(seg);
-        begin = end + 1;
+        begin = end + seg.count;
       }
     }
     built_[program] = true;
@@ -1970,7 +2184,8 @@ class Engine {
         continue;
       }
       (void)hipEventRecord(mark_ev_[program][2 * g.mark], stream_);
-      if (Status s = Dispatch(program, g.first, c); !s) return s;
+      const int tg = TileGroupAt(program, g.first, 0, plan_.program[program].size());
+      if (Status s = tg >= 0 ? LaunchTileGroup(program, tg, c) : Dispatch(program, g.first, c); !s) return s;
       (void)hipEventRecord(mark_ev_[program][2 * g.mark + 1], stream_);
     }
     if (PostsLoss(program)) {
@@ -2517,6 +2732,17 @@ class Engine {
       (void)hipEventRecord(ev[0], stream_);
       size_t fr = 0, fq = 0;
       for (size_t i = 0; i < n;) {
+        if (const int tg = use_graph_ ? TileGroupAt(program, i, 0, n) : -1; tg >= 0) {
+          if (Status s = LaunchTileGroup(program, tg, c); !s) {
+            result = s;
+            break;
+          }
+          i = tgroups_[program][tg].end;
+          while (fq < chains.size() && chains[fq].first < i) ++fq;
+          while (fr < runs.size() && runs[fr].first < i) ++fr;
+          (void)hipEventRecord(ev[i], stream_);
+          continue;
+        }
         if (fq < chains.size() && chains[fq].first == i) {
           const ChainRun& run = chains[fq++];
           if (run.kind == ChainKind::kScaleFold) {  // timed launch by launch
@@ -2562,6 +2788,17 @@ class Engine {
       fr = 0;
       fq = 0;
       for (size_t i = 0; i < n;) {
+        if (const int tg = use_graph_ ? TileGroupAt(program, i, 0, n) : -1; tg >= 0) {
+          // One launch: its time goes to the group's first instruction.
+          const size_t e = tgroups_[program][tg].end;
+          float ms = 0.0f;
+          (void)hipEventElapsedTime(&ms, ev[i], ev[e]);
+          acc[i] += ms;
+          i = e;
+          while (fq < chains.size() && chains[fq].first < i) ++fq;
+          while (fr < runs.size() && runs[fr].first < i) ++fr;
+          continue;
+        }
         if (fq < chains.size() && chains[fq].first == i) {
           const ChainRun& run = chains[fq++];
           if (run.kind == ChainKind::kScaleFold) {
@@ -2656,6 +2893,30 @@ class Engine {
   bool LaunchWork(int program, size_t idx, double* flops, double* bytes) const {
     const auto& prog = plan_.program[program];
     if (idx >= prog.size()) return false;
+    if (idx < tgroup_of_[program].size() && tgroup_of_[program][idx] >= 0) {
+      const TileGroup& g = tgroups_[program][tgroup_of_[program][idx]];
+      if (idx != g.first) return false;  // "in tile group": no launch of its own
+      // The members' launches (their rowdots included), summed.
+      double f = 0.0, b = 0.0;
+      for (const TileUnit& u : g.units) {
+        double uf = 0.0, ub = 0.0;
+        if (!UnitWork(program, u.first, &uf, &ub)) {
+          uf = GemmFlops(u.d);
+          ub = GemmOperandBytes(u.d);
+        }
+        f += uf;
+        b += ub;
+      }
+      *flops = f;
+      *bytes = b;
+      return true;
+    }
+    return UnitWork(program, idx, flops, bytes);
+  }
+
+  // A launch's work outside tile groups (LaunchWork).
+  bool UnitWork(int program, size_t idx, double* flops, double* bytes) const {
+    const auto& prog = plan_.program[program];
     if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
       const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
       if (idx != g.members.back()) {
@@ -2755,6 +3016,19 @@ class Engine {
                  : std::string();
     if (op == Op::kAttnFwd) return tf == 0 ? "P unused" : no_tail;
     if (op == Op::kAttnDP) return no_tail;
+    if (idx < tgroup_of_[program].size() && tgroup_of_[program][idx] >= 0) {
+      const TileGroup& g = tgroups_[program][tgroup_of_[program][idx]];
+      for (const TileUnit& u : g.units)
+        if (u.first == idx)
+          return idx == g.first ? UnitChoice(program, idx) + ", tile group of " +
+                                      std::to_string(g.units.size()) + " (launched first)"
+                                : std::string("in tile group");
+    }
+    return UnitChoice(program, idx);
+  }
+
+  // The launch choice of idx outside tile groups (GemmChoice).
+  std::string UnitChoice(int program, size_t idx) const {
     const ChainRun* run = ChainAt(program, idx);
     if (run && run->kind == ChainKind::kScaleFold) {
       if (idx == run->first) return "in the next GEMMs' loads";
@@ -2874,6 +3148,8 @@ class Engine {
   std::vector<FusedRun> fused_runs_[3];
   std::vector<ChainRun> chains_[3];
   std::vector<ColsumGroup> cs_groups_[3];  // PlanColsumGroups
+  std::vector<TileGroup> tgroups_[3];     // PlanTileGroups
+  std::vector<int> tgroup_of_[3];         // instruction -> its tile group, or -1
   std::vector<int> cs_group_of_[3];        // per instruction: its colsum group, or -1
   void* cs_priv_[3] = {nullptr, nullptr, nullptr};  // the groups' operand copies
   std::vector<Ranges> depends_[3];  // per instruction: DependRangesOf

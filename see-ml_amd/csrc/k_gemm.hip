@@ -196,6 +196,93 @@ bool GemmVecForm(const GemmDesc& d) {
          d.lda < (int64_t{1} << 23) && d.ldb < (int64_t{1} << 23);
 }
 
+// Validates a tile-kernel launch of d under plan (one column range, no
+// skinny kernels) and fills its kernel arguments, grid, config and load form.
+Status CheckEpilogue(const GemmDesc& d, const GemmPlan& plan) {
+  if (d.lora_t && (!d.out || d.addend || d.lora_r <= 0 || d.lora_r % 8 != 0 || d.lora_r > 16 || !d.lora_b ||
+                   !aligned16(d.lora_t) || d.lora_ldt % 4 != 0 || plan.splits != 1 ||
+                   !GemmLoraCfgOk(plan.cfg, d.b_kc) || !d.a_kc || d.b_int8 || d.batch != 1 ||
+                   d.causal != Causal::kNone || d.accumulate || d.bias || !GemmVecForm(d)))
+    return Status::Fail(kUnitEngine, "Gemm: unsupported LoRA epilogue");
+  if (d.out && !d.lora_t && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
+                d.accumulate || d.bias))
+    return Status::Fail(kUnitEngine,
+                        "Gemm: a fused AddEW needs batch 1, ldc == N and a plain epilogue "
+                        "(no accumulate, bias or causal mode)");
+  return Status::Ok();
+}
+
+Status PrepareKArgs(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx, GemmKArgs* out,
+                    dim3* grid, int* cfg_out, bool* vec_out) {
+  if (Status s = CheckEpilogue(d, plan); !s) return s;
+  if (d.b_int8 && !d.a_kc)
+    return Status::Fail(kUnitEngine, "Gemm: unsupported int8 operand layout");
+  if (!d.a_kc && d.b_kc)
+    return Status::Fail(kUnitEngine, "Gemm: unsupported operand layout (A row-major in m, B k-contiguous)");
+
+  // 16-byte vector loads need 16-byte alignment of every batch base and a
+  // contiguous extent that is a multiple of 4 (a float4 is then wholly in or
+  // out of range); per-lane offsets within a tile must fit 32 bits. Other
+  // GEMMs (int8 B, odd shapes) take the element-load form of the small tile.
+  const bool vec = GemmVecForm(d);
+  if (d.out_scaled && (!d.out || !vec))
+    return Status::Fail(kUnitEngine, "Gemm: a fused Scale + AddEW needs the 16-byte-load kernels");
+  if (d.out && !vec && d.ldo && d.ldo != d.N)
+    return Status::Fail(kUnitEngine, "Gemm: a column view's fused AddEW needs the 16-byte-load kernels");
+  if (d.out && !vec) return Status::Fail(kUnitEngine, "Gemm: a fused AddEW needs the 16-byte-load kernels");
+  const int cfg = vec ? plan.cfg : gemm::kCfgSmall;
+  const CfgInfo& c = kCfgs[cfg];
+  const int64_t tm = CeilDiv(d.M, c.mt_m), tn = CeilDiv(d.N, c.mt_n);
+  // The kernel decomposes its linear workgroup id in 32 bits.
+  if (tm * tn > 0x7FFFFFFF || d.batch > 65535 || plan.splits > 65535 ||
+      tm * tn * c.threads > 0xFFFFFFFF || tm * tn * plan.splits * d.batch > 0xFFFFFFFF)
+    return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
+
+  GemmKArgs& a = *out;
+  a = GemmKArgs{};
+  a.A = d.A;
+  a.B = d.B;
+  a.C = d.C;
+  a.ws = static_cast<float*>(ctx.ws);
+  a.M = d.M; a.N = d.N; a.K = d.K;
+  a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
+  a.heads = std::min(d.heads, d.batch);  // same (z / heads, z % heads) for z < batch; fits 32 bits
+  a.batch = d.batch;
+  a.a_sb = d.a_sb; a.a_sh = d.a_sh; a.b_sb = d.b_sb; a.b_sh = d.b_sh;
+  a.c_sb = d.c_sb; a.c_sh = d.c_sh;
+  a.alpha = d.alpha;
+  a.accumulate = d.accumulate ? 1 : 0;
+  a.bias = d.bias;
+  a.act = d.act;
+  a.causal = static_cast<int>(d.causal);
+  a.splits = plan.splits;
+  a.k_per_split = plan.splits > 1
+                      ? CeilDiv(CeilDiv(d.K, plan.splits), gemm::kSplitAlign) * gemm::kSplitAlign
+                      : d.K;
+  a.tiles_m = static_cast<int>(tm);
+  a.tiles_n = static_cast<int>(tn);
+  a.addend = d.addend;
+  a.out = d.out;
+  a.addend_first = d.addend_first ? 1 : 0;
+  a.write_c = d.write_c ? 1 : 0;
+  a.out_scale = d.out_scale;
+  a.out_scaled = d.out_scaled ? 1 : 0;
+  a.c_scaled = d.c_gets_scaled ? 1 : 0;
+  a.ldo = d.ldo ? d.ldo : d.N;
+  a.lora_t = d.lora_t;
+  a.lora_b = d.lora_b;
+  a.lora_ldt = d.lora_ldt;
+  a.lora_ldb = d.lora_ldb;
+  a.lora_r = d.lora_r;
+  a.lora_y_first = d.lora_y_first ? 1 : 0;
+
+  *grid = dim3(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
+               static_cast<unsigned>(d.batch));
+  *cfg_out = cfg;
+  *vec_out = vec;
+  return Status::Ok();
+}
+
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   if (d.M <= 0 || d.N <= 0 || d.batch <= 0 || d.heads <= 0)
     return Status::Fail(kUnitEngine, "Gemm: empty shape");
@@ -240,31 +327,9 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return Status::Fail(kUnitEngine, "Gemm: split-K needs an unbatched, non-causal GEMM");
   if (plan.splits > 1 && ctx.ws_bytes < plan.ws_bytes)
     return Status::Fail(kUnitEngine, "Gemm: workspace too small for split-K");
-  if (d.lora_t && (!d.out || d.addend || d.lora_r <= 0 || d.lora_r % 8 != 0 || d.lora_r > 16 || !d.lora_b ||
-                   !aligned16(d.lora_t) || d.lora_ldt % 4 != 0 || plan.splits != 1 ||
-                   (plan.cfg != 2 && !(plan.cfg == 0 && d.b_kc)) || !d.a_kc || d.b_int8 || d.batch != 1 ||
-                   d.causal != Causal::kNone || d.accumulate || d.bias || !GemmVecForm(d)))
-    return Status::Fail(kUnitEngine, "Gemm: unsupported LoRA epilogue");
-  if (d.out && !d.lora_t && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
-                d.accumulate || d.bias))
-    return Status::Fail(kUnitEngine,
-                        "Gemm: a fused AddEW needs batch 1, ldc == N and a plain epilogue "
-                        "(no accumulate, bias or causal mode)");
-  if (d.b_int8 && !d.a_kc)
-    return Status::Fail(kUnitEngine, "Gemm: unsupported int8 operand layout");
-  if (!d.a_kc && d.b_kc)
-    return Status::Fail(kUnitEngine, "Gemm: unsupported operand layout (A row-major in m, B k-contiguous)");
-
-  // 16-byte vector loads need 16-byte alignment of every batch base and a
-  // contiguous extent that is a multiple of 4 (a float4 is then wholly in or
-  // out of range); per-lane offsets within a tile must fit 32 bits. Other
-  // GEMMs (int8 B, odd shapes) take the element-load form of the small tile.
-  const bool vec = GemmVecForm(d);
-  if (d.out_scaled && (!d.out || !vec))
-    return Status::Fail(kUnitEngine, "Gemm: a fused Scale + AddEW needs the 16-byte-load kernels");
-  if (d.out && !vec && d.ldo && d.ldo != d.N)
-    return Status::Fail(kUnitEngine, "Gemm: a column view's fused AddEW needs the 16-byte-load kernels");
-  if (d.out && !vec) {
+  if (Status s = CheckEpilogue(d, plan); !s) return s;
+  const bool vec_form = GemmVecForm(d);
+  if (d.out && !d.lora_t && !vec_form && !d.out_scaled && !(d.ldo && d.ldo != d.N)) {
     // The element-load form has no fused epilogue: the GEMM stores C (always
     // safe: C's range is C's while the GEMM writes it), then the AddEW runs.
     GemmDesc plain = d;
@@ -274,53 +339,11 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return d.addend_first ? AddEW(d.addend, d.C, d.out, static_cast<size_t>(d.M * d.N), ctx)
                           : AddEW(d.C, d.addend, d.out, static_cast<size_t>(d.M * d.N), ctx);
   }
-  const int cfg = vec ? plan.cfg : gemm::kCfgSmall;
-  const CfgInfo& c = kCfgs[cfg];
-  const int64_t tm = CeilDiv(d.M, c.mt_m), tn = CeilDiv(d.N, c.mt_n);
-  // The kernel decomposes its linear workgroup id in 32 bits.
-  if (tm * tn > 0x7FFFFFFF || d.batch > 65535 || plan.splits > 65535 ||
-      tm * tn * c.threads > 0xFFFFFFFF || tm * tn * plan.splits * d.batch > 0xFFFFFFFF)
-    return Status::Fail(kUnitEngine, "Gemm: grid exceeds launch limits");
-
-  GemmKArgs a{};
-  a.A = d.A;
-  a.B = d.B;
-  a.C = d.C;
-  a.ws = static_cast<float*>(ctx.ws);
-  a.M = d.M; a.N = d.N; a.K = d.K;
-  a.lda = d.lda; a.ldb = d.ldb; a.ldc = d.ldc;
-  a.heads = std::min(d.heads, d.batch);  // same (z / heads, z % heads) for z < batch; fits 32 bits
-  a.batch = d.batch;
-  a.a_sb = d.a_sb; a.a_sh = d.a_sh; a.b_sb = d.b_sb; a.b_sh = d.b_sh;
-  a.c_sb = d.c_sb; a.c_sh = d.c_sh;
-  a.alpha = d.alpha;
-  a.accumulate = d.accumulate ? 1 : 0;
-  a.bias = d.bias;
-  a.act = d.act;
-  a.causal = static_cast<int>(d.causal);
-  a.splits = plan.splits;
-  a.k_per_split = plan.splits > 1
-                      ? CeilDiv(CeilDiv(d.K, plan.splits), gemm::kSplitAlign) * gemm::kSplitAlign
-                      : d.K;
-  a.tiles_m = static_cast<int>(tm);
-  a.tiles_n = static_cast<int>(tn);
-  a.addend = d.addend;
-  a.out = d.out;
-  a.addend_first = d.addend_first ? 1 : 0;
-  a.write_c = d.write_c ? 1 : 0;
-  a.out_scale = d.out_scale;
-  a.out_scaled = d.out_scaled ? 1 : 0;
-  a.c_scaled = d.c_gets_scaled ? 1 : 0;
-  a.ldo = d.ldo ? d.ldo : d.N;
-  a.lora_t = d.lora_t;
-  a.lora_b = d.lora_b;
-  a.lora_ldt = d.lora_ldt;
-  a.lora_ldb = d.lora_ldb;
-  a.lora_r = d.lora_r;
-  a.lora_y_first = d.lora_y_first ? 1 : 0;
-
-  const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
-                  static_cast<unsigned>(d.batch));
+  GemmKArgs a;
+  dim3 grid;
+  int cfg = 0;
+  bool vec = false;
+  if (Status s = PrepareKArgs(d, plan, ctx, &a, &grid, &cfg, &vec); !s) return s;
   if (d.b_int8) {
     gemm::LaunchQ8(cfg, d.b_kc, grid, ctx.stream, a);
   } else if (d.a_kc && !d.b_kc) {
@@ -337,6 +360,45 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return LaunchStatus("Gemm(split-K reduce)");
   }
   return Status::Ok();
+}
+
+bool GemmLoraCfgOk(int cfg, bool b_kc) {
+  return cfg == 2 || cfg == 4 || cfg == 5 || cfg == 8 || cfg == 9 || (cfg == 0 && b_kc);
+}
+
+bool GemmGroupFits(const GemmDesc* ds, const GemmPlan* ps, int n) {
+  if (n < 2 || n > gemm::kMaxGroup) return false;
+  for (int j = 0; j < n; ++j) {
+    const GemmDesc& d = ds[j];
+    const GemmPlan& p = ps[j];
+    if (p.cfg != ps[0].cfg || !gemm::GroupCfg(p.cfg) || p.splits != 1 || p.n_split != 0 ||
+        d.batch != 1 || d.causal != Causal::kNone || d.b_int8 || !d.a_kc || d.b_kc != ds[0].b_kc ||
+        d.scale_stream || !GemmVecForm(d) || !CheckEpilogue(d, p))
+      return false;
+  }
+  return true;
+}
+
+Status LaunchGemmGroup(const GemmDesc* ds, const GemmPlan* ps, int n, const Ctx& ctx) {
+  if (!GemmGroupFits(ds, ps, n)) return Status::Fail(kUnitEngine, "Gemm group: members do not fit one launch");
+  gemm::GemmGroupArgs g{};
+  uint64_t total = 0;
+  for (int j = 0; j < n; ++j) {
+    dim3 grid;
+    int cfg = 0;
+    bool vec = false;
+    if (Status s = PrepareKArgs(ds[j], ps[j], ctx, &g.m[j], &grid, &cfg, &vec); !s) return s;
+    total += static_cast<uint64_t>(grid.x);
+    if (total > 0x7FFFFFFF / static_cast<uint64_t>(kCfgs[cfg].threads))
+      return Status::Fail(kUnitEngine, "Gemm group: grid exceeds launch limits");
+    g.wg_end[j] = static_cast<uint32_t>(total);
+  }
+  g.count = static_cast<uint32_t>(n);
+  const dim3 grid(static_cast<unsigned>(total));
+  const bool ok = ds[0].b_kc ? gemm::LaunchGroupNT(ps[0].cfg, grid, ctx.stream, g)
+                             : gemm::LaunchGroupNN(ps[0].cfg, grid, ctx.stream, g);
+  if (!ok) return Status::Fail(kUnitEngine, "Gemm group: no group kernel for this tile config");
+  return LaunchStatus("Gemm group");
 }
 
 GemmDesc GemmNNDesc(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K) {

@@ -265,9 +265,13 @@ __device__ __forceinline__ uint32_t XcdLogical(uint32_t lin, uint32_t total) {
   return x < rem ? x * (per + 1) + idx : rem * (per + 1) + (x - rem) * per + idx;
 }
 
+// One workgroup's work item: logical id L (after the XCD remap) decomposes
+// into (tile, split slice, batch z) over `nslices` slices. FUSED and LORA
+// compile those epilogues in; each applies to a work item whose arguments
+// ask for it (p.out / p.lora_t set), any other takes the plain write-back.
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED, bool LORA = false>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
+          bool VEC, bool SCHED, bool FUSED, bool LORA>
+__device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32_t nslices) {
   using BT = typename std::conditional<B_I8, int8_t, float>::type;
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = MT_M / WAVES_M, WN = MT_N / WAVES_N;
@@ -283,12 +287,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
 
   // Logical work item of this workgroup: (tile, split slice, batch z).
   const uint32_t tiles = static_cast<uint32_t>(p.tiles_m) * static_cast<uint32_t>(p.tiles_n);
-  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  uint32_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
   const uint32_t t_id = L % tiles;
   L /= tiles;
-  const int slice = static_cast<int>(L % gridDim.y);
-  const uint32_t z = L / gridDim.y;
+  const int slice = static_cast<int>(L % nslices);
+  const uint32_t z = L / nslices;
   const uint32_t grp = t_id / (kGroupRows * static_cast<uint32_t>(p.tiles_n));
   const uint32_t first = grp * kGroupRows;
   const uint32_t gm = std::min<uint32_t>(kGroupRows, static_cast<uint32_t>(p.tiles_m) - first);
@@ -454,7 +456,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   // and columns from it, so no per-element offsets stay live. The addends
   // are loaded first, all in flight together, then the sums are stored.
   // The value summed is the one the plain epilogue would store in C.
-  if constexpr (LORA) {
+  if constexpr (LORA) if (p.lora_t) {
     // u = T B' block by block (k = 8g + 4h + j for MFMA j of group g, as in
     // the k loop above). Up to rank 16 every fragment of the wavefront's
     // blocks is loaded at once, before any MFMA, so their latencies overlap;
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
     return;
   }
   if constexpr (FUSED) {
-    if (p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
+    if (p.out && p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
       const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
       const float* ya = p.addend + lm * p.ldo + ln;
       float* oa = p.out + lm * p.ldo + ln;
@@ -549,9 +551,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
   // workgroups share a CU, the other's k loop hides this one's write-back,
   // and the back-to-back stores measured ~1% slower on it in the C4 step.
   constexpr bool kPlainFast =
-      VEC && !FUSED && !(MT_M == 128 && MT_N == 128 && KT == 32 && WAVES_M == 2 && WAVES_N == 2);
+      VEC && !(MT_M == 128 && MT_N == 128 && KT == 32 && WAVES_M == 2 && WAVES_N == 2);
   if constexpr (kPlainFast) {
-    if (p.splits == 1 && !p.accumulate && !p.bias && p.act == 0 &&
+    if (!p.out && p.splits == 1 && !p.accumulate && !p.bias && p.act == 0 &&
         p.causal != static_cast<int>(Causal::kLowerOut) && m0 + MT_M <= p.M &&
         n0 + MT_N <= p.N) {
       float* ca = C + (m0 + wm0 + 4 * h) * p.ldc + n0 + wn0 + r;
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
         if (p.bias) val = val + p.bias[n];
         val = dev_act(p.act, val);
         if (p.causal == static_cast<int>(Causal::kLowerOut) && n > m) val = 0.0f;
-        if constexpr (FUSED) {  // a partial tile
+        if (FUSED && p.out) {  // a partial tile
           const float sv = p.out_scaled ? p.out_scale * val : val;
           if (p.write_c) C[m * p.ldc + n] = p.c_scaled ? sv : val;
           const float y = p.addend[m * p.ldo + n];
@@ -596,6 +598,38 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmK
           C[m * p.ldc + n] = val;
         }
       }
+}
+
+template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
+          bool VEC, bool SCHED, bool FUSED, bool LORA = false>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
+  const uint32_t tiles = static_cast<uint32_t>(p.tiles_m) * static_cast<uint32_t>(p.tiles_n);
+  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
+  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, B_I8, VEC, SCHED, FUSED, LORA>(p, L, gridDim.y);
+}
+
+// A GEMM group: up to kMaxGroup independent GEMMs of one tile config and
+// operand layout in one launch (each unsplit and unbatched), member j
+// owning logical work items [wg_end[j-1], wg_end[j]). The XCD remap runs
+// over the whole launch, so each XCD walks a contiguous run of the members'
+// tiles. Every output is computed by the same code, k order and epilogue as
+// in the member's own launch: the same bits.
+constexpr int kMaxGroup = kGemmGroupMax;
+struct GemmGroupArgs {
+  GemmKArgs m[kMaxGroup];
+  uint32_t wg_end[kMaxGroup];
+  uint32_t count;
+};
+
+template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool LORA>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_group_kernel(GemmGroupArgs g) {
+  const uint32_t total = g.wg_end[g.count - 1];
+  uint32_t L = XcdLogical(blockIdx.x, total);
+  uint32_t j = 0;
+  while (j + 1 < g.count && L >= g.wg_end[j]) ++j;
+  if (j > 0) L -= g.wg_end[j - 1];
+  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, false, true, true, true, LORA>(g.m[j], L, 1);
 }
 
 // Launches config `cfg` of one operand-layout variant. The element-load
@@ -632,21 +666,55 @@ void LaunchVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
 }
 
 // The LoRA-epilogue instantiations (GemmKArgs::lora_t): the tiles the base
-// projection GEMMs run on. Returns false for any other config.
+// projection GEMMs run on (the large tiles of the d_model >= 2048 decoders
+// and the 128x64 / 64x64 / 64x128 tiles of the small ones). Returns false
+// for any other config.
 template <bool A_KC, bool B_KC>
 bool LaunchLoraVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+#define SEEML_LORA_CASE(I, MM, NN, KK, WM_, WN_)                                                       \
+  case I:                                                                                            \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, false, true, true, true, true>), \
+                       grid, dim3(kCfgs[I].threads), 0, s, a);                                       \
+    return true;
   switch (cfg) {
-    case 0:
-      hipLaunchKernelGGL((gemm_mfma_kernel<128, 128, 32, 2, 2, A_KC, B_KC, false, true, true, true, true>),
-                         grid, dim3(kCfgs[0].threads), 0, s, a);
-      return true;
-    case 2:
-      hipLaunchKernelGGL((gemm_mfma_kernel<256, 128, 32, 4, 2, A_KC, B_KC, false, true, true, true, true>),
-                         grid, dim3(kCfgs[2].threads), 0, s, a);
-      return true;
+    SEEML_LORA_CASE(0, 128, 128, 32, 2, 2)
+    SEEML_LORA_CASE(2, 256, 128, 32, 4, 2)
+    SEEML_LORA_CASE(4, 128, 64, 32, 2, 2)
+    SEEML_LORA_CASE(5, 64, 64, 32, 2, 2)
+    SEEML_LORA_CASE(8, 64, 128, 32, 2, 2)
+    SEEML_LORA_CASE(9, 128, 64, 32, 4, 1)
     default:
       return false;
   }
+#undef SEEML_LORA_CASE
+}
+
+// Tile configs with a group kernel (gemm_group_kernel): the configs the
+// heuristic and the autotuner pick for the decoders' projection GEMMs.
+inline constexpr bool GroupCfg(int cfg) { return cfg <= 5 || cfg == 8 || cfg == 9; }
+
+// LORA: some member takes the LoRA epilogue (its registers cost the plain
+// members occupancy, so groups without one use the kernel without it).
+template <bool B_KC, bool LORA>
+bool LaunchGroupVariant(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g) {
+#define SEEML_GROUP_CASE(I, MM, NN, KK, WM_, WN_)                                                 \
+  case I:                                                                                       \
+    hipLaunchKernelGGL((gemm_group_kernel<MM, NN, KK, WM_, WN_, true, B_KC, LORA>), grid,         \
+                       dim3(kCfgs[I].threads), 0, s, g);                                         \
+    return true;
+  switch (cfg) {
+    SEEML_GROUP_CASE(0, 128, 128, 32, 2, 2)
+    SEEML_GROUP_CASE(2, 256, 128, 32, 4, 2)
+    SEEML_GROUP_CASE(4, 128, 64, 32, 2, 2)
+    SEEML_GROUP_CASE(5, 64, 64, 32, 2, 2)
+    SEEML_GROUP_CASE(8, 64, 128, 32, 2, 2)
+    SEEML_GROUP_CASE(1, 128, 128, 32, 4, 2)
+    SEEML_GROUP_CASE(3, 128, 256, 32, 2, 4)
+    SEEML_GROUP_CASE(9, 128, 64, 32, 4, 1)
+    default:
+      return false;
+  }
+#undef SEEML_GROUP_CASE
 }
 
 // Per-layout entry points, one instantiation unit each (built in parallel).
@@ -654,6 +722,10 @@ void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
 void LaunchNT(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
 void LaunchTN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
 void LaunchQ8(int cfg, bool b_kc, dim3 grid, hipStream_t s, const GemmKArgs& a);
+// Group launches (A k-contiguous, B row- or k-contiguous); false for a
+// config without a group kernel.
+bool LaunchGroupNN(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g);
+bool LaunchGroupNT(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g);
 
 }  // namespace gemm
 }  // namespace seeml_hip

@@ -5,7 +5,7 @@ namespace seeml_hip {
 namespace gemm {
 
 void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a) {
-  if (a.lora_t) {  // the host admits only vec, one slice and configs 0 / 2
+  if (a.lora_t) {  // the host admits only vec, one slice and the LoRA configs
     (void)LaunchLoraVariant<true, false>(cfg, grid, s, a);
     return;
   }

@@ -100,8 +100,8 @@ struct GemmDesc {
   // u = T B' over lora_r (8 or 16; T [M, lora_r] with row stride
   // lora_ldt, 16-byte rows; B' [lora_r, N] with row stride lora_ldb), in
   // the k order of a tile GEMM of u, so u has that GEMM's bits. lora_y_first:
-  // c is the AddEW's first operand. Tile configs 0 and 2, one slice, A
-  // k-contiguous.
+  // c is the AddEW's first operand. Tile configs of GemmLoraCfgOk, one
+  // slice, A k-contiguous.
   const float* lora_t = nullptr;
   const float* lora_b = nullptr;
   int64_t lora_ldt = 0, lora_ldb = 0;
@@ -148,6 +148,18 @@ GemmPlan PlanGemmSplit(const GemmDesc& d, int cfg, int tail_cfg, int64_t n_split
 int GemmConfigCount();
 const char* GemmConfigName(int cfg);
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);
+// Tile configs whose kernels take the LoRA epilogue (GemmDesc::lora_t).
+bool GemmLoraCfgOk(int cfg, bool b_kc);
+// GEMM groups: 2..4 GEMMs launched as one kernel, each output with the bits
+// of its own launch. Fits: one tile config with a group kernel for all,
+// each unsplit (one slice, no column split), unbatched, non-causal, in the
+// 16-byte-load form with A k-contiguous and one B layout; any epilogue a
+// single launch of that config takes (plain, fused AddEW, LoRA). The
+// caller proves the members independent: no member reads or writes what
+// another writes.
+inline constexpr int kGemmGroupMax = 4;  // members of one group launch
+bool GemmGroupFits(const GemmDesc* ds, const GemmPlan* ps, int n);
+Status LaunchGemmGroup(const GemmDesc* ds, const GemmPlan* ps, int n, const Ctx& ctx);
 // True when a tile-kernel launch of d takes the 16-byte-load form, whose
 // epilogue can apply a fused Scale + AddEW (GemmDesc::out_scaled).
 bool GemmVecForm(const GemmDesc& d);

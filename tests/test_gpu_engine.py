@@ -593,13 +593,16 @@ def test_colsum_groups_refuse_a_hazard_between_members(torch_gpu, case):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), case
 
 
-def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
-    """With the projection GEMMs on the 256x128 tile and the rank-16
-    up-projections on a tile plan (both forced here; the C4 autotuner picks
-    them), each base GEMM, its LoRA down-projection, up-projection, Scale and
-    residual AddEW run as one LoRA run: the down-projection first, then the
-    base GEMM with u, the Scale and the sum in its epilogue. The fused graph
-    equals the eager engine bit for bit and the oracle to tolerance."""
+@pytest.mark.parametrize("cfg", [2, 4, 5, 8, 9])
+def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc, cfg):
+    """With the projection GEMMs on a LoRA-epilogue tile (256x128 as the C4
+    autotuner picks; 128x64, 64x64, 64x128 and 128x64/w4x1 as C3's does) and
+    the rank-16 up-projections on a tile plan (both forced here), each base
+    GEMM, its LoRA down-projection, up-projection, Scale and residual AddEW
+    run as one LoRA run: the down-projection first, then the base GEMM with
+    u, the Scale and the sum in its epilogue; a layer's q/k/v runs launch as
+    one tile group. The fused graph equals the eager engine bit for bit and
+    the oracle to tolerance."""
     from seeml_amd import PROGRAM_TRAIN
     w, p = compile_workload("c4m")
     ops = {planner.OP[k] for k in ("GemmNN", "GemmNT")}
@@ -613,7 +616,7 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
     for use_graph in (True, False):
         e = engine(p, use_graph=use_graph)
         for i in base:
-            assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 2, 1) == 0
+            assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, cfg, 1) == 0
         for i in up:
             assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 5, 1) == 0
         losses = []
@@ -622,8 +625,14 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc):
             losses.append(e.train_step(x, y))
         if use_graph:
             ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
-            heads = [c for c in ch if "+LoRA" in c]
+            # a LoRA run's base GEMM reports "+LoRA", or "in tile group" when
+            # an earlier run's group launch computes it
+            heads = [c for i, c in enumerate(ch)
+                     if "+LoRA" in c or (c == "in tile group" and ch[i + 1].startswith("in LoRA run"))]
             assert len(heads) >= 4, ch
+            # the q/k/v projections of a layer run as one tile-group launch
+            tg = [i for i, c in enumerate(ch) if c.endswith("tile group of 3 (launched first)")]
+            assert tg and all("+LoRA" in ch[i] for i in tg), ch
             assert sum(c.startswith("in LoRA run") for c in ch) == len(heads)
             # the q/k/v down-projections over one layer input run as one pass
             groups = [c for c in ch if c.startswith("in LoRA run: rowdot group of ")]
