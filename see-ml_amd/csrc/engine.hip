@@ -2019,7 +2019,22 @@ class Engine {
     size_t r = 0, q = 0;
     while (r < runs.size() && runs[r].first < begin) ++r;
     while (q < chains.size() && chains[q].first < begin) ++q;
+    const auto& marks = marked_[program];
     for (size_t i = begin; i < end;) {
+      // A marked launch (its tile group, if it heads one) between two wall
+      // clock stamps, captured as nodes of the program's one graph.
+      if (const auto mk = std::lower_bound(marks.begin(), marks.end(), i);
+          mk != marks.end() && *mk == i && mark_stamps_[program]) {
+        const size_t k = static_cast<size_t>(mk - marks.begin());
+        const int tg = TileGroupAt(program, i, begin, end);
+        if (Status s = WallStamp(mark_stamps_[program] + 2 * k, stream_); !s) return s;
+        if (Status s = tg >= 0 ? LaunchTileGroup(program, tg, c) : Dispatch(program, i, c); !s) return s;
+        if (Status s = WallStamp(mark_stamps_[program] + 2 * k + 1, stream_); !s) return s;
+        i = tg >= 0 ? tgroups_[program][tg].end : i + 1;
+        while (q < chains.size() && chains[q].first < i) ++q;
+        while (r < runs.size() && runs[r].first < i) ++r;
+        continue;
+      }
       if (const int tg = TileGroupAt(program, i, begin, end); tg >= 0) {
         if (Status s = LaunchTileGroup(program, tg, c); !s) return s;
         i = tgroups_[program][tg].end;
@@ -2071,7 +2086,26 @@ class Engine {
     if (Status s = HipOk(hipStreamSynchronize(stream_), "mark sync"); !s) return s;
     for (hipEvent_t e : mark_ev_[program]) (void)hipEventDestroy(e);
     mark_ev_[program].clear();
+    if (mark_stamps_[program]) (void)LockedFree(mark_stamps_[program]);
+    mark_stamps_[program] = nullptr;
     marked_[program] = v;
+    if (!v.empty()) {
+      if (wall_khz_ == 0)
+        (void)hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device_);
+      if (Status s = HipOk(LockedMalloc(&mark_stamps_[program], 2 * v.size() * sizeof(uint64_t)),
+                           "timing stamps");
+          !s)
+        return s;
+      if (h_stamps_cap_ < 2 * v.size()) {
+        if (h_stamps_) (void)LockedHostFree(h_stamps_);
+        h_stamps_ = nullptr;
+        h_stamps_cap_ = 0;
+        if (Status s = HipOk(LockedHostMalloc(&h_stamps_, 2 * v.size() * sizeof(uint64_t)), "timing stamps");
+            !s)
+          return s;
+        h_stamps_cap_ = 2 * v.size();
+      }
+    }
     for (size_t j = 0; j < 2 * v.size(); ++j) {
       hipEvent_t e = nullptr;
       if (Status s = HipOk(hipEventCreate(&e), "timing event"); !s) return s;
@@ -2085,6 +2119,18 @@ class Engine {
   Status MarkedTimes(int program, float* ms, size_t n) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     if (n < marked_[program].size()) return Status::Fail(kUnitEngine, "timing output too small");
+    if (stamped_[program] && use_graph_) {
+      const size_t m = marked_[program].size();
+      if (Status s = HipOk(hipMemcpyAsync(h_stamps_, mark_stamps_[program], 2 * m * sizeof(uint64_t),
+                                          hipMemcpyDeviceToHost, stream_),
+                           "timing read");
+          !s)
+        return s;
+      if (Status s = HipOk(hipStreamSynchronize(stream_), "timing read"); !s) return s;
+      for (size_t k = 0; k < m; ++k)
+        ms[k] = static_cast<float>(static_cast<double>(h_stamps_[2 * k + 1] - h_stamps_[2 * k]) / wall_khz_);
+      return Status::Ok();
+    }
     for (size_t k = 0; k < marked_[program].size(); ++k) {
       float t = 0.0f;
       if (Status s = HipOk(hipEventElapsedTime(&t, mark_ev_[program][2 * k],
@@ -2134,9 +2180,19 @@ class Engine {
     if (Status s = PlanFusion(program); !s) return s;
     // the colsum groups' partials can need more workspace than any launch alone
     if (Status s = EnsureWorkspace(program); !s) return s;
-    // One graph for the whole program; with marked instructions, one graph
-    // per unmarked stretch and each marked launch between them.
+    // One graph for the whole program, each marked launch between two wall
+    // clock stamp nodes (timing events do not record from inside a graph
+    // on this runtime). Without the stamp buffer or clock rate: one graph
+    // per unmarked stretch and each marked launch between them, timed by
+    // events.
     const size_t n = plan_.program[program].size();
+    stamped_[program] = false;
+    if (!marked_[program].empty() && mark_stamps_[program] && wall_khz_ > 0) {
+      if (Status s = Capture(program, 0, n); !s) return s;
+      stamped_[program] = true;
+      built_[program] = true;
+      return Status::Ok();
+    }
     size_t begin = 0;
     for (size_t k = 0; k <= marked_[program].size(); ++k) {
       const size_t end = k < marked_[program].size() ? marked_[program][k] : n;
@@ -2363,11 +2419,6 @@ class Engine {
   Status EnsureArgmaxBuffers(uint64_t rows) {
     const size_t need = ArgmaxPartials(rows);
     if (need <= argmax_cap_ && d_argmax_) return Status::Ok();
-    for (int p = 0; p < 3; ++p) {
-      for (hipEvent_t ev : mark_ev_[p]) (void)hipEventDestroy(ev);
-      mark_ev_[p].clear();
-      marked_[p].clear();
-    }
     if (d_argmax_) (void)LockedFree(d_argmax_);
     d_argmax_ = nullptr;
     argmax_cap_ = 0;
@@ -3101,6 +3152,11 @@ class Engine {
     if (ws_) (void)LockedFree(ws_);
     if (d_scalars_) (void)LockedFree(d_scalars_);
     for (int p = 0; p < 3; ++p) {
+      for (hipEvent_t ev : mark_ev_[p]) (void)hipEventDestroy(ev);
+      mark_ev_[p].clear();
+      marked_[p].clear();
+      if (mark_stamps_[p]) (void)LockedFree(mark_stamps_[p]);
+      mark_stamps_[p] = nullptr;
       if (fused_segs_[p]) (void)LockedFree(fused_segs_[p]);
       fused_segs_[p] = nullptr;
       fused_runs_[p].clear();
@@ -3115,6 +3171,9 @@ class Engine {
     if (h_count_) (void)LockedHostFree(h_count_);
     h_count_ = nullptr;
     if (h_loss_) (void)LockedHostFree(h_loss_);
+    if (h_stamps_) (void)LockedHostFree(h_stamps_);
+    h_stamps_ = nullptr;
+    h_stamps_cap_ = 0;
     if (stream_) (void)hipStreamDestroy(stream_);
     arena_ = rodata_ = nullptr;
     ws_ = nullptr;
@@ -3166,6 +3225,11 @@ class Engine {
     long mark = -1;  // >= 0: a marked launch, run eagerly between segments
   };
   std::vector<Segment> segs_[3];
+  uint64_t* mark_stamps_[3] = {nullptr, nullptr, nullptr};  // 2 wall-clock stamps per marked launch
+  uint64_t* h_stamps_ = nullptr;                            // pinned, for reading them back
+  size_t h_stamps_cap_ = 0;
+  bool stamped_[3] = {false, false, false};  // the built graph times its marks by stamps
+  int wall_khz_ = 0;                         // the device wall clock's rate
   bool built_[3] = {false, false, false};
   bool use_graph_ = true;
   uint64_t step_ = 0;

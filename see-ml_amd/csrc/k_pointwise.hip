@@ -1000,6 +1000,17 @@ Status PostLoss(const float* src, float* host_dst, hipStream_t stream) {
   return LaunchStatus("PostLoss");
 }
 
+// The device's constant-rate wall clock, written by one lane: a graph node
+// before and after a launch brackets its time on the GPU's own clock.
+__global__ void wall_stamp_kernel(uint64_t* dst) {
+  if (threadIdx.x == 0) *dst = wall_clock64();
+}
+
+Status WallStamp(uint64_t* dst, hipStream_t stream) {
+  hipLaunchKernelGGL(wall_stamp_kernel, dim3(1), dim3(64), 0, stream, dst);
+  return LaunchStatus("WallStamp");
+}
+
 StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step) {
   StepScalars s{};
   s.lr = EffectiveLr(h, step);

@@ -41,6 +41,8 @@ StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step);
 Status StageStep(const StepScalars* s, StepScalars* dst, const void* in_src, void* in_dst,
                  size_t in_bytes, const void* lab_src, void* lab_dst, size_t lab_bytes,
                  hipStream_t stream);
+// Writes the device wall clock (wall_clock64) to dst.
+Status WallStamp(uint64_t* dst, hipStream_t stream);
 // Copies the loss scalar into mapped pinned host memory from the device.
 Status PostLoss(const float* src, float* host_dst, hipStream_t stream);
 

@@ -163,6 +163,37 @@ def test_train_and_evaluate_token_records_c3s(torch_dev):
                  lambda: fo.Dataset.from_tokens(toks, records, seq), steps=5, shuffle_seed=2)
 
 
+def test_timed_launches_survive_an_evaluation(torch_dev):
+    """Launches marked for timing stay marked, and timed, across an
+    evaluation that allocates the accuracy buffers: the train graph keeps
+    its stamp nodes and its results are those of an unmarked engine."""
+    w = configs.make("c1")
+    plan = planner.compile_update(w.model, w.cfg)
+    gemms = [i for i, ins in enumerate(plan.train)
+             if planner.OP_NAME[ins["opcode"]] in ("GemmNN", "GemmNT")]
+    rng = np.random.default_rng(5)
+    n = 96
+    X = rng.standard_normal((n, 256)).astype(f32)
+    y = rng.integers(0, 256, n).astype(np.int32).tobytes()
+    runs = []
+    for mark in (False, True):
+        e = DeviceUpdateEngine(plan.blob)
+        if mark:
+            e.mark_timed(0, gemms)
+        x0, y0 = configs.batch(w, 0)
+        losses = [e.train_step(x0, y0)]
+        m = e.evaluate_metrics(feeder.Dataset.from_memory(X, y, n, 256, 1))
+        x1, y1 = configs.batch(w, 1)
+        losses.append(e.train_step(x1, y1))
+        if mark:
+            t = e.marked_times(0)
+            assert t.shape == (len(gemms),) and np.all(t > 0) and np.all(t < 100.0)
+        runs.append((np.array(losses, f32), m["loss"], m["accuracy"]))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert runs[0][1:] == runs[1][1:]
+
+
 def test_train_rejects_mismatched_dataset(torch_dev):
     w = configs.make("c1")
     plan = planner.compile_update(w.model, w.cfg)
