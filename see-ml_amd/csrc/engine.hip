@@ -352,11 +352,12 @@ class Engine {
   }
 
   // True when the value instruction k of `program` leaves in the arena bytes
-  // [off, off + bytes) is observed by nothing: it is transient, and walking
-  // the program from k + 1 every byte of it is overwritten before any later
-  // instruction depends on it (or the program ends).
+  // [off, off + bytes) is observed by nothing: walking the program from
+  // k + 1, no later instruction depends on a byte of it before that byte is
+  // overwritten, and no byte still holding it when the program ends is one
+  // the host reads then (the observed ranges are read only between
+  // programs, so bytes overwritten within the program never show the value).
   bool DeadAfter(int program, size_t k, uint64_t off, uint64_t bytes) const {
-    if (Overlaps(observed_, off, bytes)) return false;
     Ranges live{{off, bytes}};  // the bytes still holding the value
     for (size_t j = k + 1; j < depends_[program].size() && !live.empty(); ++j) {
       for (const auto& r : live)
@@ -373,6 +374,8 @@ class Engine {
         live.swap(rest);
       }
     }
+    for (const auto& r : live)
+      if (Overlaps(observed_, r.first, r.second)) return false;
     return true;
   }
 

@@ -278,7 +278,6 @@ bool RangesOf(const UpdateInstruction& ins, bool writes,
               std::vector<std::pair<uint64_t, uint64_t>>* ranges) {
   Operand ops[8];
   size_t n = 0;
-  ranges->clear();
   if (!OperandsOf(ins, ops, &n)) return false;
   for (size_t i = 0; i < n; ++i) {
     if (ops[i].write != writes || IsRodataRef(ops[i].ref)) continue;

@@ -51,8 +51,9 @@ uint64_t ContentHash64(const uint8_t* data, size_t size);
 uint64_t PlanSelfHash(const uint8_t* plan, size_t size, size_t hash_offset);
 
 // Arena byte ranges [offset, offset + bytes) an instruction writes (rodata is
-// never written), from the validator's operand table; false when the dims
-// are malformed.
+// never written), from the validator's operand table, appended to *ranges
+// (so one vector can gather several instructions'); false when the dims are
+// malformed.
 bool WriteRangesOf(const UpdateInstruction& ins,
                    std::vector<std::pair<uint64_t, uint64_t>>* ranges);
 // The same for the arena ranges an instruction reads.
