@@ -756,6 +756,7 @@ class Engine {
     PlanPointwiseRuns(program);
     PlanScaleFolds(program);
     PlanDualRuns(program);
+    PlanRopePairs(program);
     PlanRowdotGroups(program);
     if (Status s = PlanColsumGroups(program); !s) return s;
     PlanTileGroups(program);
@@ -856,7 +857,7 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd, kAddRow };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd, kAddRow, kRopePair };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -1308,6 +1309,54 @@ class Engine {
     if (added)
       std::sort(chains_[program].begin(), chains_[program].end(),
                 [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  // RoPE pairs (RopeWithTable's x2/y2): two adjacent RopeFwd or two
+  // RopeBwd of one geometry through one angle table (a layer's q and k) in
+  // one launch. Each thread loads both tensors' float4s before it stores
+  // either, first y then y2, so the bits are the two launches' when the four
+  // ranges are pairwise identical or disjoint and the second does not read
+  // the first's output.
+  void PlanRopePairs(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    auto rope = [&](size_t k) {
+      const auto op = static_cast<Op>(prog[k].opcode);
+      return op == Op::kRopeFwd || op == Op::kRopeBwd;
+    };
+    for (size_t i = 0; i + 1 < prog.size(); ++i) {
+      if (taken[i] || taken[i + 1] || !rope(i) || prog[i + 1].opcode != prog[i].opcode) continue;
+      const UpdateInstruction& a = prog[i];
+      const UpdateInstruction& b = prog[i + 1];
+      if (a.out[0] != b.out[0] || a.out[1] != b.out[1] || a.out[2] != b.out[2]) continue;
+      const float* t = RopeTableOf(Lo(a.out[0]), Lo(a.out[1]), a.out[2]);
+      const uint64_t S = Lo(a.out[0]), d = Lo(a.out[1]);
+      if (!t || d % 4 != 0 || S * d > 0xFFFFFFFFu ||
+          Hi(a.out[0]) * S * Hi(a.out[1]) * d / 4 > 0xFFFFFFFFu)
+        continue;
+      const uint64_t refs[4] = {a.in[0], a.in[1], b.in[0], b.in[1]};
+      bool ok = b.in[0] != a.in[1];
+      for (uint64_t r : refs) ok = ok && !IsRodataRef(r) && aligned16(RP(r));
+      const uint64_t bytes = Hi(a.out[0]) * Lo(a.out[0]) * Hi(a.out[1]) * Lo(a.out[1]) * sizeof(float);
+      for (int x = 0; x < 4 && ok; ++x)
+        for (int z = x + 1; z < 4 && ok; ++z)
+          ok = refs[x] == refs[z] || !Overlaps(Ranges{{RefOffset(refs[x]), bytes}}, RefOffset(refs[z]), bytes);
+      if (!ok) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = 2;
+      run.kind = ChainKind::kRopePair;
+      chains_[program].push_back(run);
+      taken[i] = taken[i + 1] = 1;
+      ++i;
+    }
+    std::sort(chains_[program].begin(), chains_[program].end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
   }
 
   void PlanDualRuns(int program) {
@@ -1992,6 +2041,14 @@ class Engine {
         }
         return Status::Ok();
       case ChainKind::kDual: return LaunchDual(program, run.first, 3, nullptr, 1.0f, c);
+      case ChainKind::kRopePair: {
+        const UpdateInstruction& a = plan_.program[program][run.first];
+        const UpdateInstruction& b = plan_.program[program][run.first + 1];
+        const int dir = static_cast<Op>(a.opcode) == Op::kRopeFwd ? 1 : -1;
+        return RopeWithTable(RP(a.in[0]), WP(a.in[1]), Hi(a.out[0]), Lo(a.out[0]), Hi(a.out[1]),
+                             Lo(a.out[1]), RopeTableOf(Lo(a.out[0]), Lo(a.out[1]), a.out[2]), dir, c,
+                             RP(b.in[0]), WP(b.in[1]));
+      }
       case ChainKind::kAddRow: {
         const UpdateInstruction& g = plan_.program[program][run.first + 1];
         if (static_cast<Op>(g.opcode) == Op::kLayerNormFwd)
@@ -2654,6 +2711,63 @@ class Engine {
   // splits, n_split) instead of a timed launch, and nothing is launched (the
   // reference's injected reward closure, test/compiler/backend/tuner_test.cc:130-145).
   using RewardFn = double (*)(void*, uint64_t, uint64_t, int, int, uint64_t);
+  // The tile groups the per-shape picks form, re-tuned as launches: a
+  // group holds two to four times one GEMM's tiles, so its best tile can
+  // differ from the lone GEMM's. Arms: every tile config the members fit as
+  // one group (their epilogues included) at one slice, the current pick
+  // first; reward as in Autotune. Any tile config keeps the summation order.
+  Status TuneTileGroups(int program, int budget, hipEvent_t t0, hipEvent_t t1) {
+    if (Status s = EnsureWorkspace(program); !s) return s;
+    if (Status s = PlanFusion(program); !s) return s;
+    const auto& prog = plan_.program[program];
+    const std::vector<TileGroup> groups = tgroups_[program];
+    const Ctx c = MakeCtx();
+    for (const TileGroup& g : groups) {
+      const int n = static_cast<int>(g.units.size());
+      GemmDesc ds[kGemmGroupMax];
+      double flops = 0.0;
+      for (int j = 0; j < n; ++j) {
+        ds[j] = g.units[j].d;
+        flops += GemmFlops(ds[j]);
+      }
+      std::vector<int> arms{g.units[0].plan.cfg};
+      for (int cfg = 0; cfg < GemmSkinnyConfig(); ++cfg) {
+        if (cfg == arms[0]) continue;
+        GemmPlan ps[kGemmGroupMax];
+        bool ok = true;
+        for (int j = 0; j < n && ok; ++j) {
+          ps[j] = PlanGemmWith(DescOf(prog[g.units[j].first]), cfg, 1);
+          ok = GemmPlanKeepsOrder(DescOf(prog[g.units[j].first]), ps[j]);
+        }
+        if (ok && GemmGroupFits(ds, ps, n)) arms.push_back(cfg);
+      }
+      if (arms.size() < 2) continue;
+      auto launch = [&](int cfg) {
+        GemmPlan ps[kGemmGroupMax];
+        for (int j = 0; j < n; ++j) ps[j] = PlanGemmWith(DescOf(prog[g.units[j].first]), cfg, 1);
+        return LaunchGemmGroup(ds, ps, n, c);
+      };
+      for (int cfg : arms)  // one untimed warm-up launch per arm
+        if (Status s = launch(cfg); !s) return s;
+      Ucb1 bandit(arms.size());
+      const int trials = std::max<int>(budget, 2 * static_cast<int>(arms.size()));
+      for (int t = 0; t < trials; ++t) {
+        const size_t arm = bandit.Select();
+        (void)hipEventRecord(t0, stream_);
+        if (Status s = launch(arms[arm]); !s) return s;
+        (void)hipEventRecord(t1, stream_);
+        (void)hipEventSynchronize(t1);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, t0, t1);
+        bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
+      }
+      const int best = arms[bandit.Best(kAutotuneTileTolerance)];
+      for (const TileUnit& u : g.units)
+        plans_[program][u.first] = PlanGemmWith(DescOf(prog[u.first]), best, 1);
+    }
+    return Status::Ok();
+  }
+
   Status Autotune(int budget, RewardFn inject = nullptr, void* inject_ctx = nullptr) {
     loss_posted_ = false;  // runs instructions outside Run()
     const int program = static_cast<int>(Program::kTrain);
@@ -2754,6 +2868,7 @@ class Engine {
       const GemmPlan best = arms[bandit.Best(kAutotuneTileTolerance)];
       for (size_t i : idxs) plans_[program][i] = best;
     }
+    if (result && !inject) result = TuneTileGroups(program, budget, t0, t1);
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);
     if (!result) return result;
@@ -3027,6 +3142,12 @@ class Engine {
       *bytes = b;
       return true;
     }
+    if (run->kind == ChainKind::kRopePair) {
+      const UpdateInstruction& g = prog[idx];
+      *flops = 0.0;
+      *bytes = 2.0 * 8.0 * static_cast<double>(Hi(g.out[0]) * Lo(g.out[0]) * Hi(g.out[1]) * Lo(g.out[1]));
+      return true;
+    }
     if (run->kind == ChainKind::kAddRow) {
       const UpdateInstruction& g = prog[idx + 1];
       const bool ln = static_cast<Op>(g.opcode) == Op::kLayerNormFwd;
@@ -3108,6 +3229,7 @@ class Engine {
         case ChainKind::kPointwise: return "in pointwise run";
         case ChainKind::kRowAdd: return "in row epilogue";
         case ChainKind::kAddRow: return "in row prologue";
+        case ChainKind::kRopePair: return "in rope pair";
         default: return "in chain";
       }
     }
@@ -3117,6 +3239,7 @@ class Engine {
       return run->ra.store_dx ? "with the next AddEW (dx stored)" : "with the next AddEW";
     if (run && run->kind == ChainKind::kAddRow)
       return run->pa.store_sum ? "with the next norm (sum stored)" : "with the next norm";
+    if (run && run->kind == ChainKind::kRopePair) return "rope pair";
     if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
       const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
       return idx == g.members.back()

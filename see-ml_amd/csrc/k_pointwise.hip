@@ -579,17 +579,22 @@ __global__ __launch_bounds__(kBlock) void rope_angle_table_kernel(float* __restr
 // the row width (in float4s), S and d are powers of two, and the element's
 // row, column and position come from shifts and masks (nv_shift = log2 of
 // the row width) rather than three integer divisions per float4.
-template <int DIR, bool NT, bool POW2>
-__global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restrict__ x,
-                                                            float* __restrict__ y,
+// PAIR: a second tensor of the same geometry (x2 -> y2) in the same
+// launch, as the instruction after the first would run it. Each thread
+// loads both tensors' float4s before it stores either, and stores y before
+// y2, so the two may share ranges as long as every pair of ranges is
+// identical or disjoint and x2 is not y (the host's conditions).
+template <int DIR, bool NT, bool POW2, bool PAIR = false>
+__global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* x, float* y,
                                                             const float* __restrict__ table,
                                                             uint32_t nv_row, uint32_t total4,
                                                             uint32_t S, uint32_t d,
-                                                            uint32_t nv_shift) {
+                                                            uint32_t nv_shift, const float* x2,
+                                                            float* y2) {
   constexpr int kU = Unroll(NT);
   const uint32_t stride = gridDim.x * kBlock * kU;
   for (uint32_t base = blockIdx.x * kBlock * kU + threadIdx.x; base < total4; base += stride) {
-    float4 v[kU], t[kU];
+    float4 v[kU], t[kU], v2[PAIR ? kU : 1];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const uint32_t i = base + u * kBlock;
@@ -605,6 +610,7 @@ __global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restr
         pos = row % S;
       }
       v[u] = ld4(x + 4 * static_cast<size_t>(i), NT);
+      if constexpr (PAIR) v2[u] = ld4(x2 + 4 * static_cast<size_t>(i), NT);
       t[u] = *reinterpret_cast<const float4*>(table + 2 * (pos * (d / 2) + c2));
     }
 #pragma unroll
@@ -612,20 +618,23 @@ __global__ __launch_bounds__(kBlock) void rope_table_kernel(const float* __restr
       const uint32_t i = base + u * kBlock;
       if (i >= total4) continue;
       const float c0 = t[u].x, s0 = t[u].y, c1 = t[u].z, s1 = t[u].w;
-      const float4 w = v[u];
-      float4 o;
-      if constexpr (DIR > 0) {
-        o.x = w.x * c0 - w.y * s0;
-        o.y = w.x * s0 + w.y * c0;
-        o.z = w.z * c1 - w.w * s1;
-        o.w = w.z * s1 + w.w * c1;
-      } else {
-        o.x = w.x * c0 + w.y * s0;
-        o.y = -w.x * s0 + w.y * c0;
-        o.z = w.z * c1 + w.w * s1;
-        o.w = -w.z * s1 + w.w * c1;
-      }
-      st4(y + 4 * static_cast<size_t>(i), o, NT);
+      auto rot = [&](const float4 w) {
+        float4 o;
+        if constexpr (DIR > 0) {
+          o.x = w.x * c0 - w.y * s0;
+          o.y = w.x * s0 + w.y * c0;
+          o.z = w.z * c1 - w.w * s1;
+          o.w = w.z * s1 + w.w * c1;
+        } else {
+          o.x = w.x * c0 + w.y * s0;
+          o.y = -w.x * s0 + w.y * c0;
+          o.z = w.z * c1 + w.w * s1;
+          o.w = -w.z * s1 + w.w * c1;
+        }
+        return o;
+      };
+      st4(y + 4 * static_cast<size_t>(i), rot(v[u]), NT);
+      if constexpr (PAIR) st4(y2 + 4 * static_cast<size_t>(i), rot(v2[u]), NT);
     }
   }
 }
@@ -901,14 +910,16 @@ Status RopeTable(float* table, size_t S, size_t d, float base, const Ctx& c) {
 }
 
 Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
-                     const float* table, int dir, const Ctx& c) {
+                     const float* table, int dir, const Ctx& c, const float* x2, float* y2) {
   const size_t rows = B * S, width = H * d;
   if (rows == 0 || width == 0) return Status::Ok();
+  const bool pair = x2 != nullptr;
   if (d % 4 != 0 || S == 0 || !aligned16(x) || !aligned16(y) || !aligned16(table) ||
+      (pair && (!y2 || !aligned16(x2) || !aligned16(y2) || x2 == y)) ||
       rows * width / 4 > 0xFFFFFFFFu || S * d > 0xFFFFFFFFu)
     return Status::Fail(kUnitEngine, "Rope: the table form needs d % 4 == 0 and aligned operands");
   const uint32_t total4 = static_cast<uint32_t>(rows * width / 4);
-  const bool nt = StreamPolicy(8 * rows * width);
+  const bool nt = StreamPolicy((pair ? 16 : 8) * rows * width);
   const size_t work = (total4 + Unroll(nt) - 1) / Unroll(nt);
   const dim3 grid(grid_for(work, kBlock, nt ? kStreamGridCap : kGridCap));
   const uint32_t nv_row = static_cast<uint32_t>(width / 4), S32 = static_cast<uint32_t>(S),
@@ -917,9 +928,11 @@ Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, siz
   const bool p2 = pow2(nv_row) && pow2(S32) && pow2(d32);
   uint32_t shift = 0;
   while (p2 && (1u << shift) < nv_row) ++shift;
-#define SEEML_ROPE(D, N, P)                                                                  \
-  hipLaunchKernelGGL((rope_table_kernel<D, N, P>), grid, dim3(kBlock), 0, c.stream, x, y, table, \
-                     nv_row, total4, S32, d32, shift)
+#define SEEML_ROPE1(D, N, P, Q)                                                                 \
+  hipLaunchKernelGGL((rope_table_kernel<D, N, P, Q>), grid, dim3(kBlock), 0, c.stream, x, y, table, \
+                     nv_row, total4, S32, d32, shift, x2, y2)
+#define SEEML_ROPE(D, N, P) \
+  do { if (pair) SEEML_ROPE1(D, N, P, true); else SEEML_ROPE1(D, N, P, false); } while (0)
   if (dir > 0) {
     if (p2) { if (nt) SEEML_ROPE(1, true, true); else SEEML_ROPE(1, false, true); }
     else { if (nt) SEEML_ROPE(1, true, false); else SEEML_ROPE(1, false, false); }
@@ -928,6 +941,7 @@ Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, siz
     else { if (nt) SEEML_ROPE(-1, true, false); else SEEML_ROPE(-1, false, false); }
   }
 #undef SEEML_ROPE
+#undef SEEML_ROPE1
   return LaunchStatus(dir > 0 ? "RopeFwd" : "RopeBwd");
 }
 

@@ -318,9 +318,12 @@ Status RopeBwd(const float* dy, float* dx, size_t B, size_t S, size_t H, size_t 
 size_t RopeTableFloats(size_t S, size_t d);
 Status RopeTable(float* table, size_t S, size_t d, float base, const Ctx& c);
 // RopeFwd (dir +1) / RopeBwd (dir -1) reading a RopeTable: a pure stream
-// (d % 4 == 0; x, y and the table 16-byte aligned).
+// (d % 4 == 0; x, y and the table 16-byte aligned). With x2 set, a second
+// tensor of the same geometry, x2 -> y2, in the same launch, as if run after
+// the first: every pair of the four ranges identical or disjoint, x2 != y.
 Status RopeWithTable(const float* x, float* y, size_t B, size_t S, size_t H, size_t d,
-                     const float* table, int dir, const Ctx& c);
+                     const float* table, int dir, const Ctx& c, const float* x2 = nullptr,
+                     float* y2 = nullptr);
 
 // ---- row / reduction family (k_rows.hip) ----------------------------------
 size_t MseFwdWorkspace(size_t n);

@@ -698,6 +698,12 @@ def test_fusions_are_planned(torch_gpu):
     assert all(planner.OP_NAME[p.train[i]["opcode"]] == "RmsNormBwd" for i in rows)
     assert all(ch[i + 1] == "in row epilogue" for i in rows)
     assert {i + 1 for i in rows} == {i for i, c in enumerate(ch) if c == "in row epilogue"}
+    # a layer's q and k rotations (forward and backward) in one launch
+    pairs = [i for i, c in enumerate(ch) if c == "rope pair"]
+    assert pairs, ch
+    assert all(ch[i + 1] == "in rope pair" for i in pairs)
+    assert all(planner.OP_NAME[p.train[i]["opcode"]] == planner.OP_NAME[p.train[i + 1]["opcode"]]
+               in ("RopeFwd", "RopeBwd") for i in pairs)
     # the residual sums entering the next block's RMSNorm, in its load
     pre = [i for i, c in enumerate(ch) if c.startswith("with the next norm")]
     assert pre, ch
@@ -709,7 +715,8 @@ def test_fusions_are_planned(torch_gpu):
     e.train_step(x, y)
     for i in range(len(p.train)):
         c = e.gemm_choice(PROGRAM_TRAIN, i)
-        assert not (c.startswith("in ") or "AddEW" in c or "run of" in c or "chain of" in c), c
+        assert not (c.startswith("in ") or "AddEW" in c or "run of" in c or "chain of" in c or
+                    "pair" in c or "group" in c), c
     e.close()
 
 
