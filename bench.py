@@ -11,9 +11,10 @@ north-star target is stated on: V32000, 16 layers, 16x128 heads, seq 1024 x
 
 Emits ONE JSON line (rank 0) with, besides the driver's fields:
   roofline      the dominant kernel — the (opcode, shape, tile) group with
-                the largest share of step time — one launch timed with HIP
-                events on the engine stream: algorithmic FLOPs (or bytes) of
-                one launch / mean launch time, vs MI355X peak; `traffic` is
+                the largest share of step time — its launches timed inside
+                the train graph by device wall-clock stamp nodes over the
+                timed steps: algorithmic FLOPs (or bytes) of one launch /
+                mean launch time, vs MI355X peak; `traffic` is
                 the HBM bytes per launch from the committed rocprofv3 PMC
                 summary for that kernel (profiles/), when one matches
   cpu_baseline  the reference's own executor kernels (oracle/_ref, built
@@ -164,15 +165,16 @@ def main():
     xb, yb = batches[0]
     losses.append(e.train_step(xb, yb))  # first replay of the rebuilt graph, untimed
 
+    e.marked_times(PROGRAM_TRAIN)  # restarts the device-side sums: the timed steps' alone
     torch.cuda.synchronize()
-    launch_ms = []
     t0 = time.perf_counter()
     for s in range(args.steps):
         xb, yb = batches[s % 2]
         losses.append(e.train_step(xb, yb))  # returns after the step's loss read (synchronized)
-        launch_ms.append(e.marked_times(PROGRAM_TRAIN))
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    # each marked launch's mean over the K timed steps, summed on the device
+    launch_ms = [e.marked_times(PROGRAM_TRAIN)]
     ms_per_step = dt / args.steps * 1e3
     tokens_per_s = w.cfg.batch * args.steps / dt
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.1f} tok/s")
@@ -213,8 +215,9 @@ def main():
     roof.update(kernel=kernel, launches_per_step=len(dom_idx),
                 step_share=round(dom_total / summ["total_ms"], 4),
                 launch_ms=round(dom_ms, 4),
-                timing=f"HIP events around its {len(dom_idx)} launches per step inside the "
-                       f"train graph, over the {args.steps} timed steps",
+                timing=f"device wall-clock stamp nodes around its {len(dom_idx)} launches per "
+                       f"step inside the train graph, summed on the device over the "
+                       f"{args.steps} timed steps",
                 traffic=traffic, traffic_source=traffic_src,
                 algorithmic=(f"{dom_row['flops']} FLOP" if roof["bound"] == "mfma"
                              else f"{dom_row['bytes']} B"),

@@ -313,12 +313,16 @@ int seeml_hip_checkpoint_read(const char* path, uint64_t plan_hash, uint64_t siz
  * side effects happen `reps` times (optimizer state moves). */
 int seeml_hip_profile_program(seeml_hip_engine* e, int program, int reps, float* ms_out,
                               uint64_t count);
-/* Timing inside ordinary replays: the program's graph is split at `indices`
- * (rebuilt on next run); each marked launch runs between graph segments on
- * the engine stream, bracketed by HIP events. seeml_hip_marked_times returns
- * each marked launch's duration (ms) in the latest completed replay, in
- * ascending index order. Marked AdamW steps are left out of multi-tensor
- * fusion. count = 0 removes the marks. */
+/* Timing inside ordinary replays: the launches of `indices` (a marked tile
+ * group's first instruction times the whole group launch) run between two
+ * wall-clock stamp nodes of the program's one graph (rebuilt on next run),
+ * which accumulate each launch's time on the device.
+ * seeml_hip_marked_times returns each marked launch's mean duration (ms)
+ * over the replays since the marks were set or last read, in ascending
+ * index order, and restarts the sums. Without a graph (or a device wall
+ * clock), HIP events around each marked launch give the latest replay's
+ * duration. Marked instructions are left out of the other fusions.
+ * count = 0 removes the marks. */
 int seeml_hip_mark_timed(seeml_hip_engine* e, int program, const uint64_t* indices,
                          uint64_t count);
 int seeml_hip_marked_times(seeml_hip_engine* e, int program, float* ms_out, uint64_t count);

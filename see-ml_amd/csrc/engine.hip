@@ -2087,9 +2087,9 @@ class Engine {
           mk != marks.end() && *mk == i && mark_stamps_[program]) {
         const size_t k = static_cast<size_t>(mk - marks.begin());
         const int tg = TileGroupAt(program, i, begin, end);
-        if (Status s = WallStamp(mark_stamps_[program] + 2 * k, stream_); !s) return s;
+        if (Status s = WallStamp(mark_stamps_[program] + 3 * k, false, stream_); !s) return s;
         if (Status s = tg >= 0 ? LaunchTileGroup(program, tg, c) : Dispatch(program, i, c); !s) return s;
-        if (Status s = WallStamp(mark_stamps_[program] + 2 * k + 1, stream_); !s) return s;
+        if (Status s = WallStamp(mark_stamps_[program] + 3 * k, true, stream_); !s) return s;
         i = tg >= 0 ? tgroups_[program][tg].end : i + 1;
         while (q < chains.size() && chains[q].first < i) ++q;
         while (r < runs.size() && runs[r].first < i) ++r;
@@ -2152,18 +2152,16 @@ class Engine {
     if (!v.empty()) {
       if (wall_khz_ == 0)
         (void)hipDeviceGetAttribute(&wall_khz_, hipDeviceAttributeWallClockRate, device_);
-      if (Status s = HipOk(LockedMalloc(&mark_stamps_[program], 2 * v.size() * sizeof(uint64_t)),
-                           "timing stamps");
-          !s)
+      const size_t bytes = 3 * v.size() * sizeof(uint64_t);
+      if (Status s = HipOk(LockedMalloc(&mark_stamps_[program], bytes), "timing stamps"); !s) return s;
+      if (Status s = HipOk(hipMemsetAsync(mark_stamps_[program], 0, bytes, stream_), "timing stamps"); !s)
         return s;
-      if (h_stamps_cap_ < 2 * v.size()) {
+      if (h_stamps_cap_ < 3 * v.size()) {
         if (h_stamps_) (void)LockedHostFree(h_stamps_);
         h_stamps_ = nullptr;
         h_stamps_cap_ = 0;
-        if (Status s = HipOk(LockedHostMalloc(&h_stamps_, 2 * v.size() * sizeof(uint64_t)), "timing stamps");
-            !s)
-          return s;
-        h_stamps_cap_ = 2 * v.size();
+        if (Status s = HipOk(LockedHostMalloc(&h_stamps_, bytes), "timing stamps"); !s) return s;
+        h_stamps_cap_ = 3 * v.size();
       }
     }
     for (size_t j = 0; j < 2 * v.size(); ++j) {
@@ -2175,20 +2173,27 @@ class Engine {
     return Status::Ok();
   }
 
-  // Durations (ms) of the marked launches in the most recent completed replay.
+  // Durations (ms) of the marked launches: with stamp nodes, the mean over the
+  // replays since the last read; with events, the most recent replay's.
   Status MarkedTimes(int program, float* ms, size_t n) {
     if (program < 0 || program > 2) return Status::Fail(kUnitEngine, "unknown program id");
     if (n < marked_[program].size()) return Status::Fail(kUnitEngine, "timing output too small");
     if (stamped_[program] && use_graph_) {
+      // The mean over the replays since the previous read (the sums restart).
       const size_t m = marked_[program].size();
-      if (Status s = HipOk(hipMemcpyAsync(h_stamps_, mark_stamps_[program], 2 * m * sizeof(uint64_t),
-                                          hipMemcpyDeviceToHost, stream_),
+      const size_t bytes = 3 * m * sizeof(uint64_t);
+      if (Status s = HipOk(hipMemcpyAsync(h_stamps_, mark_stamps_[program], bytes, hipMemcpyDeviceToHost,
+                                          stream_),
                            "timing read");
           !s)
         return s;
+      if (Status s = HipOk(hipMemsetAsync(mark_stamps_[program], 0, bytes, stream_), "timing reset"); !s)
+        return s;
       if (Status s = HipOk(hipStreamSynchronize(stream_), "timing read"); !s) return s;
-      for (size_t k = 0; k < m; ++k)
-        ms[k] = static_cast<float>(static_cast<double>(h_stamps_[2 * k + 1] - h_stamps_[2 * k]) / wall_khz_);
+      for (size_t k = 0; k < m; ++k) {
+        const uint64_t n = h_stamps_[3 * k + 2];
+        ms[k] = n ? static_cast<float>(static_cast<double>(h_stamps_[3 * k + 1]) / n / wall_khz_) : 0.0f;
+      }
       return Status::Ok();
     }
     for (size_t k = 0; k < marked_[program].size(); ++k) {
@@ -2713,8 +2718,10 @@ class Engine {
   using RewardFn = double (*)(void*, uint64_t, uint64_t, int, int, uint64_t);
   // The tile groups the per-shape picks form, re-tuned as launches: a
   // group holds two to four times one GEMM's tiles, so its best tile can
-  // differ from the lone GEMM's. Arms: every tile config the members fit as
-  // one group (their epilogues included) at one slice, the current pick
+  // differ from the lone GEMM's. Groups of one signature (each member's
+  // opcode, shape and epilogue kind, in order) are tuned once, on the first
+  // such group, and share the pick. Arms: every tile config the members fit
+  // as one group (their epilogues included) at one slice, the current pick
   // first; reward as in Autotune. Any tile config keeps the summation order.
   Status TuneTileGroups(int program, int budget, hipEvent_t t0, hipEvent_t t1) {
     if (Status s = EnsureWorkspace(program); !s) return s;
@@ -2722,8 +2729,24 @@ class Engine {
     const auto& prog = plan_.program[program];
     const std::vector<TileGroup> groups = tgroups_[program];
     const Ctx c = MakeCtx();
+    auto signature = [&](const TileGroup& g) {
+      std::vector<uint64_t> key;
+      for (const TileUnit& u : g.units) {
+        const UpdateInstruction& ins = prog[u.first];
+        key.insert(key.end(), {ins.opcode, ins.out[0], ins.out[1], ins.out[2],
+                               static_cast<uint64_t>(u.d.lora_t ? 2 : u.d.out ? 1 : 0)});
+      }
+      return key;
+    };
+    std::map<std::vector<uint64_t>, int> picked;
     for (const TileGroup& g : groups) {
       const int n = static_cast<int>(g.units.size());
+      const auto key = signature(g);
+      if (const auto it = picked.find(key); it != picked.end()) {
+        for (const TileUnit& u : g.units)
+          plans_[program][u.first] = PlanGemmWith(DescOf(prog[u.first]), it->second, 1);
+        continue;
+      }
       GemmDesc ds[kGemmGroupMax];
       double flops = 0.0;
       for (int j = 0; j < n; ++j) {
@@ -2731,6 +2754,7 @@ class Engine {
         flops += GemmFlops(ds[j]);
       }
       std::vector<int> arms{g.units[0].plan.cfg};
+      picked[key] = arms[0];
       for (int cfg = 0; cfg < GemmSkinnyConfig(); ++cfg) {
         if (cfg == arms[0]) continue;
         GemmPlan ps[kGemmGroupMax];
@@ -2762,6 +2786,7 @@ class Engine {
         bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
       }
       const int best = arms[bandit.Best(kAutotuneTileTolerance)];
+      picked[key] = best;
       for (const TileUnit& u : g.units)
         plans_[program][u.first] = PlanGemmWith(DescOf(prog[u.first]), best, 1);
     }
@@ -3351,7 +3376,7 @@ class Engine {
     long mark = -1;  // >= 0: a marked launch, run eagerly between segments
   };
   std::vector<Segment> segs_[3];
-  uint64_t* mark_stamps_[3] = {nullptr, nullptr, nullptr};  // 2 wall-clock stamps per marked launch
+  uint64_t* mark_stamps_[3] = {nullptr, nullptr, nullptr};  // per marked launch: start, tick sum, count
   uint64_t* h_stamps_ = nullptr;                            // pinned, for reading them back
   size_t h_stamps_cap_ = 0;
   bool stamped_[3] = {false, false, false};  // the built graph times its marks by stamps

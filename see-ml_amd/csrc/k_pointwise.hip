@@ -1014,14 +1014,25 @@ Status PostLoss(const float* src, float* host_dst, hipStream_t stream) {
   return LaunchStatus("PostLoss");
 }
 
-// The device's constant-rate wall clock, written by one lane: a graph node
-// before and after a launch brackets its time on the GPU's own clock.
-__global__ void wall_stamp_kernel(uint64_t* dst) {
-  if (threadIdx.x == 0) *dst = wall_clock64();
+// The device's constant-rate wall clock, read by one lane: a graph node
+// before a launch stores it (slot[0]); one after adds the elapsed ticks to
+// slot[1] and counts the interval in slot[2], so repeated replays
+// accumulate with no host read between them (one stream: the nodes of one
+// slot never run concurrently).
+__global__ void wall_stamp_kernel(uint64_t* slot, int close) {
+  if (threadIdx.x == 0) {
+    const uint64_t now = wall_clock64();
+    if (close) {
+      slot[1] += now - slot[0];
+      slot[2] += 1;
+    } else {
+      slot[0] = now;
+    }
+  }
 }
 
-Status WallStamp(uint64_t* dst, hipStream_t stream) {
-  hipLaunchKernelGGL(wall_stamp_kernel, dim3(1), dim3(64), 0, stream, dst);
+Status WallStamp(uint64_t* slot, bool close, hipStream_t stream) {
+  hipLaunchKernelGGL(wall_stamp_kernel, dim3(1), dim3(64), 0, stream, slot, close ? 1 : 0);
   return LaunchStatus("WallStamp");
 }
 

@@ -41,8 +41,10 @@ StepScalars MakeStepScalars(const PlanHeader& h, uint64_t step);
 Status StageStep(const StepScalars* s, StepScalars* dst, const void* in_src, void* in_dst,
                  size_t in_bytes, const void* lab_src, void* lab_dst, size_t lab_bytes,
                  hipStream_t stream);
-// Writes the device wall clock (wall_clock64) to dst.
-Status WallStamp(uint64_t* dst, hipStream_t stream);
+// Interval timing on the device wall clock (wall_clock64): close = false
+// stores the start in slot[0]; close = true adds the ticks since then to
+// slot[1] and increments the count in slot[2].
+Status WallStamp(uint64_t* slot, bool close, hipStream_t stream);
 // Copies the loss scalar into mapped pinned host memory from the device.
 Status PostLoss(const float* src, float* host_dst, hipStream_t stream);
 
