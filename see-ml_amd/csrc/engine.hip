@@ -317,9 +317,11 @@ class Engine {
   // nothing observes. The plan's transient segment is assigned by liveness
   // within one program (arena_binder.cc:25-98; the values that must outlive
   // it, the loss and the gradients, are pinned there), so a transient value
-  // never carries from one run of a program into another. Observed are the
-  // persistent segment, the I/O slots, the loss, the eval probabilities and
-  // the merge deltas the host reads back.
+  // never carries from one run of a program into another. Observed after
+  // every program: the persistent segment and the I/O slots; after the train
+  // and eval programs also the loss, after the eval program the probabilities
+  // its accuracy reads, after the merge program the deltas the host reads
+  // back. (Bytes one program leaves behind are no other program's input.)
   using Ranges = std::vector<std::pair<uint64_t, uint64_t>>;
 
   static bool Overlaps(const Ranges& rs, uint64_t off, uint64_t bytes) {
@@ -330,15 +332,22 @@ class Engine {
 
   void PlanLiveness() {
     const PlanHeader& h = plan_.header;
-    observed_.clear();
-    observed_.emplace_back(0, h.persistent_size);
-    if (h.input_ref != kNullRef) observed_.emplace_back(RefOffset(h.input_ref), h.input_floats * 4);
-    if (h.label_ref != kNullRef) observed_.emplace_back(RefOffset(h.label_ref), h.label_bytes);
-    if (h.loss_ref != kNullRef) observed_.emplace_back(RefOffset(h.loss_ref), sizeof(float));
-    if (plan_.eval_probs_ref != kNullRef)
-      observed_.emplace_back(RefOffset(plan_.eval_probs_ref),
-                             plan_.eval_softmax_rows * plan_.eval_softmax_cols * sizeof(float));
-    for (const EmitEntry& e : plan_.emit) observed_.emplace_back(e.arena_offset, e.byte_size);
+    const int kTr = static_cast<int>(Program::kTrain), kEv = static_cast<int>(Program::kEval),
+              kMg = static_cast<int>(Program::kMerge);
+    for (int p = 0; p < 3; ++p) {
+      Ranges& o = observed_[p];
+      o.clear();
+      o.emplace_back(0, h.persistent_size);
+      if (h.input_ref != kNullRef) o.emplace_back(RefOffset(h.input_ref), h.input_floats * 4);
+      if (h.label_ref != kNullRef) o.emplace_back(RefOffset(h.label_ref), h.label_bytes);
+      if (h.loss_ref != kNullRef && (p == kTr || p == kEv))
+        o.emplace_back(RefOffset(h.loss_ref), sizeof(float));
+      if (plan_.eval_probs_ref != kNullRef && p == kEv)
+        o.emplace_back(RefOffset(plan_.eval_probs_ref),
+                       plan_.eval_softmax_rows * plan_.eval_softmax_cols * sizeof(float));
+      if (p == kMg)
+        for (const EmitEntry& e : plan_.emit) o.emplace_back(e.arena_offset, e.byte_size);
+    }
     for (int p = 0; p < 3; ++p) {
       const auto& prog = plan_.program[p];
       depends_[p].assign(prog.size(), Ranges{});
@@ -375,7 +384,7 @@ class Engine {
       }
     }
     for (const auto& r : live)
-      if (Overlaps(observed_, r.first, r.second)) return false;
+      if (Overlaps(observed_[program], r.first, r.second)) return false;
     return true;
   }
 
@@ -432,7 +441,7 @@ class Engine {
                                                     : (r.out[0] == bs && r.out[1] == hd);
         return same && AttnFusedPath({RP(r.in[0]), RP(r.in[1]), WP(r.in[2])}, rB, rS, rH, rd);
       };
-      bool tail = Overlaps(observed_, RefOffset(ref), bytes), read = tail;
+      bool tail = Overlaps(observed_[program], RefOffset(ref), bytes), read = tail;
       Ranges live{{RefOffset(ref), bytes}};
       for (size_t j = k + 1; j < prog.size() && !live.empty() && !tail; ++j) {
         bool touches = false;
@@ -757,6 +766,7 @@ class Engine {
     PlanScaleFolds(program);
     PlanDualRuns(program);
     PlanRopePairs(program);
+    PlanXentPasses(program);
     PlanRowdotGroups(program);
     if (Status s = PlanColsumGroups(program); !s) return s;
     PlanTileGroups(program);
@@ -857,7 +867,7 @@ class Engine {
   // Pointwise runs (kernels.h PointwiseRun): see PlanPointwiseRuns.
   //
   // Scale folds: see PlanScaleFolds.
-  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd, kAddRow, kRopePair };
+  enum class ChainKind { kSkinny, kDense, kPointwise, kScaleFold, kLoraBase, kDual, kRowAdd, kAddRow, kRopePair, kXentPass };
   struct ChainRun {
     size_t first = 0, count = 0;
     ChainKind kind = ChainKind::kSkinny;
@@ -866,6 +876,7 @@ class Engine {
     PointwiseRun pw;     // pointwise
     RowAddend ra;        // row + AddEW: the AddEW in the norm backward's write-back
     RowPreAdd pa;        // AddEW + row: the AddEW in the norm forward's load
+    bool store_p = true; // loss pass: P has a later reader
     uint64_t bytes = 0;  // skinny, pointwise: HBM bytes the fused launch moves
     const float* fold_x = nullptr;  // scale fold: the Scale's input and factor
     float fold_alpha = 1.0f;
@@ -1354,6 +1365,69 @@ class Engine {
       chains_[program].push_back(run);
       taken[i] = taken[i + 1] = 1;
       ++i;
+    }
+    std::sort(chains_[program].begin(), chains_[program].end(),
+              [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+  }
+
+  // Loss passes (SoftmaxXEntFwdBwd): SoftmaxXEntFwd, the Fill of the
+  // gradient seed and SoftmaxXEntBwd over the forward's probabilities, in
+  // plan order, as one pass over the logits: the backward runs on each row's
+  // probabilities in registers, and P is stored only if a later
+  // instruction reads it. The written ranges (dl, P, the seed, the loss)
+  // must be apart from each other and from what the pass reads (logits,
+  // labels), since the rows' reads and writes interleave across workgroups;
+  // dl alone may be exactly the logits (each row is its workgroup's own).
+  void PlanXentPasses(int program) {
+    const auto& prog = plan_.program[program];
+    std::vector<char> taken(prog.size(), 0);
+    for (const FusedRun& r : fused_runs_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const ChainRun& r : chains_[program])
+      for (size_t k = r.first; k < r.first + r.count; ++k) taken[k] = 1;
+    for (const size_t k : marked_[program]) taken[k] = 1;
+    for (size_t i = 0; i + 2 < prog.size(); ++i) {
+      const UpdateInstruction& f = prog[i];
+      const UpdateInstruction& z = prog[i + 1];
+      const UpdateInstruction& b = prog[i + 2];
+      if (taken[i] || taken[i + 1] || taken[i + 2] || static_cast<Op>(f.opcode) != Op::kSoftmaxXEntFwd ||
+          static_cast<Op>(z.opcode) != Op::kFill || static_cast<Op>(b.opcode) != Op::kSoftmaxXEntBwd)
+        continue;
+      const uint64_t N = f.out[0], C = f.out[1];
+      if (b.out[0] != N || b.out[1] != C || z.out[0] != 1 || b.in[0] != f.in[3] || b.in[1] != f.in[1] ||
+          b.in[2] != z.in[0])
+        continue;
+      const uint64_t L = f.in[0], lab = f.in[1], loss = f.in[2], P = f.in[3], S = z.in[0], D = b.in[3];
+      bool ok = true;
+      for (uint64_t r : {loss, P, S, D}) ok = ok && !IsRodataRef(r);
+      if (!ok) continue;
+      const uint64_t mat = N * C * sizeof(float);
+      const bool store_p = !DeadAfter(program, i + 2, RefOffset(P), mat);
+      if (!XEntFwdBwdFits(RP(L), store_p ? RP(P) : nullptr, RP(D), N, C)) continue;
+      // written ranges, then read ones
+      Ranges w{{RefOffset(D), mat}, {RefOffset(S), sizeof(float)}, {RefOffset(loss), sizeof(float)}};
+      if (store_p) w.emplace_back(RefOffset(P), mat);
+      // dl may be the logits exactly (row by row in place); nothing else may
+      // touch what the pass reads.
+      Ranges r;
+      if (!IsRodataRef(L)) r.emplace_back(RefOffset(L), mat);
+      if (!IsRodataRef(lab)) r.emplace_back(RefOffset(lab), N * sizeof(int32_t));
+      for (size_t x = 0; x < w.size() && ok; ++x) {
+        const bool in_place = x == 0 && D == L;
+        ok = in_place ? !Overlaps(Ranges{r.begin() + 1, r.end()}, w[x].first, w[x].second)
+                      : !Overlaps(r, w[x].first, w[x].second);
+        for (size_t y = x + 1; y < w.size() && ok; ++y)
+          ok = !Overlaps(Ranges{w[x]}, w[y].first, w[y].second);
+      }
+      if (!ok) continue;
+      ChainRun run;
+      run.first = i;
+      run.count = 3;
+      run.kind = ChainKind::kXentPass;
+      run.store_p = store_p;
+      chains_[program].push_back(run);
+      taken[i] = taken[i + 1] = taken[i + 2] = 1;
+      i += 2;
     }
     std::sort(chains_[program].begin(), chains_[program].end(),
               [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
@@ -2041,6 +2115,13 @@ class Engine {
         }
         return Status::Ok();
       case ChainKind::kDual: return LaunchDual(program, run.first, 3, nullptr, 1.0f, c);
+      case ChainKind::kXentPass: {
+        const UpdateInstruction& f = plan_.program[program][run.first];
+        const UpdateInstruction& z = plan_.program[program][run.first + 1];
+        const UpdateInstruction& b = plan_.program[program][run.first + 2];
+        return SoftmaxXEntFwdBwd(RP(f.in[0]), IP(f.in[1]), WP(f.in[2]), run.store_p ? WP(f.in[3]) : nullptr,
+                                 Bits(z.in[1]), WP(z.in[0]), WP(b.in[3]), f.out[0], f.out[1], c);
+      }
       case ChainKind::kRopePair: {
         const UpdateInstruction& a = plan_.program[program][run.first];
         const UpdateInstruction& b = plan_.program[program][run.first + 1];
@@ -3167,6 +3248,14 @@ class Engine {
       *bytes = b;
       return true;
     }
+    if (run->kind == ChainKind::kXentPass) {
+      const UpdateInstruction& g = prog[idx];
+      const double mat = 4.0 * static_cast<double>(g.out[0]) * static_cast<double>(g.out[1]);
+      // logits read, dl (and P) written; labels, per-row terms, loss, seed
+      *flops = 0.0;
+      *bytes = mat * (run->store_p ? 3.0 : 2.0) + 16.0 * static_cast<double>(g.out[0]) + 8.0;
+      return true;
+    }
     if (run->kind == ChainKind::kRopePair) {
       const UpdateInstruction& g = prog[idx];
       *flops = 0.0;
@@ -3255,6 +3344,7 @@ class Engine {
         case ChainKind::kRowAdd: return "in row epilogue";
         case ChainKind::kAddRow: return "in row prologue";
         case ChainKind::kRopePair: return "in rope pair";
+        case ChainKind::kXentPass: return "in loss pass";
         default: return "in chain";
       }
     }
@@ -3265,6 +3355,8 @@ class Engine {
     if (run && run->kind == ChainKind::kAddRow)
       return run->pa.store_sum ? "with the next norm (sum stored)" : "with the next norm";
     if (run && run->kind == ChainKind::kRopePair) return "rope pair";
+    if (run && run->kind == ChainKind::kXentPass)
+      return run->store_p ? "one pass with the backward" : "one pass with the backward, P not stored";
     if (idx < cs_group_of_[program].size() && cs_group_of_[program][idx] >= 0) {
       const ColsumGroup& g = cs_groups_[program][cs_group_of_[program][idx]];
       return idx == g.members.back()
@@ -3364,7 +3456,7 @@ class Engine {
   void* cs_priv_[3] = {nullptr, nullptr, nullptr};  // the groups' operand copies
   std::vector<Ranges> depends_[3];  // per instruction: DependRangesOf
   std::vector<Ranges> writes_[3];   // per instruction: WriteRangesOf
-  Ranges observed_;
+  Ranges observed_[3];  // per program (PlanLiveness)
   std::vector<uint64_t> causal_rows_[3];  // per instruction: S, or 0
   std::vector<uint8_t> tails_[3];         // per instruction: kAttnStore* (PlanCausalTails)
   bool loss_posted_ = false;  // the last program run wrote its loss to h_loss_

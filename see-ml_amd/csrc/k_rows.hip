@@ -147,12 +147,23 @@ __global__ __launch_bounds__(kBlock) void xent_fwd_rows(const float* __restrict_
 // e * (1/sum), the label term from the same expression as p[label].
 constexpr int kXentVec = 8;
 
-template <int NT>
-__global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict__ logits,
+// BWD: the backward in the same pass (SoftmaxXEntFwdBwd): with the row's
+// probabilities still in registers, dl = scale * p, and at the label
+// scale * p - scale, scale = seed / N (the backward kernel's expressions on
+// the same p values); probs stored only when store_p; block 0 also writes
+// the seed to its slot, as the Fill between the two would. dl may be the
+// logits themselves (the plans compute it in place): a row's workgroup has
+// consumed all of the row's loads before its first barrier, and the label's
+// logit is taken from the registers of the thread holding it, so no load
+// can follow a store of the row.
+template <int NT, bool BWD = false>
+__global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* logits,
                                                         const int32_t* __restrict__ labels,
-                                                        float* __restrict__ probs, size_t N,
+                                                        float* probs, size_t N,
                                                         size_t C, double* __restrict__ terms,
-                                                        int nt) {
+                                                        int nt, float* dl = nullptr,
+                                                        float seed = 0.0f, float* seed_slot = nullptr,
+                                                        int store_p = 1) {
   __shared__ float fscratch[NT / kWave];
   const size_t n = blockIdx.x;
   const int nv = static_cast<int>(C / 4);
@@ -167,7 +178,19 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
     v[i] = ld4(logits + n * C + 4 * static_cast<size_t>(min(t + i * NT, nv - 1)), nt);
   int32_t lab = 0;
   float xl = 0.0f;
-  if (t == 0) {
+  bool own = false;  // BWD: this thread holds the label's logit in v
+  if constexpr (BWD) {
+    lab = labels[n];
+    if (lab >= 0 && static_cast<size_t>(lab) < C) {
+#pragma unroll
+      for (int i = 0; i < kXentVec; ++i)
+        if (t + i * NT == lab / 4) {
+          own = true;
+          const int e = lab % 4;
+          xl = e == 0 ? v[i].x : e == 1 ? v[i].y : e == 2 ? v[i].z : v[i].w;
+        }
+    }
+  } else if (t == 0) {
     lab = labels[n];
     if (lab >= 0 && static_cast<size_t>(lab) < C) xl = logits[n * C + lab];
   }
@@ -193,16 +216,39 @@ __global__ __launch_bounds__(NT) void xent_fwd_rows_reg(const float* __restrict_
   }
   const float sum = block_sum<float, NT>(sacc, fscratch);
   const float inv = 1.0f / sum;
+  if constexpr (BWD) {
+    if (n == 0 && t == 0) *seed_slot = seed;
+    const float scale = seed / static_cast<float>(N);
+    const size_t lc = lab >= 0 ? static_cast<size_t>(lab) : ~size_t{0};
 #pragma unroll
-  for (int i = 0; i < kXentVec; ++i) {
-    const int j = t + i * NT;
-    if (j < nv)
-      st4(probs + n * C + 4 * static_cast<size_t>(j),
-          make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), nt);
+    for (int i = 0; i < kXentVec; ++i) {
+      const int j = t + i * NT;
+      if (j < nv) {
+        const float4 pv = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+        if (store_p) st4(probs + n * C + 4 * static_cast<size_t>(j), pv, nt);
+        float4 o = make_float4(scale * pv.x, scale * pv.y, scale * pv.z, scale * pv.w);
+        if (lc / 4 == static_cast<size_t>(j)) {
+          if (lc % 4 == 0) o.x -= scale;
+          else if (lc % 4 == 1) o.y -= scale;
+          else if (lc % 4 == 2) o.z -= scale;
+          else o.w -= scale;
+        }
+        st4(dl + n * C + 4 * static_cast<size_t>(j), o, nt);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kXentVec; ++i) {
+      const int j = t + i * NT;
+      if (j < nv)
+        st4(probs + n * C + 4 * static_cast<size_t>(j),
+            make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), nt);
+    }
   }
-  if (t == 0) {
+  const bool in_range = lab >= 0 && static_cast<size_t>(lab) < C;
+  if (BWD ? (own || (t == 0 && !in_range)) : t == 0) {
     double term;
-    if (lab < 0 || static_cast<size_t>(lab) >= C) {
+    if (!in_range) {
       term = __builtin_nan("");  // outside the feeder contract: poison the loss
     } else {
       const float pl = expf(xl - mx) * inv;  // same expression as p[lab]
@@ -968,6 +1014,34 @@ Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, f
   hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, terms, N,
                      static_cast<double>(N), loss);
   return LaunchStatus("SoftmaxXEntFwd");
+}
+
+bool XEntFwdBwdFits(const float* logits, const float* probs, const float* dl, size_t N, size_t C) {
+  return C >= 2048 && C % 4 == 0 && C <= static_cast<size_t>(1024 * 4 * kXentVec) && aligned16(logits) &&
+         (!probs || aligned16(probs)) && aligned16(dl) && N > 0 && N <= 0x7FFFFFFF;
+}
+
+Status SoftmaxXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                         float seed, float* seed_slot, float* dl, size_t N, size_t C, const Ctx& c) {
+  if (!XEntFwdBwdFits(logits, probs, dl, N, C) || !seed_slot)
+    return Status::Fail(kUnitEngine, "SoftmaxXEntFwdBwd: shape or alignment outside the one-pass form");
+  if (c.ws_bytes < N * sizeof(double))
+    return Status::Fail(kUnitEngine, "SoftmaxXEntFwdBwd: workspace too small");
+  double* terms = static_cast<double*>(c.ws);
+  const int nt = StreamPolicy(8 * N * C) ? 1 : 0;
+  const int sp = probs ? 1 : 0;
+  if (C <= static_cast<size_t>(256 * 4 * kXentVec))
+    hipLaunchKernelGGL((xent_fwd_rows_reg<256, true>), dim3(static_cast<unsigned>(N)), dim3(256), 0,
+                       c.stream, logits, labels, probs, N, C, terms, nt, dl, seed, seed_slot, sp);
+  else if (C <= static_cast<size_t>(512 * 4 * kXentVec))
+    hipLaunchKernelGGL((xent_fwd_rows_reg<512, true>), dim3(static_cast<unsigned>(N)), dim3(512), 0,
+                       c.stream, logits, labels, probs, N, C, terms, nt, dl, seed, seed_slot, sp);
+  else
+    hipLaunchKernelGGL((xent_fwd_rows_reg<1024, true>), dim3(static_cast<unsigned>(N)), dim3(1024), 0,
+                       c.stream, logits, labels, probs, N, C, terms, nt, dl, seed, seed_slot, sp);
+  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, terms, N,
+                     static_cast<double>(N), loss);
+  return LaunchStatus("SoftmaxXEntFwdBwd");
 }
 
 size_t KLDistillFwdWorkspace(size_t N) { return N * sizeof(double); }

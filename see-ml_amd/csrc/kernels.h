@@ -335,6 +335,15 @@ Status ClipNorm(float* g, size_t n, float max_norm, const Ctx& c);
 size_t SoftmaxXEntFwdWorkspace(size_t N);
 Status SoftmaxXEntFwd(const float* logits, const int32_t* labels, float* loss, float* probs,
                       size_t N, size_t C, const Ctx& c);
+// SoftmaxXEntFwd, the Fill of the gradient seed (seed_slot = seed) and
+// SoftmaxXEntBwd (dl from those probabilities and the seed) in one pass over
+// the logits, with the three instructions' bits; probs null: not stored (no
+// later reader). Fits: 16-byte aligned rows, C % 4 == 0, 2048 <= C <= 32768;
+// dl, probs, the seed slot and the loss apart from the labels and from each
+// other, and from the logits except dl, which may be the logits exactly.
+bool XEntFwdBwdFits(const float* logits, const float* probs, const float* dl, size_t N, size_t C);
+Status SoftmaxXEntFwdBwd(const float* logits, const int32_t* labels, float* loss, float* probs,
+                         float seed, float* seed_slot, float* dl, size_t N, size_t C, const Ctx& c);
 size_t KLDistillFwdWorkspace(size_t N);
 Status KLDistillFwd(const float* s, const float* t, float* loss, float* p_s, float* p_t, size_t N,
                     size_t C, float T, const Ctx& c);

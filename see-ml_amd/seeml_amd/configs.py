@@ -204,6 +204,9 @@ def make(name: str) -> Workload:
         "c4m": (1000, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
         # c4m at S = 48: row widths and positions that are not powers of two
         "c4m48": (1000, 256, 2, 2, 512, 48, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
+        # c4m over a 2048-token vocabulary: the loss forward and backward run
+        # as one pass over the logits (rows of at least 2048 classes)
+        "c4mv": (2048, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),
         # c4m at rank 128: the LoRA up-projections are dense tile GEMMs
         # (rank > 64) with the Scale and the residual AddEW in their epilogue
         "c4mr": (1000, 256, 2, 2, 512, 128, 2, 128, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),

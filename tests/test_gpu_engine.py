@@ -234,7 +234,7 @@ def test_c5_structure_100_steps_per_tensor(torch_gpu, orc):
     e.close()
 
 
-@pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr", "c5s64"])
+@pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr", "c4mv", "c5s64"])
 def test_bitwise_determinism_and_graph_equals_eager(torch_gpu, name):
     w, p = compile_workload(name)
     runs = []
@@ -649,6 +649,30 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc, cfg):
         lr = r.train_step(x, y)
         assert abs(runs[0][0][s] - lr) <= TOL_STEP * max(abs(lr), 1e-3), (s, runs[0][0][s], lr)
     assert rel_err(runs[0][1], persistent(r, p)) <= TOL_STEP
+
+
+def test_loss_pass_is_planned_and_matches_the_oracle(torch_gpu, orc):
+    """Over a vocabulary of 2048 the loss forward, the seed Fill and the loss
+    backward run as one pass over the logits, P not stored (its only reader
+    is the backward); the graph == eager test above compares that pass with
+    the three launches bit for bit, and here the step's loss and state match
+    the oracle."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c4mv")
+    e = engine(p)
+    x, y = configs.batch(w, 0)
+    lg = e.train_step(x, y)
+    ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+    xp = [i for i, c in enumerate(ch) if c.startswith("one pass with the backward")]
+    assert len(xp) == 1 and ch[xp[0]].endswith("P not stored"), ch
+    assert ch[xp[0] + 1] == ch[xp[0] + 2] == "in loss pass"
+    assert [planner.OP_NAME[p.train[xp[0] + k]["opcode"]] for k in range(3)] == [
+        "SoftmaxXEntFwd", "Fill", "SoftmaxXEntBwd"]
+    r = HostPlanRunner(p, orc)
+    lr = r.train_step(x, y)
+    assert abs(lg - lr) <= TOL_STEP * abs(lr), (lg, lr)
+    assert rel_err(persistent(e, p), persistent(r, p)) <= TOL_STEP
+    e.close()
 
 
 def test_dense_scale_chains_are_planned(torch_gpu):
