@@ -2493,18 +2493,39 @@ class Engine {
   Status TrainStep(const void* input, size_t input_bytes, const void* labels, size_t label_bytes,
                    bool on_device, float* loss) {
     if (on_device) {
-      // One launch stages the device batch and the next step's scalars.
+      // One launch stages a small device batch and the next step's scalars;
+      // a large batch (C2's 134 MB inputs) goes through the runtime's copy,
+      // which moves it faster than the staging kernel's.
       if (Status s = CheckStaged(input, input_bytes, labels, label_bytes, on_device); !s) return s;
       const PlanHeader& h = plan_.header;
-      const bool lab = h.label_kind != 0 && labels && label_bytes;
+      bool lab = h.label_kind != 0 && labels && label_bytes;
+      bool inp = input_bytes != 0;
+      constexpr size_t kKernelCopyMax = size_t{8} << 20;
+      if (inp && input_bytes > kKernelCopyMax) {
+        if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.input_ref), input, input_bytes,
+                                            hipMemcpyDeviceToDevice, stream_),
+                             "input staging");
+            !s)
+          return s;
+        inp = false;
+      }
+      if (lab && label_bytes > kKernelCopyMax) {
+        if (Status s = HipOk(hipMemcpyAsync(arena_ + RefOffset(h.label_ref), labels, label_bytes,
+                                            hipMemcpyDeviceToDevice, stream_),
+                             "label staging");
+            !s)
+          return s;
+        lab = false;
+      }
       const StepScalars sc = MakeStepScalars(plan_.header, step_ + 1);
-      if (Status s = StageStep(&sc, d_scalars_, input_bytes ? input : nullptr,
-                               arena_ + RefOffset(h.input_ref), input_bytes, lab ? labels : nullptr,
+      if (Status s = StageStep(&sc, d_scalars_, inp ? input : nullptr, arena_ + RefOffset(h.input_ref),
+                               inp ? input_bytes : 0, lab ? labels : nullptr,
                                lab ? arena_ + RefOffset(h.label_ref) : nullptr, lab ? label_bytes : 0,
                                stream_);
           !s)
         return s;
       step_ = step_ + 1;
+      loss_posted_ = false;
     } else {
       if (Status s = Stage(input, input_bytes, labels, label_bytes, on_device); !s) return s;
       if (Status s = SetStep(step_ + 1); !s) return s;
