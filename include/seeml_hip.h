@@ -382,6 +382,17 @@ int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const flo
 int seeml_hip_gemm_skinny_group(int kind, const float* x, uint64_t T, uint64_t D,
                                 const float* const* a, uint64_t r, float* const* out, int n,
                                 void* stream);
+/* GEMMs as one tile-group launch (the engine groups a plan's consecutive
+ * independent GEMM launches; tests call it directly): n = 2..4 members of
+ * one layout (0 NN, 1 NT), all on tile config `cfg`; member j is C[j] =
+ * A[j] B[j] of shape (M, N, K) = dims[3j .. 3j + 2], and with addend[j] set
+ * (addend may be null), the fused AddEW out[j] = addend[j] + C[j] with C[j]
+ * not stored. Each output has the bits of its member's own launch. No
+ * reference counterpart: the reference runs each GEMM on its own
+ * (gemm.cc:173-200). */
+int seeml_hip_gemm_group(int layout, int cfg, int n, const float* const* A, const float* const* B,
+                         float* const* C, const uint64_t* dims, const float* const* addend,
+                         float* const* out, void* stream);
 /* GEMM as two launches over column ranges (tests): columns [0, n_split) on
  * tile config `cfg`, the rest on `tail_cfg` (both one split); with `out`,
  * the fused AddEW out = addend + C. n_split = 0: one launch of `cfg`. */

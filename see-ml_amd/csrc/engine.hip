@@ -3879,6 +3879,30 @@ int seeml_hip_gemm_forced(int layout, const float* A, const float* B, float* C, 
                                         : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
   return RunGemm(d, stream, cfg, splits);
 }
+int seeml_hip_gemm_group(int layout, int cfg, int n, const float* const* A, const float* const* B,
+                         float* const* C, const uint64_t* dims, const float* const* addend,
+                         float* const* out, void* stream) {
+  if (n < 2 || n > seeml_hip::kGemmGroupMax || !A || !B || !C || !dims || (layout != 0 && layout != 1) ||
+      cfg < 0 || cfg >= seeml_hip::GemmConfigCount() - 1)
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine, "gemm group: bad arguments"));
+  seeml_hip::GemmDesc ds[seeml_hip::kGemmGroupMax];
+  seeml_hip::GemmPlan ps[seeml_hip::kGemmGroupMax];
+  for (int j = 0; j < n; ++j) {
+    const uint64_t M = dims[3 * j], N = dims[3 * j + 1], K = dims[3 * j + 2];
+    ds[j] = layout == 1 ? seeml_hip::GemmNTDesc(A[j], B[j], C[j], M, N, K)
+                        : seeml_hip::GemmNNDesc(A[j], B[j], C[j], M, N, K);
+    if (addend && addend[j]) {
+      if (!out || !out[j])
+        return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine, "gemm group: addend without out"));
+      ds[j].addend = addend[j];
+      ds[j].out = out[j];
+      ds[j].write_c = false;
+    }
+    ps[j] = seeml_hip::PlanGemmWith(ds[j], cfg, 1);
+  }
+  SEEML_CTX(0);
+  return seeml_hip::Report(seeml_hip::LaunchGemmGroup(ds, ps, n, ctx));
+}
 int seeml_hip_gemm_skinny_dual(const float* x, uint64_t T, uint64_t D, const float* b,
                                uint64_t r_rd, float* dt, const float* t, uint64_t r_cs, float* db,
                                int which, int scaled, float scale, void* stream) {

@@ -198,6 +198,52 @@ def test_gemm_skinny(env, orc, layout, M, N, K):
         assert rel_err(env.H(generic), got) <= TOL_STEP
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 8, 9])
+def test_gemm_group_members_are_bitwise_their_own_launches(env, orc, layout, cfg):
+    """Two to four GEMMs of different (ragged) shapes as one tile-group
+    launch, plain and fused-AddEW members mixed: each member's output has
+    the bits of its own launch on the same tile config (the AddEW's sum
+    those of the GEMM then AddEW) and matches the oracle's GEMM."""
+    import ctypes
+    shapes = [(256, 192, 96), (200, 136, 64), (384, 128, 160), (72, 264, 32)]
+    for n in (2, 3, 4):
+        A, B, C, adds, outs, want, fused = [], [], [], [], [], [], []
+        for j, (M, N, K) in enumerate(shapes[:n]):
+            a = rnd(M * K, 300 + 10 * j + n)
+            b = rnd(K * N, 301 + 10 * j + n)
+            w = np.zeros(M * N, f32)
+            if layout == 0:
+                orc.gemm_nn(a, b, w, M, N, K, None, 0)
+            else:
+                orc.gemm_nt(a, b, w, M, N, K)
+            fz = j % 2 == 1
+            A.append(env.T(a))
+            B.append(env.T(b))
+            C.append(env.T(np.full(M * N, np.nan, f32)))
+            adds.append(env.T(rnd(M * N, 302 + 10 * j + n)) if fz else None)
+            outs.append(env.T(np.full(M * N, np.nan, f32)) if fz else None)
+            want.append(w)
+            fused.append(fz)
+        ptrs = lambda ts: (ctypes.c_void_p * n)(*[t.data_ptr() if t is not None else None for t in ts])
+        dims = (ctypes.c_uint64 * (3 * n))(*[v for sh in shapes[:n] for v in sh])
+        pa, pb, pc, pad, po = ptrs(A), ptrs(B), ptrs(C), ptrs(adds), ptrs(outs)
+        env.call("seeml_hip_gemm_group", layout, cfg, n, ctypes.addressof(pa), ctypes.addressof(pb),
+                 ctypes.addressof(pc), ctypes.addressof(dims), ctypes.addressof(pad), ctypes.addressof(po))
+        for j, (M, N, K) in enumerate(shapes[:n]):
+            lone = env.T(np.full(M * N, np.nan, f32))
+            env.call("seeml_hip_gemm_forced", layout, A[j], B[j], lone, M, N, K, cfg, 1)
+            if fused[j]:
+                lone_sum = env.T(np.full(M * N, np.nan, f32))
+                env.call("seeml_hip_add_ew", adds[j], lone, lone_sum, M * N)
+                assert same_bits(env.H(outs[j]), env.H(lone_sum)), (n, j)
+                assert np.all(np.isnan(env.H(C[j]))), (n, j)  # C is not stored
+            else:
+                got = env.H(C[j])
+                assert same_bits(got, env.H(lone)), (n, j)
+                assert rel_err(got, want[j]) <= TOL_STEP, (n, j)
+
+
 @pytest.mark.parametrize("T,D,r_rd,r_cs,scaled", [
     (8192, 2048, 16, 16, 1), (4096, 512, 8, 8, 0), (300, 260, 5, 16, 1), (257, 1028, 16, 3, 0),
     (256, 256, 1, 1, 1)])
