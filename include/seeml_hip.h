@@ -395,7 +395,8 @@ int seeml_hip_gemm_group(int layout, int cfg, int n, const float* const* A, cons
                          float* const* out, void* stream);
 /* GEMM as two launches over column ranges (tests): columns [0, n_split) on
  * tile config `cfg`, the rest on `tail_cfg` (both one split); with `out`,
- * the fused AddEW out = addend + C. n_split = 0: one launch of `cfg`. */
+ * the fused AddEW out = addend + C, and C not stored when C is null.
+ * n_split = 0: one launch of `cfg`. */
 int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
                                 uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
                                 const float* addend, float* out, void* stream);

@@ -3935,12 +3935,17 @@ int seeml_hip_gemm_skinny_group(int kind, const float* x, uint64_t T, uint64_t D
 int seeml_hip_gemm_forced_split(int layout, const float* A, const float* B, float* C, uint64_t M,
                                 uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
                                 const float* addend, float* out, void* stream) {
+  // With out set and C null, C is not stored (the engine's form of a fused
+  // AddEW whose product is read by nothing else).
+  const bool c_dead = out && !C;
+  if (c_dead) C = out;
   seeml_hip::GemmDesc d = layout == 1   ? seeml_hip::GemmNTDesc(A, B, C, M, N, K)
                           : layout == 2 ? seeml_hip::GemmTNDesc(A, B, C, M, N, K)
                                         : seeml_hip::GemmNNDesc(A, B, C, M, N, K);
   if (addend || out) {
     d.addend = addend;
     d.out = out;
+    d.write_c = !c_dead;
   }
   const seeml_hip::GemmPlan plan =
       n_split > 0 ? seeml_hip::PlanGemmSplit(d, cfg, tail_cfg, static_cast<int64_t>(n_split))

@@ -413,6 +413,82 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
     __syncthreads();
   };
 
+  // Early epilogue loads (kEarly: the 256x128 tile, one workgroup per CU,
+  // whose epilogue has no other workgroup's k loop to hide under; 128x256
+  // has no registers to spare for them in its NN group kernel): issued
+  // ahead of the last stage's MFMAs, so that their latency runs under them,
+  // into registers that take the dead k-loop staging registers' place. A
+  // fused AddEW's addend on a whole tile, or a LoRA epilogue's T and B'
+  // fragments, in one array `ep`: a work item takes at most one of them.
+  // Each addend load's address is a wave-uniform tile base plus a 32-bit
+  // byte offset (per-lane part + wave-uniform part), so loads in flight hold
+  // no 64-bit addresses. The values summed and their order are those of the
+  // loads after the k loop that the other tiles issue: the same bits.
+  // Measured on 8192x2048x2048 / 8192x2048x5504 / 8192x5504x2048 alone:
+  // +AddEW 3-15 us and NT +LoRA 29-85 us less per launch, plain unchanged.
+  constexpr bool kEarly = MT_M == 256 && MT_N == 128;
+  constexpr int kLoraG = 2;  // LoRA k groups held at once: rank <= 16
+  constexpr int kEp = std::max(BM * BN * 16, (BM + BN) * kLoraG * 4);
+  const bool lora_epi = LORA && p.lora_t;
+  const bool addend_early = kEarly && FUSED && !lora_epi && p.out && p.splits == 1 &&
+                            m0 + MT_M <= p.M && n0 + MT_N <= p.N &&
+                            MT_M * p.ldo * 4 < (int64_t{1} << 30);
+  float ep[kEp];
+  auto yv_at = [](int i, int j, int v) { return (i * BN + j) * 16 + v; };
+  auto ta_at = [](int i, int g, int q) { return (i * kLoraG + g) * 4 + q; };
+  auto tb_at = [](int j, int g, int q) { return BM * kLoraG * 4 + (j * kLoraG + g) * 4 + q; };
+  auto load_early = [&]() {
+    if constexpr (FUSED) {
+      if (addend_early) {
+        const char* y_base = reinterpret_cast<const char*>(p.addend + m0 * p.ldo + n0);
+        const uint32_t y_lane = static_cast<uint32_t>(((wm0 + 4 * h) * p.ldo + wn0 + r) * 4);
+#pragma unroll
+        for (int i = 0; i < BM; ++i)
+#pragma unroll
+          for (int j = 0; j < BN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const uint32_t uoff = static_cast<uint32_t>(
+                  ((32 * i + 8 * (v >> 2) + (v & 3)) * p.ldo + 32 * j) * 4);
+              ep[yv_at(i, j, v)] = *reinterpret_cast<const float*>(y_base + (y_lane + uoff));
+            }
+      }
+    }
+    if constexpr (LORA) {
+      if (lora_epi) {
+        // Unconditional loads (a k group beyond the rank reads group 0 and
+        // is zeroed), so that no branch splits the loads in flight.
+        const int ng = p.lora_r / KG;  // 1 or 2
+#pragma unroll
+        for (int i = 0; i < BM; ++i) {
+          const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
+#pragma unroll
+          for (int g = 0; g < kLoraG; ++g) {
+            const int k0 = (g < ng ? g : 0) * KG + 4 * h;
+            const float4 q = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
+            ep[ta_at(i, g, 0)] = g < ng ? q.x : 0.0f;
+            ep[ta_at(i, g, 1)] = g < ng ? q.y : 0.0f;
+            ep[ta_at(i, g, 2)] = g < ng ? q.z : 0.0f;
+            ep[ta_at(i, g, 3)] = g < ng ? q.w : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < BN; ++j) {
+          const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
+#pragma unroll
+          for (int g = 0; g < kLoraG; ++g)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              const int k = (g < ng ? g : 0) * KG + 4 * h + jj;
+              const float x = p.lora_b[k * p.lora_ldb + col];
+              ep[tb_at(j, g, jj)] = g < ng ? x : 0.0f;
+            }
+        }
+      }
+    }
+  };
+
+  int64_t t = 0;
   if (ntiles > 0) {
     sa0.init(p.lda, m0, p.M);
     sb0.init(p.ldb, n0, p.N);
@@ -424,20 +500,38 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
     sb0.store(b_buf(0));
     __syncthreads();
 
-    int64_t t = 0;
     for (; t + 3 < nfull; t += 2) {
       steady(sa0, sb0, sa1, sb1, t, 0);
       steady(sa1, sb1, sa0, sb0, t + 1, 1);
     }
     // The remaining stages (fewer than four): masked loads where needed.
-    for (; t < ntiles; ++t) {
-      const int cur = static_cast<int>(t & 1);
-      if (t + 2 < ntiles) {
-        if (cur) load_any(sa1, sb1, t + 2);
-        else load_any(sa0, sb0, t + 2);
+    if constexpr (!kEarly) {
+      for (; t < ntiles; ++t) {
+        const int cur = static_cast<int>(t & 1);
+        if (t + 2 < ntiles) {
+          if (cur) load_any(sa1, sb1, t + 2);
+          else load_any(sa0, sb0, t + 2);
+        }
+        compute(a_buf(cur), b_buf(cur));
+        if (t + 1 < ntiles) {
+          if (cur) {
+            sa0.store(a_buf(0));
+            sb0.store(b_buf(0));
+          } else {
+            sa1.store(a_buf(1));
+            sb1.store(b_buf(1));
+          }
+          __syncthreads();
+        }
       }
-      compute(a_buf(cur), b_buf(cur));
-      if (t + 1 < ntiles) {
+    } else {
+      for (; t + 1 < ntiles; ++t) {
+        const int cur = static_cast<int>(t & 1);
+        if (t + 2 < ntiles) {
+          if (cur) load_any(sa1, sb1, t + 2);
+          else load_any(sa0, sb0, t + 2);
+        }
+        compute(a_buf(cur), b_buf(cur));
         if (cur) {
           sa0.store(a_buf(0));
           sb0.store(b_buf(0));
@@ -448,6 +542,17 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
         __syncthreads();
       }
     }
+  }
+  if constexpr (kEarly) {
+    // The last stage, with the early epilogue loads in flight under its MFMAs
+    // (one program point for the loads, whether or not there is a stage).
+    // s_waitcnt vmcnt(0) (0x0F70: expcnt and lgkmcnt not waited on). No
+    // k-loop load is pending here; stated, it keeps the compiler from
+    // placing waits on the early loads inside the last stage's MFMAs.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    load_early();
+    __builtin_amdgcn_sched_barrier(0);
+    if (ntiles > 0) compute(a_buf(static_cast<int>(t & 1)), b_buf(static_cast<int>(t & 1)));
   }
 
   // A fused AddEW (GemmKArgs::out; FUSED instantiations, launched with one
@@ -463,28 +568,45 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
     // each block's outputs are stored right after its MFMAs (stores from one
     // base pointer per lane, with no per-element bounds, measured 5% slower:
     // the per-element form spreads them between the next block's MFMAs).
-    constexpr int kLoraG = 2;  // k groups held at once: rank <= 16
     float ta[BM][kLoraG][4], tb[BN][kLoraG][4];
     const int ng = p.lora_r / KG;
+    if constexpr (kEarly) {  // loaded ahead of the last stage
 #pragma unroll
-    for (int i = 0; i < BM; ++i) {
-      const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
+      for (int i = 0; i < BM; ++i)
 #pragma unroll
-      for (int g = 0; g < kLoraG; ++g) {
-        const int k0 = g * KG + 4 * h;
-        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (g < ng) q = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
-        ta[i][g][0] = q.x; ta[i][g][1] = q.y; ta[i][g][2] = q.z; ta[i][g][3] = q.w;
+        for (int g = 0; g < kLoraG; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ta[i][g][q] = ep[ta_at(i, g, q)];
+    } else {
+#pragma unroll
+      for (int i = 0; i < BM; ++i) {
+        const int64_t row = std::min<int64_t>(m0 + wm0 + 32 * i + r, p.M - 1);
+#pragma unroll
+        for (int g = 0; g < kLoraG; ++g) {
+          const int k0 = g * KG + 4 * h;
+          float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (g < ng) q = *reinterpret_cast<const float4*>(p.lora_t + row * p.lora_ldt + k0);
+          ta[i][g][0] = q.x; ta[i][g][1] = q.y; ta[i][g][2] = q.z; ta[i][g][3] = q.w;
+        }
       }
     }
+    if constexpr (kEarly) {
 #pragma unroll
-    for (int j = 0; j < BN; ++j) {
-      const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
+      for (int j = 0; j < BN; ++j)
 #pragma unroll
-      for (int g = 0; g < kLoraG; ++g)
+        for (int g = 0; g < kLoraG; ++g)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          tb[j][g][jj] = g < ng ? p.lora_b[(g * KG + 4 * h + jj) * p.lora_ldb + col] : 0.0f;
+          for (int q = 0; q < 4; ++q) tb[j][g][q] = ep[tb_at(j, g, q)];
+    } else {
+#pragma unroll
+      for (int j = 0; j < BN; ++j) {
+        const int64_t col = std::min<int64_t>(n0 + wn0 + 32 * j + r, p.N - 1);
+#pragma unroll
+        for (int g = 0; g < kLoraG; ++g)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            tb[j][g][jj] = g < ng ? p.lora_b[(g * KG + 4 * h + jj) * p.lora_ldb + col] : 0.0f;
+      }
     }
 #pragma unroll
     for (int i = 0; i < BM; ++i)
@@ -511,6 +633,27 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
         }
       }
     return;
+  }
+  if constexpr (FUSED && kEarly) {
+    if (addend_early) {
+      const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
+      float* oa = p.out + lm * p.ldo + ln;
+      float* ca = C + lm * p.ldc + ln;
+#pragma unroll
+      for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = 32 * i + 8 * (v >> 2) + (v & 3);
+            const float val = dev_act(p.act, p.alpha * acc[i][j][v]);
+            const float sv = p.out_scaled ? p.out_scale * val : val;
+            if (p.write_c) ca[row * p.ldc + 32 * j] = p.c_scaled ? sv : val;
+            const float y = ep[yv_at(i, j, v)];
+            oa[row * p.ldo + 32 * j] = p.addend_first ? y + sv : sv + y;
+          }
+      return;
+    }
   }
   if constexpr (FUSED) {
     if (p.out && p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {

@@ -331,6 +331,12 @@ def test_gemm_column_split_is_bitwise_one_launch(env, layout, M, N, K, tail, n_s
     assert same_bits(outs[0][0], env.H(whole)) and same_bits(outs[1][0], env.H(whole))
     assert same_bits(outs[1][1], outs[0][1])
     assert same_bits(outs[0][1], (Y + env.H(whole)).astype(f32))
+    # C null: the engine's form, C not stored and the same sums.
+    for ns, tl in ((0, 0), (n_split, tail)):
+        o = env.T(np.full(M * N, np.nan, f32))
+        env.call("seeml_hip_gemm_forced_split", layout, env.T(A), env.T(B), None, M, N, K, 2, tl, ns,
+                 env.T(Y), o)
+        assert same_bits(env.H(o), outs[0][1]), ns
 
 
 @pytest.mark.parametrize("layout,M,N,K,r,cfg,tail,n_split", [
