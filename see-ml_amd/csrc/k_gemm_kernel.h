@@ -424,8 +424,9 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
   // byte offset (per-lane part + wave-uniform part), so loads in flight hold
   // no 64-bit addresses. The values summed and their order are those of the
   // loads after the k loop that the other tiles issue: the same bits.
-  // Measured on 8192x2048x2048 / 8192x2048x5504 / 8192x5504x2048 alone:
-  // +AddEW 3-15 us and NT +LoRA 29-85 us less per launch, plain unchanged.
+  // Measured alone on 8192x2048x2048, 8192x2048x5504 and 8192x5504x2048:
+  // the fused AddEW 0-6 us and the NT LoRA epilogue 30-86 us less per
+  // launch than with the loads after the k loop; the plain form unchanged.
   constexpr bool kEarly = MT_M == 256 && MT_N == 128;
   constexpr int kLoraG = 2;  // LoRA k groups held at once: rank <= 16
   constexpr int kEp = std::max(BM * BN * 16, (BM + BN) * kLoraG * 4);
