@@ -366,11 +366,15 @@ class Engine {
   // overwritten, and no byte still holding it when the program ends is one
   // the host reads then (the observed ranges are read only between
   // programs, so bytes overwritten within the program never show the value).
-  bool DeadAfter(int program, size_t k, uint64_t off, uint64_t bytes) const {
+  // Instructions [skip_lo, skip_hi) count with their writes only: a caller
+  // that knows they take the value another way.
+  bool DeadAfter(int program, size_t k, uint64_t off, uint64_t bytes, size_t skip_lo = 0,
+                 size_t skip_hi = 0) const {
     Ranges live{{off, bytes}};  // the bytes still holding the value
     for (size_t j = k + 1; j < depends_[program].size() && !live.empty(); ++j) {
-      for (const auto& r : live)
-        if (Overlaps(depends_[program][j], r.first, r.second)) return false;
+      if (j < skip_lo || j >= skip_hi)
+        for (const auto& r : live)
+          if (Overlaps(depends_[program][j], r.first, r.second)) return false;
       for (const auto& w : writes_[program][j]) {
         Ranges rest;
         for (const auto& r : live) {
@@ -887,6 +891,17 @@ class Engine {
     int rd_mode = 0;
     size_t grp_first = 0, grp_end = 0;
     std::vector<size_t> grp_rowdots;
+    // SiLU recomputed (PlanSiluRecompute). A SwiGLU backward run launches
+    // pw_alt (reading g, not s) when the executed range begins at or before
+    // the SiluFwd at recompute_from; the forward run holding that SiluFwd
+    // skips step cond_step's store (s) when the range ends at or after
+    // cond_until, the backward run's end.
+    static constexpr size_t kNoIndex = ~size_t{0};
+    PointwiseRun pw_alt;
+    uint64_t bytes_alt = 0;
+    size_t recompute_from = kNoIndex;
+    int cond_step = -1;
+    size_t cond_until = 0;
   };
 
   void PlanChains(int program) {
@@ -1017,6 +1032,73 @@ class Engine {
     }
     std::sort(chains_[program].begin(), chains_[program].end(),
               [](const ChainRun& a, const ChainRun& b) { return a.first < b.first; });
+    PlanSiluRecompute(program);
+  }
+
+  // SiLU recomputed in the SwiGLU backward. Its pointwise run (ds = dh u,
+  // du = dh s, dg = silu'(ds, g)) reads s = silu(g), which the forward's
+  // SiluFwd stored from g. Where that SiluFwd is the last writer of any
+  // byte of s before the run and nothing in between writes g, the run can
+  // form du = dh silu(g) from g, which it reads anyway: the same function
+  // of the same bits, so the same du, and s is not read (4n bytes). If the
+  // forward's own pointwise run then leaves s to no other reader, it skips
+  // s's store (4n bytes more). Both hold only when one executed range holds
+  // the SiluFwd and the whole backward run (the host touches nothing in
+  // between): the backward run recomputes when the range begins at or
+  // before the SiluFwd, and the forward run skips the store when the range
+  // ends at or after the backward run, which then recomputes. A range that
+  // splits them keeps s stored and read.
+  void PlanSiluRecompute(int program) {
+    const auto& prog = plan_.program[program];
+    auto& chains = chains_[program];
+    for (ChainRun& r : chains) {
+      if (r.kind != ChainKind::kPointwise || r.pw.program != kPwSwiGluBwd || r.count != 3) continue;
+      const UpdateInstruction& m2 = prog[r.first + 1];  // du = dh * s
+      const UpdateInstruction& sb = prog[r.first + 2];  // dg = silu'(ds, g)
+      const uint64_t sref = m2.in[1], gref = sb.in[1];
+      if (IsRodataRef(sref)) continue;
+      const uint64_t bytes = r.pw.n * sizeof(float);
+      const uint64_t soff = RefOffset(sref);
+      const bool g_rod = IsRodataRef(gref);
+      const uint64_t goff = g_rod ? 0 : RefOffset(gref);
+      if (!g_rod && goff < soff + bytes && soff < goff + bytes) continue;
+      size_t f = ChainRun::kNoIndex;
+      bool ok = true;
+      for (size_t j = r.first; j-- > 0;) {
+        const Ranges& w = writes_[program][j];
+        if (Overlaps(w, soff, bytes)) {
+          const UpdateInstruction& a = prog[j];
+          if (static_cast<Op>(a.opcode) == Op::kSiluFwd && a.in[1] == sref && a.in[0] == gref &&
+              a.out[0] == r.pw.n)
+            f = j;
+          break;
+        }
+        if (!g_rod && Overlaps(w, goff, bytes)) {
+          ok = false;
+          break;
+        }
+      }
+      if (!ok || f == ChainRun::kNoIndex) continue;
+      r.pw_alt = r.pw;
+      r.pw_alt.program = kPwSwiGluBwdRecompute;
+      r.pw_alt.in[2] = RP(gref);
+      r.pw_alt.in[3] = nullptr;
+      r.recompute_from = f;
+      r.bytes_alt = r.bytes - bytes;
+      // The forward run holding the SiluFwd: s's store is needed only by
+      // this backward run's plain form when nothing else reads it.
+      for (ChainRun& fr : chains) {
+        if (fr.kind != ChainKind::kPointwise || f < fr.first || f >= fr.first + fr.count) continue;
+        const int st = static_cast<int>(f - fr.first);
+        if (fr.pw.out[st] != WP(sref) || fr.cond_step >= 0) break;
+        if (!DeadAfter(program, fr.first + fr.count - 1, soff, bytes, r.first, r.first + r.count))
+          break;
+        fr.cond_step = st;
+        fr.cond_until = r.first + r.count;
+        fr.bytes_alt = fr.bytes - bytes;
+        break;
+      }
+    }
   }
 
   bool BuildPointwiseRun(int program, size_t i, const std::vector<char>& taken, ChainRun* out) {
@@ -2106,7 +2188,15 @@ class Engine {
         }
         return LaunchGemm(run.d, plans_[program][run.first], c);
       }
-      case ChainKind::kPointwise: return LaunchPointwiseRun(run.pw, c);
+      case ChainKind::kPointwise:
+        if (run.recompute_from != ChainRun::kNoIndex && begin <= run.recompute_from)
+          return LaunchPointwiseRun(run.pw_alt, c);
+        if (run.cond_step >= 0 && end >= run.cond_until) {
+          PointwiseRun pw = run.pw;
+          pw.out[run.cond_step] = nullptr;
+          return LaunchPointwiseRun(pw, c);
+        }
+        return LaunchPointwiseRun(run.pw, c);
       case ChainKind::kScaleFold:
         for (size_t k = run.first + 1; k < run.first + run.count;) {
           Status s = Status::Ok();
@@ -3369,8 +3459,15 @@ class Engine {
         default: return "in chain";
       }
     }
-    if (run && run->kind == ChainKind::kPointwise)
-      return "pointwise run of " + std::to_string(run->count) + " B=" + std::to_string(run->bytes);
+    if (run && run->kind == ChainKind::kPointwise) {
+      // As a whole program launches it (the bytes its HBM traffic counts).
+      const std::string head = "pointwise run of " + std::to_string(run->count);
+      if (run->recompute_from != ChainRun::kNoIndex)
+        return head + " (SiLU recomputed) B=" + std::to_string(run->bytes_alt);
+      if (run->cond_step >= 0)
+        return head + " (SiLU output not stored) B=" + std::to_string(run->bytes_alt);
+      return head + " B=" + std::to_string(run->bytes);
+    }
     if (run && run->kind == ChainKind::kRowAdd)
       return run->ra.store_dx ? "with the next AddEW (dx stored)" : "with the next AddEW";
     if (run && run->kind == ChainKind::kAddRow)

@@ -148,7 +148,13 @@ constexpr PwProg kPwProgs[] = {
     {3, 3, {PwOp::kAdd, PwOp::kGeluBwd, PwOp::kScale}, {0, 4, 5}, {1, 2, 5}},
     // LoRA branch scaled and added (when no skinny GEMM chain absorbed it)
     {2, 2, {PwOp::kScale, PwOp::kAdd}, {0, 1}, {0, 4}},
+    // SwiGLU backward over (dh, u, g): du = dh * silu(g) from g, whose
+    // SiluFwd output s it would otherwise read (same function, same bits)
+    {3, 3, {PwOp::kMul, PwOp::kMulSilu, PwOp::kSiluBwd}, {0, 0, 4}, {1, 2, 2}},
 };
+static_assert(kPwProgs[kPwSwiGluBwd].op[2] == PwOp::kSiluBwd &&
+                  kPwProgs[kPwSwiGluBwdRecompute].op[1] == PwOp::kMulSilu,
+              "the SwiGLU backward programs' indices");
 constexpr int kNumPwProgs = sizeof(kPwProgs) / sizeof(kPwProgs[0]);
 
 template <PwOp OP>
@@ -162,6 +168,7 @@ __device__ __forceinline__ float PwApply(float a, float b, float alpha) {
   else if constexpr (OP == PwOp::kGeluBwd) return GeluBwdF()(a, b);
   else if constexpr (OP == PwOp::kSilu) return SiluF()(a);
   else if constexpr (OP == PwOp::kSiluBwd) return SiluBwdF()(a, b);
+  else if constexpr (OP == PwOp::kMulSilu) return MulF()(a, SiluF()(b));
   else return a;  // kCopy
 }
 
@@ -727,9 +734,10 @@ Status LaunchPointwiseRun(const PointwiseRun& r, const Ctx& c) {
     case 2: LaunchPw<2>(r, nv, nt, grid, c.stream); break;
     case 3: LaunchPw<3>(r, nv, nt, grid, c.stream); break;
     case 4: LaunchPw<4>(r, nv, nt, grid, c.stream); break;
-    default: LaunchPw<5>(r, nv, nt, grid, c.stream); break;
+    case 5: LaunchPw<5>(r, nv, nt, grid, c.stream); break;
+    default: LaunchPw<6>(r, nv, nt, grid, c.stream); break;
   }
-  static_assert(kNumPwProgs == 6, "one launch case per program");
+  static_assert(kNumPwProgs == 7, "one launch case per program");
   return LaunchStatus("pointwise run");
 }
 

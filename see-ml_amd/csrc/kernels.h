@@ -242,7 +242,9 @@ GemmDesc GemmTNDesc(const float* A, const float* B, float* C, int64_t M, int64_t
 // run's. The kernels are compiled per program (PwProgramOf: the wirings the
 // compiler's lowering produces); out[j] receives step j's result, or nothing
 // when null (dead, or overwritten later in the run).
-enum class PwOp : int { kAdd, kMul, kScale, kRelu, kReluBwd, kGelu, kGeluBwd, kSilu, kSiluBwd, kCopy };
+// kMulSilu: a * silu(b), the product with a SiLU output formed from its
+// input (a recomputed SiLU; no instruction maps to it).
+enum class PwOp : int { kAdd, kMul, kScale, kRelu, kReluBwd, kGelu, kGeluBwd, kSilu, kSiluBwd, kCopy, kMulSilu };
 inline constexpr int kPwIn = 4, kPwOps = 4;
 struct PwStep {
   PwOp op = PwOp::kCopy;
@@ -257,6 +259,9 @@ struct PointwiseRun {
 };
 // Index of the compiled program for these steps over nin inputs, or -1.
 int PwProgramOf(int nin, const PwStep* steps, int nops);
+// The SwiGLU backward's programs: over (dh, u, s, g), and over (dh, u, g)
+// with s = silu(g) formed in registers (the same du bits).
+inline constexpr int kPwSwiGluBwd = 1, kPwSwiGluBwdRecompute = 6;
 Status LaunchPointwiseRun(const PointwiseRun& run, const Ctx& c);
 
 Status AddEW(const float* x, const float* y, float* out, size_t n, const Ctx& c);

@@ -708,6 +708,13 @@ def test_fusions_are_planned(torch_gpu):
     for i in heads:
         k = int(ch[i].split()[3])
         assert all(c == "in pointwise run" for c in ch[i + 1:i + k])
+    # the SwiGLU backward forms silu(g) from g rather than reading the stored
+    # s, and the forward's run then stores no s
+    rec = [i for i in heads if "(SiLU recomputed)" in ch[i]]
+    skip = [i for i in heads if "(SiLU output not stored)" in ch[i]]
+    assert rec and len(skip) == len(rec), ch
+    assert all(planner.OP_NAME[p.train[i]["opcode"]] == "SiluFwd" for i in skip)
+    assert all(planner.OP_NAME[p.train[i + 2]["opcode"]] == "SiluBwd" for i in rec)
     # Scales folded into the skinny GEMMs that stream their output
     folds = [i for i, c in enumerate(ch) if c == "in the next GEMMs' loads"]
     assert folds, ch
