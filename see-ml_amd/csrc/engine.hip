@@ -3064,8 +3064,20 @@ class Engine {
       }
       const Ctx c = MakeCtx();
       const double flops = 2.0 * static_cast<double>(d.M) * d.N * d.K;
-      for (const auto& a : arms)  // one untimed warm-up launch per arm
-        if (Status s = LaunchGemm(d, a, c); !s) { result = s; break; }
+      // One warm-up launch per arm, timed: a pull of an arm then times
+      // enough back-to-back launches to fill ~0.2 ms (at most 16), so that
+      // the short GEMMs (the K = rank up-projections, ~20 us) are ranked by
+      // more than one launch's event-timing noise.
+      std::vector<int> reps(arms.size(), 1);
+      for (size_t a = 0; a < arms.size() && result; ++a) {
+        (void)hipEventRecord(t0, stream_);
+        if (Status s = LaunchGemm(d, arms[a], c); !s) { result = s; break; }
+        (void)hipEventRecord(t1, stream_);
+        (void)hipEventSynchronize(t1);
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, t0, t1);
+        if (ms > 0.0f) reps[a] = std::clamp(static_cast<int>(0.2f / ms), 1, 16);
+      }
       if (!result) break;
       // Rewards are the fraction of fp32 MFMA peak (UCB1's [0, 1] scale);
       // every arm is pulled at least twice.
@@ -3074,11 +3086,14 @@ class Engine {
       for (int t = 0; t < trials; ++t) {
         const size_t arm = bandit.Select();
         (void)hipEventRecord(t0, stream_);
-        if (Status s = LaunchGemm(d, arms[arm], c); !s) { result = s; break; }
+        for (int r = 0; r < reps[arm] && result; ++r)
+          if (Status s = LaunchGemm(d, arms[arm], c); !s) result = s;
+        if (!result) break;
         (void)hipEventRecord(t1, stream_);
         (void)hipEventSynchronize(t1);
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, t0, t1);
+        ms /= static_cast<float>(reps[arm]);
         bandit.Update(arm, ms > 0.0f ? flops / (ms * 1e-3) / kPeakFp32MfmaFlops : 0.0);
       }
       if (!result) break;
