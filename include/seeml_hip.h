@@ -411,6 +411,15 @@ int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float
                                uint64_t N, uint64_t K, int cfg, int tail_cfg, uint64_t n_split,
                                const float* t, const float* bl, uint64_t r, int scaled,
                                float scale, int y_first, void* stream);
+/* GEMM with a Scale folded into its streamed operand's loads (tests): C =
+ * A B with the stream read as fl(scale * x), on tile config `cfg` with
+ * `splits` split-K slices. layout 1: NT rowdot shape (N <= 64, A the
+ * stream); layout 2: TN colsum shape with M <= 64 (B the stream). Same bits
+ * as a Scale into a buffer, then the GEMM on that plan. No reference
+ * counterpart: the reference runs the Scale and the GEMM (gemm.cc:173-200). */
+int seeml_hip_gemm_forced_scaled(int layout, const float* A, const float* B, float* C, uint64_t M,
+                                 uint64_t N, uint64_t K, int cfg, int splits, float scale,
+                                 void* stream);
 int seeml_hip_gemm_config_count(void);
 /* Name of tile config `cfg` ("MTMxMTNxKT/wWMxWN"), "?" when out of range. */
 const char* seeml_hip_gemm_config_name(int cfg);

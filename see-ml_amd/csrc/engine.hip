@@ -1191,11 +1191,13 @@ class Engine {
     return true;
   }
 
-  // Scale folds: a Scale s = alpha x whose only readers are the skinny
-  // rowdot / colsum GEMMs right after it, each streaming exactly s. Those
-  // kernels then read x and scale each element as loaded (the same float
-  // product), and the Scale launches nothing. Conditions: s is dead after the
-  // last of them; they write neither x nor s; x is 16-byte aligned like s.
+  // Scale folds: a Scale s = alpha x whose only readers are the rowdot /
+  // colsum GEMMs right after it, each streaming exactly s, on the skinny
+  // kernels or on a tile plan with scaled loads (GemmScaledOk: the rank-64
+  // LoRA backward's dt = s B^T and dB = t^T s). Those kernels then read x
+  // and scale each element as loaded (the same float product), and the
+  // Scale launches nothing. Conditions: s is dead after the last of them;
+  // they write neither x nor s; x is 16-byte aligned like s.
   void PlanScaleFolds(int program) {
     const auto& prog = plan_.program[program];
     std::vector<char> taken(prog.size(), 0);
@@ -1212,12 +1214,18 @@ class Engine {
       if (IsRodataRef(sref) || !aligned16(RP(x))) continue;
       size_t j = i + 1;
       for (; j < prog.size() && !taken[j] && IsGemmOp(prog[j].opcode); ++j) {
-        if (plans_[program][j].cfg != GemmSkinnyConfig()) break;
         const GemmDesc d = DescOf(prog[j]);
         int64_t elems = 0;
         const void* stream = SkinnyStream(d, &elems);
         if (stream != WP(sref) || static_cast<uint64_t>(elems) != sc.out[0]) break;
         if ((d.A == stream ? d.B : d.A) == WP(sref)) break;  // s as the small operand too
+        if (plans_[program][j].cfg != GemmSkinnyConfig()) {
+          GemmDesc f = d;
+          if (f.A == stream) f.A = RP(x);
+          else f.B = RP(x);
+          f.scale_stream = true;
+          if (!GemmScaledOk(f, plans_[program][j])) break;
+        }
         bool clash = false;
         for (const auto& w : writes_[program][j])
           if (Overlaps(Ranges{w}, RefOffset(sref), bytes) ||
@@ -3451,6 +3459,10 @@ class Engine {
       if (pair >= 0 && pair >= static_cast<int64_t>(run->first) &&
           pair < static_cast<int64_t>(run->first + run->count))
         return pair > static_cast<int64_t>(idx) ? "skinny/dual dt+dB scaled loads" : "in the dual pass";
+      const GemmPlan& gp = plans_[program][idx];
+      if (gp.cfg != GemmSkinnyConfig())
+        return std::string(GemmConfigName(gp.cfg)) + " splits=" + std::to_string(gp.splits) +
+               " scaled loads";
       return std::string(SkinnyKindName(SkinnyKindOf(DescOf(plan_.program[program][idx])))) +
              " scaled loads";
     }
@@ -4091,6 +4103,23 @@ int seeml_hip_gemm_forced_lora(int layout, const float* A, const float* B, float
   if (n_split > 0 && plan.n_split != static_cast<int64_t>(n_split))
     return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
                                                      "Gemm: the column split does not apply to this GEMM"));
+  SEEML_CTX(plan.ws_bytes);
+  return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
+}
+int seeml_hip_gemm_forced_scaled(int layout, const float* A, const float* B, float* C, uint64_t M,
+                                 uint64_t N, uint64_t K, int cfg, int splits, float scale,
+                                 void* stream) {
+  if (layout != 1 && layout != 2)
+    return seeml_hip::Report(seeml_hip::Status::Fail(seeml_hip::kUnitEngine,
+                                                     "Gemm: scaled loads take layout 1 (NT) or 2 (TN)"));
+  seeml_hip::GemmDesc d = layout == 1 ? seeml_hip::GemmNTDesc(A, B, C, M, N, K)
+                                      : seeml_hip::GemmTNDesc(A, B, C, M, N, K);
+  d.scale_stream = true;
+  d.stream_scale = scale;
+  const seeml_hip::GemmPlan plan = seeml_hip::PlanGemmWith(d, cfg, splits);
+  if (!seeml_hip::GemmScaledOk(d, plan))
+    return seeml_hip::Report(seeml_hip::Status::Fail(
+        seeml_hip::kUnitEngine, "Gemm: no scaled-load plan for this shape and tile config"));
   SEEML_CTX(plan.ws_bytes);
   return seeml_hip::Report(seeml_hip::LaunchGemm(d, plan, ctx));
 }

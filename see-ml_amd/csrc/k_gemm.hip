@@ -275,6 +275,7 @@ Status PrepareKArgs(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx, Gem
   a.lora_ldb = d.lora_ldb;
   a.lora_r = d.lora_r;
   a.lora_y_first = d.lora_y_first ? 1 : 0;
+  a.op_scale = d.scale_stream ? d.stream_scale : 1.0f;
 
   *grid = dim3(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                static_cast<unsigned>(d.batch));
@@ -314,8 +315,9 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     if (Status s = LaunchGemm(left, pl, ctx); !s) return s;
     return LaunchGemm(right, pr, ctx);
   }
-  if (d.scale_stream && plan.cfg != kNumCfgs)
-    return Status::Fail(kUnitEngine, "Gemm: a scaled stream needs the skinny kernels");
+  if (d.scale_stream && plan.cfg != kNumCfgs && !GemmScaledOk(d, plan))
+    return Status::Fail(kUnitEngine,
+                        "Gemm: a scaled stream needs the skinny kernels or a scaled tile config");
   if (plan.cfg == kNumCfgs) {
     if (d.out) return Status::Fail(kUnitEngine, "Gemm: the skinny kernels take no fused AddEW");
     if (ctx.ws_bytes < SkinnyWorkspace(d))
@@ -344,7 +346,11 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   int cfg = 0;
   bool vec = false;
   if (Status s = PrepareKArgs(d, plan, ctx, &a, &grid, &cfg, &vec); !s) return s;
-  if (d.b_int8) {
+  if (d.scale_stream) {  // GemmScaledOk: NT with A the stream, or TN with B
+    const bool launched = d.a_kc ? gemm::LaunchScaledNT(cfg, grid, ctx.stream, a)
+                                 : gemm::LaunchScaledTN(cfg, grid, ctx.stream, a);
+    if (!launched) return Status::Fail(kUnitEngine, "Gemm: no scaled-load kernel for this tile config");
+  } else if (d.b_int8) {
     gemm::LaunchQ8(cfg, d.b_kc, grid, ctx.stream, a);
   } else if (d.a_kc && !d.b_kc) {
     gemm::LaunchNN(cfg, vec, grid, ctx.stream, a);
@@ -360,6 +366,18 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
     return LaunchStatus("Gemm(split-K reduce)");
   }
   return Status::Ok();
+}
+
+bool GemmScaledOk(const GemmDesc& d, const GemmPlan& plan) {
+  if (plan.n_split != 0 || !gemm::ScaledCfg(plan.cfg) || !GemmVecForm(d) || d.out || d.lora_t ||
+      d.b_int8 || d.batch != 1 || d.causal != Causal::kNone)
+    return false;
+  int64_t elems = 0;
+  const void* stream = SkinnyStream(d, &elems);
+  if (!stream) return false;
+  if (d.a_kc && d.b_kc) return stream == d.A;
+  if (!d.a_kc && !d.b_kc) return stream == d.B;
+  return false;
 }
 
 bool GemmLoraCfgOk(int cfg, bool b_kc) {

@@ -106,6 +106,9 @@ struct GemmKArgs {
   int64_t lora_ldt, lora_ldb;
   int lora_r;
   int lora_y_first;
+  // A Scale folded into the operand loads (GemmDesc::scale_stream, the
+  // SCL instantiations): the scaled operand is read as fl(op_scale * x).
+  float op_scale;
 };
 
 // Tile configurations (the autotuner's arms).
@@ -134,14 +137,24 @@ inline constexpr int kCfgDefault = 0, kCfgSmall = 5, kCfgSkinnyN = 6, kCfgSkinny
 // !VEC (int8 B, odd shapes): element loads with an in-range mask applied at
 // the LDS store. Both forms are branch-free per element, so a stage's loads
 // are all in flight together and the first wait is at the LDS store.
-template <int MT, int KT, bool KC, typename T, int NT, bool VEC>
+//
+// SC (VEC only): every loaded element in range is scaled, fl(sc * x), as a
+// Scale instruction would have stored it; zeros past the reduction's end
+// stay +0. A whole stage is scaled at its LDS store, where its loads are
+// waited for anyway (scaled as loaded, each stage's loads would be waited
+// for at once, a stage early: 2.5x slower on the rank-64 shapes); a final
+// partial stage is scaled as loaded, under its in-range masks.
+template <int MT, int KT, bool KC, typename T, int NT, bool VEC, bool SC = false>
 struct Stage {
   static constexpr int kVecs = MT * KT / 4;
   static constexpr int kPer = kVecs / NT;
   static_assert(kVecs % NT == 0 && kPer * 4 <= 64, "stage shape");
+  static_assert(!SC || VEC, "scaled loads need the vector form");
   float r[kPer][4];
   uint32_t off[kPer];  // VEC: element offset of vector i from the stage origin
   uint64_t ok;         // !VEC: bit 4i+e set when element e of vector i is in range
+  float sc;            // SC: the factor
+  bool pend;           // SC: loaded unscaled (a whole stage), scaled at the store
 
   __device__ __forceinline__ static void coords(int v, int& o, int& k) {
     if constexpr (KC) {
@@ -174,6 +187,7 @@ struct Stage {
       const float4 q = *reinterpret_cast<const float4*>(org + off[i]);
       r[i][0] = q.x; r[i][1] = q.y; r[i][2] = q.z; r[i][3] = q.w;
     }
+    if constexpr (SC) pend = true;
   }
 
   // Any stage: k beyond ke (and, for !VEC, rows beyond oe) read as zero.
@@ -191,7 +205,9 @@ struct Stage {
           coords(static_cast<int>(threadIdx.x) + i * NT, o, k);
           const bool in = k < kvalid;  // a KC vector is wholly in or out (K % 4 == 0)
           const int64_t back = KC ? k : static_cast<int64_t>(k) * ld;
-          const float4 q = *reinterpret_cast<const float4*>(org + (off[i] - (in ? 0 : back)));
+          float4 q = *reinterpret_cast<const float4*>(org + (off[i] - (in ? 0 : back)));
+          if constexpr (SC) q = make_float4(sc * q.x, sc * q.y, sc * q.z, sc * q.w);
+          if constexpr (SC) pend = false;
           r[i][0] = in ? q.x : 0.0f;
           r[i][1] = in ? q.y : 0.0f;
           r[i][2] = in ? q.z : 0.0f;
@@ -226,6 +242,8 @@ struct Stage {
       float4 q;
       if constexpr (VEC) {
         q = make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
+        if constexpr (SC)
+          if (pend) q = make_float4(sc * q.x, sc * q.y, sc * q.z, sc * q.w);
       } else {
         q.x = (ok >> (4 * i + 0)) & 1 ? r[i][0] : 0.0f;
         q.y = (ok >> (4 * i + 1)) & 1 ? r[i][1] : 0.0f;
@@ -269,8 +287,9 @@ __device__ __forceinline__ uint32_t XcdLogical(uint32_t lin, uint32_t total) {
 // into (tile, split slice, batch z) over `nslices` slices. FUSED and LORA
 // compile those epilogues in; each applies to a work item whose arguments
 // ask for it (p.out / p.lora_t set), any other takes the plain write-back.
+// SCL: a Scale folded into the loads of A (1) or B (2), factor p.op_scale.
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED, bool LORA>
+          bool VEC, bool SCHED, bool FUSED, bool LORA, int SCL = 0>
 __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32_t nslices) {
   using BT = typename std::conditional<B_I8, int8_t, float>::type;
   constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -331,8 +350,8 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   constexpr bool kVecB = VEC && !B_I8;
-  using StageA = Stage<MT_M, KT, A_KC, float, NT, VEC>;
-  using StageB = Stage<MT_N, KT, B_KC, BT, NT, kVecB>;
+  using StageA = Stage<MT_M, KT, A_KC, float, NT, VEC, SCL == 1>;
+  using StageB = Stage<MT_N, KT, B_KC, BT, NT, kVecB, SCL == 2>;
   // Two register sets: stage s is loaded into set s % 2 two iterations
   // before it is computed, stored to LDS buffer s % 2 one iteration before.
   StageA sa0, sa1;
@@ -495,6 +514,8 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
     sb0.init(p.ldb, n0, p.N);
     sa1.init(p.lda, m0, p.M);
     sb1.init(p.ldb, n0, p.N);
+    if constexpr (SCL == 1) sa0.sc = sa1.sc = p.op_scale;
+    if constexpr (SCL == 2) sb0.sc = sb1.sc = p.op_scale;
     load_any(sa0, sb0, 0);
     if (ntiles > 1) load_any(sa1, sb1, 1);
     sa0.store(a_buf(0));
@@ -745,12 +766,13 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
 }
 
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED, bool LORA = false>
+          bool VEC, bool SCHED, bool FUSED, bool LORA = false, int SCL = 0>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
   const uint32_t tiles = static_cast<uint32_t>(p.tiles_m) * static_cast<uint32_t>(p.tiles_n);
   const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const uint32_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
-  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, B_I8, VEC, SCHED, FUSED, LORA>(p, L, gridDim.y);
+  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, B_I8, VEC, SCHED, FUSED, LORA, SCL>(
+      p, L, gridDim.y);
 }
 
 // A GEMM group: up to kMaxGroup independent GEMMs of one tile config and
@@ -861,6 +883,32 @@ bool LaunchGroupVariant(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& 
 #undef SEEML_GROUP_CASE
 }
 
+// Tile configs with scaled-load instantiations (LaunchScaledVariant): the
+// small tiles the rank-64 LoRA backward's dt = s du B^T (NT, A scaled) and
+// dB = t^T (s du) (TN, B scaled) run on.
+inline constexpr bool ScaledCfg(int cfg) { return cfg == 4 || cfg == 5 || (cfg >= 8 && cfg <= 11); }
+
+template <bool A_KC, bool B_KC, int SCL>
+bool LaunchScaledVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+#define SEEML_SCALED_CASE(I, MM, NN, KK, WM_, WN_)                                                     \
+  case I:                                                                                            \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, false, true, true, false, false, \
+                                         SCL>),                                                      \
+                       grid, dim3(kCfgs[I].threads), 0, s, a);                                       \
+    return true;
+  switch (cfg) {
+    SEEML_SCALED_CASE(4, 128, 64, 32, 2, 2)
+    SEEML_SCALED_CASE(5, 64, 64, 32, 2, 2)
+    SEEML_SCALED_CASE(8, 64, 128, 32, 2, 2)
+    SEEML_SCALED_CASE(9, 128, 64, 32, 4, 1)
+    SEEML_SCALED_CASE(10, 128, 128, 16, 2, 2)
+    SEEML_SCALED_CASE(11, 64, 128, 16, 2, 2)
+    default:
+      return false;
+  }
+#undef SEEML_SCALED_CASE
+}
+
 // Per-layout entry points, one instantiation unit each (built in parallel).
 void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
 void LaunchNT(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
@@ -870,6 +918,10 @@ void LaunchQ8(int cfg, bool b_kc, dim3 grid, hipStream_t s, const GemmKArgs& a);
 // config without a group kernel.
 bool LaunchGroupNN(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g);
 bool LaunchGroupNT(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g);
+// Scaled-load launches: NT with A scaled, TN with B scaled; false for a
+// config without the instantiation.
+bool LaunchScaledNT(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a);
+bool LaunchScaledTN(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a);
 
 }  // namespace gemm
 }  // namespace seeml_hip

@@ -111,9 +111,10 @@ struct GemmDesc {
   int64_t lora_ldt = 0, lora_ldb = 0;
   int lora_r = 0;
   bool lora_y_first = true;
-  // A Scale folded into the skinny rowdot / colsum kernels: their streamed
-  // operand (rowdot: A; colsum: the [K, W] one) is read as
-  // fl(stream_scale * x), element by element, as the Scale would have stored it.
+  // A Scale folded into the skinny rowdot / colsum kernels, or the tile
+  // plans GemmScaledOk admits: their streamed operand (rowdot: A; colsum:
+  // the [K, W] one) is read as fl(stream_scale * x), element by element, as
+  // the Scale would have stored it.
   bool scale_stream = false;
   float stream_scale = 1.0f;
 };
@@ -154,6 +155,11 @@ const char* GemmConfigName(int cfg);
 Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx);
 // Tile configs whose kernels take the LoRA epilogue (GemmDesc::lora_t).
 bool GemmLoraCfgOk(int cfg, bool b_kc);
+// A tile plan that takes GemmDesc::scale_stream: a rowdot-shaped NT GEMM
+// (A the stream) or a colsum-shaped TN GEMM with B the stream, on a small
+// tile config with scaled-load kernels, one launch (no column split), the
+// 16-byte-load form and a plain epilogue.
+bool GemmScaledOk(const GemmDesc& d, const GemmPlan& plan);
 // GEMM groups: 2..4 GEMMs launched as one kernel, each output with the bits
 // of its own launch. Fits: one tile config with a group kernel for all,
 // each unsplit (one slice, no column split), unbatched, non-causal, in the

@@ -199,6 +199,10 @@ def make(name: str) -> Workload:
         "c5s": (1000, 128, 2, 4, 512, 64, 2, 16, (), 1e-3, "layer", "gelu"),
         # C5's rank 64 on every MatMul (the head included), reduced
         "c5s64": (1000, 128, 2, 4, 512, 64, 2, 64, (), 1e-3, "layer", "gelu"),
+        # rank 64 at widths where the backward's dt = (s du) B^T and
+        # dB = t^T (s du) are rowdot / colsum shapes on tile plans: the Scale
+        # folds into their loads
+        "c5m64": (1000, 256, 2, 4, 512, 128, 2, 64, (), 1e-3, "layer", "gelu"),
         # head widths 64 and 128: the fused attention kernels' shapes
         "c3m": (512, 128, 2, 2, 192, 64, 4, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),
         "c4m": (1000, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),

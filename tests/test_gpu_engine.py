@@ -234,7 +234,7 @@ def test_c5_structure_100_steps_per_tensor(torch_gpu, orc):
     e.close()
 
 
-@pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr", "c4mv", "c5s64"])
+@pytest.mark.parametrize("name", ["c1", "c3s", "c4m", "c4mr", "c4mv", "c5s64", "c5m64"])
 def test_bitwise_determinism_and_graph_equals_eager(torch_gpu, name):
     w, p = compile_workload(name)
     runs = []
@@ -748,6 +748,28 @@ def test_fusions_are_planned(torch_gpu):
         c = e.gemm_choice(PROGRAM_TRAIN, i)
         assert not (c.startswith("in ") or "AddEW" in c or "run of" in c or "chain of" in c or
                     "pair" in c or "group" in c), c
+    e.close()
+
+
+def test_scale_folds_into_rank_64_tile_gemms(torch_gpu):
+    """At rank 64 the LoRA backward's dt = (s du) B^T and dB = t^T (s du)
+    run on tile plans; the Scale s du folds into their loads (the Scale
+    launches nothing, the consumers report a tile config with scaled loads),
+    and the graph == eager test above compares that against the Scale and
+    the GEMMs run one by one."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c5m64")
+    x, y = configs.batch(w, 0)
+    e = engine(p)
+    e.train_step(x, y)
+    ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+    folds = [i for i, c in enumerate(ch) if c == "in the next GEMMs' loads"]
+    assert folds, ch
+    tiled = [i for i, c in enumerate(ch) if c.endswith(" scaled loads") and not c.startswith("skinny")]
+    assert len(tiled) >= 2 * len(folds) - 2, ch
+    for i in folds:
+        assert planner.OP_NAME[p.train[i]["opcode"]] == "Scale"
+        assert ch[i + 1].endswith("scaled loads") and ch[i + 2].endswith("scaled loads"), ch[i:i + 3]
     e.close()
 
 

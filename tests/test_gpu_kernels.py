@@ -105,6 +105,43 @@ def test_gemm_every_tile_config_and_split(env, orc, layout):
             assert rel_err(env.H(out), want) <= TOL_STEP, (cfg, splits)
 
 
+@pytest.mark.parametrize("layout,M,N,K", [(1, 512, 64, 512), (1, 300, 64, 292), (1, 256, 48, 1024),
+                                           (2, 64, 512, 512), (2, 48, 260, 300), (2, 64, 136, 1024)])
+def test_gemm_scaled_loads_are_bitwise_the_scale_then_the_gemm(env, orc, layout, M, N, K):
+    """A Scale folded into a tile GEMM's streamed operand (the rank-64 LoRA
+    backward's dt = (s du) B^T, NT with A scaled, and dB = t^T (s du), TN with
+    B scaled) equals, bit for bit, the Scale into a buffer and then the GEMM
+    on the same plan: every scaled tile config, split-K or not, a K with a
+    partial last stage, and a negative factor."""
+    A, B = rnd(M * K, 81), rnd(K * N, 82)
+    scale = f32(-0.37)
+    sa = layout == 1  # NT: A is the stream; TN: B
+    x = A if sa else B
+    xs = env.T(np.full(x.size, np.nan, f32))
+    env.call("seeml_hip_scale", env.T(x), xs, scale, x.size)
+    assert same_bits(env.H(xs), (scale * x).astype(f32))
+    a_dev, b_dev = env.T(A), env.T(B)
+    ran = 0
+    for cfg in (4, 5, 8, 9, 10, 11):
+        for splits in (1, 4):
+            want = env.T(np.full(M * N, np.nan, f32))
+            env.call("seeml_hip_gemm_forced", layout, xs if sa else a_dev, b_dev if sa else xs, want,
+                     M, N, K, cfg, splits)
+            got = env.T(np.full(M * N, np.nan, f32))
+            env.call("seeml_hip_gemm_forced_scaled", layout, a_dev, b_dev, got, M, N, K, cfg, splits,
+                     scale)
+            assert same_bits(env.H(got), env.H(want)), (cfg, splits)
+            ran += 1
+    assert ran == 12
+    # and the product is the oracle's on the scaled operand
+    ref = np.zeros(M * N, f32)
+    if layout == 1:
+        orc.gemm_nt((scale * A).astype(f32), B, ref, M, N, K)
+    else:
+        orc.gemm_tn(A, (scale * B).astype(f32), ref, M, N, K)
+    assert rel_err(env.H(got), ref) <= TOL_STEP
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 136, 520), (256, 192, 128), (130, 68, 96)])
 def test_gemm_nn_equals_nt_on_the_transposed_operand_bitwise(env, M, N, K):
     """The engine runs a GemmNN on a frozen weight as GemmNT on a transposed
