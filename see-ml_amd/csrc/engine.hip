@@ -1832,8 +1832,79 @@ class Engine {
     run.count = k - i + 1;
     run.kind = ChainKind::kDense;
     run.d = d;
+    run.count += PlanPostAddBias(program, k, c, cdst, write_c, y, o, reads, &run.d,
+                                 plans_[program][i]);
     chains_[program].push_back(run);
     return run.count;
+  }
+
+  // The AddBias of the chain's sum o at k + 1 (h = o + b by column, the
+  // biased MLP layers' up and down projections), and an activation of h at
+  // k + 2 (g = act(h)), folded into the same epilogue (GemmDesc::post_bias)
+  // when the GEMM's plan has the post-AddEW kernels (GemmPostOk). o and h
+  // are stored only while a later instruction reads them. Every written
+  // array (C's store, o, h, g) must be the same range as the addend y or
+  // apart from it, apart from each other unless one overwrites the other,
+  // apart from what the GEMM reads, and apart from the bias: each element
+  // is read and written by one lane, in the unfused order. Returns the
+  // instructions added to the chain (0: none); on 0, *d is unchanged.
+  size_t PlanPostAddBias(int program, size_t k, uint64_t c, uint64_t cdst, bool write_c,
+                         uint64_t y, uint64_t o, const Ranges& gemm_reads, GemmDesc* d,
+                         const GemmPlan& plan) {
+    const auto& prog = plan_.program[program];
+    auto marked = [&](size_t j) {
+      return std::binary_search(marked_[program].begin(), marked_[program].end(), j);
+    };
+    if (k + 1 >= prog.size() || marked(k + 1)) return 0;
+    const UpdateInstruction& ab = prog[k + 1];
+    if (static_cast<Op>(ab.opcode) != Op::kAddBias || ab.in[0] != o) return 0;
+    if (static_cast<int64_t>(ab.out[0]) != d->M || static_cast<int64_t>(ab.out[1]) != d->N ||
+        (d->ldo && d->ldo != d->N))
+      return 0;
+    const uint64_t bias = ab.in[1], h = ab.in[2];
+    const uint64_t n = ab.out[0] * ab.out[1], bytes = n * sizeof(float);
+    if (IsRodataRef(h)) return 0;
+    size_t add = 1;
+    int act = 0;
+    uint64_t g = kNullRef;
+    if (k + 2 < prog.size() && !marked(k + 2)) {
+      const UpdateInstruction& a = prog[k + 2];
+      const auto op = static_cast<Op>(a.opcode);
+      const int code = op == Op::kReluFwd ? 1 : op == Op::kGeluFwd ? 2 : op == Op::kSiluFwd ? 3 : 0;
+      if (code && a.in[0] == h && a.out[0] == n && !IsRodataRef(a.in[1])) {
+        act = code;
+        g = a.in[1];
+        add = 2;
+      }
+    }
+    const size_t last = k + add;
+    const bool o_live = o != h && !(add == 2 && o == g) && !DeadAfter(program, last, RefOffset(o), bytes);
+    const bool h_live = add == 1 || (h != g && !DeadAfter(program, last, RefOffset(h), bytes));
+    // The arrays written, each with its range.
+    std::vector<uint64_t> outs;
+    if (write_c) outs.push_back(cdst);
+    if (o_live) outs.push_back(o);
+    if (h_live) outs.push_back(h);
+    if (add == 2) outs.push_back(g);
+    for (size_t x1 = 0; x1 < outs.size(); ++x1) {
+      const uint64_t r1 = RefOffset(outs[x1]);
+      if (Overlaps(gemm_reads, r1, bytes)) return 0;
+      if (!IsRodataRef(bias) && Overlaps(Ranges{{RefOffset(bias), d->N * sizeof(float)}}, r1, bytes))
+        return 0;
+      if (!IsRodataRef(y) && outs[x1] != y && Overlaps(Ranges{{RefOffset(y), bytes}}, r1, bytes)) return 0;
+      for (size_t x2 = x1 + 1; x2 < outs.size(); ++x2)
+        if (Overlaps(Ranges{{RefOffset(outs[x2]), bytes}}, r1, bytes)) return 0;
+    }
+    (void)c;
+    GemmDesc e = *d;
+    e.post_bias = RP(bias);
+    e.post_h = h_live ? WP(h) : nullptr;
+    e.post_g = add == 2 ? WP(g) : nullptr;
+    e.post_act = act;
+    e.write_out = o_live;
+    if (!aligned16(RP(bias)) || !GemmPostOk(e, plan)) return 0;
+    *d = e;
+    return add;
   }
 
   // Tile groups (kernels.h LaunchGemmGroup): 2..4 consecutive GEMM
@@ -3365,6 +3436,15 @@ class Engine {
       return true;
     }
     if (idx != run->first) return false;
+    if (run->kind == ChainKind::kDense && run->d.post_bias) {
+      const GemmDesc& d = run->d;
+      const double mn = 4.0 * static_cast<double>(d.M) * static_cast<double>(d.N);
+      *flops = GemmFlops(d);
+      *bytes = 4.0 * d.M * d.K + 4.0 * d.K * d.N + mn /* addend */ + (d.write_c ? mn : 0.0) +
+               (d.write_out ? mn : 0.0) + (d.post_h ? mn : 0.0) + (d.post_g ? mn : 0.0) +
+               4.0 * static_cast<double>(d.N);
+      return true;
+    }
     if (run->kind == ChainKind::kLoraBase) {
       const GemmDesc g0 = DescOf(prog[idx]), up = DescOf(prog[idx + 2]);
       double f = GemmFlops(g0) + GemmFlops(up);
@@ -3522,6 +3602,11 @@ class Engine {
     if (run && run->kind == ChainKind::kLoraBase)
       return tiles + " splits=" + std::to_string(p.splits) + " +LoRA" +
              (run->count == 5 ? " +Scale" : "") + " +AddEW";
+    if (run && run->d.post_bias) {  // the bytes as the launch moves them (UnitWork)
+      static const char* kAct[] = {"", " +ReLU", " +GELU", " +SiLU"};
+      return tiles + " splits=" + std::to_string(p.splits) +
+             (run->d.out_scaled ? " +Scale+AddEW" : " +AddEW") + " +Bias" + kAct[run->d.post_act & 3];
+    }
     return tiles + " splits=" + std::to_string(p.splits) +
            (run ? (run->count == 3 ? " +Scale+AddEW" : " +AddEW") : "");
   }

@@ -204,6 +204,10 @@ Status CheckEpilogue(const GemmDesc& d, const GemmPlan& plan) {
                    !GemmLoraCfgOk(plan.cfg, d.b_kc) || !d.a_kc || d.b_int8 || d.batch != 1 ||
                    d.causal != Causal::kNone || d.accumulate || d.bias || !GemmVecForm(d)))
     return Status::Fail(kUnitEngine, "Gemm: unsupported LoRA epilogue");
+  if (d.post_bias && !GemmPostOk(d, plan))
+    return Status::Fail(kUnitEngine, "Gemm: unsupported AddBias after the fused AddEW");
+  if (!d.post_bias && (d.post_h || d.post_g || !d.write_out))
+    return Status::Fail(kUnitEngine, "Gemm: post-AddEW outputs without the AddBias");
   if (d.out && !d.lora_t && (!d.addend || d.batch != 1 || d.ldc != (d.ldo ? d.ldo : d.N) || d.causal != Causal::kNone ||
                 d.accumulate || d.bias))
     return Status::Fail(kUnitEngine,
@@ -276,6 +280,11 @@ Status PrepareKArgs(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx, Gem
   a.lora_r = d.lora_r;
   a.lora_y_first = d.lora_y_first ? 1 : 0;
   a.op_scale = d.scale_stream ? d.stream_scale : 1.0f;
+  a.pbias = d.post_bias;
+  a.hout = d.post_h;
+  a.gout = d.post_g;
+  a.pact = d.post_act;
+  a.write_out = d.write_out ? 1 : 0;
 
   *grid = dim3(static_cast<unsigned>(tm * tn), static_cast<unsigned>(plan.splits),
                static_cast<unsigned>(d.batch));
@@ -346,7 +355,10 @@ Status LaunchGemm(const GemmDesc& d, const GemmPlan& plan, const Ctx& ctx) {
   int cfg = 0;
   bool vec = false;
   if (Status s = PrepareKArgs(d, plan, ctx, &a, &grid, &cfg, &vec); !s) return s;
-  if (d.scale_stream) {  // GemmScaledOk: NT with A the stream, or TN with B
+  if (d.post_bias) {  // GemmPostOk: NN
+    if (!gemm::LaunchPostNN(cfg, grid, ctx.stream, a))
+      return Status::Fail(kUnitEngine, "Gemm: no post-AddEW kernel for this tile config");
+  } else if (d.scale_stream) {  // GemmScaledOk: NT with A the stream, or TN with B
     const bool launched = d.a_kc ? gemm::LaunchScaledNT(cfg, grid, ctx.stream, a)
                                  : gemm::LaunchScaledTN(cfg, grid, ctx.stream, a);
     if (!launched) return Status::Fail(kUnitEngine, "Gemm: no scaled-load kernel for this tile config");
@@ -380,6 +392,13 @@ bool GemmScaledOk(const GemmDesc& d, const GemmPlan& plan) {
   return false;
 }
 
+bool GemmPostOk(const GemmDesc& d, const GemmPlan& plan) {
+  return d.post_bias && d.out && d.addend && !d.lora_t && !d.scale_stream && d.a_kc && !d.b_kc &&
+         !d.b_int8 && d.batch == 1 && d.causal == Causal::kNone && !d.accumulate && !d.bias &&
+         d.act == 0 && plan.splits == 1 && plan.n_split == 0 && gemm::ScaledCfg(plan.cfg) &&
+         GemmVecForm(d) && (d.post_act >= 0 && d.post_act <= 3);
+}
+
 bool GemmLoraCfgOk(int cfg, bool b_kc) {
   return cfg == 2 || cfg == 4 || cfg == 5 || cfg == 8 || cfg == 9 || (cfg == 0 && b_kc);
 }
@@ -391,7 +410,7 @@ bool GemmGroupFits(const GemmDesc* ds, const GemmPlan* ps, int n) {
     const GemmPlan& p = ps[j];
     if (p.cfg != ps[0].cfg || !gemm::GroupCfg(p.cfg) || p.splits != 1 || p.n_split != 0 ||
         d.batch != 1 || d.causal != Causal::kNone || d.b_int8 || !d.a_kc || d.b_kc != ds[0].b_kc ||
-        d.scale_stream || !GemmVecForm(d) || !CheckEpilogue(d, p))
+        d.scale_stream || d.post_bias || !GemmVecForm(d) || !CheckEpilogue(d, p))
       return false;
   }
   return true;

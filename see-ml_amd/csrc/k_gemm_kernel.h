@@ -109,7 +109,31 @@ struct GemmKArgs {
   // A Scale folded into the operand loads (GemmDesc::scale_stream, the
   // SCL instantiations): the scaled operand is read as fl(op_scale * x).
   float op_scale;
+  // The AddBias (+ activation) after the fused AddEW (GemmDesc::post_bias,
+  // the POST instantiations): h = o + pbias[n] to hout, act(h) to gout
+  // (each when set), o to out only with write_out.
+  const float* pbias;
+  float* hout;
+  float* gout;
+  int pact;
+  int write_out;
 };
+
+// The fused AddEW's sum o of value v and addend y, stored with what follows
+// it (POST: the AddBias of bias value b, then the activation) at element
+// offset `at` of the out / hout / gout arrays (one layout, row stride ldo).
+template <bool POST>
+__device__ __forceinline__ void FusedSum(const GemmKArgs& p, int64_t at, float y, float sv, float b) {
+  const float o = p.addend_first ? y + sv : sv + y;
+  if constexpr (!POST) {
+    p.out[at] = o;
+  } else {
+    if (p.write_out) p.out[at] = o;
+    const float h = o + b;
+    if (p.hout) p.hout[at] = h;
+    if (p.gout) p.gout[at] = dev_act(p.pact, h);
+  }
+}
 
 // Tile configurations (the autotuner's arms).
 struct CfgInfo {
@@ -288,9 +312,11 @@ __device__ __forceinline__ uint32_t XcdLogical(uint32_t lin, uint32_t total) {
 // compile those epilogues in; each applies to a work item whose arguments
 // ask for it (p.out / p.lora_t set), any other takes the plain write-back.
 // SCL: a Scale folded into the loads of A (1) or B (2), factor p.op_scale.
+// POST (with FUSED): the AddBias (+ activation) after the fused AddEW.
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED, bool LORA, int SCL = 0>
+          bool VEC, bool SCHED, bool FUSED, bool LORA, int SCL = 0, bool POST = false>
 __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32_t nslices) {
+  static_assert(!POST || (FUSED && !LORA && !(MT_M == 256 && MT_N == 128)), "post-AddEW variants");
   using BT = typename std::conditional<B_I8, int8_t, float>::type;
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = MT_M / WAVES_M, WN = MT_N / WAVES_N;
@@ -678,12 +704,21 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
     }
   }
   if constexpr (FUSED) {
-    if (p.out && p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N) {
+    if (p.out && p.splits == 1 && m0 + MT_M <= p.M && n0 + MT_N <= p.N &&
+        (!POST || MT_M * p.ldo * 4 < (int64_t{1} << 30))) {
       const int64_t lm = m0 + wm0 + 4 * h, ln = n0 + wn0 + r;
       const float* ya = p.addend + lm * p.ldo + ln;
       float* oa = p.out + lm * p.ldo + ln;
       float* ca = C + lm * p.ldc + ln;
       float yv[BM][BN][16];
+      float pb[BN];  // POST: the AddBias values of the lane's columns
+#pragma unroll
+      for (int j = 0; j < BN; ++j) pb[j] = POST ? p.pbias[ln + 32 * j] : 0.0f;
+      const int64_t tile0 = m0 * p.ldo + n0;
+      char* post_o = POST ? reinterpret_cast<char*>(p.out + tile0) : nullptr;
+      char* post_h = POST && p.hout ? reinterpret_cast<char*>(p.hout + tile0) : nullptr;
+      char* post_g = POST && p.gout ? reinterpret_cast<char*>(p.gout + tile0) : nullptr;
+      const uint32_t post_lane = static_cast<uint32_t>(((lm - m0) * p.ldo + (ln - n0)) * 4);
 #pragma unroll
       for (int i = 0; i < BM; ++i)
 #pragma unroll
@@ -702,7 +737,19 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
             const float sv = p.out_scaled ? p.out_scale * val : val;
             if (p.write_c) ca[row * p.ldc + 32 * j] = p.c_scaled ? sv : val;
             const float y = yv[i][j][v];
-            oa[row * p.ldo + 32 * j] = p.addend_first ? y + sv : sv + y;
+            if constexpr (POST) {
+              // 32-bit byte offsets from the tile's wave-uniform origin (the
+              // tile's span is checked to fit): three output arrays with no
+              // 64-bit address per element.
+              const uint32_t at = post_lane + static_cast<uint32_t>((row * p.ldo + 32 * j) * 4);
+              const float o = p.addend_first ? y + sv : sv + y;
+              if (p.write_out) *reinterpret_cast<float*>(post_o + at) = o;
+              const float hv = o + pb[j];
+              if (p.hout) *reinterpret_cast<float*>(post_h + at) = hv;
+              if (p.gout) *reinterpret_cast<float*>(post_g + at) = dev_act(p.pact, hv);
+            } else {
+              oa[row * p.ldo + 32 * j] = p.addend_first ? y + sv : sv + y;
+            }
           }
       return;
     }
@@ -758,7 +805,10 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
           const float sv = p.out_scaled ? p.out_scale * val : val;
           if (p.write_c) C[m * p.ldc + n] = p.c_scaled ? sv : val;
           const float y = p.addend[m * p.ldo + n];
-          p.out[m * p.ldo + n] = p.addend_first ? y + sv : sv + y;
+          if constexpr (POST)
+            FusedSum<true>(p, m * p.ldo + n, y, sv, p.pbias[n]);
+          else
+            p.out[m * p.ldo + n] = p.addend_first ? y + sv : sv + y;
         } else {
           C[m * p.ldc + n] = val;
         }
@@ -766,12 +816,12 @@ __device__ __forceinline__ void gemm_tile(const GemmKArgs& p, uint32_t L, uint32
 }
 
 template <int MT_M, int MT_N, int KT, int WAVES_M, int WAVES_N, bool A_KC, bool B_KC, bool B_I8,
-          bool VEC, bool SCHED, bool FUSED, bool LORA = false, int SCL = 0>
+          bool VEC, bool SCHED, bool FUSED, bool LORA = false, int SCL = 0, bool POST = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_mfma_kernel(GemmKArgs p) {
   const uint32_t tiles = static_cast<uint32_t>(p.tiles_m) * static_cast<uint32_t>(p.tiles_n);
   const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const uint32_t L = XcdLogical(lin, tiles * gridDim.y * gridDim.z);
-  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, B_I8, VEC, SCHED, FUSED, LORA, SCL>(
+  gemm_tile<MT_M, MT_N, KT, WAVES_M, WAVES_N, A_KC, B_KC, B_I8, VEC, SCHED, FUSED, LORA, SCL, POST>(
       p, L, gridDim.y);
 }
 
@@ -909,6 +959,30 @@ bool LaunchScaledVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) 
 #undef SEEML_SCALED_CASE
 }
 
+// The post-AddEW instantiations (GemmKArgs::pbias): the fused AddEW's GEMM
+// with an AddBias (+ activation) after it, on the small tile configs (the
+// rank-64 LoRA up-projections u = t B feeding the biased MLP layers).
+template <bool A_KC, bool B_KC>
+bool LaunchPostVariant(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a) {
+#define SEEML_POST_CASE(I, MM, NN, KK, WM_, WN_)                                                      \
+  case I:                                                                                            \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MM, NN, KK, WM_, WN_, A_KC, B_KC, false, true, true, true, false, \
+                                         0, true>),                                                  \
+                       grid, dim3(kCfgs[I].threads), 0, s, a);                                       \
+    return true;
+  switch (cfg) {
+    SEEML_POST_CASE(4, 128, 64, 32, 2, 2)
+    SEEML_POST_CASE(5, 64, 64, 32, 2, 2)
+    SEEML_POST_CASE(8, 64, 128, 32, 2, 2)
+    SEEML_POST_CASE(9, 128, 64, 32, 4, 1)
+    SEEML_POST_CASE(10, 128, 128, 16, 2, 2)
+    SEEML_POST_CASE(11, 64, 128, 16, 2, 2)
+    default:
+      return false;
+  }
+#undef SEEML_POST_CASE
+}
+
 // Per-layout entry points, one instantiation unit each (built in parallel).
 void LaunchNN(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
 void LaunchNT(int cfg, bool vec, dim3 grid, hipStream_t s, const GemmKArgs& a);
@@ -922,6 +996,8 @@ bool LaunchGroupNT(int cfg, dim3 grid, hipStream_t s, const GemmGroupArgs& g);
 // config without the instantiation.
 bool LaunchScaledNT(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a);
 bool LaunchScaledTN(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a);
+// Post-AddEW launches (NN); false for a config without the instantiation.
+bool LaunchPostNN(int cfg, dim3 grid, hipStream_t s, const GemmKArgs& a);
 
 }  // namespace gemm
 }  // namespace seeml_hip

@@ -98,6 +98,15 @@ struct GemmDesc {
   bool out_scaled = false;
   float out_scale = 1.0f;
   bool c_gets_scaled = false;
+  // After the fused AddEW (GemmPostOk): an AddBias of its sum o, and
+  // optionally an activation of that: h = fl(o + post_bias[n]) stored to
+  // post_h (when set), g = act(h) (post_act as dev_act) stored to post_g
+  // (when set); o itself is stored to out only with write_out.
+  const float* post_bias = nullptr;
+  float* post_h = nullptr;
+  float* post_g = nullptr;
+  int post_act = 0;
+  bool write_out = true;
   int64_t ldo = 0;  // row stride of addend and out (0: N, the fused-AddEW default)
   // A LoRA up-projection folded into the epilogue (with out; addend unused):
   // out = c (+) fl(out_scale * u) (out_scale only when out_scaled), where
@@ -160,6 +169,10 @@ bool GemmLoraCfgOk(int cfg, bool b_kc);
 // tile config with scaled-load kernels, one launch (no column split), the
 // 16-byte-load form and a plain epilogue.
 bool GemmScaledOk(const GemmDesc& d, const GemmPlan& plan);
+// A tile plan that takes the AddBias (+ activation) after a fused AddEW
+// (GemmDesc::post_bias): NN, a small tile config with the post-AddEW
+// instantiation, one slice, no column split, the 16-byte-load form.
+bool GemmPostOk(const GemmDesc& d, const GemmPlan& plan);
 // GEMM groups: 2..4 GEMMs launched as one kernel, each output with the bits
 // of its own launch. Fits: one tile config with a group kernel for all,
 // each unsplit (one slice, no column split), unbatched, non-causal, in the

@@ -651,6 +651,51 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc, cfg):
     assert rel_err(runs[0][1], persistent(r, p)) <= TOL_STEP
 
 
+def test_bias_and_activation_after_the_fused_addew(torch_gpu, orc):
+    """With the rank-64 up-projections u = t B on a tile that has the
+    post-AddEW kernels (64x128x16, forced here as C5's autotuner picks it),
+    the chain GEMM + Scale + AddEW also takes the biased MLP layers' AddBias
+    and the GELU after it (up projection) or the AddBias alone (down
+    projection) into its epilogue. The fused graph equals the eager engine
+    (every instruction on its own) bit for bit and the oracle to tolerance."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c5m64")
+    r = w.cfg.lora.rank
+    up = [i for i, ins in enumerate(p.train)
+          if ins["opcode"] == planner.OP["GemmNN"] and ins["out"][2] == r and ins["out"][0] == w.cfg.batch]
+    assert up
+    runs = []
+    for use_graph in (True, False):
+        e = engine(p, use_graph=use_graph)
+        for i in up:
+            assert e._L.seeml_hip_set_gemm_plan(e._h, PROGRAM_TRAIN, i, 11, 1) == 0
+        losses = []
+        for s in range(2):
+            x, y = configs.batch(w, s)
+            losses.append(e.train_step(x, y))
+        if use_graph:
+            ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+            gelu = [i for i, c in enumerate(ch) if c.endswith("+AddEW +Bias +GELU")]
+            bias = [i for i, c in enumerate(ch) if c.endswith("+AddEW +Bias")]
+            assert gelu and bias, ch
+            for i in gelu + bias:
+                k = i + (3 if "+Scale" in ch[i] else 2)  # the AddBias
+                assert planner.OP_NAME[p.train[k]["opcode"]] == "AddBias"
+                assert ch[k] == "in GEMM epilogue"
+            for i in gelu:
+                k = i + (4 if "+Scale" in ch[i] else 3)
+                assert planner.OP_NAME[p.train[k]["opcode"]] == "GeluFwd" and ch[k] == "in GEMM epilogue"
+        runs.append((np.array(losses, np.float32), persistent(e, p)))
+        e.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    hr = HostPlanRunner(p, orc)
+    for s in range(2):
+        x, y = configs.batch(w, s)
+        lr = hr.train_step(x, y)
+        assert abs(runs[0][0][s] - lr) <= TOL_STEP * max(abs(lr), 1e-3), (s, runs[0][0][s], lr)
+
+
 def test_loss_pass_is_planned_and_matches_the_oracle(torch_gpu, orc):
     """Over a vocabulary of 2048 the loss forward, the seed Fill and the loss
     backward run as one pass over the logits, P not stored (its only reader
