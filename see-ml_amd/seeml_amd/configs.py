@@ -203,6 +203,9 @@ def make(name: str) -> Workload:
         # dB = t^T (s du) are rowdot / colsum shapes on tile plans: the Scale
         # folds into their loads
         "c5m64": (1000, 256, 2, 4, 512, 128, 2, 64, (), 1e-3, "layer", "gelu"),
+        # odd widths (200 tokens, an MLP of 520): partial tiles in both
+        # dimensions for the fused epilogues
+        "c5o64": (1000, 256, 1, 4, 520, 100, 2, 64, (), 1e-3, "layer", "gelu"),
         # head widths 64 and 128: the fused attention kernels' shapes
         "c3m": (512, 128, 2, 2, 192, 64, 4, 8, ("wq", "wv"), 1e-3, "rms", "swiglu"),
         "c4m": (1000, 256, 2, 2, 512, 128, 2, 16, ("wq", "wk", "wv", "wo"), 1e-4, "rms", "swiglu"),

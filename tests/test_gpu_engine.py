@@ -651,15 +651,18 @@ def test_lora_base_runs_are_planned_and_bitwise(torch_gpu, orc, cfg):
     assert rel_err(runs[0][1], persistent(r, p)) <= TOL_STEP
 
 
-def test_bias_and_activation_after_the_fused_addew(torch_gpu, orc):
+@pytest.mark.parametrize("name", ["c5m64", "c5o64"])
+def test_bias_and_activation_after_the_fused_addew(torch_gpu, orc, name):
     """With the rank-64 up-projections u = t B on a tile that has the
     post-AddEW kernels (64x128x16, forced here as C5's autotuner picks it),
     the chain GEMM + Scale + AddEW also takes the biased MLP layers' AddBias
     and the GELU after it (up projection) or the AddBias alone (down
-    projection) into its epilogue. The fused graph equals the eager engine
-    (every instruction on its own) bit for bit and the oracle to tolerance."""
+    projection) into its epilogue; c5o64's 200 tokens and MLP of 520 put
+    partial tiles in both dimensions. The fused graph equals the eager
+    engine (every instruction on its own) bit for bit and the oracle to
+    tolerance."""
     from seeml_amd import PROGRAM_TRAIN
-    w, p = compile_workload("c5m64")
+    w, p = compile_workload(name)
     r = w.cfg.lora.rank
     up = [i for i, ins in enumerate(p.train)
           if ins["opcode"] == planner.OP["GemmNN"] and ins["out"][2] == r and ins["out"][0] == w.cfg.batch]
