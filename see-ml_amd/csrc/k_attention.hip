@@ -147,8 +147,11 @@ __device__ __forceinline__ void MaskDiagonal(floatx16& sc, int t, int i, int h, 
 
 // S^T tile (32 keys x 32 queries) from the LDS K tile and the lane's Q
 // fragments: MFMA (g, jj) takes feature 8g + 4h + jj on both operands. Two
-// accumulators (even/odd g) keep consecutive MFMAs independent.
-template <int D>
+// accumulators (even/odd g) keep consecutive MFMAs independent. ORDER pins
+// the issue order (below); the forward leaves it to the scheduler, which
+// interleaves its parked-score traffic better (C4 step: AttnFwd 5.69 ->
+// 5.90 ms per 16 launches with the order pinned, AttnDP 2.69 -> 2.67 ms).
+template <int D, bool ORDER = false>
 __device__ __forceinline__ floatx16 ScoreTile(const float* __restrict__ kt,
                                               const float4 (&qf)[D / 8], int h, int r) {
   floatx16 a0, a1;
@@ -170,6 +173,17 @@ __device__ __forceinline__ floatx16 ScoreTile(const float* __restrict__ kt,
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.y, qf[g].y, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.z, qf[g].z, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(f.w, qf[g].w, acc, 0, 0, 0);
+  }
+  // Issue order as written: read g + 1, then g's four MFMAs, so each read's
+  // latency runs under them (left alone, the scheduler pairs the reads and
+  // waits on each right after issuing it).
+  if constexpr (ORDER) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int g = 0; g < D / 8; ++g) {
+      if (g + 1 < D / 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
   }
   return a0 + a1;
 }
@@ -200,7 +214,7 @@ __device__ __forceinline__ Frag<D> ReadFrag(const float* __restrict__ tile, int 
   return f;
 }
 
-template <int D, typename PV>
+template <int D, bool ORDER = false, typename PV>
 __device__ __forceinline__ void AccumulateTile(const float* __restrict__ tile, const PV& pv, int h,
                                                int r, floatx16 (&acc)[D / 32]) {
   constexpr int NB = D / 32;
@@ -212,6 +226,17 @@ __device__ __forceinline__ void AccumulateTile(const float* __restrict__ tile, c
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
       acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[e & 1].v[nb], pv[e], acc[nb], 0, 0, 0);
+  }
+  // ORDER: issue order as written (read e + 1, then e's NB MFMAs), as in
+  // ScoreTile (C4 step: AttnDQ 2.74 -> 2.64 ms, AttnDV 3.00 -> 2.84 ms and
+  // AttnDK 2.91 -> 2.88 ms per 16 launches, with dK/dV's column loads).
+  if constexpr (ORDER) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (e + 1 < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+    }
   }
 }
 
@@ -451,7 +476,7 @@ __device__ __forceinline__ void AttnDpWave(const float* __restrict__ dh, const f
   for (int t = 0; t < tiles_wg; ++t) {
     if (t + 1 < tiles_wg) vs.load(vh, ld, (t + 1) * kAttnK, S);
     if (t < tiles_w) {
-      floatx16 sc = ScoreTile<D>(vt + (t & 1) * kBuf, qf, h, r);
+      floatx16 sc = ScoreTile<D, true>(vt + (t & 1) * kBuf, qf, h, r);
       if (t == tiles_w - 1) MaskDiagonal(sc, t, i, h, 0.0f);
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
@@ -573,7 +598,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dq_fused(
           if (j > i) g[e] = 0.0f;
         }
       }
-      AccumulateTile<D>(kt[t & 1], g, h, r, acc);
+      AccumulateTile<D, true>(kt[t & 1], g, h, r, acc);
     }
     if (t + 1 < tiles_wg) {
       ks.store(kt[(t + 1) & 1]);
@@ -616,48 +641,62 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_dkv_fused(
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
-  // Column entries (i = 32t + 8*(e/4) + 4h + e%4, j) of query tile t.
+  // Column entries (i = 32t + 8*(e/4) + 4h + e%4, j) of query tile t, loaded
+  // unconditionally from rows clamped into the slab (32-bit offsets: S*S
+  // fits), so the loads carry no branches; entries outside the causal half
+  // (i < j, i >= S, j >= S) are zeroed where used, by an AND of the bits.
+  const float* pcol = ph + min(j, S - 1);
   auto load_col = [&](int t, float (&g)[16]) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int ii = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
-      g[e] = (col_ok && t >= tw && ii < S && ii >= j) ? ph[static_cast<int64_t>(ii) * S + j] : 0.0f;
+      const int ii = min(t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3), S - 1);
+      g[e] = pcol[static_cast<uint32_t>(ii) * static_cast<uint32_t>(S)];
     }
   };
+  // One query tile: the next tile's X rows and column entries are loaded
+  // into the other register set (gn) while this tile's (gc) are used, so
+  // no copy between them waits for the loads in flight. The loads and the
+  // LDS store are unconditional (the last tile reloads itself into the idle
+  // buffer), so every path through a tile leaves the same loads in flight
+  // and the waits before the MFMAs count only the older set.
   KvTile<D> xs;
-  float g[16], gn[16];
+  auto tile = [&](int t, float (&gc)[16], float (&gn)[16]) {
+    const int tn = min(t + 1, ntiles - 1);
+    xs.load(xh, ld, tn * kAttnK, S);
+    load_col(tn, gn);
+    if (t >= tw && kw < S) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int ii = t * kAttnK + 8 * (e >> 2) + 4 * h + (e & 3);
+        const unsigned keep = static_cast<unsigned>(col_ok) & static_cast<unsigned>(ii < S) &
+                              static_cast<unsigned>(ii >= j);
+        gc[e] = __uint_as_float(__float_as_uint(gc[e]) & (0u - keep));
+        if constexpr (SCALED) gc[e] = gc[e] * scale;
+      }
+      AccumulateTile<D, true>(xt[(t - t0) & 1], gc, h, r, acc);
+    }
+    xs.store(xt[(t + 1 - t0) & 1]);
+    __syncthreads();
+  };
+  float ga[16], gb[16];
   xs.load(xh, ld, t0 * kAttnK, S);
-  load_col(t0, g);
+  load_col(t0, ga);
   xs.store(xt[0]);
   __syncthreads();
-  for (int t = t0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) {
-      xs.load(xh, ld, (t + 1) * kAttnK, S);
-      load_col(t + 1, gn);
-    }
-    if (t >= tw && kw < S) {
-      if constexpr (SCALED) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) g[e] = g[e] * scale;
-      }
-      AccumulateTile<D>(xt[(t - t0) & 1], g, h, r, acc);
-    }
-    if (t + 1 < ntiles) {
-      xs.store(xt[(t + 1 - t0) & 1]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) g[e] = gn[e];
-    }
-    __syncthreads();
+  for (int t = t0; t < ntiles; t += 2) {
+    tile(t, ga, gb);
+    if (t + 1 < ntiles) tile(t + 1, gb, ga);
   }
   if (col_ok) StoreRow<D>(oh + static_cast<int64_t>(j) * ld, acc, h);
 }
 
 // The fused kernels' shape gate: d in {64, 128}, S % 4 == 0 (16-byte P
-// rows), 16-byte aligned operands, 32-bit grid indices.
+// rows), S * S < 2^31 (32-bit offsets inside one (b, h) slab of P),
+// 16-byte aligned operands, 32-bit grid indices.
 bool FusedEligible(std::initializer_list<const float*> ptrs, size_t B, size_t S, size_t H,
                    size_t d) {
   if (d != 64 && d != 128) return false;
-  if (S == 0 || S % 4 != 0) return false;
+  if (S == 0 || S % 4 != 0 || S > 46340) return false;
   for (const float* p : ptrs)
     if (!aligned16(p)) return false;
   const size_t blocks = B * H * ((S + kAttnQ - 1) / kAttnQ);

@@ -60,7 +60,12 @@ size_t PartialBlocks(size_t n) {
 }
 
 // Block b owns the contiguous range [b*chunk, (b+1)*chunk): a shape-only
-// decomposition, like ParallelFor's.
+// decomposition, like ParallelFor's. Each thread sums its elements in index
+// order (DIFF: (a - b)^2, else a^2, in double); the block's threads are
+// then reduced in a fixed tree. VEC (16-byte operands, chunk % 4 == 0):
+// the thread's elements are whole float4 runs, four runs of each operand in
+// flight per step, and only the last block can have a scalar tail.
+template <bool VEC, bool DIFF>
 __global__ __launch_bounds__(kBlock) void sq_diff_partials(const float* __restrict__ a,
                                                            const float* __restrict__ b,
                                                            size_t n, size_t chunk,
@@ -68,14 +73,74 @@ __global__ __launch_bounds__(kBlock) void sq_diff_partials(const float* __restri
   __shared__ double scratch[kBlock / kWave];
   const size_t begin = static_cast<size_t>(blockIdx.x) * chunk;
   const size_t end = begin + chunk < n ? begin + chunk : n;
+  auto term = [&](float x, float y) {
+    const double d = DIFF ? static_cast<double>(x) - static_cast<double>(y) : static_cast<double>(x);
+    return d * d;
+  };
   double acc = 0.0;
-  for (size_t i = begin + threadIdx.x; i < end; i += kBlock) {
-    const double d = b ? static_cast<double>(a[i]) - static_cast<double>(b[i])
-                       : static_cast<double>(a[i]);
-    acc += d * d;
+  size_t tail = begin + threadIdx.x;
+  if constexpr (VEC) {
+    const float4* a4 = reinterpret_cast<const float4*>(a);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    const size_t v1 = end / 4;
+    size_t i = begin / 4 + threadIdx.x;
+    for (; i + 3 * kBlock < v1; i += 4 * kBlock) {
+      float4 x[4], y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x[u] = a4[i + u * kBlock];
+        if constexpr (DIFF) y[u] = b4[i + u * kBlock];
+        else y[u] = x[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc += term(x[u].x, y[u].x);
+        acc += term(x[u].y, y[u].y);
+        acc += term(x[u].z, y[u].z);
+        acc += term(x[u].w, y[u].w);
+      }
+    }
+    for (; i < v1; i += kBlock) {
+      const float4 x = a4[i];
+      const float4 y = DIFF ? b4[i] : x;
+      acc += term(x.x, y.x);
+      acc += term(x.y, y.y);
+      acc += term(x.z, y.z);
+      acc += term(x.w, y.w);
+    }
+    tail = 4 * v1 + threadIdx.x;
   }
+  for (size_t k = tail; k < end; k += kBlock) acc += term(a[k], DIFF ? b[k] : 0.0f);
   const double t = block_sum<double, kBlock>(acc, scratch);
   if (threadIdx.x == 0) out[blockIdx.x] = t;
+}
+
+// The partials' geometry: at most PartialBlocks(n) blocks; with VEC the
+// chunk is rounded up to whole float4s (fewer blocks, never more).
+struct PartialGeo {
+  size_t blocks, chunk;
+  bool vec;
+};
+
+PartialGeo MakePartialGeo(size_t n, const float* a, const float* b) {
+  const size_t g = PartialBlocks(n);
+  size_t chunk = (n + g - 1) / g;
+  const bool vec = aligned16(a) && (!b || aligned16(b));
+  if (vec) chunk = (chunk + 3) / 4 * 4;
+  return {(n + chunk - 1) / chunk, chunk, vec};
+}
+
+void LaunchSqPartials(const PartialGeo& pg, const float* a, const float* b, size_t n,
+                      double* partials, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(pg.blocks));
+  if (pg.vec && b)
+    hipLaunchKernelGGL((sq_diff_partials<true, true>), grid, dim3(kBlock), 0, stream, a, b, n, pg.chunk, partials);
+  else if (pg.vec)
+    hipLaunchKernelGGL((sq_diff_partials<true, false>), grid, dim3(kBlock), 0, stream, a, b, n, pg.chunk, partials);
+  else if (b)
+    hipLaunchKernelGGL((sq_diff_partials<false, true>), grid, dim3(kBlock), 0, stream, a, b, n, pg.chunk, partials);
+  else
+    hipLaunchKernelGGL((sq_diff_partials<false, false>), grid, dim3(kBlock), 0, stream, a, b, n, pg.chunk, partials);
 }
 
 // ClipNorm decision + scale on device (optimizer.cc:28-34): sum the
@@ -958,13 +1023,12 @@ size_t MseFwdWorkspace(size_t n) { return PartialBlocks(n) * sizeof(double); }
 
 Status MseFwd(const float* pred, const float* target, float* loss, size_t n, const Ctx& c) {
   if (n == 0) return Status::Fail(kUnitEngine, "MseFwd: empty input");
-  const size_t g = PartialBlocks(n);
-  if (c.ws_bytes < g * sizeof(double)) return Status::Fail(kUnitEngine, "MseFwd: workspace too small");
-  const size_t chunk = (n + g - 1) / g;
+  const PartialGeo pg = MakePartialGeo(n, pred, target);
+  if (c.ws_bytes < pg.blocks * sizeof(double))
+    return Status::Fail(kUnitEngine, "MseFwd: workspace too small");
   double* partials = static_cast<double*>(c.ws);
-  hipLaunchKernelGGL(sq_diff_partials, dim3(static_cast<unsigned>(g)), dim3(kBlock), 0, c.stream,
-                     pred, target, n, chunk, partials);
-  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, partials, g,
+  LaunchSqPartials(pg, pred, target, n, partials, c.stream);
+  hipLaunchKernelGGL(finish_mean_kernel, dim3(1), dim3(kBlock), 0, c.stream, partials, pg.blocks,
                      static_cast<double>(n), loss);
   return LaunchStatus("MseFwd");
 }
@@ -973,15 +1037,13 @@ size_t ClipNormWorkspace(size_t n) { return PartialBlocks(n) * sizeof(double); }
 
 Status ClipNorm(float* g, size_t n, float max_norm, const Ctx& c) {
   if (n == 0) return Status::Ok();
-  const size_t blocks = PartialBlocks(n);
-  if (c.ws_bytes < blocks * sizeof(double))
+  const PartialGeo pg = MakePartialGeo(n, g, nullptr);
+  if (c.ws_bytes < pg.blocks * sizeof(double))
     return Status::Fail(kUnitEngine, "ClipNorm: workspace too small");
-  const size_t chunk = (n + blocks - 1) / blocks;
   double* partials = static_cast<double*>(c.ws);
-  hipLaunchKernelGGL(sq_diff_partials, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
-                     c.stream, g, nullptr, n, chunk, partials);
+  LaunchSqPartials(pg, g, nullptr, n, partials, c.stream);
   hipLaunchKernelGGL(clip_apply_kernel, dim3(grid_for(n, kBlock, 4096)), dim3(kBlock), 0,
-                     c.stream, g, n, partials, blocks, max_norm);
+                     c.stream, g, n, partials, pg.blocks, max_norm);
   return LaunchStatus("ClipNorm");
 }
 
