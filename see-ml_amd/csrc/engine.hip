@@ -3064,6 +3064,31 @@ class Engine {
     return Status::Ok();
   }
 
+  // The Scale whose output GEMM g would read through PlanScaleFolds' fold
+  // (its pattern, without the liveness and hazard checks made when the graph
+  // is built): the Scale right before the run of GEMMs that holds g, each
+  // streaming its output, the Scale's output in the arena (transient, so
+  // autotuning may run it), its input 16-byte aligned. -1 if none.
+  long FoldScaleOf(int program, size_t g) const {
+    const auto& prog = plan_.program[program];
+    size_t i = g;
+    while (i > 0 && IsGemmOp(prog[i - 1].opcode)) --i;
+    if (i == 0 || static_cast<Op>(prog[i - 1].opcode) != Op::kScale) return -1;
+    const UpdateInstruction& sc = prog[i - 1];
+    if (IsRodataRef(sc.in[1]) || RefOffset(sc.in[1]) < plan_.header.persistent_size ||
+        !aligned16(RP(sc.in[0])))
+      return -1;
+    for (size_t j = i; j <= g; ++j) {
+      const GemmDesc d = DescOf(prog[j]);
+      int64_t elems = 0;
+      const void* stream = SkinnyStream(d, &elems);
+      if (stream != WP(sc.in[1]) || static_cast<uint64_t>(elems) != sc.out[0] ||
+          (d.A == stream ? d.B : d.A) == WP(sc.in[1]))
+        return -1;
+    }
+    return static_cast<long>(i - 1);
+  }
+
   Status Autotune(int budget, RewardFn inject = nullptr, void* inject_ctx = nullptr) {
     loss_posted_ = false;  // runs instructions outside Run()
     const int program = static_cast<int>(Program::kTrain);
@@ -3130,6 +3155,23 @@ class Engine {
         for (size_t i : idxs) plans_[program][i] = best;
         continue;
       }
+      // A Scale that PlanScaleFolds would fold into this GEMM's stream loads
+      // is launched only when the GEMM's plan cannot take the fold: an arm
+      // that takes it is timed as the folded launch (reading x with the
+      // factor applied), any other as its own launch plus the Scale's.
+      const long fold_at = FoldScaleOf(program, first);
+      GemmDesc fd = d;
+      std::vector<char> folds(arms.size(), 0);
+      if (fold_at >= 0) {
+        const UpdateInstruction& sc = prog[static_cast<size_t>(fold_at)];
+        int64_t elems = 0;
+        const void* stream = SkinnyStream(d, &elems);
+        if (fd.A == stream) fd.A = RP(sc.in[0]);
+        else fd.B = RP(sc.in[0]);
+        fd.scale_stream = true;
+        fd.stream_scale = Bits(sc.in[2]);
+        for (size_t a = 0; a < arms.size(); ++a) folds[a] = GemmScaledOk(fd, arms[a]) ? 1 : 0;
+      }
       size_t need = 0;
       for (const auto& a : arms) need = std::max(need, a.ws_bytes);
       if (need > ws_bytes_) {
@@ -3143,6 +3185,12 @@ class Engine {
       }
       const Ctx c = MakeCtx();
       const double flops = 2.0 * static_cast<double>(d.M) * d.N * d.K;
+      auto launch = [&](size_t a) -> Status {
+        if (folds[a]) return LaunchGemm(fd, arms[a], c);
+        if (fold_at >= 0)
+          if (Status s = Dispatch(program, static_cast<size_t>(fold_at), c); !s) return s;
+        return LaunchGemm(d, arms[a], c);
+      };
       // One warm-up launch per arm, timed: a pull of an arm then times
       // enough back-to-back launches to fill ~0.2 ms (at most 16), so that
       // the short GEMMs (the K = rank up-projections, ~20 us) are ranked by
@@ -3150,7 +3198,7 @@ class Engine {
       std::vector<int> reps(arms.size(), 1);
       for (size_t a = 0; a < arms.size() && result; ++a) {
         (void)hipEventRecord(t0, stream_);
-        if (Status s = LaunchGemm(d, arms[a], c); !s) { result = s; break; }
+        if (Status s = launch(a); !s) { result = s; break; }
         (void)hipEventRecord(t1, stream_);
         (void)hipEventSynchronize(t1);
         float ms = 0.0f;
@@ -3166,7 +3214,7 @@ class Engine {
         const size_t arm = bandit.Select();
         (void)hipEventRecord(t0, stream_);
         for (int r = 0; r < reps[arm] && result; ++r)
-          if (Status s = LaunchGemm(d, arms[arm], c); !s) result = s;
+          if (Status s = launch(arm); !s) result = s;
         if (!result) break;
         (void)hipEventRecord(t1, stream_);
         (void)hipEventSynchronize(t1);
