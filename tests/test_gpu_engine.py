@@ -821,6 +821,30 @@ def test_scale_folds_into_rank_64_tile_gemms(torch_gpu):
     e.close()
 
 
+def test_autotune_keeps_the_scale_folds(torch_gpu):
+    """Autotuning times an arm that cannot take a pending Scale fold as the
+    Scale's launch plus its own (one that can, as the folded launch), so on
+    the rank-64 plan every Scale that folds under the heuristic plans still
+    folds after tuning; the tuned step has the untuned step's bits (no arm
+    changes a GEMM's summation order)."""
+    from seeml_amd import PROGRAM_TRAIN
+    w, p = compile_workload("c5m64")
+    x, y = configs.batch(w, 0)
+    folds, losses, states = [], [], []
+    for tune in (False, True):
+        e = engine(p)
+        if tune:
+            e.autotune(8)
+        losses.append(e.train_step(x, y))
+        ch = [e.gemm_choice(PROGRAM_TRAIN, i) for i in range(len(p.train))]
+        folds.append({i for i, c in enumerate(ch) if c == "in the next GEMMs' loads"})
+        states.append(persistent(e, p))
+        e.close()
+    assert folds[0] and folds[0] <= folds[1], (sorted(folds[0]), sorted(folds[1]))
+    assert np.float32(losses[0]).tobytes() == np.float32(losses[1]).tobytes(), losses
+    assert np.array_equal(states[0].view(np.uint32), states[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("name,norm", [("c3s", "RmsNormBwd"), ("c5s64", "LayerNormBwd")])
 def test_norm_kernels_run_the_adjacent_addews(torch_gpu, name, norm):
     """The residual stream's AddEWs next to a norm run inside the norm
